@@ -1,0 +1,167 @@
+/* trit_hip: Trit's decoder token loop on MI355X (gfx950), behind a C ABI.
+ *
+ * This library replaces, for one GPU, the products and the token loop that
+ * Trit runs on its CPU kernels. Each entry point names the reference
+ * interface it stands in for (paths into Hi9841/trit).
+ *
+ * Rules for every function (as in the reference's include/trit.h:8-17 and
+ * ffi/src/lib.rs:1-46):
+ * - A call that fails returns -1 (or NULL) and sets the calling thread's
+ *   error text, which trit_hip_last_error() returns. No C++ exception
+ *   crosses the ABI.
+ * - Pointers named host_* or taking plain `const float*` inputs in the
+ *   layer and session calls are host memory; *_device calls take device
+ *   pointers and a hipStream_t (NULL: the library's stream).
+ * - Layer and decoder handles are immutable after creation and may be
+ *   shared across threads. A session belongs to one thread at a time.
+ * - Weights are copied into device memory at creation; the handle owns
+ *   them. A decoder keeps its layers alive: the caller may free its layer
+ *   handles right after trit_hip_decoder_new.
+ */
+#ifndef TRIT_HIP_H
+#define TRIT_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct TritHipLayer TritHipLayer;
+typedef struct TritHipDecoder TritHipDecoder;
+typedef struct TritHipSession TritHipSession;
+
+/* Library version text. Static. */
+const char *trit_hip_version(void);
+
+/* Error of the last failed call on this thread, "" after a success.
+ * Mirrors trit_last_error (reference include/trit.h:44-46,
+ * ffi/src/lib.rs:20-46). */
+const char *trit_hip_last_error(void);
+
+/* Selects and initialises `device` for this thread and creates the
+ * library's stream on it. Stands in for gpu::Gpu::get
+ * (reference src/gpu/mod.rs:36-128). 0 on success. */
+int trit_hip_init(int device);
+
+/* ---- Layers: the Dense seam (reference src/cpu/gemm.rs:15-35,500-542) --- */
+
+enum {
+    TRIT_HIP_Q8_0 = 1,    /* ggml Q8_0: 32 int8 codes + f16 scale per block   */
+    TRIT_HIP_INT8 = 2,    /* Trit int8: one f32 scale per row and 128 inputs  */
+    TRIT_HIP_TERNARY = 3, /* codes 0..2, w = scale * (code - 1), 128 groups   */
+    TRIT_HIP_Q4_K = 4,    /* ggml Q4_K super-blocks, run as Trit's Q8_0 codes */
+    TRIT_HIP_F16 = 5      /* f16 weights, f32 math (token tables, the head)   */
+};
+
+/* ggml Q8_0 weights as stored in GGUF: n*k/32 blocks of 34 bytes (f16 d,
+ * little endian, then 32 int8 codes), row-major n x k. bias: n floats or
+ * NULL. Replaces Dense::q8_0 + Int8::from_q8_0
+ * (reference src/cpu/gemm.rs:225-247, src/cpu/int8.rs:256-289,
+ * src/cpu/tensors.rs:282-305). k % 32 == 0. */
+int trit_hip_layer_q8_0(int n, int k, const void *blocks, const float *bias, TritHipLayer **out);
+
+/* Trit int8 weights: codes row-major n x k, scales n x (k/128).
+ * Replaces Int8::quantize's layer (reference src/cpu/int8.rs:292-369). */
+int trit_hip_layer_int8(int n, int k, const int8_t *codes, const float *scales, const float *bias,
+                        TritHipLayer **out);
+
+/* Ternary weights: codes 0..2 row-major n x k, scales n x (k/128).
+ * Replaces Ternary::from_rows (reference src/cpu/kernels.rs:136-202). */
+int trit_hip_layer_ternary(int n, int k, const uint8_t *codes, const float *scales, TritHipLayer **out);
+
+/* Ternary weights as the model file stores them: ceil(k/5) base-3 bytes per
+ * row, five digits each, least significant first. Replaces
+ * Ternary::from_base3 (reference src/cpu/kernels.rs:91-130). */
+int trit_hip_layer_ternary_base3(int n, int k, const uint8_t *packed, const float *scales,
+                                 TritHipLayer **out);
+
+/* ggml Q4_K weights as stored in GGUF: n*k/256 super-blocks of 144 bytes.
+ * Results are Trit's: the values are those of expand-then-Blocks::quantize
+ * (reference src/cpu/ggml_quants.rs:168-196, src/cpu/gemm.rs:58-76,
+ * src/cpu/tensors.rs:263-286), computed from the 4-bit codes on the fly.
+ * k % 256 == 0. */
+int trit_hip_layer_q4_k(int n, int k, const void *blocks, TritHipLayer **out);
+
+/* f16 weights (bits), row-major n x k. Replaces Dense::half / Dense::table
+ * with F16 weights (reference src/cpu/gemm.rs:206-221,383-409). k % 16 == 0. */
+int trit_hip_layer_f16(int n, int k, const uint16_t *weights, const float *bias, TritHipLayer **out);
+
+/* y = x * W^T (+ bias, then max(y, 0) when relu): x is m x k f32, y m x n
+ * f32, host memory. Replaces Dense::forward / forward_relu
+ * (reference src/cpu/gemm.rs:500-542). */
+int trit_hip_layer_forward(const TritHipLayer *layer, const float *x, int m, int relu, float *y);
+
+/* The same on device pointers, enqueued on `stream` (a hipStream_t; NULL:
+ * the library's stream), without a wait. */
+int trit_hip_layer_forward_device(const TritHipLayer *layer, const float *x, int m, int relu, float *y,
+                                  void *stream);
+
+/* Shape and kind of a layer; device_bytes: the bytes its weights hold. */
+int trit_hip_layer_info(const TritHipLayer *layer, int *n, int *k, int *kind, int64_t *device_bytes);
+
+/* Row `index` of a token table as f32 (Dense::row, reference
+ * src/cpu/gemm.rs:412-429). F16 layers only. */
+int trit_hip_layer_row(const TritHipLayer *layer, int index, float *out);
+
+void trit_hip_layer_free(TritHipLayer *layer);
+
+/* ---- Decoder: CausalLm (reference src/models/parts/causal_lm.rs) ------- */
+
+typedef struct {
+    int d, ffn, layers, heads, kv_heads, head_dim, vocab;
+    float eps;        /* rms_norm_eps, 1e-6 when the config has none       */
+    float rope_base;  /* rope_theta, 1e6 when the config has none          */
+    int qk_norm;      /* Qwen3's per-head q and k norms                     */
+} TritHipLmConfig;
+
+/* A decoder from its layers (CausalLm::from_tensors, reference
+ * causal_lm.rs:141-198). linears: 4 per layer, in order qkv (q, k, v rows
+ * stacked), o, gate_up (gate rows then up rows), down. norms (host f32):
+ * per layer norm_attn[d], norm_mlp[d], q_norm[hd], k_norm[hd] (the last two
+ * only with qk_norm), then the final norm[d]. embed: an F16 vocab x d
+ * table; head: the output projection, or NULL when tied to embed. */
+int trit_hip_decoder_new(const TritHipLmConfig *config, const TritHipLayer *const *linears,
+                         const float *norms, const TritHipLayer *embed, const TritHipLayer *head,
+                         TritHipDecoder **out);
+void trit_hip_decoder_free(TritHipDecoder *decoder);
+
+enum {
+    TRIT_HIP_EXACT = 1, /* every sum in Trit's order, f32 keys and values    */
+    TRIT_HIP_KV_F32 = 2 /* f32 keys and values without the rest of EXACT     */
+};
+
+/* Per-call state: the key/value caches of up to max_positions positions
+ * (the Vec caches of CausalLm::generate, reference causal_lm.rs:224-240). */
+int trit_hip_session_new(const TritHipDecoder *decoder, int max_positions, int flags, TritHipSession **out);
+
+/* Runs `n` tokens at the next positions and extends the caches; logits
+ * (vocab floats, host) after the last token, or NULL. CausalLm::forward
+ * (reference causal_lm.rs:363-371). */
+int trit_hip_session_prefill(TritHipSession *session, const int32_t *tokens, int n, float *logits);
+
+/* As trit_hip_session_prefill from embeddings, n x d host floats
+ * (CausalLm::forward_rows, reference causal_lm.rs:374-389; the rows of
+ * generate_rows and answer, :254-282). */
+int trit_hip_session_prefill_rows(TritHipSession *session, const float *rows, int n, float *logits);
+
+/* Greedy tokens from the last logits (CausalLm::greedy, reference
+ * causal_lm.rs:284-302): argmax (the first of equal values), stop check,
+ * forward of the kept token, until a stop token or max_new tokens. The loop
+ * stays on the device. Returns the token count written to out. */
+int trit_hip_session_generate(TritHipSession *session, int max_new, const int32_t *stop, int n_stop,
+                              int32_t *out);
+
+/* Clears the caches (a new call). */
+int trit_hip_session_reset(TritHipSession *session);
+
+/* Position count the caches hold. */
+int trit_hip_session_position(const TritHipSession *session);
+
+void trit_hip_session_free(TritHipSession *session);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

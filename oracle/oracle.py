@@ -1,0 +1,265 @@
+"""ctypes view of the oracle library (test infrastructure only).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module, and only as the checker or the timed CPU baseline.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "libtrit_oracle.so")
+
+SCALAR, AVX2, AVX512 = 0, 1, 2
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = _bind(C.CDLL(LIB_PATH))
+    return _lib
+
+
+class LmConfig(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("d", "ffn", "layers", "heads", "kv_heads", "head_dim", "vocab")] + [
+        ("eps", C.c_float), ("rope_base", C.c_float), ("qk_norm", C.c_int)]
+
+
+def _bind(L):
+    p, i, f, i64 = C.c_void_p, C.c_int, C.c_float, C.c_int64
+    sig = {
+        "or_isa_best": (i, []),
+        "or_team_start": (i, [i, i]),
+        "or_team_size": (i, []),
+        "or_f32_to_f16": (C.c_uint16, [f]),
+        "or_f16_to_f32": (f, [C.c_uint16]),
+        "or_exp": (f, [f]),
+        "or_silu": (None, [p, i64]),
+        "or_quantize": (None, [i, p, i, i, i, i, p, p, p]),
+        "or_q8_0_quantize": (None, [p, i64, p, p]),
+        "or_q8_0_parse": (None, [p, i64, p, p]),
+        "or_q4_k_expand": (None, [p, i64, p]),
+        "or_int8_new": (p, [i, i, i, i, i, p, p]),
+        "or_int8_forward": (None, [p, p, i, p]),
+        "or_int8_free": (None, [p]),
+        "or_ternary_new": (p, [i, i, i, p, p]),
+        "or_ternary_forward": (None, [p, p, i, p]),
+        "or_ternary_free": (None, [p]),
+        "or_ternary_from_base3": (i, [p, i, i, p]),
+        "or_matmul_f16": (None, [i, p, i, i, p, i, p]),
+        "or_matmul_f32": (None, [i, p, i, i, p, i, p]),
+        "or_rmsnorm": (None, [p, i, f, p, i]),
+        "or_rope_table": (None, [i, f, i, p, p]),
+        "or_rope": (None, [p, i, i, i, i, i, f]),
+        "or_attention": (None, [p, i, p, p, i, i, i, i, i, i, i, p]),
+        "or_argmax": (i, [p, i]),
+        "or_lm_new": (p, [i, C.POINTER(LmConfig)]),
+        "or_lm_set_layer": (i, [p, i, p, p, p, p, p, p, p, p]),
+        "or_lm_set_embed": (i, [p, p, p]),
+        "or_lm_generate": (i, [p, p, i, i, p, i, p, p]),
+        "or_lm_forward": (i, [p, p, i, p]),
+        "or_lm_reset": (None, [p]),
+        "or_lm_free": (None, [p]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    return L
+
+
+def ptr(a: np.ndarray):
+    assert a.flags.c_contiguous
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def isa_best() -> int:
+    return lib().or_isa_best()
+
+
+def team_start(spread: int = 0, threads: int = 0) -> int:
+    return lib().or_team_start(spread, threads)
+
+
+def quantize(x: np.ndarray, group: int, half_scales: bool, isa: int = SCALAR):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m, k = x.shape
+    codes = np.empty((m, k), np.int8)
+    scales = np.empty((m, k // group), np.float32)
+    sums = np.empty((m, k // group), np.int32)
+    lib().or_quantize(isa, ptr(x), m, k, group, int(half_scales), ptr(codes), ptr(scales), ptr(sums))
+    return codes, scales, sums
+
+
+def q8_0_parse(blocks: np.ndarray, n: int, k: int):
+    codes = np.empty((n, k), np.int8)
+    scales = np.empty((n, k // 32), np.float32)
+    lib().or_q8_0_parse(ptr(np.ascontiguousarray(blocks, np.uint8)), n * k // 32, ptr(codes), ptr(scales))
+    return codes, scales
+
+
+def q8_0_quantize(values: np.ndarray):
+    v = np.ascontiguousarray(values, np.float32).reshape(-1)
+    codes = np.empty(v.size, np.int8)
+    scales = np.empty(v.size // 32, np.float32)
+    lib().or_q8_0_quantize(ptr(v), v.size, ptr(codes), ptr(scales))
+    return codes, scales
+
+
+def q4_k_expand(blocks: np.ndarray) -> np.ndarray:
+    b = np.ascontiguousarray(blocks, np.uint8).reshape(-1)
+    nb = b.size // 144
+    out = np.empty(nb * 256, np.float32)
+    lib().or_q4_k_expand(ptr(b), nb, ptr(out))
+    return out
+
+
+class Int8:
+    def __init__(self, codes, scales, group: int, half_scales: bool, isa: int = SCALAR):
+        codes = np.ascontiguousarray(codes, np.int8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        self.n, self.k = codes.shape
+        self.h = lib().or_int8_new(isa, self.n, self.k, group, int(half_scales), ptr(codes), ptr(scales))
+        assert self.h
+
+    def __call__(self, x):
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.k)
+        out = np.empty((x.shape[0], self.n), np.float32)
+        lib().or_int8_forward(self.h, ptr(x), x.shape[0], ptr(out))
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().or_int8_free(self.h)
+
+
+class Ternary:
+    def __init__(self, codes, scales, isa: int = SCALAR):
+        codes = np.ascontiguousarray(codes, np.uint8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        self.n, self.k = codes.shape
+        self.h = lib().or_ternary_new(isa, self.n, self.k, ptr(codes), ptr(scales))
+        assert self.h
+
+    def __call__(self, x):
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.k)
+        out = np.empty((x.shape[0], self.n), np.float32)
+        lib().or_ternary_forward(self.h, ptr(x), x.shape[0], ptr(out))
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().or_ternary_free(self.h)
+
+
+def matmul_f16(x, w_bits, isa: int = SCALAR):
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w_bits, np.uint16)
+    m, k = x.shape
+    n = w.shape[0]
+    out = np.empty((m, n), np.float32)
+    lib().or_matmul_f16(isa, ptr(x), m, k, ptr(w), n, ptr(out))
+    return out
+
+
+def matmul_f32(x, w, isa: int = SCALAR):
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    m, k = x.shape
+    n = w.shape[0]
+    out = np.empty((m, n), np.float32)
+    lib().or_matmul_f32(isa, ptr(x), m, k, ptr(w), n, ptr(out))
+    return out
+
+
+def rmsnorm(x, weight, eps):
+    x = np.array(x, np.float32, copy=True, order="C")
+    w = np.ascontiguousarray(weight, np.float32)
+    d = w.size
+    lib().or_rmsnorm(ptr(w), d, eps, ptr(x), x.size // d)
+    return x
+
+
+def rope_table(dims, base, positions):
+    s = np.empty((positions, dims // 2), np.float32)
+    c = np.empty((positions, dims // 2), np.float32)
+    lib().or_rope_table(dims, base, positions, ptr(s), ptr(c))
+    return s, c
+
+
+def attention(q, k, v, heads, kv_heads, hd, causal=True):
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    tq, tk = q.shape[0], k.shape[0]
+    out = np.empty((tq, heads * hd), np.float32)
+    lib().or_attention(ptr(q), q.shape[1], ptr(k), ptr(v), k.shape[1], tq, tk, heads, kv_heads, hd, int(causal),
+                       ptr(out))
+    return out
+
+
+def exp(x: float) -> float:
+    return lib().or_exp(x)
+
+
+def silu(x):
+    x = np.array(x, np.float32, copy=True, order="C")
+    lib().or_silu(ptr(x), x.size)
+    return x
+
+
+def argmax(v) -> int:
+    v = np.ascontiguousarray(v, np.float32)
+    return lib().or_argmax(ptr(v), v.size)
+
+
+class Lm:
+    """CausalLm with Q8_0 linears and a tied f16 table."""
+
+    def __init__(self, cfg: dict, weights, isa: int = SCALAR):
+        c = LmConfig(cfg["d"], cfg["ffn"], cfg["layers"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"],
+                     cfg["vocab"], cfg["eps"], cfg["rope_base"], int(cfg.get("qk_norm", 1)))
+        self.cfg = cfg
+        self.h = lib().or_lm_new(isa, C.byref(c))
+        assert self.h
+        for li, L in enumerate(weights.layers):
+            rc = lib().or_lm_set_layer(self.h, li, ptr(L.qkv), ptr(L.o), ptr(L.gate_up), ptr(L.down),
+                                       ptr(L.norm_attn), ptr(L.norm_mlp), ptr(L.q_norm), ptr(L.k_norm))
+            assert rc == 0
+        assert lib().or_lm_set_embed(self.h, ptr(weights.embed), ptr(weights.final_norm)) == 0
+
+    def generate(self, prompt, max_new, stop=()):
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        stop = np.ascontiguousarray(np.array(stop, np.int32).reshape(-1))
+        out = np.empty(max(max_new, 1), np.int32)
+        logits = np.empty(self.cfg["vocab"], np.float32)
+        n = lib().or_lm_generate(self.h, ptr(prompt), prompt.size, max_new, ptr(stop) if stop.size else None,
+                                 stop.size, ptr(out), ptr(logits))
+        assert n >= 0
+        return out[:n].copy(), logits
+
+    def reset(self):
+        lib().or_lm_reset(self.h)
+
+    def forward(self, tokens):
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        logits = np.empty(self.cfg["vocab"], np.float32)
+        assert lib().or_lm_forward(self.h, ptr(tokens), tokens.size, ptr(logits)) == 0
+        return logits
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().or_lm_free(self.h)

@@ -1,0 +1,136 @@
+"""GPU products against the oracle, bit for bit (integer dots and f32 outputs).
+
+Each case prints its name before it runs, so a failing GPU step names itself.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from trit_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def bits_equal(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+def q8_layer(seed, n, k, scale="uniform"):
+    codes, sbits = synth.q8_0_matrix(seed, n, k, scale=scale)
+    return codes, sbits, synth.q8_0_blocks(codes, sbits)
+
+
+@pytest.mark.parametrize("n,k,m", [(2048, 2048, 1), (4096, 1024, 1), (1024, 2048, 1), (6144, 1024, 1),
+                                   (1024, 3072, 1), (2048, 2048, 8), (4096, 1024, 3), (32, 32, 1),
+                                   (96, 160, 5), (1024, 8192, 2)])
+def test_q8_0(gpu, n, k, m):
+    print(f"case q8_0 n={n} k={k} m={m}", flush=True)
+    codes, sbits, blocks = q8_layer(synth.seed_for(1, n + k), n, k)
+    x = synth.activations(synth.seed_for(1, 7 + m), m, k)
+    ref = O.Int8(codes, sbits.view(np.float16).astype(np.float32), 32, True)(x)
+    layer = gpu.Dense.q8_0(n, k, blocks)
+    got = layer.forward(x)
+    assert bits_equal(got, ref), np.max(np.abs(got - ref))
+
+
+def test_q8_0_bias_relu(gpu):
+    n, k = 256, 512
+    codes, sbits, blocks = q8_layer(11, n, k)
+    bias = synth.activations(12, 1, n)[0]
+    x = synth.activations(13, 2, k)
+    ref = O.Int8(codes, sbits.view(np.float16).astype(np.float32), 32, True)(x) + bias
+    ref = np.maximum(ref, 0)
+    got = gpu.Dense.q8_0(n, k, blocks, bias).forward(x, relu=True)
+    assert bits_equal(got, ref)
+
+
+@pytest.mark.parametrize("n,k,m", [(512, 1024, 1), (384, 2048, 4)])
+def test_int8(gpu, n, k, m):
+    print(f"case int8 n={n} k={k} m={m}", flush=True)
+    codes = synth.Streams(21, n).ints(k, -127, 127).astype(np.int8)
+    scales = (0.001 + 0.01 * synth.Streams(22, n).uniform(k // 128)).astype(np.float32)
+    x = synth.activations(23, m, k)
+    ref = O.Int8(codes, scales, 128, False)(x)
+    got = gpu.Dense.int8(codes, scales).forward(x)
+    assert bits_equal(got, ref)
+
+
+def ternary_inputs(n, k):
+    u = synth.Streams(31, n).uniform(k)
+    codes = np.where(u < 0.25, 0, np.where(u < 0.75, 1, 2)).astype(np.uint8)
+    row_scale = (0.01 + 0.04 * synth.Streams(32, n).uniform(1)).astype(np.float32)
+    scales = np.repeat(row_scale, k // 128, axis=1)
+    return codes, scales
+
+
+@pytest.mark.parametrize("m", [1, 8])
+def test_ternary_4096(gpu, m):
+    print(f"case ternary 4096x4096 m={m}", flush=True)
+    n = k = 4096
+    codes, scales = ternary_inputs(n, k)
+    x = synth.activations(33 + m, m, k)
+    ref = O.Ternary(codes, scales)(x)
+    got = gpu.Dense.ternary(codes, scales).forward(x)
+    assert bits_equal(got, ref)
+
+
+def test_ternary_base3(gpu):
+    n, k = 64, 640
+    codes, scales = ternary_inputs(n, k)
+    row_bytes = (k + 4) // 5
+    packed = np.zeros((n, row_bytes), np.uint8)
+    for d in range(5):
+        idx = np.arange(row_bytes) * 5 + d
+        valid = idx < k
+        packed[:, valid] += (codes[:, idx[valid]] * 3 ** d).astype(np.uint8)
+    x = synth.activations(35, 2, k)
+    ref = O.Ternary(codes, scales)(x)
+    got = gpu.Dense.ternary_base3(n, k, packed, scales).forward(x)
+    assert bits_equal(got, ref)
+
+
+def q4_k_blocks(seed, n, k):
+    """Random Q4_K super-blocks: codes 0..15, 6-bit scales and mins, f16 d and dmin in [1e-3, 1e-2]."""
+    nb = n * k // 256
+    s = synth.Streams(seed, nb)
+    out = np.zeros((nb, 144), np.uint8)
+    dd = (1e-3 + 9e-3 * s.uniform(2)).astype(np.float32)
+    out[:, 0:4] = synth.f16_bits(dd).view(np.uint8).reshape(nb, 4)
+    out[:, 4:16] = s.ints(12, 0, 255).astype(np.uint8)
+    out[:, 16:] = s.ints(128, 0, 255).astype(np.uint8)
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("n,k,m", [(4096, 3072, 1), (3072, 8192, 4), (256, 512, 3)])
+def test_q4_k(gpu, n, k, m):
+    print(f"case q4_k n={n} k={k} m={m}", flush=True)
+    blocks = q4_k_blocks(41 + n, n, k)
+    vals = O.q4_k_expand(blocks)
+    codes, scales = O.q8_0_quantize(vals)
+    x = synth.activations(42 + m, m, k)
+    ref = O.Int8(codes.reshape(n, k), scales.reshape(n, k // 32), 32, True)(x)
+    got = gpu.Dense.q4_k(n, k, blocks).forward(x)
+    assert bits_equal(got, ref)
+
+
+@pytest.mark.parametrize("n,k,m", [(4096, 1024, 1), (1000, 1024, 3), (300, 2048, 2), (77, 160, 5)])
+def test_f16(gpu, n, k, m):
+    print(f"case f16 n={n} k={k} m={m}", flush=True)
+    w = synth.f16_bits(synth.activations(51 + n, n, k) * 0.02).reshape(n, k)
+    x = synth.activations(52 + m, m, k)
+    ref = O.matmul_f16(x, w)
+    layer = gpu.Dense.f16(w)
+    got = layer.forward(x)
+    assert bits_equal(got, ref)
+    row = layer.row(n // 2)
+    assert np.array_equal(row, w[n // 2].view(np.float16).astype(np.float32))
+
+
+def test_errors(gpu):
+    from trit_amd.hip import TritError
+
+    with pytest.raises(TritError, match="multiple of 32"):
+        gpu.Dense.q8_0(32, 48, np.zeros(32 * 48 // 32 * 34 + 34, np.uint8)[: 32 * 48 // 32 * 34])
+    with pytest.raises(TritError, match="does not exist"):
+        gpu.init(99)

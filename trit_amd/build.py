@@ -1,0 +1,64 @@
+"""Builds libtrit_hip.so (the HIP kernels and the C ABI) for gfx950, in tree.
+
+Run as `python -m trit_amd.build`. hipcc cross-compiles on a host without a
+GPU; the built library sits next to this file and travels with the tree.
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+OUT = os.path.join(HERE, "lib", "libtrit_hip.so")
+SOURCES = ["layer.hip", "gemv.hip", "gemv_f16.hip", "decoder.hip"]
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    # Every fused multiply-add is explicit in the source; nothing else fuses.
+    "-ffp-contract=off",
+    # Packed FP32 instructions stay off.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+]
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(os.path.dirname(OUT), exist_ok=True)
+    objs = []
+    for src in SOURCES:
+        path = os.path.join(CSRC, src)
+        if not os.path.exists(path):
+            continue
+        obj = os.path.join(HERE, "lib", src.replace(".hip", ".o"))
+        cmd = [HIPCC, *FLAGS, "-c", path, "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        run(cmd)
+        objs.append(obj)
+    tmp = OUT + ".tmp"
+    run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
+    os.replace(tmp, OUT)
+    for obj in objs:
+        os.remove(obj)
+    return OUT
+
+
+def run(cmd):
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = ("packed-fp32-ops", "not a recognized feature", "is not a recognized feature")
+    err = "\n".join(line for line in res.stderr.splitlines() if not any(n in line for n in noise))
+    if res.returncode != 0:
+        raise RuntimeError(f"build failed: {' '.join(cmd)}\n{err}")
+    if err.strip():
+        print(err, file=sys.stderr)
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,73 @@
+// Device-side helpers shared by the trit_hip kernels (gfx950, wave64).
+// Every fused multiply-add is an explicit __builtin_fmaf: the library is
+// built with -ffp-contract=off so that every other product and sum rounds
+// on its own, as Trit's Rust code does.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace trit {
+
+constexpr int WAVE = 64;
+
+__device__ __forceinline__ float f16_to_f32(uint16_t bits) {
+    _Float16 h;
+    __builtin_memcpy(&h, &bits, 2);
+    return (float)h;
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16(float v) {
+    _Float16 h = (_Float16)v;
+    uint16_t bits;
+    __builtin_memcpy(&bits, &h, 2);
+    return bits;
+}
+
+// f32 -> f16 (nearest even) -> f32, as Trit stores Q8_0 scales
+// (src/cpu/tensors.rs:542-595).
+__device__ __forceinline__ float f16_round(float v) { return (float)(_Float16)v; }
+
+// Cephes expf with the steps of Trit's fused paths
+// (src/cpu/activation.rs:8-38,357-375; src/cpu/v2/activation.rs:45-56).
+__device__ __forceinline__ float exp_trit(float x) {
+    constexpr float LOG2E = 1.44269504088896340736f;
+    constexpr float LN2_HI = 0.693359375f;
+    constexpr float LN2_LO = -2.12194440e-4f;
+    x = __builtin_fminf(__builtin_fmaxf(x, -87.3f), 88.0f);
+    int n_int = (int)__builtin_rintf(x * LOG2E);
+    float n = (float)n_int;
+    float r = __builtin_fmaf(-n, LN2_HI, x);
+    r = __builtin_fmaf(-n, LN2_LO, r);
+    float p = 1.9875691e-4f;
+    p = __builtin_fmaf(p, r, 1.3981999e-3f);
+    p = __builtin_fmaf(p, r, 8.333452e-3f);
+    p = __builtin_fmaf(p, r, 4.1665796e-2f);
+    p = __builtin_fmaf(p, r, 0.16666665f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    float y = __builtin_fmaf(p, r * r, r + 1.0f);
+    return y * __builtin_bit_cast(float, (uint32_t)(n_int + 127) << 23);
+}
+
+// v / (1 + exp(0 - v)) (src/cpu/activation.rs:54-56,330).
+__device__ __forceinline__ float silu_trit(float v) { return v / (1.0f + exp_trit(0.0f - v)); }
+
+// Activation code: round to nearest even, then the +-127 limits; a NaN
+// becomes -127 as cvtps2dq + clamp gives it (src/cpu/v2/quantize.rs:140-149).
+__device__ __forceinline__ int act_code(float scaled) {
+    float r = __builtin_rintf(scaled);
+    r = __builtin_fminf(__builtin_fmaxf(r, -127.0f), 127.0f);
+    return (int)r;
+}
+
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+           ((uint32_t)(d & 0xff) << 24);
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+}  // namespace trit

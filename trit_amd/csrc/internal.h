@@ -1,0 +1,138 @@
+// Internal declarations of the trit_hip library (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace trit {
+
+struct Error : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+[[noreturn]] void fail(const std::string& message);
+
+// The calling thread's error text (trit_hip_last_error).
+std::string& error_text();
+
+// Runs `body`; an exception becomes the thread's error text and `failed`
+// (the reference's guard, ffi/src/lib.rs:29-46). No exception crosses the ABI.
+template <class T, class F>
+T guard(T failed, F&& body) {
+    error_text().clear();
+    try {
+        return body();
+    } catch (const std::exception& e) {
+        error_text() = e.what();
+    } catch (...) {
+        error_text() = "unknown error";
+    }
+    return failed;
+}
+
+#define TRIT_HIP(expr)                                                                               \
+    do {                                                                                             \
+        hipError_t trit_e_ = (expr);                                                                 \
+        if (trit_e_ != hipSuccess) ::trit::fail(std::string(#expr) + ": " + hipGetErrorString(trit_e_)); \
+    } while (0)
+
+// The stream of the calling thread's device (created by trit_hip_init or on
+// first use).
+hipStream_t stream();
+int device_id();
+
+// Device memory owned by one object.
+struct DeviceMemory {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    DeviceMemory() = default;
+    explicit DeviceMemory(size_t n) { alloc(n); }
+    DeviceMemory(const DeviceMemory&) = delete;
+    DeviceMemory& operator=(const DeviceMemory&) = delete;
+    ~DeviceMemory() { release(); }
+    void alloc(size_t n) {
+        release();
+        if (n) TRIT_HIP(hipMalloc(&ptr, n));
+        bytes = n;
+    }
+    void release() {
+        if (ptr) (void)hipFree(ptr);
+        ptr = nullptr;
+        bytes = 0;
+    }
+    template <class T>
+    T* as() const {
+        return static_cast<T*>(ptr);
+    }
+    void upload(const void* host, size_t n, size_t offset = 0) {
+        TRIT_HIP(hipMemcpy(static_cast<char*>(ptr) + offset, host, n, hipMemcpyHostToDevice));
+    }
+};
+
+// A layer's weights in device memory. Layouts:
+//  Q8_0, Q4_K (after requantization), INT8: codes int8 row-major n x k;
+//    scales row-major n x (k/group): f16 bits for Q8_0/Q4_K, f32 for INT8.
+//  TERNARY: codes 2 bits each, row-major n x k/4 bytes; in each 16-code
+//    span (4 bytes) byte j holds codes j, 4+j, 8+j, 12+j at bits 0,2,4,6;
+//    scales f32 n x (k/128).
+//  F16: for each row, the 16 lane chains of the 16-lane sum order: element
+//    kk = 16*s + i at [row][i][s] (k/16 values per chain).
+enum Kind { Q8_0 = 1, INT8 = 2, TERNARY = 3, Q4_K = 4, F16 = 5 };
+
+struct Layer {
+    int kind = 0, n = 0, k = 0, group = 0;
+    DeviceMemory codes, scales, bias;
+    int64_t weight_bytes() const { return (int64_t)(codes.bytes + scales.bytes); }
+};
+
+using LayerRef = std::shared_ptr<Layer>;
+
+// ---- GEMV launches -------------------------------------------------------
+
+// Epilogues a product can fuse.
+enum Epilogue {
+    EPI_STORE = 0,     // y = x W^T (+ bias, relu)
+    EPI_RESIDUAL = 1,  // y = residual + x W^T (may alias)
+    EPI_SILU_PAIR = 2  // rows r and r + n/2: y[r] = silu(a_r) * b_r, y is m x n/2
+};
+
+struct GemvArgs {
+    const float* x = nullptr;  // m x k f32 (device)
+    int m = 1;
+    // RMSNorm applied to each row of x before quantization: x * (inv * w).
+    const float* norm_w = nullptr;    // k floats or null
+    const float* norm_inv = nullptr;  // m floats (exact mode) or null: computed in the block
+    float eps = 1e-6f;
+    float* y = nullptr;
+    const float* residual = nullptr;
+    int epilogue = EPI_STORE;
+    int relu = 0;
+};
+
+// Integer products (Q8_0, Q4_K, INT8, TERNARY), m <= 8.
+void gemv_int(const Layer& L, const GemvArgs& a, hipStream_t s);
+// f16 products, m <= 8.
+void gemv_f16(const Layer& L, const GemvArgs& a, hipStream_t s);
+// Any layer kind.
+void layer_forward(const Layer& L, const GemvArgs& a, hipStream_t s);
+
+// Requantizes Q4_K super-blocks (device bytes) into Q8_0 codes and f16
+// scales in L.codes / L.scales.
+void q4_k_requantize(const uint8_t* blocks, int n, int k, Layer& L, hipStream_t s);
+// Repacks f16 row-major weights (device) into the lane-chain layout.
+void f16_repack(const uint16_t* src, int n, int k, uint16_t* dst, hipStream_t s);
+// Row `index` of an F16 layer as f32 (device out).
+void f16_row(const Layer& L, int index, float* out, hipStream_t s);
+
+}  // namespace trit
+
+struct TritHipLayer;
+namespace trit {
+LayerRef layer_ref(const TritHipLayer* handle);
+}  // namespace trit

@@ -1,0 +1,365 @@
+// The layer half of the C ABI (include/trit_hip.h): construction of the
+// device weight cache for each weight kind, and the products.
+#include <cstring>
+#include <mutex>
+
+#include "../../include/trit_hip.h"
+#include "device.h"
+#include "internal.h"
+
+namespace trit {
+
+namespace {
+thread_local std::string g_error;
+thread_local int g_device = -1;
+thread_local hipStream_t g_stream = nullptr;
+}  // namespace
+
+[[noreturn]] void fail(const std::string& message) { throw Error(message); }
+
+std::string& error_text() { return g_error; }
+
+int device_id() {
+    if (g_device < 0) {
+        int count = 0;
+        if (hipGetDeviceCount(&count) != hipSuccess || count == 0) fail("no HIP device is visible");
+        TRIT_HIP(hipGetDevice(&g_device));
+    }
+    return g_device;
+}
+
+hipStream_t stream() {
+    if (!g_stream) {
+        device_id();
+        TRIT_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+    }
+    return g_stream;
+}
+
+namespace {
+
+// Q4_K super-block (144 bytes): f16 d, f16 dmin, 12 scale bytes, 128 bytes
+// of 4-bit codes. Expanded as ggml's dequantize_row_q4_K
+// (src/cpu/ggml_quants.rs:168-196): y = d*sc*q - dmin*m with two roundings;
+// then each 32-value block requantized as Blocks::quantize
+// (src/cpu/gemm.rs:58-76): d8 = max|y|/127, code = round(y * (1/d8)) half
+// away from zero, d8 stored as f16. One thread per 32-value block.
+__global__ void q4_k_requant_kernel(const uint8_t* __restrict__ blocks, int64_t nsub, int8_t* __restrict__ codes,
+                                    uint16_t* __restrict__ scales) {
+    for (int64_t sb = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; sb < nsub;
+         sb += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t super = sb / 8;
+        const int j = (int)(sb % 8);
+        const uint8_t* p = blocks + super * 144;
+        const float d = f16_to_f32((uint16_t)(p[0] | (p[1] << 8)));
+        const float dmin = f16_to_f32((uint16_t)(p[2] | (p[3] << 8)));
+        const uint8_t* sc = p + 4;
+        int s, mn;
+        if (j < 4) {
+            s = sc[j] & 63;
+            mn = sc[j + 4] & 63;
+        } else {
+            s = (sc[j + 4] & 0xF) | ((sc[j - 4] >> 6) << 4);
+            mn = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+        }
+        const float d1 = d * (float)s;
+        const float m1 = dmin * (float)mn;
+        const uint8_t* q = p + 16 + (j / 2) * 32;
+        const int shift = (j & 1) * 4;
+        float y[32];
+        float mx = 0.0f;
+        for (int l = 0; l < 32; ++l) {
+            const float t = d1 * (float)((q[l] >> shift) & 0xF);
+            y[l] = t - m1;
+            mx = __builtin_fmaxf(mx, __builtin_fabsf(y[l]));
+        }
+        const float d8 = mx / 127.0f;
+        const float inverse = d8 != 0.0f ? 1.0f / d8 : 0.0f;
+        for (int l = 0; l < 32; ++l) {
+            float r = __builtin_roundf(y[l] * inverse);
+            r = __builtin_fminf(__builtin_fmaxf(r, -128.0f), 127.0f);
+            codes[sb * 32 + l] = (int8_t)(int)r;
+        }
+        scales[sb] = f32_to_f16(d8);
+    }
+}
+
+}  // namespace
+
+void q4_k_requantize(const uint8_t* blocks, int n, int k, Layer& L, hipStream_t s) {
+    const int64_t nsub = (int64_t)n * k / 32;
+    L.codes.alloc((size_t)n * k);
+    L.scales.alloc((size_t)nsub * 2);
+    hipLaunchKernelGGL(q4_k_requant_kernel, dim3(2048), dim3(256), 0, s, blocks, nsub, L.codes.as<int8_t>(),
+                       L.scales.as<uint16_t>());
+    TRIT_HIP(hipGetLastError());
+}
+
+void layer_forward(const Layer& L, const GemvArgs& a, hipStream_t s) {
+    if (L.kind == F16) return gemv_f16(L, a, s);
+    return gemv_int(L, a, s);
+}
+
+// Per-thread staging buffers of the host-pointer forward.
+struct Staging {
+    DeviceMemory x, y;
+};
+thread_local Staging g_staging;
+
+}  // namespace trit
+
+struct TritHipLayer {
+    trit::LayerRef layer;
+};
+
+using namespace trit;
+
+namespace {
+
+void upload_bias(Layer& L, const float* bias) {
+    if (!bias) return;
+    L.bias.alloc((size_t)L.n * 4);
+    L.bias.upload(bias, (size_t)L.n * 4);
+}
+
+void check_shape(int n, int k, int k_multiple, const char* what) {
+    if (n <= 0 || k <= 0) fail(std::string(what) + ": empty layer");
+    if (k % k_multiple != 0)
+        fail(std::string(what) + ": k = " + std::to_string(k) + " is not a multiple of " + std::to_string(k_multiple));
+}
+
+int finish(std::shared_ptr<Layer> L, TritHipLayer** out) {
+    if (!out) fail("out is NULL");
+    TRIT_HIP(hipStreamSynchronize(stream()));
+    *out = new TritHipLayer{std::move(L)};
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* trit_hip_version(void) { return "trit_hip 0.1.0 (gfx950)"; }
+
+const char* trit_hip_last_error(void) { return g_error.c_str(); }
+
+int trit_hip_init(int device) {
+    return guard(-1, [&] {
+        int count = 0;
+        TRIT_HIP(hipGetDeviceCount(&count));
+        if (device < 0 || device >= count)
+            fail("device " + std::to_string(device) + " does not exist (" + std::to_string(count) + " visible)");
+        TRIT_HIP(hipSetDevice(device));
+        g_device = device;
+        stream();
+        return 0;
+    });
+}
+
+int trit_hip_layer_q8_0(int n, int k, const void* blocks, const float* bias, TritHipLayer** out) {
+    return guard(-1, [&] {
+        check_shape(n, k, 32, "Q8_0 layer");
+        if (!blocks) fail("Q8_0 layer: blocks is NULL");
+        auto L = std::make_shared<Layer>();
+        L->kind = Q8_0;
+        L->n = n;
+        L->k = k;
+        L->group = 32;
+        const size_t nb = (size_t)n * k / 32;
+        std::vector<int8_t> codes((size_t)n * k);
+        std::vector<uint16_t> scales(nb);
+        const uint8_t* p = static_cast<const uint8_t*>(blocks);
+        for (size_t b = 0; b < nb; ++b) {
+            scales[b] = (uint16_t)(p[b * 34] | (p[b * 34 + 1] << 8));
+            std::memcpy(&codes[b * 32], p + b * 34 + 2, 32);
+        }
+        L->codes.alloc(codes.size());
+        L->codes.upload(codes.data(), codes.size());
+        L->scales.alloc(nb * 2);
+        L->scales.upload(scales.data(), nb * 2);
+        upload_bias(*L, bias);
+        return finish(L, out);
+    });
+}
+
+int trit_hip_layer_int8(int n, int k, const int8_t* codes, const float* scales, const float* bias,
+                        TritHipLayer** out) {
+    return guard(-1, [&] {
+        check_shape(n, k, 128, "int8 layer");
+        if (!codes || !scales) fail("int8 layer: codes or scales is NULL");
+        auto L = std::make_shared<Layer>();
+        L->kind = INT8;
+        L->n = n;
+        L->k = k;
+        L->group = 128;
+        L->codes.alloc((size_t)n * k);
+        L->codes.upload(codes, (size_t)n * k);
+        L->scales.alloc((size_t)n * (k / 128) * 4);
+        L->scales.upload(scales, (size_t)n * (k / 128) * 4);
+        upload_bias(*L, bias);
+        return finish(L, out);
+    });
+}
+
+static int ternary_from_codes(int n, int k, const uint8_t* codes, const float* scales, TritHipLayer** out) {
+    check_shape(n, k, 128, "ternary layer");
+    if (!codes || !scales) fail("ternary layer: codes or scales is NULL");
+    auto L = std::make_shared<Layer>();
+    L->kind = TERNARY;
+    L->n = n;
+    L->k = k;
+    L->group = 128;
+    std::vector<uint8_t> packed((size_t)n * k / 4);
+    for (int r = 0; r < n; ++r) {
+        for (int span = 0; span < k / 16; ++span) {
+            const uint8_t* c = codes + (size_t)r * k + span * 16;
+            for (int j = 0; j < 4; ++j) {
+                for (int t = 0; t < 4; ++t)
+                    if (c[4 * t + j] > 2) fail("ternary layer: a code above 2 in row " + std::to_string(r));
+                packed[(size_t)r * (k / 4) + span * 4 + j] =
+                    (uint8_t)(c[j] | (c[4 + j] << 2) | (c[8 + j] << 4) | (c[12 + j] << 6));
+            }
+        }
+    }
+    L->codes.alloc(packed.size());
+    L->codes.upload(packed.data(), packed.size());
+    L->scales.alloc((size_t)n * (k / 128) * 4);
+    L->scales.upload(scales, (size_t)n * (k / 128) * 4);
+    return finish(L, out);
+}
+
+int trit_hip_layer_ternary(int n, int k, const uint8_t* codes, const float* scales, TritHipLayer** out) {
+    return guard(-1, [&] { return ternary_from_codes(n, k, codes, scales, out); });
+}
+
+int trit_hip_layer_ternary_base3(int n, int k, const uint8_t* packed, const float* scales, TritHipLayer** out) {
+    return guard(-1, [&] {
+        if (!packed) fail("ternary layer: packed is NULL");
+        check_shape(n, k, 128, "ternary layer");
+        const int row_bytes = (k + 4) / 5;
+        std::vector<uint8_t> codes((size_t)n * k);
+        for (int r = 0; r < n; ++r) {
+            for (int b = 0; b < row_bytes; ++b) {
+                int v = packed[(size_t)r * row_bytes + b];
+                if (v > 242) fail("ternary byte above 242 in row " + std::to_string(r));
+                for (int digit = 0; digit < 5; ++digit) {
+                    const int kk = b * 5 + digit;
+                    if (kk < k) codes[(size_t)r * k + kk] = (uint8_t)(v % 3);
+                    v /= 3;
+                }
+            }
+        }
+        return ternary_from_codes(n, k, codes.data(), scales, out);
+    });
+}
+
+int trit_hip_layer_q4_k(int n, int k, const void* blocks, TritHipLayer** out) {
+    return guard(-1, [&] {
+        check_shape(n, k, 256, "Q4_K layer");
+        if (!blocks) fail("Q4_K layer: blocks is NULL");
+        auto L = std::make_shared<Layer>();
+        L->kind = Q4_K;
+        L->n = n;
+        L->k = k;
+        L->group = 32;
+        const size_t bytes = (size_t)n * k / 256 * 144;
+        DeviceMemory raw(bytes);
+        raw.upload(blocks, bytes);
+        q4_k_requantize(raw.as<uint8_t>(), n, k, *L, stream());
+        TRIT_HIP(hipStreamSynchronize(stream()));
+        return finish(L, out);
+    });
+}
+
+int trit_hip_layer_f16(int n, int k, const uint16_t* weights, const float* bias, TritHipLayer** out) {
+    return guard(-1, [&] {
+        check_shape(n, k, 16, "f16 layer");
+        if (!weights) fail("f16 layer: weights is NULL");
+        auto L = std::make_shared<Layer>();
+        L->kind = F16;
+        L->n = n;
+        L->k = k;
+        const size_t bytes = (size_t)n * k * 2;
+        DeviceMemory raw(bytes);
+        raw.upload(weights, bytes);
+        L->codes.alloc(bytes);
+        f16_repack(raw.as<uint16_t>(), n, k, L->codes.as<uint16_t>(), stream());
+        upload_bias(*L, bias);
+        TRIT_HIP(hipStreamSynchronize(stream()));
+        return finish(L, out);
+    });
+}
+
+int trit_hip_layer_forward_device(const TritHipLayer* layer, const float* x, int m, int relu, float* y,
+                                  void* s) {
+    return guard(-1, [&] {
+        if (!layer || !x || !y) fail("layer, x or y is NULL");
+        GemvArgs a;
+        a.x = x;
+        a.m = m;
+        a.y = y;
+        a.relu = relu;
+        hipStream_t st = s ? (hipStream_t)s : stream();
+        const Layer& L = *layer->layer;
+        // Rows in calls of up to 8.
+        for (int r0 = 0; r0 < m; r0 += 8) {
+            a.x = x + (size_t)r0 * L.k;
+            a.y = y + (size_t)r0 * L.n;
+            a.m = m - r0 < 8 ? m - r0 : 8;
+            layer_forward(L, a, st);
+        }
+        return 0;
+    });
+}
+
+int trit_hip_layer_forward(const TritHipLayer* layer, const float* x, int m, int relu, float* y) {
+    return guard(-1, [&] {
+        if (!layer || !x || !y) fail("layer, x or y is NULL");
+        if (m <= 0) fail("m must be positive");
+        const Layer& L = *layer->layer;
+        const size_t xb = (size_t)m * L.k * 4, yb = (size_t)m * L.n * 4;
+        if (g_staging.x.bytes < xb) g_staging.x.alloc(xb);
+        if (g_staging.y.bytes < yb) g_staging.y.alloc(yb);
+        hipStream_t st = stream();
+        TRIT_HIP(hipMemcpyAsync(g_staging.x.ptr, x, xb, hipMemcpyHostToDevice, st));
+        if (trit_hip_layer_forward_device(layer, g_staging.x.as<float>(), m, relu, g_staging.y.as<float>(), st) != 0)
+            fail(g_error);
+        TRIT_HIP(hipMemcpyAsync(y, g_staging.y.ptr, yb, hipMemcpyDeviceToHost, st));
+        TRIT_HIP(hipStreamSynchronize(st));
+        return 0;
+    });
+}
+
+int trit_hip_layer_info(const TritHipLayer* layer, int* n, int* k, int* kind, int64_t* device_bytes) {
+    return guard(-1, [&] {
+        if (!layer) fail("layer is NULL");
+        const Layer& L = *layer->layer;
+        if (n) *n = L.n;
+        if (k) *k = L.k;
+        if (kind) *kind = L.kind;
+        if (device_bytes) *device_bytes = L.weight_bytes();
+        return 0;
+    });
+}
+
+int trit_hip_layer_row(const TritHipLayer* layer, int index, float* out) {
+    return guard(-1, [&] {
+        if (!layer || !out) fail("layer or out is NULL");
+        const Layer& L = *layer->layer;
+        if (L.kind != F16) fail("row: only F16 token tables");
+        if (index < 0 || index >= L.n) fail("row: index out of range");
+        DeviceMemory d((size_t)L.k * 4);
+        f16_row(L, index, d.as<float>(), stream());
+        TRIT_HIP(hipMemcpyAsync(out, d.ptr, (size_t)L.k * 4, hipMemcpyDeviceToHost, stream()));
+        TRIT_HIP(hipStreamSynchronize(stream()));
+        return 0;
+    });
+}
+
+void trit_hip_layer_free(TritHipLayer* layer) { delete layer; }
+
+}  // extern "C"
+
+namespace trit {
+LayerRef layer_ref(const TritHipLayer* h) { return h ? h->layer : nullptr; }
+}  // namespace trit

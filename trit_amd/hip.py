@@ -1,0 +1,257 @@
+"""ctypes driver of libtrit_hip.so, shaped like Trit's Rust interface.
+
+`Dense` mirrors src/cpu/gemm.rs's Dense (constructors per weight kind,
+`forward(x, rows)`, `row(index)`); `CausalLm` and `Session` mirror
+src/models/parts/causal_lm.rs (`generate`, `forward`, `greedy`). Every call
+goes through the C ABI; there is no CPU fallback: a missing library or a
+failed call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libtrit_hip.so")
+
+Q8_0, INT8, TERNARY, Q4_K, F16 = 1, 2, 3, 4, 5
+EXACT, KV_F32 = 1, 2
+
+_lib = None
+
+
+class TritError(RuntimeError):
+    pass
+
+
+class LmConfig(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("d", "ffn", "layers", "heads", "kv_heads", "head_dim", "vocab")] + [
+        ("eps", C.c_float), ("rope_base", C.c_float), ("qk_norm", C.c_int)]
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise TritError(f"{LIB_PATH} is missing: build it with `python -m trit_amd.build`")
+        L = C.CDLL(LIB_PATH)
+        p, i, f = C.c_void_p, C.c_int, C.c_float
+        pp = C.POINTER(C.c_void_p)
+        sig = {
+            "trit_hip_version": (C.c_char_p, []),
+            "trit_hip_last_error": (C.c_char_p, []),
+            "trit_hip_init": (i, [i]),
+            "trit_hip_layer_q8_0": (i, [i, i, p, p, pp]),
+            "trit_hip_layer_int8": (i, [i, i, p, p, p, pp]),
+            "trit_hip_layer_ternary": (i, [i, i, p, p, pp]),
+            "trit_hip_layer_ternary_base3": (i, [i, i, p, p, pp]),
+            "trit_hip_layer_q4_k": (i, [i, i, p, pp]),
+            "trit_hip_layer_f16": (i, [i, i, p, p, pp]),
+            "trit_hip_layer_forward": (i, [p, p, i, i, p]),
+            "trit_hip_layer_forward_device": (i, [p, p, i, i, p, p]),
+            "trit_hip_layer_info": (i, [p, C.POINTER(i), C.POINTER(i), C.POINTER(i), C.POINTER(C.c_int64)]),
+            "trit_hip_layer_row": (i, [p, i, p]),
+            "trit_hip_layer_free": (None, [p]),
+            "trit_hip_decoder_new": (i, [C.POINTER(LmConfig), p, p, p, p, pp]),
+            "trit_hip_decoder_free": (None, [p]),
+            "trit_hip_session_new": (i, [p, i, i, pp]),
+            "trit_hip_session_prefill": (i, [p, p, i, p]),
+            "trit_hip_session_prefill_rows": (i, [p, p, i, p]),
+            "trit_hip_session_generate": (i, [p, i, p, i, p]),
+            "trit_hip_session_reset": (i, [p]),
+            "trit_hip_session_position": (i, [p]),
+            "trit_hip_session_free": (None, [p]),
+        }
+        for name, (res, args) in sig.items():
+            if not hasattr(L, name):
+                continue
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc is None or (isinstance(rc, int) and rc < 0):
+        raise TritError(lib().trit_hip_last_error().decode())
+    return rc
+
+
+def ptr(a):
+    if a is None:
+        return None
+    assert a.flags.c_contiguous
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def init(device: int = 0):
+    check(lib().trit_hip_init(device))
+
+
+class Dense:
+    """A layer on the device (src/cpu/gemm.rs:15-35)."""
+
+    def __init__(self, handle, n, k):
+        self.h, self.n, self.k = handle, n, k
+
+    @staticmethod
+    def _make(fn, n, k, *args):
+        out = C.c_void_p()
+        check(fn(n, k, *args, C.byref(out)))
+        return Dense(out, n, k)
+
+    @classmethod
+    def q8_0(cls, n, k, blocks, bias=None):
+        blocks = np.ascontiguousarray(blocks, np.uint8)
+        assert blocks.size == n * k // 32 * 34
+        bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        return cls._make(lib().trit_hip_layer_q8_0, n, k, ptr(blocks), ptr(bias))
+
+    @classmethod
+    def int8(cls, codes, scales, bias=None):
+        codes = np.ascontiguousarray(codes, np.int8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        n, k = codes.shape
+        return cls._make(lib().trit_hip_layer_int8, n, k, ptr(codes), ptr(scales), ptr(bias))
+
+    @classmethod
+    def ternary(cls, codes, scales):
+        codes = np.ascontiguousarray(codes, np.uint8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        n, k = codes.shape
+        return cls._make(lib().trit_hip_layer_ternary, n, k, ptr(codes), ptr(scales))
+
+    @classmethod
+    def ternary_base3(cls, n, k, packed, scales):
+        packed = np.ascontiguousarray(packed, np.uint8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        return cls._make(lib().trit_hip_layer_ternary_base3, n, k, ptr(packed), ptr(scales))
+
+    @classmethod
+    def q4_k(cls, n, k, blocks):
+        blocks = np.ascontiguousarray(blocks, np.uint8)
+        assert blocks.size == n * k // 256 * 144
+        return cls._make(lib().trit_hip_layer_q4_k, n, k, ptr(blocks))
+
+    @classmethod
+    def f16(cls, weights_bits, bias=None):
+        w = np.ascontiguousarray(weights_bits, np.uint16)
+        bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        n, k = w.shape
+        return cls._make(lib().trit_hip_layer_f16, n, k, ptr(w), ptr(bias))
+
+    def forward(self, x, rows=None, relu=False):
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.k)
+        m = x.shape[0] if rows is None else rows
+        y = np.empty((m, self.n), np.float32)
+        check(lib().trit_hip_layer_forward(self.h, ptr(x), m, int(relu), ptr(y)))
+        return y
+
+    def row(self, index):
+        out = np.empty(self.k, np.float32)
+        check(lib().trit_hip_layer_row(self.h, index, ptr(out)))
+        return out
+
+    def info(self):
+        n, k, kind, b = C.c_int(), C.c_int(), C.c_int(), C.c_int64()
+        check(lib().trit_hip_layer_info(self.h, C.byref(n), C.byref(k), C.byref(kind), C.byref(b)))
+        return {"n": n.value, "k": k.value, "kind": kind.value, "bytes": b.value}
+
+    def free(self):
+        if self.h:
+            lib().trit_hip_layer_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class CausalLm:
+    """The decoder on the device (src/models/parts/causal_lm.rs:93-481)."""
+
+    def __init__(self, cfg: dict, linears, norms, embed: Dense, head: Dense | None = None):
+        c = LmConfig(cfg["d"], cfg["ffn"], cfg["layers"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"],
+                     cfg["vocab"], cfg["eps"], cfg["rope_base"], int(cfg.get("qk_norm", 1)))
+        self.cfg = cfg
+        arr = (C.c_void_p * len(linears))(*[l.h for l in linears])
+        norms = np.ascontiguousarray(norms, np.float32)
+        out = C.c_void_p()
+        check(lib().trit_hip_decoder_new(C.byref(c), arr, ptr(norms), embed.h, head.h if head else None,
+                                         C.byref(out)))
+        self.h = out
+
+    def session(self, max_positions, flags=0):
+        return Session(self, max_positions, flags)
+
+    def generate(self, prompt, max_new, stop=(), flags=0):
+        """CausalLm::generate without a prefix (causal_lm.rs:217-249)."""
+        s = self.session(len(prompt) + max_new + 1, flags)
+        try:
+            s.prefill(prompt)
+            return s.generate(max_new, stop)
+        finally:
+            s.free()
+
+    def free(self):
+        if self.h:
+            lib().trit_hip_decoder_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Session:
+    def __init__(self, lm: CausalLm, max_positions, flags=0):
+        self.lm = lm
+        out = C.c_void_p()
+        check(lib().trit_hip_session_new(lm.h, max_positions, flags, C.byref(out)))
+        self.h = out
+
+    def prefill(self, tokens, want_logits=True):
+        t = np.ascontiguousarray(tokens, np.int32)
+        logits = np.empty(self.lm.cfg["vocab"], np.float32) if want_logits else None
+        check(lib().trit_hip_session_prefill(self.h, ptr(t), t.size, ptr(logits)))
+        return logits
+
+    def prefill_rows(self, rows, want_logits=True):
+        r = np.ascontiguousarray(rows, np.float32).reshape(-1, self.lm.cfg["d"])
+        logits = np.empty(self.lm.cfg["vocab"], np.float32) if want_logits else None
+        check(lib().trit_hip_session_prefill_rows(self.h, ptr(r), r.shape[0], ptr(logits)))
+        return logits
+
+    def generate(self, max_new, stop=()):
+        stop = np.ascontiguousarray(np.array(stop, np.int32).reshape(-1))
+        out = np.empty(max(max_new, 1), np.int32)
+        n = check(lib().trit_hip_session_generate(self.h, max_new, ptr(stop) if stop.size else None, stop.size,
+                                                  ptr(out)))
+        return out[:n].copy()
+
+    def reset(self):
+        check(lib().trit_hip_session_reset(self.h))
+
+    @property
+    def position(self):
+        return check(lib().trit_hip_session_position(self.h))
+
+    def free(self):
+        if self.h:
+            lib().trit_hip_session_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
