@@ -48,8 +48,8 @@ def test_q8_0_bias_relu(gpu):
 @pytest.mark.parametrize("n,k,m", [(512, 1024, 1), (384, 2048, 4)])
 def test_int8(gpu, n, k, m):
     print(f"case int8 n={n} k={k} m={m}", flush=True)
-    codes = synth.Streams(21, n).ints(k, -127, 127).astype(np.int8)
-    scales = (0.001 + 0.01 * synth.Streams(22, n).uniform(k // 128)).astype(np.float32)
+    codes = synth.ints(21, (n, k), -127, 127).astype(np.int8)
+    scales = (0.001 + 0.01 * synth.uniform(22, (n, k // 128))).astype(np.float32)
     x = synth.activations(23, m, k)
     ref = O.Int8(codes, scales, 128, False)(x)
     got = gpu.Dense.int8(codes, scales).forward(x)
@@ -57,9 +57,9 @@ def test_int8(gpu, n, k, m):
 
 
 def ternary_inputs(n, k):
-    u = synth.Streams(31, n).uniform(k)
+    u = synth.uniform(31, (n, k))
     codes = np.where(u < 0.25, 0, np.where(u < 0.75, 1, 2)).astype(np.uint8)
-    row_scale = (0.01 + 0.04 * synth.Streams(32, n).uniform(1)).astype(np.float32)
+    row_scale = (0.01 + 0.04 * synth.uniform(32, (n, 1))).astype(np.float32)
     scales = np.repeat(row_scale, k // 128, axis=1)
     return codes, scales
 
@@ -90,22 +90,10 @@ def test_ternary_base3(gpu):
     assert bits_equal(got, ref)
 
 
-def q4_k_blocks(seed, n, k):
-    """Random Q4_K super-blocks: codes 0..15, 6-bit scales and mins, f16 d and dmin in [1e-3, 1e-2]."""
-    nb = n * k // 256
-    s = synth.Streams(seed, nb)
-    out = np.zeros((nb, 144), np.uint8)
-    dd = (1e-3 + 9e-3 * s.uniform(2)).astype(np.float32)
-    out[:, 0:4] = synth.f16_bits(dd).view(np.uint8).reshape(nb, 4)
-    out[:, 4:16] = s.ints(12, 0, 255).astype(np.uint8)
-    out[:, 16:] = s.ints(128, 0, 255).astype(np.uint8)
-    return out.reshape(-1)
-
-
 @pytest.mark.parametrize("n,k,m", [(4096, 3072, 1), (3072, 8192, 4), (256, 512, 3)])
 def test_q4_k(gpu, n, k, m):
     print(f"case q4_k n={n} k={k} m={m}", flush=True)
-    blocks = q4_k_blocks(41 + n, n, k)
+    blocks = synth.q4_k_blocks(41 + n, n, k)
     vals = O.q4_k_expand(blocks)
     codes, scales = O.q8_0_quantize(vals)
     x = synth.activations(42 + m, m, k)

@@ -1,0 +1,339 @@
+"""Pins the oracle (the CPU restatement of Trit's kernels) without the reference.
+
+Trit has no unit tests or golden vectors (its checks are end-to-end WER
+runs), so each function is pinned here by what the mathematics fixes:
+hand-made known answers, closed forms, exhaustive checks against IEEE
+conversions, brute force on small inputs, and Trit's own rule that every
+SIMD path gives the scalar path's bits.
+"""
+
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from trit_amd import synth
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "known_answers.json")
+
+
+def bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def test_f16_to_f32_exhaustive():
+    L = O.lib()
+    h = np.arange(65536, dtype=np.uint16)
+    want = h.view(np.float16).astype(np.float32)
+    got = np.array([L.or_f16_to_f32(int(v)) for v in h], np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(bits(got[~nan]), bits(want[~nan]))
+    assert np.all(np.isnan(got[nan]))
+
+
+def test_f32_to_f16_rounding():
+    L = O.lib()
+    rng = np.random.default_rng(7)
+    v = (rng.standard_normal(20000) * 10.0 ** rng.integers(-9, 6, 20000)).astype(np.float32)
+    # Ties, the subnormal edge and the overflow edge.
+    edge = np.array([65504, 65519.99, 65520, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26, 2.0 ** -14,
+                     1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11, -0.0, np.inf, -np.inf], np.float32)
+    v = np.concatenate([v, edge])
+    with np.errstate(over="ignore"):
+        want = v.astype(np.float16).view(np.uint16)
+    got = np.array([L.or_f32_to_f16(float(x)) for x in v], np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_quantizer_known_answers():
+    # Peak 127 gives scale 1, so each code is the value rounded half to even.
+    x = np.zeros((1, 32), np.float32)
+    x[0, :12] = [127, 63.5, 62.5, -0.5, 0.5, 1.5, 2.5, -2.5, -126.5, 0.49999997, 3.2, -3.7]
+    codes, scales, sums = O.quantize(x, 32, False)
+    assert scales[0, 0] == 1.0
+    assert codes[0, :12].tolist() == [127, 64, 62, 0, 0, 2, 2, -2, -126, 0, 3, -4]
+    assert sums[0, 0] == sum(codes[0].tolist())
+    # An all-zero group: scale 1, codes 0 (src/cpu/v2/quantize.rs:130-135).
+    codes, scales, sums = O.quantize(np.zeros((2, 64), np.float32), 32, True)
+    assert np.all(codes == 0) and np.all(scales == 1.0) and np.all(sums == 0)
+
+
+def test_quantizer_half_scales():
+    # Codes come from the f32 scale; only the stored scale is rounded to f16.
+    x = np.linspace(-1, 1, 32, dtype=np.float32).reshape(1, 32) * np.float32(0.3)
+    c32, s32, _ = O.quantize(x, 32, False)
+    c16, s16, _ = O.quantize(x, 32, True)
+    assert np.array_equal(c32, c16)
+    assert s32[0, 0] == np.float32(0.3) / np.float32(127)
+    assert s16[0, 0] == np.float32(np.float16(s32[0, 0]))
+    assert s16[0, 0] != s32[0, 0]
+
+
+@pytest.mark.parametrize("isa", [O.AVX2, O.AVX512])
+def test_quantizer_paths_agree(isa):
+    if isa > O.isa_best():
+        pytest.skip("CPU lacks the path")
+    x = synth.activations(3, 9, 1024) * np.float32(5)
+    for group, half in [(32, True), (128, False)]:
+        a = O.quantize(x, group, half, O.SCALAR)
+        b = O.quantize(x, group, half, isa)
+        for p, q in zip(a, b):
+            assert np.array_equal(p, q)
+
+
+def test_int8_product_closed_form():
+    # Unit scales and codes from a known quantizer give integer outputs in any order.
+    n, k, m = 64, 256, 3
+    codes = synth.ints(1, (n, k), -127, 127).astype(np.int8)
+    ones = np.ones((n, k // 32), np.float32)
+    x = synth.ints(2, (m, k), -127, 127).astype(np.float32)
+    x[:, ::32] = 127  # every group's peak is 127: scale 1, codes = x
+    out = O.Int8(codes, ones, 32, False)(x)
+    want = x.astype(np.int64) @ codes.astype(np.int64).T
+    assert np.array_equal(out, want.astype(np.float32))
+
+
+@pytest.mark.parametrize("isa", [O.AVX2, O.AVX512])
+def test_int8_paths_agree(isa):
+    if isa > O.isa_best():
+        pytest.skip("CPU lacks the path")
+    n, k = 96, 512
+    codes, sbits = synth.q8_0_matrix(5, n, k)
+    sc = sbits.view(np.float16).astype(np.float32)
+    for m in (1, 5, 7):
+        x = synth.activations(6 + m, m, k)
+        a = O.Int8(codes, sc, 32, True, O.SCALAR)(x)
+        b = O.Int8(codes, sc, 32, True, isa)(x)
+        assert np.array_equal(bits(a), bits(b))
+
+
+def _f32(v):
+    return float(np.float32(v))
+
+
+def test_int8_group_chain_order():
+    """The f32 chain is total = fma(f32(dot_g), ws_g * xs_g, total) over the
+    groups in order from 0. The inputs are searched so that each plausible
+    misreading gives other bits: no fusion, the first set's scalar order
+    (dot * ws * xs added), and the groups in reverse. Values stay within a
+    narrow exponent range, so float64 holds every product and sum exactly
+    and one rounding to float32 models a fused multiply-add exactly."""
+    rng = np.random.default_rng(5)
+    groups, k = 3, 96
+    for _ in range(2000):
+        wcodes = rng.integers(60, 127, groups)
+        ws = (rng.uniform(1.0, 2.0, groups)).astype(np.float32)
+        peaks = rng.uniform(1.0, 2.0, groups).astype(np.float32)
+        codes = np.zeros((32, k), np.int8)
+        x = np.zeros((1, k), np.float32)
+        for g in range(groups):
+            codes[0, 32 * g] = wcodes[g]
+            x[0, 32 * g] = peaks[g]
+        _, xs, _ = O.quantize(x, 32, False)
+        dots = [127 * int(c) for c in wcodes]
+        sc = [_f32(float(ws[g]) * float(xs[0, g])) for g in range(groups)]
+
+        def chain(order, fused=True, first_set=False):
+            t = 0.0
+            for g in order:
+                if first_set:
+                    t = _f32(t + _f32(_f32(dots[g] * float(ws[g])) * float(xs[0, g])))
+                elif fused:
+                    t = _f32(dots[g] * sc[g] + t)
+                else:
+                    t = _f32(t + _f32(dots[g] * sc[g]))
+            return t
+
+        want = chain(range(groups))
+        others = [chain(range(groups), fused=False), chain(range(groups), first_set=True),
+                  chain(reversed(range(groups)))]
+        if all(o != want for o in others):
+            break
+    else:
+        pytest.fail("no distinguishing inputs found")
+    sc_rows = np.ones((32, groups), np.float32)
+    sc_rows[0] = ws
+    out = O.Int8(codes, sc_rows, 32, False)(x)
+    assert out[0, 0] == np.float32(want)
+
+
+def test_ternary_brute_force():
+    n, k, m = 32, 256, 2
+    codes = synth.ints(8, (n, k), 0, 2).astype(np.uint8)
+    scales = np.ones((n, k // 128), np.float32)
+    x = synth.ints(9, (m, k), -127, 127).astype(np.float32)
+    x[:, ::128] = 127
+    out = O.Ternary(codes, scales)(x)
+    want = x.astype(np.int64) @ (codes.astype(np.int64) - 1).T
+    assert np.array_equal(out, want.astype(np.float32))
+    if O.isa_best() >= O.AVX512:
+        y = synth.activations(10, 3, k)
+        assert np.array_equal(bits(O.Ternary(codes, scales)(y)), bits(O.Ternary(codes, scales, O.AVX512)(y)))
+
+
+def test_ternary_base3_digits():
+    # Byte 5 = 2 + 1*3 -> digits [2, 1, 0, 0, 0]; byte 242 -> [2, 2, 2, 2, 2].
+    packed = np.array([[5, 242]], np.uint8)
+    codes = np.zeros((1, 10), np.uint8)
+    assert O.lib().or_ternary_from_base3(O.ptr(packed), 1, 10, O.ptr(codes)) == 0
+    assert codes[0].tolist() == [2, 1, 0, 0, 0, 2, 2, 2, 2, 2]
+    bad = np.array([[243, 0]], np.uint8)
+    assert O.lib().or_ternary_from_base3(O.ptr(bad), 1, 10, O.ptr(codes)) == -1
+
+
+def test_q8_0_quantize_known_answer():
+    # d = 127/127 = 1 for a block whose peak is 127: codes round half away from zero.
+    v = np.zeros(32, np.float32)
+    v[:8] = [127, 0.5, -0.5, 1.5, 2.5, -2.5, 3.49, -126.6]
+    codes, scales = O.q8_0_quantize(v)
+    assert scales[0] == 1.0
+    assert codes[:8].tolist() == [127, 1, -1, 2, 3, -3, 3, -127]
+    z, zs = O.q8_0_quantize(np.zeros(32, np.float32))
+    assert np.all(z == 0) and zs[0] == 0.0
+
+
+def test_q4_k_known_answer():
+    # d = 1, dmin = 0.5; sub-block scales 1..8 and mins 0..7 in the 6-bit packing.
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.array([np.float16(1.0)]).view(np.uint8)
+    blk[2:4] = np.array([np.float16(0.5)]).view(np.uint8)
+    sc = list(range(1, 9))
+    mn = list(range(0, 8))
+    for j in range(4):
+        blk[4 + j] = sc[j]
+        blk[8 + j] = mn[j]
+    for j in range(4, 8):
+        blk[12 + j - 4] = (sc[j] & 0xF) | ((mn[j] & 0xF) << 4)
+        blk[4 + j - 4] |= (sc[j] >> 4) << 6
+        blk[8 + j - 4] |= (mn[j] >> 4) << 6
+    q = (np.arange(128) % 16).astype(np.uint8)
+    blk[16:] = q | (((15 - q) & 0xF) << 4)
+    y = O.q4_k_expand(blk)
+    for j in range(8):
+        pair, high = divmod(j, 2)
+        nib = (15 - q[pair * 32:(pair + 1) * 32]) if high else q[pair * 32:(pair + 1) * 32]
+        want = sc[j] * nib.astype(np.float32) - np.float32(0.5) * mn[j]
+        assert np.array_equal(y[j * 32:(j + 1) * 32], want.astype(np.float32)), j
+
+
+def test_matmul_f16_contract():
+    n, k = 50, 200
+    w = synth.f16_bits(synth.activations(11, n, k) * 0.1).reshape(n, k)
+    x = synth.activations(12, 3, k)
+    out = O.matmul_f16(x, w)
+    ref = x.astype(np.float64) @ w.view(np.float16).astype(np.float64).T
+    assert np.max(np.abs(out - ref)) < 1e-5 * np.max(np.abs(ref)) * k
+    # 16 lanes with the tree: with small integers every order is exact.
+    wi = synth.f16_bits(synth.ints(13, (n, k), -3, 3).astype(np.float32)).reshape(n, k)
+    xi = synth.ints(14, (2, k), -3, 3).astype(np.float32)
+    want = xi @ wi.view(np.float16).astype(np.float32).T
+    assert np.array_equal(O.matmul_f16(xi, wi), want)
+    if O.isa_best() >= O.AVX512:
+        assert np.array_equal(bits(out), bits(O.matmul_f16(x, w, O.AVX512)))
+
+
+def test_matmul_f16_lane_order():
+    """Lane i sums x[16s+i]*w[16s+i]; then i+8, i+4, i+2, last two. Values
+    chosen so a plain serial sum gives other bits."""
+    k = 32
+    x = np.zeros((1, k), np.float32)
+    w = np.ones((1, k), np.float16).view(np.uint16)
+    x[0, 0] = 1.0          # lane 0
+    x[0, 16] = 2.0 ** -24  # lane 0, second step: 1 + 2^-24 -> 1
+    x[0, 8] = 2.0 ** -24   # lane 8
+    out = O.matmul_f16(x, w)[0, 0]
+    # lane0 = 1, lane8 = 2^-24: half[0] = 1 + 2^-24 -> 1 (even); serial order would also give 1;
+    # so use lanes that pair up: lane 1 and lane 9 hold 2^-24 each.
+    x2 = np.zeros((1, k), np.float32)
+    x2[0, 0] = 1.0
+    x2[0, 1] = 2.0 ** -24
+    x2[0, 9] = 2.0 ** -24
+    tree = O.matmul_f16(x2, w)[0, 0]
+    # Tree: half[1] = 2^-24 + 2^-24 = 2^-23; then 1 + 2^-23 survives.
+    assert tree == np.float32(1 + 2.0 ** -23)
+    assert out == np.float32(1.0)
+
+
+def test_exp_accuracy_and_clamp():
+    L = O.lib()
+    xs = np.linspace(-87, 88, 20001).astype(np.float32)
+    got = np.array([L.or_exp(float(v)) for v in xs], np.float64)
+    ref = np.exp(xs.astype(np.float64))
+    ulp = np.abs(got - ref) / np.spacing(ref.astype(np.float32)).astype(np.float64)
+    assert ulp.max() <= 2.0
+    assert L.or_exp(0.0) == 1.0
+    assert L.or_exp(float("-inf")) == L.or_exp(-87.3)
+    assert L.or_exp(-1000.0) > 0.0
+
+
+def test_silu_and_argmax():
+    v = np.array([-3, -0.5, 0, 0.5, 3, 20], np.float32)
+    got = O.silu(v)
+    ref = v.astype(np.float64) / (1 + np.exp(-v.astype(np.float64)))
+    assert np.allclose(got, ref, rtol=3e-7, atol=1e-30)
+    assert O.argmax(np.array([1, 3, 2, 3], np.float32)) == 1
+    assert O.argmax(np.array([-np.inf, -5], np.float32)) == 1
+
+
+def test_rmsnorm_and_rope():
+    x = synth.activations(20, 3, 128)
+    w = (1 + 0.1 * synth.activations(21, 1, 128)[0]).astype(np.float32)
+    got = O.rmsnorm(x, w, 1e-6)
+    ref = x.astype(np.float64) / np.sqrt((x.astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-6) * w
+    assert np.max(np.abs(got - ref)) < 1e-5
+    s, c = O.rope_table(128, 1e6, 5)
+    assert np.all(s[0] == 0) and np.all(c[0] == 1)
+    i = np.arange(64)
+    ang = 3 * np.power(1e6, -2.0 * i / 128)
+    assert np.allclose(s[3], np.sin(ang), atol=2e-6) and np.allclose(c[3], np.cos(ang), atol=2e-6)
+
+
+def test_attention_against_float64():
+    heads, kvh, hd, tq, tk = 4, 2, 32, 3, 9
+    q = synth.activations(30, tq, heads * hd)
+    k = synth.activations(31, tk, kvh * hd)
+    v = synth.activations(32, tk, kvh * hd)
+    out = O.attention(q, k, v, heads, kvh, hd, causal=True)
+    ref = np.zeros((tq, heads * hd))
+    for i in range(tq):
+        vis = tk - tq + i + 1
+        for h in range(heads):
+            g = h // (heads // kvh)
+            qh = q[i, h * hd:(h + 1) * hd].astype(np.float64) / math.sqrt(hd)
+            sc = k[:vis, g * hd:(g + 1) * hd].astype(np.float64) @ qh
+            p = np.exp(sc - sc.max())
+            p /= p.sum()
+            ref[i, h * hd:(h + 1) * hd] = p @ v[:vis, g * hd:(g + 1) * hd]
+    assert np.max(np.abs(out - ref)) < 1e-5
+
+
+def test_golden_known_answers():
+    """Hand-derived vectors committed under tests/golden (see make_vectors.py)."""
+    with open(GOLDEN) as f:
+        g = json.load(f)
+    for case in g["quantize"]:
+        x = np.array(case["x"], np.float32).reshape(1, -1)
+        codes, scales, sums = O.quantize(x, case["group"], case["half"])
+        assert codes[0].tolist() == case["codes"], case["name"]
+        assert scales[0].tolist() == [np.float32(s) for s in case["scales"]], case["name"]
+    for case in g["f16"]:
+        assert O.lib().or_f32_to_f16(case["value"]) == case["bits"], case
+    for case in g["q8_0"]:
+        codes, scales = O.q8_0_quantize(np.array(case["x"], np.float32))
+        assert codes.tolist() == case["codes"] and scales.tolist() == case["scales"], case["name"]
+
+
+def test_lm_paths_agree():
+    cfg = dict(d=128, ffn=256, layers=2, heads=4, kv_heads=2, head_dim=32, vocab=300, eps=1e-6, rope_base=1e6,
+               qk_norm=1)
+    w = synth.lm_weights(cfg, config=77, sigma=0.2, norm_jitter=0.1)
+    p = synth.prompt(77, 11, cfg["vocab"])
+    a, la = O.Lm(cfg, w, O.SCALAR).generate(p, 8)
+    if O.isa_best() >= O.AVX512:
+        b, lb = O.Lm(cfg, w, O.AVX512).generate(p, 8)
+        assert a.tolist() == b.tolist()
+        assert np.array_equal(bits(la), bits(lb))
+    assert len(a) == 8

@@ -1,0 +1,751 @@
+// The decoder half of the C ABI: CausalLm's token loop on the device
+// (src/models/parts/causal_lm.rs:17-481).
+//
+// A session owns the key/value caches and the activations. Every kernel
+// reads the cache position from device memory, so one decode step
+// (argmax + stop check + embedding + 28 layers + head) is position-free and
+// is captured once as a HIP graph, then replayed per token without a trip
+// to the host. A `done` flag in device memory turns the rest of the replays
+// into no-ops after a stop token or max_new tokens.
+//
+// Per layer and step: [RMSNorm factor] -> qkv product (RMSNorm and the
+// activation quantizer fused in its prologue) -> q/k norm + RoPE + cache
+// append -> attention -> o product (+ residual) -> [RMSNorm factor] ->
+// gate_up product (SwiGLU fused in its epilogue) -> down product
+// (+ residual). The bracketed kernels run in exact mode only: there the
+// RMSNorm sum is Trit's serial chain; in fast mode each product block
+// computes it with a fixed tree.
+#include <cmath>
+#include <cstring>
+
+#include "../../include/trit_hip.h"
+#include "device.h"
+#include "internal.h"
+
+namespace trit {
+namespace {
+
+constexpr int MAX_STOP = 64;
+constexpr int MAX_HD = 256;
+constexpr int ATT_THREADS = 256;
+
+// Device state of a session.
+struct State {
+    int pos;        // positions in the caches
+    int done;       // nonzero: the decode loop has ended
+    int n_out;      // tokens written by the loop
+    int max_new;    // loop limit
+    int n_stop;     // stop tokens
+    int token;      // the last token chosen
+    int stop[MAX_STOP];
+};
+
+// ---- small kernels ----------------------------------------------------
+
+// Exact RMSNorm factor of each row: 1 / sqrt(serial sum of v*v / d + eps)
+// (src/layers.rs:139). The squares are made in parallel; one lane adds
+// them in Trit's order.
+__global__ void norm_inv_kernel(const float* __restrict__ x, int d, float eps, float* __restrict__ inv,
+                                const State* st) {
+    if (st && st->done) return;
+    extern __shared__ float sq[];
+    const float* row = x + (size_t)blockIdx.x * d;
+    for (int i = threadIdx.x; i < d; i += blockDim.x) {
+        const float v = row[i];
+        sq[i] = v * v;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float sum = 0.0f;
+        for (int i = 0; i < d; ++i) sum = sum + sq[i];
+        inv[blockIdx.x] = 1.0f / __builtin_sqrtf(sum / (float)d + eps);
+    }
+}
+
+// out = x * (inv * w), inv from `inv` (exact) or a fixed tree (fast).
+__global__ void rmsnorm_kernel(const float* __restrict__ x, int d, const float* __restrict__ w, float eps,
+                               const float* __restrict__ inv_in, float* __restrict__ out, const State* st) {
+    if (st && st->done) return;
+    __shared__ float red[256];
+    __shared__ float inv_s;
+    const float* row = x + (size_t)blockIdx.x * d;
+    if (inv_in) {
+        if (threadIdx.x == 0) inv_s = inv_in[blockIdx.x];
+    } else {
+        float part = 0.0f;
+        for (int i = threadIdx.x; i < d; i += 256) {
+            const float v = row[i];
+            part += v * v;
+        }
+        red[threadIdx.x] = part;
+        __syncthreads();
+        for (int s = 128; s > 0; s >>= 1) {
+            if ((int)threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
+            __syncthreads();
+        }
+        if (threadIdx.x == 0) inv_s = 1.0f / __builtin_sqrtf(red[0] / (float)d + eps);
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    for (int i = threadIdx.x; i < d; i += 256) out[(size_t)blockIdx.x * d + i] = row[i] * (inv * w[i]);
+}
+
+// Embedding rows of `tokens` (or of st->token when tokens is null) from the
+// lane-chain f16 table (Dense::row, src/cpu/gemm.rs:412-429).
+__global__ void embed_kernel(const uint16_t* __restrict__ table, int k, const int* __restrict__ tokens,
+                             float* __restrict__ x, const State* st) {
+    if (st->done) return;
+    const int token = tokens ? tokens[blockIdx.x] : st->token;
+    const int s_count = k / 16;
+    for (int kk = threadIdx.x; kk < k; kk += blockDim.x) {
+        const int s = kk / 16, i = kk % 16;
+        x[(size_t)blockIdx.x * k + kk] = f16_to_f32(table[((size_t)token * 16 + i) * s_count + s]);
+    }
+}
+
+// Per (row, head) of the qkv product: Qwen3's per-head RMSNorm of q and k
+// (serial sums, causal_lm.rs:428-433), the rotary halves at the row's
+// position (src/layers.rs:303-334, no fused steps), then k and v appended
+// to the caches at that position (causal_lm.rs:443-446); q is rotated in
+// place. Heads: [0, heads) q, [heads, heads+kvh) k, then v.
+template <typename KV>
+__global__ void qk_rope_kernel(float* __restrict__ qkv, int stride, int heads, int kvh, int hd, int qk_norm,
+                               const float* __restrict__ q_norm, const float* __restrict__ k_norm, float eps,
+                               const float* __restrict__ rope_sin, const float* __restrict__ rope_cos,
+                               KV* __restrict__ kcache, KV* __restrict__ vcache, int max_pos,
+                               const State* st) {
+    if (st->done) return;
+    __shared__ float v[MAX_HD];
+    __shared__ float inv_s;
+    const int row = blockIdx.x / (heads + 2 * kvh);
+    const int head = blockIdx.x % (heads + 2 * kvh);
+    const int e = threadIdx.x;
+    const int pos = st->pos + row;
+    float* src = qkv + (size_t)row * stride + (size_t)head * hd;
+    const bool is_q = head < heads, is_k = !is_q && head < heads + kvh;
+    if (e < hd) v[e] = src[e];
+    __syncthreads();
+    if (qk_norm && (is_q || is_k)) {
+        if (e == 0) {
+            float sum = 0.0f;
+            for (int i = 0; i < hd; ++i) sum = sum + v[i] * v[i];
+            inv_s = 1.0f / __builtin_sqrtf(sum / (float)hd + eps);
+        }
+        __syncthreads();
+        const float* w = is_q ? q_norm : k_norm;
+        float t = 0.0f;
+        if (e < hd) t = v[e] * (inv_s * w[e]);
+        __syncthreads();
+        if (e < hd) v[e] = t;
+        __syncthreads();
+    }
+    float out = 0.0f;
+    if (e < hd) {
+        out = v[e];
+        if (is_q || is_k) {
+            const int half = hd / 2;
+            const int i = e < half ? e : e - half;
+            const float s = rope_sin[(size_t)pos * half + i], c = rope_cos[(size_t)pos * half + i];
+            if (e < half) {
+                const float a = v[e], b = v[e + half];
+                const float ac = a * c, bs = b * s;
+                out = ac - bs;
+            } else {
+                const float a = v[e - half], b = v[e];
+                const float bc = b * c, as = a * s;
+                out = bc + as;
+            }
+        }
+    }
+    if (e < hd) {
+        if (is_q) {
+            src[e] = out;
+        } else {
+            const int g = is_k ? head - heads : head - heads - kvh;
+            KV* cache = is_k ? kcache : vcache;
+            cache[((size_t)g * max_pos + pos) * hd + e] = (KV)out;
+        }
+    }
+}
+
+__device__ __forceinline__ float kv_load(const float* p) { return *p; }
+__device__ __forceinline__ float kv_load(const _Float16* p) { return (float)*p; }
+
+// Attention of row `row` of this forward for query head blockIdx.x over
+// the cache (src/layers.rs:442-504,571-587 with the AVX-512 orders): qh =
+// q * (1/sqrt(hd)); score_j = fused chain over e from 0; keys past the
+// row's position are -inf; max; e_j = exp(s_j - max); sum over j (serial
+// in exact mode); p_j = e_j * (1/sum); out_e = fused chain of p_j * v_je
+// over every key of the forward, from 0.
+template <typename KV>
+__global__ __launch_bounds__(ATT_THREADS) void attention_kernel(
+    const float* __restrict__ qkv, int stride, int heads, int kvh, int hd, const KV* __restrict__ kcache,
+    const KV* __restrict__ vcache, int max_pos, int rows, float* __restrict__ out, int exact, const State* st) {
+    if (st->done) return;
+    extern __shared__ float sm[];  // qh[hd] | probs[tk] | red[ATT_THREADS]
+    const int h = blockIdx.x;
+    const int row = blockIdx.y;
+    const int g = h / (heads / kvh);
+    const int tk = st->pos + rows;       // keys in the caches for this forward
+    const int visible = st->pos + row + 1;
+    float* qh = sm;
+    float* probs = sm + MAX_HD;
+    float* red = probs + tk;
+    const float scale = 1.0f / __builtin_sqrtf((float)hd);
+    const float* q = qkv + (size_t)row * stride + (size_t)h * hd;
+    for (int e = threadIdx.x; e < hd; e += ATT_THREADS) qh[e] = q[e] * scale;
+    __syncthreads();
+    const KV* K = kcache + (size_t)g * max_pos * hd;
+    const KV* V = vcache + (size_t)g * max_pos * hd;
+    float best = -INFINITY;
+    for (int j = threadIdx.x; j < tk; j += ATT_THREADS) {
+        float acc = 0.0f;
+        if (j < visible) {
+            const KV* kr = K + (size_t)j * hd;
+            for (int e = 0; e < hd; ++e) acc = __builtin_fmaf(qh[e], kv_load(kr + e), acc);
+        } else {
+            acc = -INFINITY;
+        }
+        probs[j] = acc;
+        best = __builtin_fmaxf(best, acc);
+    }
+    red[threadIdx.x] = best;
+    __syncthreads();
+    for (int s = ATT_THREADS / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) red[threadIdx.x] = __builtin_fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
+        __syncthreads();
+    }
+    const float mx = red[0];
+    __syncthreads();
+    float part = 0.0f;
+    for (int j = threadIdx.x; j < tk; j += ATT_THREADS) {
+        const float e = exp_trit(probs[j] - mx);
+        probs[j] = e;
+        part += e;
+    }
+    red[threadIdx.x] = part;
+    __syncthreads();
+    if (exact) {
+        if (threadIdx.x == 0) {
+            float sum = 0.0f;
+            for (int j = 0; j < tk; ++j) sum = sum + probs[j];
+            red[0] = sum;
+        }
+        __syncthreads();
+    } else {
+        for (int s = ATT_THREADS / 2; s > 0; s >>= 1) {
+            if ((int)threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
+            __syncthreads();
+        }
+    }
+    const float inv = 1.0f / red[0];
+    __syncthreads();
+    for (int j = threadIdx.x; j < tk; j += ATT_THREADS) probs[j] = probs[j] * inv;
+    __syncthreads();
+    for (int e = threadIdx.x; e < hd; e += ATT_THREADS) {
+        float acc = 0.0f;
+        for (int j = 0; j < tk; ++j) acc = __builtin_fmaf(probs[j], kv_load(V + (size_t)j * hd + e), acc);
+        out[(size_t)row * heads * hd + (size_t)h * hd + e] = acc;
+    }
+}
+
+// Greedy choice (CausalLm::greedy, causal_lm.rs:284-302): the first index
+// of the largest logit (src/layers.rs:604-612); a stop token ends the loop
+// without being kept; max_new kept tokens end it too.
+__global__ void choose_kernel(const float* __restrict__ logits, int n, State* st, int* __restrict__ out) {
+    if (st->done) return;
+    __shared__ float bv[1024];
+    __shared__ int bi[1024];
+    // Each thread keeps the first of its largest values (strict >, indices ascending).
+    int index = (int)threadIdx.x < n ? (int)threadIdx.x : 0;
+    float best = logits[index];
+    for (int i = threadIdx.x + blockDim.x; i < n; i += blockDim.x) {
+        const float v = logits[i];
+        if (v > best) {
+            best = v;
+            index = i;
+        }
+    }
+    bv[threadIdx.x] = best;
+    bi[threadIdx.x] = index;
+    __syncthreads();
+    for (int s = blockDim.x / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) {
+            const float v = bv[threadIdx.x + s];
+            const int i = bi[threadIdx.x + s];
+            if (v > bv[threadIdx.x] || (v == bv[threadIdx.x] && i < bi[threadIdx.x])) {
+                bv[threadIdx.x] = v;
+                bi[threadIdx.x] = i;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const int token = bi[0];
+        st->token = token;
+        bool stop = false;
+        for (int s = 0; s < st->n_stop; ++s) stop |= st->stop[s] == token;
+        if (stop || st->n_out >= st->max_new) {
+            st->done = 1;
+            return;
+        }
+        out[st->n_out] = token;
+        st->n_out += 1;
+        // The forward of the last kept token gives logits nobody reads.
+        if (st->n_out >= st->max_new) st->done = 1;
+    }
+}
+
+__global__ void advance_kernel(State* st, int rows) {
+    if (st->done) return;
+    st->pos += rows;
+}
+
+}  // namespace
+
+// ---- host side ------------------------------------------------------------
+
+struct DecoderImpl {
+    TritHipLmConfig c{};
+    std::vector<LayerRef> qkv, o, gate_up, down;
+    LayerRef embed, head;
+    DeviceMemory norms;  // per layer: attn[d] mlp[d] q[hd] k[hd]; then final[d]
+    size_t layer_norm_stride = 0;
+    const float* norm_attn(int l) const { return norms.as<float>() + l * layer_norm_stride; }
+    const float* norm_mlp(int l) const { return norm_attn(l) + c.d; }
+    const float* q_norm(int l) const { return norm_attn(l) + 2 * c.d; }
+    const float* k_norm(int l) const { return q_norm(l) + c.head_dim; }
+    const float* final_norm() const { return norms.as<float>() + c.layers * layer_norm_stride; }
+};
+
+struct SessionImpl {
+    std::shared_ptr<DecoderImpl> dec;
+    int max_pos = 0, flags = 0;
+    bool exact = false, kv32 = false;
+    int rows_cap = 0;
+    DeviceMemory kcache, vcache, rope_sin, rope_cos;
+    DeviceMemory x, qkv, att, hid, inv, normed, logits, state, tokens_in, tokens_out;
+    int host_pos = 0;
+    hipGraphExec_t graph = nullptr;
+    int graph_out_cap = 0;
+
+    ~SessionImpl() {
+        if (graph) (void)hipGraphExecDestroy(graph);
+    }
+    State* st() const { return state.as<State>(); }
+};
+
+namespace {
+
+// Host rotary table, the glibc calls Trit makes on Linux (src/layers.rs:
+// 291-299,318): inv_freq[i] = base^(-(2i)/dims), angle = pos * inv_freq[i].
+void rope_table(int dims, float base, int positions, std::vector<float>& sn, std::vector<float>& cs) {
+    float (*volatile f_pow)(float, float) = powf;
+    float (*volatile f_sin)(float) = sinf;
+    float (*volatile f_cos)(float) = cosf;
+    const int half = dims / 2;
+    std::vector<float> inv(half);
+    for (int i = 0; i < half; ++i) inv[i] = f_pow(base, -(float)(2 * i) / (float)dims);
+    sn.resize((size_t)positions * half);
+    cs.resize((size_t)positions * half);
+    for (int p = 0; p < positions; ++p)
+        for (int i = 0; i < half; ++i) {
+            const float angle = (float)p * inv[i];
+            sn[(size_t)p * half + i] = f_sin(angle);
+            cs[(size_t)p * half + i] = f_cos(angle);
+        }
+}
+
+void ensure_rows(SessionImpl& S, int rows) {
+    if (rows <= S.rows_cap) return;
+    const auto& c = S.dec->c;
+    const int qd = c.heads * c.head_dim, kv = c.kv_heads * c.head_dim;
+    S.x.alloc((size_t)rows * c.d * 4);
+    S.qkv.alloc((size_t)rows * (qd + 2 * kv) * 4);
+    S.att.alloc((size_t)rows * qd * 4);
+    S.hid.alloc((size_t)rows * c.ffn * 4);
+    S.inv.alloc((size_t)rows * 4);
+    S.normed.alloc((size_t)c.d * 4);
+    S.tokens_in.alloc((size_t)rows * 4);
+    S.rows_cap = rows;
+    if (S.graph) {
+        (void)hipGraphExecDestroy(S.graph);
+        S.graph = nullptr;
+    }
+}
+
+// Integer product of `rows` rows in launches of up to 8.
+void product(const Layer& L, GemvArgs a, int rows, hipStream_t s, int y_stride) {
+    for (int r0 = 0; r0 < rows; r0 += 8) {
+        GemvArgs b = a;
+        b.m = rows - r0 < 8 ? rows - r0 : 8;
+        b.x = a.x + (size_t)r0 * L.k;
+        b.y = a.y + (size_t)r0 * y_stride;
+        if (a.residual) b.residual = a.residual + (size_t)r0 * y_stride;
+        if (a.norm_inv) b.norm_inv = a.norm_inv + r0;
+        layer_forward(L, b, s);
+    }
+}
+
+// One forward of `rows` rows whose embeddings are in S.x, at positions
+// st->pos.., ending with the logits of the last row.
+void forward(SessionImpl& S, int rows, hipStream_t s) {
+    const DecoderImpl& D = *S.dec;
+    const auto& c = D.c;
+    const int hd = c.head_dim, qd = c.heads * hd, kv = c.kv_heads * hd, stride = qd + 2 * kv;
+    State* st = S.st();
+    float* x = S.x.as<float>();
+    for (int l = 0; l < c.layers; ++l) {
+        GemvArgs a;
+        a.eps = c.eps;
+        a.skip = &st->done;
+        // qkv with the attention norm in the prologue.
+        if (S.exact) {
+            hipLaunchKernelGGL(norm_inv_kernel, dim3(rows), dim3(256), c.d * 4, s, x, c.d, c.eps,
+                               S.inv.as<float>(), st);
+            a.norm_inv = S.inv.as<float>();
+        }
+        a.x = x;
+        a.norm_w = D.norm_attn(l);
+        a.y = S.qkv.as<float>();
+        product(*D.qkv[l], a, rows, s, stride);
+        // q/k norm, rotary, cache append.
+        if (S.kv32) {
+            hipLaunchKernelGGL(qk_rope_kernel<float>, dim3(rows * (c.heads + 2 * c.kv_heads)), dim3(hd < 64 ? 64 : hd),
+                               0, s, S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd, c.qk_norm, D.q_norm(l),
+                               D.k_norm(l), c.eps, S.rope_sin.as<float>(), S.rope_cos.as<float>(),
+                               S.kcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd,
+                               S.vcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, st);
+        } else {
+            hipLaunchKernelGGL(qk_rope_kernel<_Float16>, dim3(rows * (c.heads + 2 * c.kv_heads)),
+                               dim3(hd < 64 ? 64 : hd), 0, s, S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
+                               c.qk_norm, D.q_norm(l), D.k_norm(l), c.eps, S.rope_sin.as<float>(),
+                               S.rope_cos.as<float>(),
+                               S.kcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd,
+                               S.vcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, st);
+        }
+        TRIT_HIP(hipGetLastError());
+        // Attention over the caches: the host sizes shared memory for the
+        // largest key count this forward can see.
+        const size_t lds = (size_t)(MAX_HD + S.max_pos + ATT_THREADS) * 4;
+        if (S.kv32) {
+            hipLaunchKernelGGL(attention_kernel<float>, dim3(c.heads, rows), dim3(ATT_THREADS), lds, s,
+                               S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
+                               S.kcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd,
+                               S.vcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, rows,
+                               S.att.as<float>(), (int)S.exact, st);
+        } else {
+            hipLaunchKernelGGL(attention_kernel<_Float16>, dim3(c.heads, rows), dim3(ATT_THREADS), lds, s,
+                               S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
+                               S.kcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd,
+                               S.vcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, rows,
+                               S.att.as<float>(), (int)S.exact, st);
+        }
+        TRIT_HIP(hipGetLastError());
+        // o with the residual add.
+        GemvArgs o;
+        o.skip = &st->done;
+        o.x = S.att.as<float>();
+        o.y = x;
+        o.residual = x;
+        o.epilogue = EPI_RESIDUAL;
+        product(*D.o[l], o, rows, s, c.d);
+        // gate_up with the MLP norm in the prologue and SwiGLU after.
+        GemvArgs gu;
+        gu.skip = &st->done;
+        gu.eps = c.eps;
+        if (S.exact) {
+            hipLaunchKernelGGL(norm_inv_kernel, dim3(rows), dim3(256), c.d * 4, s, x, c.d, c.eps,
+                               S.inv.as<float>(), st);
+            gu.norm_inv = S.inv.as<float>();
+        }
+        gu.x = x;
+        gu.norm_w = D.norm_mlp(l);
+        gu.y = S.hid.as<float>();
+        gu.epilogue = EPI_SILU_PAIR;
+        product(*D.gate_up[l], gu, rows, s, c.ffn);
+        // down with the residual add.
+        GemvArgs dn;
+        dn.skip = &st->done;
+        dn.x = S.hid.as<float>();
+        dn.y = x;
+        dn.residual = x;
+        dn.epilogue = EPI_RESIDUAL;
+        product(*D.down[l], dn, rows, s, c.d);
+    }
+    // Final norm of the last row, then the head.
+    const float* last = x + (size_t)(rows - 1) * c.d;
+    if (S.exact) {
+        hipLaunchKernelGGL(norm_inv_kernel, dim3(1), dim3(256), c.d * 4, s, last, c.d, c.eps, S.inv.as<float>(), st);
+    }
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(256), 0, s, last, c.d, D.final_norm(), c.eps,
+                       S.exact ? S.inv.as<float>() : nullptr, S.normed.as<float>(), st);
+    TRIT_HIP(hipGetLastError());
+    GemvArgs h;
+    h.skip = &st->done;
+    h.x = S.normed.as<float>();
+    h.y = S.logits.as<float>();
+    layer_forward(D.head ? *D.head : *D.embed, h, s);
+    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, st, rows);
+    TRIT_HIP(hipGetLastError());
+}
+
+void read_logits(SessionImpl& S, float* logits) {
+    hipStream_t s = stream();
+    if (logits)
+        TRIT_HIP(hipMemcpyAsync(logits, S.logits.ptr, (size_t)S.dec->c.vocab * 4, hipMemcpyDeviceToHost, s));
+    TRIT_HIP(hipStreamSynchronize(s));
+}
+
+void reset_state(SessionImpl& S) {
+    State init{};
+    TRIT_HIP(hipMemcpy(S.state.ptr, &init, sizeof(State), hipMemcpyHostToDevice));
+    S.host_pos = 0;
+}
+
+// Clears `done` and sets the loop limits for a generate call, keeping pos.
+void arm_state(SessionImpl& S, int max_new, const int32_t* stop, int n_stop) {
+    State h{};
+    TRIT_HIP(hipMemcpy(&h, S.state.ptr, sizeof(State), hipMemcpyDeviceToHost));
+    h.done = 0;
+    h.n_out = 0;
+    h.max_new = max_new;
+    h.n_stop = n_stop;
+    for (int i = 0; i < n_stop; ++i) h.stop[i] = stop[i];
+    TRIT_HIP(hipMemcpy(S.state.ptr, &h, sizeof(State), hipMemcpyHostToDevice));
+}
+
+void build_graph(SessionImpl& S) {
+    if (S.graph) return;
+    hipStream_t s = stream();
+    const auto& c = S.dec->c;
+    hipGraph_t g = nullptr;
+    TRIT_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    try {
+        hipLaunchKernelGGL(choose_kernel, dim3(1), dim3(1024), 0, s, S.logits.as<float>(), c.vocab, S.st(),
+                           S.tokens_out.as<int>());
+        hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, s, S.dec->embed->codes.as<uint16_t>(), c.d,
+                           (const int*)nullptr, S.x.as<float>(), S.st());
+        forward(S, 1, s);
+    } catch (...) {
+        (void)hipStreamEndCapture(s, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+    }
+    TRIT_HIP(hipStreamEndCapture(s, &g));
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    TRIT_HIP(e);
+    S.graph = exec;
+}
+
+}  // namespace
+}  // namespace trit
+
+struct TritHipDecoder {
+    std::shared_ptr<trit::DecoderImpl> impl;
+};
+struct TritHipSession {
+    trit::SessionImpl impl;
+};
+
+using namespace trit;
+
+extern "C" {
+
+int trit_hip_decoder_new(const TritHipLmConfig* config, const TritHipLayer* const* linears, const float* norms,
+                         const TritHipLayer* embed, const TritHipLayer* head, TritHipDecoder** out) {
+    return guard(-1, [&] {
+        if (!config || !linears || !norms || !embed || !out) fail("decoder: a required argument is NULL");
+        const TritHipLmConfig& c = *config;
+        if (c.heads <= 0 || c.kv_heads <= 0 || c.heads % c.kv_heads != 0)
+            fail("decoder: the query heads do not share the key heads evenly");
+        if (c.head_dim <= 0 || c.head_dim > MAX_HD || c.head_dim % 2 != 0)
+            fail("decoder: head_dim must be even and at most 256");
+        auto D = std::make_shared<DecoderImpl>();
+        D->c = c;
+        const int hd = c.head_dim, qkv_rows = (c.heads + 2 * c.kv_heads) * hd;
+        auto want = [&](const TritHipLayer* h, int n, int k, const char* what, int l) {
+            LayerRef L = layer_ref(h);
+            if (!L) fail(std::string("decoder: layer ") + std::to_string(l) + " " + what + " is NULL");
+            if (L->n != n || L->k != k)
+                fail(std::string("decoder: layer ") + std::to_string(l) + " " + what + " is " + std::to_string(L->n) +
+                     "x" + std::to_string(L->k) + ", expected " + std::to_string(n) + "x" + std::to_string(k));
+            if (L->kind == F16 || L->kind == TERNARY)
+                fail(std::string("decoder: layer ") + std::to_string(l) + " " + what +
+                     " must be Q8_0, Q4_K or int8");
+            return L;
+        };
+        for (int l = 0; l < c.layers; ++l) {
+            D->qkv.push_back(want(linears[4 * l], qkv_rows, c.d, "qkv", l));
+            D->o.push_back(want(linears[4 * l + 1], c.d, c.heads * hd, "o", l));
+            D->gate_up.push_back(want(linears[4 * l + 2], 2 * c.ffn, c.d, "gate_up", l));
+            D->down.push_back(want(linears[4 * l + 3], c.d, c.ffn, "down", l));
+        }
+        D->embed = layer_ref(embed);
+        if (D->embed->kind != F16 || D->embed->n != c.vocab || D->embed->k != c.d)
+            fail("decoder: embed must be an F16 vocab x d table");
+        if (head) {
+            D->head = layer_ref(head);
+            if (D->head->n != c.vocab || D->head->k != c.d) fail("decoder: head must be vocab x d");
+        }
+        D->layer_norm_stride = (size_t)2 * c.d + (c.qk_norm ? 2 * hd : 0);
+        const size_t count = D->layer_norm_stride * c.layers + c.d;
+        // q/k norm slots exist even without qk_norm so the pointers stay valid.
+        D->layer_norm_stride = (size_t)2 * c.d + 2 * hd;
+        std::vector<float> packed(D->layer_norm_stride * c.layers + c.d, 1.0f);
+        const float* src = norms;
+        for (int l = 0; l < c.layers; ++l) {
+            float* dst = packed.data() + l * D->layer_norm_stride;
+            std::memcpy(dst, src, (size_t)2 * c.d * 4);
+            src += 2 * c.d;
+            if (c.qk_norm) {
+                std::memcpy(dst + 2 * c.d, src, (size_t)2 * hd * 4);
+                src += 2 * hd;
+            }
+        }
+        std::memcpy(packed.data() + D->layer_norm_stride * c.layers, src, (size_t)c.d * 4);
+        (void)count;
+        D->norms.alloc(packed.size() * 4);
+        D->norms.upload(packed.data(), packed.size() * 4);
+        *out = new TritHipDecoder{D};
+        return 0;
+    });
+}
+
+void trit_hip_decoder_free(TritHipDecoder* decoder) { delete decoder; }
+
+int trit_hip_session_new(const TritHipDecoder* decoder, int max_positions, int flags, TritHipSession** out) {
+    return guard(-1, [&] {
+        if (!decoder || !out) fail("session: decoder or out is NULL");
+        if (max_positions <= 0) fail("session: max_positions must be positive");
+        auto* S = new TritHipSession();
+        try {
+            SessionImpl& s = S->impl;
+            s.dec = decoder->impl;
+            const auto& c = s.dec->c;
+            s.max_pos = max_positions;
+            s.flags = flags;
+            s.exact = (flags & TRIT_HIP_EXACT) != 0;
+            s.kv32 = s.exact || (flags & TRIT_HIP_KV_F32) != 0;
+            const size_t lds = (size_t)(MAX_HD + max_positions + ATT_THREADS) * 4;
+            if (lds > 64 * 1024) fail("session: max_positions above the attention kernel's limit (16000)");
+            const size_t kvb = (size_t)c.layers * c.kv_heads * max_positions * c.head_dim * (s.kv32 ? 4 : 2);
+            s.kcache.alloc(kvb);
+            s.vcache.alloc(kvb);
+            std::vector<float> sn, cs;
+            rope_table(c.head_dim, c.rope_base, max_positions, sn, cs);
+            s.rope_sin.alloc(sn.size() * 4);
+            s.rope_sin.upload(sn.data(), sn.size() * 4);
+            s.rope_cos.alloc(cs.size() * 4);
+            s.rope_cos.upload(cs.data(), cs.size() * 4);
+            s.logits.alloc((size_t)c.vocab * 4);
+            s.state.alloc(sizeof(State));
+            ensure_rows(s, 8);
+            reset_state(s);
+        } catch (...) {
+            delete S;
+            throw;
+        }
+        *out = S;
+        return 0;
+    });
+}
+
+static int prefill_common(TritHipSession* session, int n, float* logits, const int32_t* tokens, const float* rows) {
+    if (!session) fail("session is NULL");
+    if (n <= 0) fail("prefill: no rows");
+    SessionImpl& S = session->impl;
+    const auto& c = S.dec->c;
+    if (S.host_pos + n > S.max_pos)
+        fail("prefill: " + std::to_string(S.host_pos + n) + " positions exceed the session's " +
+             std::to_string(S.max_pos));
+    ensure_rows(S, n);
+    hipStream_t s = stream();
+    // A forward after a finished loop continues from the kept positions.
+    State h{};
+    TRIT_HIP(hipMemcpy(&h, S.state.ptr, sizeof(State), hipMemcpyDeviceToHost));
+    h.done = 0;
+    TRIT_HIP(hipMemcpy(S.state.ptr, &h, sizeof(State), hipMemcpyHostToDevice));
+    if (tokens) {
+        for (int i = 0; i < n; ++i)
+            if (tokens[i] < 0 || tokens[i] >= c.vocab) fail("prefill: token " + std::to_string(tokens[i]) + " out of range");
+        TRIT_HIP(hipMemcpyAsync(S.tokens_in.ptr, tokens, (size_t)n * 4, hipMemcpyHostToDevice, s));
+        hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, s, S.dec->embed->codes.as<uint16_t>(), c.d,
+                           S.tokens_in.as<int>(), S.x.as<float>(), S.st());
+        TRIT_HIP(hipGetLastError());
+    } else {
+        TRIT_HIP(hipMemcpyAsync(S.x.ptr, rows, (size_t)n * c.d * 4, hipMemcpyHostToDevice, s));
+    }
+    forward(S, n, s);
+    S.host_pos += n;
+    read_logits(S, logits);
+    return 0;
+}
+
+int trit_hip_session_prefill(TritHipSession* session, const int32_t* tokens, int n, float* logits) {
+    return guard(-1, [&] {
+        if (!tokens) fail("prefill: tokens is NULL");
+        return prefill_common(session, n, logits, tokens, nullptr);
+    });
+}
+
+int trit_hip_session_prefill_rows(TritHipSession* session, const float* rows, int n, float* logits) {
+    return guard(-1, [&] {
+        if (!rows) fail("prefill: rows is NULL");
+        return prefill_common(session, n, logits, nullptr, rows);
+    });
+}
+
+int trit_hip_session_generate(TritHipSession* session, int max_new, const int32_t* stop, int n_stop, int32_t* out) {
+    return guard(-1, [&] {
+        if (!session) fail("session is NULL");
+        SessionImpl& S = session->impl;
+        if (S.host_pos == 0) fail("generate: prefill a prompt first");
+        if (max_new <= 0) return 0;
+        if (!out) fail("generate: out is NULL");
+        if (n_stop < 0 || n_stop > MAX_STOP) fail("generate: at most 64 stop tokens");
+        if (n_stop && !stop) fail("generate: stop is NULL");
+        // The loop forwards up to max_new - 1 new tokens.
+        if (S.host_pos + max_new - 1 > S.max_pos)
+            fail("generate: " + std::to_string(max_new) + " tokens exceed the session's positions");
+        if (S.graph_out_cap < max_new) {
+            S.tokens_out.alloc((size_t)max_new * 4);
+            S.graph_out_cap = max_new;
+            if (S.graph) {
+                (void)hipGraphExecDestroy(S.graph);
+                S.graph = nullptr;
+            }
+        }
+        arm_state(S, max_new, stop, n_stop);
+        build_graph(S);
+        hipStream_t s = stream();
+        for (int i = 0; i < max_new; ++i) TRIT_HIP(hipGraphLaunch(S.graph, s));
+        State h{};
+        TRIT_HIP(hipMemcpyAsync(&h, S.state.ptr, sizeof(State), hipMemcpyDeviceToHost, s));
+        TRIT_HIP(hipStreamSynchronize(s));
+        TRIT_HIP(hipMemcpy(out, S.tokens_out.ptr, (size_t)h.n_out * 4, hipMemcpyDeviceToHost));
+        S.host_pos = h.pos;
+        return h.n_out;
+    });
+}
+
+int trit_hip_session_reset(TritHipSession* session) {
+    return guard(-1, [&] {
+        if (!session) fail("session is NULL");
+        reset_state(session->impl);
+        return 0;
+    });
+}
+
+int trit_hip_session_position(const TritHipSession* session) {
+    return guard(-1, [&] {
+        if (!session) fail("session is NULL");
+        return session->impl.host_pos;
+    });
+}
+
+void trit_hip_session_free(TritHipSession* session) { delete session; }
+
+}  // extern "C"

@@ -164,6 +164,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
                                                         const float* __restrict__ bias, int n, int k,
                                                         GemvArgs a) {
     extern __shared__ __align__(16) char smem_raw[];
+    if (a.skip && *a.skip) return;
     const int m = a.m;
     const int groups = k / W::G;
     const int rows_tile = P * R;

@@ -23,6 +23,7 @@ template <int S8>  // S8 = 16-byte loads per chain (k / 128); 0: any k (2-byte l
 __global__ __launch_bounds__(THREADS) void f16_kernel(const uint16_t* __restrict__ w, const float* __restrict__ bias,
                                                       int n, int k, GemvArgs a) {
     extern __shared__ __align__(16) float xs[];  // m x k
+    if (a.skip && *a.skip) return;
     const int m = a.m;
     for (int i = threadIdx.x; i < m * k; i += THREADS) xs[i] = a.x[i];
     __syncthreads();

@@ -113,6 +113,8 @@ struct GemvArgs {
     const float* residual = nullptr;
     int epilogue = EPI_STORE;
     int relu = 0;
+    // Device flag: nonzero skips the launch (a finished decode loop).
+    const int* skip = nullptr;
 };
 
 // Integer products (Q8_0, Q4_K, INT8, TERNARY), m <= 8.
