@@ -184,6 +184,7 @@ def main():
     print("[bench] warm-up done", file=sys.stderr, flush=True)
 
     sess.reset()
+    print("[bench] timed prefill + decode ...", file=sys.stderr, flush=True)
     t0 = time.perf_counter()
     sess.prefill(prompt, want_logits=False)
     t_prefill = time.perf_counter() - t0
@@ -194,6 +195,7 @@ def main():
     print(f"[bench] gpu decode {value:.1f} tok/s, prefill {args.prompt / t_prefill:.1f} tok/s",
           file=sys.stderr, flush=True)
 
+    print("[bench] roofline sweep ...", file=sys.stderr, flush=True)
     H = Hip()
     roof = gemv_roofline(H, linears, cfg, args.sweeps)
     print(f"[bench] roofline {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}%)", file=sys.stderr, flush=True)

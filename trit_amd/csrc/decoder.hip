@@ -16,6 +16,7 @@
 // RMSNorm sum is Trit's serial chain; in fast mode each product block
 // computes it with a fixed tree.
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 
 #include "../../include/trit_hip.h"
@@ -37,8 +38,12 @@ struct State {
     int max_new;    // loop limit
     int n_stop;     // stop tokens
     int token;      // the last token chosen
+    unsigned int arrived;  // blocks of the greedy choice that are done (back to 0 after)
     int stop[MAX_STOP];
 };
+
+constexpr int CHOOSE_THREADS = 256;
+constexpr int CHOOSE_SPAN = CHOOSE_THREADS * 4;  // logits per block
 
 // ---- small kernels ----------------------------------------------------
 
@@ -57,7 +62,15 @@ __global__ void norm_inv_kernel(const float* __restrict__ x, int d, float eps, f
     __syncthreads();
     if (threadIdx.x == 0) {
         float sum = 0.0f;
-        for (int i = 0; i < d; ++i) sum = sum + sq[i];
+        int i = 0;
+        for (; i + 4 <= d; i += 4) {
+            const float4 q4 = *(const float4*)(sq + i);
+            sum = sum + q4.x;
+            sum = sum + q4.y;
+            sum = sum + q4.z;
+            sum = sum + q4.w;
+        }
+        for (; i < d; ++i) sum = sum + sq[i];
         inv[blockIdx.x] = 1.0f / __builtin_sqrtf(sum / (float)d + eps);
     }
 }
@@ -126,9 +139,19 @@ __global__ void qk_rope_kernel(float* __restrict__ qkv, int stride, int heads, i
     if (e < hd) v[e] = src[e];
     __syncthreads();
     if (qk_norm && (is_q || is_k)) {
+        __shared__ __align__(16) float sq[MAX_HD];
+        if (e < hd) sq[e] = v[e] * v[e];
+        __syncthreads();
         if (e == 0) {
+            // Trit's serial sum of the rounded squares (src/layers.rs:139).
             float sum = 0.0f;
-            for (int i = 0; i < hd; ++i) sum = sum + v[i] * v[i];
+            for (int i = 0; i < hd; i += 4) {
+                const float4 q4 = *(const float4*)(sq + i);
+                sum = sum + q4.x;
+                sum = sum + q4.y;
+                sum = sum + q4.z;
+                sum = sum + q4.w;
+            }
             inv_s = 1.0f / __builtin_sqrtf(sum / (float)hd + eps);
         }
         __syncthreads();
@@ -171,6 +194,22 @@ __global__ void qk_rope_kernel(float* __restrict__ qkv, int stride, int heads, i
 __device__ __forceinline__ float kv_load(const float* p) { return *p; }
 __device__ __forceinline__ float kv_load(const _Float16* p) { return (float)*p; }
 
+// Eight consecutive cache values (16- or 32-byte aligned) as f32.
+__device__ __forceinline__ void kv_load8(const float* p, float* out) {
+    const float4 a = ((const float4*)p)[0], b = ((const float4*)p)[1];
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+    out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+}
+__device__ __forceinline__ void kv_load8(const _Float16* p, float* out) {
+    const uint4 v = *(const uint4*)p;
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        out[2 * i] = f16_to_f32((uint16_t)(w[i] & 0xffff));
+        out[2 * i + 1] = f16_to_f32((uint16_t)(w[i] >> 16));
+    }
+}
+
 // Attention of row `row` of this forward for query head blockIdx.x over
 // the cache (src/layers.rs:442-504,571-587 with the AVX-512 orders): qh =
 // q * (1/sqrt(hd)); score_j = fused chain over e from 0; keys past the
@@ -202,7 +241,12 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(
         float acc = 0.0f;
         if (j < visible) {
             const KV* kr = K + (size_t)j * hd;
-            for (int e = 0; e < hd; ++e) acc = __builtin_fmaf(qh[e], kv_load(kr + e), acc);
+            for (int e = 0; e < hd; e += 8) {
+                float kv[8];
+                kv_load8(kr + e, kv);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(qh[e + u], kv[u], acc);
+            }
         } else {
             acc = -INFINITY;
         }
@@ -228,7 +272,15 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(
     if (exact) {
         if (threadIdx.x == 0) {
             float sum = 0.0f;
-            for (int j = 0; j < tk; ++j) sum = sum + probs[j];
+            int j = 0;
+            for (; j + 4 <= tk; j += 4) {
+                const float4 p4 = *(const float4*)(probs + j);
+                sum = sum + p4.x;
+                sum = sum + p4.y;
+                sum = sum + p4.z;
+                sum = sum + p4.w;
+            }
+            for (; j < tk; ++j) sum = sum + probs[j];
             red[0] = sum;
         }
         __syncthreads();
@@ -244,55 +296,250 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(
     __syncthreads();
     for (int e = threadIdx.x; e < hd; e += ATT_THREADS) {
         float acc = 0.0f;
-        for (int j = 0; j < tk; ++j) acc = __builtin_fmaf(probs[j], kv_load(V + (size_t)j * hd + e), acc);
+        int j = 0;
+        for (; j + 16 <= tk; j += 16) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v[u] = kv_load(V + (size_t)(j + u) * hd + e);
+#pragma unroll
+            for (int u = 0; u < 16; ++u) acc = __builtin_fmaf(probs[j + u], v[u], acc);
+        }
+        for (; j < tk; ++j) acc = __builtin_fmaf(probs[j], kv_load(V + (size_t)j * hd + e), acc);
         out[(size_t)row * heads * hd + (size_t)h * hd + e] = acc;
+    }
+}
+
+// Keys per block of the split attention: 64 with f16 caches, 32 with f32,
+// so the staged chunk of keys and values is 32 KB either way.
+template <typename KV>
+struct Split {
+    static constexpr int CH = sizeof(KV) == 2 ? 64 : 32;
+};
+
+// Fast-mode attention (split over the keys, "flash decoding"): block
+// (g, split, row) stages keys and values [split*CH, split*CH+CH) of
+// key/value head g in LDS with one round of 16-byte loads, scores them
+// against the query heads that share g (16 lanes per dot product), and
+// keeps the chunk's maximum, sum of exp(s - max) and unnormalised p.V. The
+// last block of (row, g) merges the chunks with the usual rescaling. Keys
+// past the row's position get no weight. The sums run in parallel, so the
+// values are within rounding of the exact kernel's, not equal to them.
+template <typename KV>
+__global__ __launch_bounds__(ATT_THREADS) void attention_split_kernel(
+    const float* __restrict__ qkv, int stride, int heads, int kvh, int hd, const KV* __restrict__ kcache,
+    const KV* __restrict__ vcache, int max_pos, int rows, float* __restrict__ out, float* __restrict__ part,
+    unsigned int* __restrict__ arrived, int max_splits, const State* st) {
+    constexpr int CH = Split<KV>::CH;
+    constexpr int PER = 16 / sizeof(KV);  // cache values per 16-byte load
+    if (st->done) return;
+    extern __shared__ __align__(16) char smem[];
+    KV* Ks = (KV*)smem;
+    KV* Vs = Ks + CH * hd;
+    __shared__ float qh[4 * 128];
+    __shared__ float sc[4][CH];
+    __shared__ float mrow[4], lrow[4];
+    __shared__ bool last;
+    const int g = blockIdx.x, split = blockIdx.y, row = blockIdx.z;
+    const int group = heads / kvh;
+    const int tk = st->pos + rows;
+    const int visible = st->pos + row + 1;
+    const int j0 = split * CH;
+    const int splits = (tk + CH - 1) / CH;
+    if (split >= splits) return;
+    const int nk = min(CH, tk - j0);
+    const uint4* K = (const uint4*)(kcache + ((size_t)g * max_pos + j0) * hd);
+    const uint4* V = (const uint4*)(vcache + ((size_t)g * max_pos + j0) * hd);
+    // Stage the chunk: every load is issued before the first store waits.
+    const int units = nk * hd / PER;
+    constexpr int UPT = CH * 128 / (16 / (int)sizeof(KV)) / ATT_THREADS;  // units per thread at hd 128
+    uint4 kr[UPT], vr[UPT];
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+        // Past the chunk, re-read its first unit (in bounds); the store skips it.
+        const int u = (int)threadIdx.x + i * ATT_THREADS;
+        const int uc = u < units ? u : 0;
+        kr[i] = K[uc];
+        vr[i] = V[uc];
+    }
+    const float scale = 1.0f / __builtin_sqrtf((float)hd);
+    for (int i = threadIdx.x; i < group * hd; i += ATT_THREADS) {
+        const int h = g * group + i / hd;
+        qh[i] = qkv[(size_t)row * stride + (size_t)h * hd + i % hd] * scale;
+    }
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+        const int u = (int)threadIdx.x + i * ATT_THREADS;
+        if (u < units) {
+            ((uint4*)Ks)[u] = kr[i];
+            ((uint4*)Vs)[u] = vr[i];
+        }
+    }
+    for (int u = (int)threadIdx.x + UPT * ATT_THREADS; u < units; u += ATT_THREADS) {
+        ((uint4*)Ks)[u] = K[u];
+        ((uint4*)Vs)[u] = V[u];
+    }
+    __syncthreads();
+    // Scores: 16 lanes per (head, key), 8 dims per lane and step.
+    const int lane16 = threadIdx.x & 15;
+    for (int pi = threadIdx.x >> 4; pi < group * CH; pi += ATT_THREADS / 16) {
+        const int hl = pi / CH, j = pi % CH;
+        float acc = 0.0f;
+        if (j < nk) {
+            const float* q = qh + hl * hd;
+            for (int e = lane16 * 8; e < hd; e += 128) {
+                float kv[8];
+                kv_load8(Ks + (size_t)j * hd + e, kv);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(q[e + u], kv[u], acc);
+            }
+        }
+        acc += __shfl_xor(acc, 8);
+        acc += __shfl_xor(acc, 4);
+        acc += __shfl_xor(acc, 2);
+        acc += __shfl_xor(acc, 1);
+        if (lane16 == 0) sc[hl][j] = (j < nk && j0 + j < visible) ? acc : -INFINITY;
+    }
+    __syncthreads();
+    if (threadIdx.x < group) {
+        const int hl = threadIdx.x;
+        float mx = -INFINITY;
+        for (int j = 0; j < nk; ++j) mx = __builtin_fmaxf(mx, sc[hl][j]);
+        float l = 0.0f;
+        for (int j = 0; j < nk; ++j) {
+            const float e = sc[hl][j] == -INFINITY ? 0.0f : exp_trit(sc[hl][j] - mx);
+            sc[hl][j] = e;
+            l += e;
+        }
+        mrow[hl] = mx;
+        lrow[hl] = l;
+    }
+    __syncthreads();
+    const size_t slot = ((size_t)row * heads + g * group) * max_splits;
+    for (int t = threadIdx.x; t < group * hd; t += ATT_THREADS) {
+        const int hl = t / hd, e = t % hd;
+        float acc = 0.0f;
+        for (int j = 0; j < nk; ++j) acc = __builtin_fmaf(sc[hl][j], kv_load(Vs + (size_t)j * hd + e), acc);
+        float* p = part + (slot + (size_t)hl * max_splits + split) * (hd + 2);
+        p[2 + e] = acc;
+        if (e == 0) {
+            p[0] = mrow[hl];
+            p[1] = lrow[hl];
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence();
+        unsigned int* ctr = arrived + (size_t)row * kvh + g;
+        last = atomicAdd(ctr, 1u) == (unsigned)splits - 1;
+        if (last) *ctr = 0;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    for (int t = threadIdx.x; t < group * hd; t += ATT_THREADS) {
+        const int hl = t / hd, e = t % hd;
+        const float* base = part + (slot + (size_t)hl * max_splits) * (hd + 2);
+        float M = -INFINITY;
+        for (int s2 = 0; s2 < splits; ++s2) M = __builtin_fmaxf(M, base[(size_t)s2 * (hd + 2)]);
+        float L = 0.0f, O = 0.0f;
+        for (int s2 = 0; s2 < splits; ++s2) {
+            const float* p = base + (size_t)s2 * (hd + 2);
+            if (p[0] == -INFINITY) continue;
+            const float w = exp_trit(p[0] - M);
+            L = __builtin_fmaf(p[1], w, L);
+            O = __builtin_fmaf(p[2 + e], w, O);
+        }
+        out[(size_t)row * heads * hd + (size_t)(g * group + hl) * hd + e] = O / L;
     }
 }
 
 // Greedy choice (CausalLm::greedy, causal_lm.rs:284-302): the first index
 // of the largest logit (src/layers.rs:604-612); a stop token ends the loop
-// without being kept; max_new kept tokens end it too.
-__global__ void choose_kernel(const float* __restrict__ logits, int n, State* st, int* __restrict__ out) {
+// without being kept; max_new kept tokens end it too. Each block takes
+// CHOOSE_SPAN logits; the last block to arrive reduces the blocks' winners,
+// commits the token and writes its embedding row (the next forward's input).
+__device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+__global__ __launch_bounds__(CHOOSE_THREADS) void choose_kernel(const float* __restrict__ logits, int n, State* st,
+                                                                 int* __restrict__ out, float2* __restrict__ part,
+                                                                 const uint16_t* __restrict__ table, int d,
+                                                                 float* __restrict__ x) {
     if (st->done) return;
-    __shared__ float bv[1024];
-    __shared__ int bi[1024];
-    // Each thread keeps the first of its largest values (strict >, indices ascending).
-    int index = (int)threadIdx.x < n ? (int)threadIdx.x : 0;
-    float best = logits[index];
-    for (int i = threadIdx.x + blockDim.x; i < n; i += blockDim.x) {
-        const float v = logits[i];
-        if (v > best) {
-            best = v;
-            index = i;
+    __shared__ float bv[CHOOSE_THREADS];
+    __shared__ int bi[CHOOSE_THREADS];
+    __shared__ bool last;
+    const int i0 = blockIdx.x * CHOOSE_SPAN + (int)threadIdx.x * 4;
+    float best = -INFINITY;
+    int index = 0x7fffffff;
+    for (int j = 0; j < 4; ++j) {
+        const int i = i0 + j;
+        if (i < n) {
+            const float v = logits[i];
+            if (index == 0x7fffffff || v > best) {
+                best = v;
+                index = i;
+            }
         }
     }
     bv[threadIdx.x] = best;
     bi[threadIdx.x] = index;
     __syncthreads();
-    for (int s = blockDim.x / 2; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s) {
-            const float v = bv[threadIdx.x + s];
-            const int i = bi[threadIdx.x + s];
-            if (v > bv[threadIdx.x] || (v == bv[threadIdx.x] && i < bi[threadIdx.x])) {
-                bv[threadIdx.x] = v;
-                bi[threadIdx.x] = i;
-            }
-        }
+    for (int s = CHOOSE_THREADS / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) better(bv[threadIdx.x], bi[threadIdx.x], bv[threadIdx.x + s], bi[threadIdx.x + s]);
         __syncthreads();
     }
     if (threadIdx.x == 0) {
+        part[blockIdx.x] = make_float2(bv[0], __int_as_float(bi[0]));
+        __threadfence();
+        last = atomicAdd(&st->arrived, 1u) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    best = -INFINITY;
+    index = 0x7fffffff;
+    for (int b = threadIdx.x; b < (int)gridDim.x; b += CHOOSE_THREADS) {
+        const float2 p = part[b];
+        better(best, index, p.x, __float_as_int(p.y));
+    }
+    bv[threadIdx.x] = best;
+    bi[threadIdx.x] = index;
+    __syncthreads();
+    for (int s = CHOOSE_THREADS / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) better(bv[threadIdx.x], bi[threadIdx.x], bv[threadIdx.x + s], bi[threadIdx.x + s]);
+        __syncthreads();
+    }
+    __shared__ int commit;
+    if (threadIdx.x == 0) {
+        st->arrived = 0;
         const int token = bi[0];
         st->token = token;
         bool stop = false;
         for (int s = 0; s < st->n_stop; ++s) stop |= st->stop[s] == token;
+        commit = 0;
         if (stop || st->n_out >= st->max_new) {
             st->done = 1;
-            return;
+        } else {
+            out[st->n_out] = token;
+            st->n_out += 1;
+            // The forward of the last kept token gives logits nobody reads.
+            if (st->n_out >= st->max_new) st->done = 1;
+            else commit = 1;
         }
-        out[st->n_out] = token;
-        st->n_out += 1;
-        // The forward of the last kept token gives logits nobody reads.
-        if (st->n_out >= st->max_new) st->done = 1;
+    }
+    __syncthreads();
+    if (!commit) return;
+    // Dense::row of the chosen token (src/cpu/gemm.rs:412-429).
+    const int token = bi[0];
+    const int s_count = d / 16;
+    for (int kk = threadIdx.x; kk < d; kk += CHOOSE_THREADS) {
+        const int s = kk / 16, i = kk % 16;
+        x[kk] = f16_to_f32(table[((size_t)token * 16 + i) * s_count + s]);
     }
 }
 
@@ -324,7 +571,9 @@ struct SessionImpl {
     bool exact = false, kv32 = false;
     int rows_cap = 0;
     DeviceMemory kcache, vcache, rope_sin, rope_cos;
-    DeviceMemory x, qkv, att, hid, inv, normed, logits, state, tokens_in, tokens_out;
+    DeviceMemory x, qkv, att, hid, inv, normed, logits, state, tokens_in, tokens_out, partials;
+    DeviceMemory att_part, att_arrived;  // split attention: chunk partials, per (row, kv head) counters
+    int max_splits = 0;
     int host_pos = 0;
     hipGraphExec_t graph = nullptr;
     int graph_out_cap = 0;
@@ -367,6 +616,10 @@ void ensure_rows(SessionImpl& S, int rows) {
     S.inv.alloc((size_t)rows * 4);
     S.normed.alloc((size_t)c.d * 4);
     S.tokens_in.alloc((size_t)rows * 4);
+    S.max_splits = (S.max_pos + Split<float>::CH - 1) / Split<float>::CH;
+    S.att_part.alloc((size_t)rows * c.heads * S.max_splits * (c.head_dim + 2) * 4);
+    S.att_arrived.alloc((size_t)rows * c.kv_heads * 4);
+    TRIT_HIP(hipMemset(S.att_arrived.ptr, 0, (size_t)rows * c.kv_heads * 4));
     S.rows_cap = rows;
     if (S.graph) {
         (void)hipGraphExecDestroy(S.graph);
@@ -425,21 +678,35 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
                                S.vcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, st);
         }
         TRIT_HIP(hipGetLastError());
-        // Attention over the caches: the host sizes shared memory for the
-        // largest key count this forward can see.
-        const size_t lds = (size_t)(MAX_HD + S.max_pos + ATT_THREADS) * 4;
-        if (S.kv32) {
+        // Attention over the caches.
+        if (S.exact) {
+            // The host sizes shared memory for the largest key count this forward can see.
+            const size_t lds = (size_t)(MAX_HD + S.max_pos + ATT_THREADS) * 4;
             hipLaunchKernelGGL(attention_kernel<float>, dim3(c.heads, rows), dim3(ATT_THREADS), lds, s,
                                S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
                                S.kcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd,
                                S.vcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, rows,
-                               S.att.as<float>(), (int)S.exact, st);
+                               S.att.as<float>(), 1, st);
         } else {
-            hipLaunchKernelGGL(attention_kernel<_Float16>, dim3(c.heads, rows), dim3(ATT_THREADS), lds, s,
-                               S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
-                               S.kcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd,
-                               S.vcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, rows,
-                               S.att.as<float>(), (int)S.exact, st);
+            if (S.kv32) {
+                const dim3 grid(c.kv_heads, (S.max_pos + Split<float>::CH - 1) / Split<float>::CH, rows);
+                const size_t lds = (size_t)2 * Split<float>::CH * hd * 4;
+                hipLaunchKernelGGL(attention_split_kernel<float>, grid, dim3(ATT_THREADS), lds, s, S.qkv.as<float>(),
+                                   stride, c.heads, c.kv_heads, hd,
+                                   S.kcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd,
+                                   S.vcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, rows,
+                                   S.att.as<float>(), S.att_part.as<float>(), S.att_arrived.as<unsigned int>(),
+                                   S.max_splits, st);
+            } else {
+                const dim3 grid(c.kv_heads, (S.max_pos + Split<_Float16>::CH - 1) / Split<_Float16>::CH, rows);
+                const size_t lds = (size_t)2 * Split<_Float16>::CH * hd * 2;
+                hipLaunchKernelGGL(attention_split_kernel<_Float16>, grid, dim3(ATT_THREADS), lds, s,
+                                   S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
+                                   S.kcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd,
+                                   S.vcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos,
+                                   rows, S.att.as<float>(), S.att_part.as<float>(),
+                                   S.att_arrived.as<unsigned int>(), S.max_splits, st);
+            }
         }
         TRIT_HIP(hipGetLastError());
         // o with the residual add.
@@ -515,18 +782,30 @@ void arm_state(SessionImpl& S, int max_new, const int32_t* stop, int n_stop) {
     TRIT_HIP(hipMemcpy(S.state.ptr, &h, sizeof(State), hipMemcpyHostToDevice));
 }
 
+// One greedy step: choose, embed the chosen token, forward it.
+void step(SessionImpl& S, hipStream_t s) {
+    const auto& c = S.dec->c;
+    const int blocks = (c.vocab + CHOOSE_SPAN - 1) / CHOOSE_SPAN;
+    hipLaunchKernelGGL(choose_kernel, dim3(blocks), dim3(CHOOSE_THREADS), 0, s, S.logits.as<float>(), c.vocab,
+                       S.st(), S.tokens_out.as<int>(), S.partials.as<float2>(), S.dec->embed->codes.as<uint16_t>(),
+                       c.d, S.x.as<float>());
+    forward(S, 1, s);
+}
+
+// TRIT_HIP_GRAPH=0 launches each step's kernels one by one instead of
+// replaying a captured graph (same kernels, same results).
+bool use_graph() {
+    const char* v = getenv("TRIT_HIP_GRAPH");
+    return !(v && v[0] == '0');
+}
+
 void build_graph(SessionImpl& S) {
     if (S.graph) return;
     hipStream_t s = stream();
-    const auto& c = S.dec->c;
     hipGraph_t g = nullptr;
     TRIT_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
     try {
-        hipLaunchKernelGGL(choose_kernel, dim3(1), dim3(1024), 0, s, S.logits.as<float>(), c.vocab, S.st(),
-                           S.tokens_out.as<int>());
-        hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, s, S.dec->embed->codes.as<uint16_t>(), c.d,
-                           (const int*)nullptr, S.x.as<float>(), S.st());
-        forward(S, 1, s);
+        step(S, s);
     } catch (...) {
         (void)hipStreamEndCapture(s, &g);
         if (g) (void)hipGraphDestroy(g);
@@ -561,8 +840,9 @@ int trit_hip_decoder_new(const TritHipLmConfig* config, const TritHipLayer* cons
         const TritHipLmConfig& c = *config;
         if (c.heads <= 0 || c.kv_heads <= 0 || c.heads % c.kv_heads != 0)
             fail("decoder: the query heads do not share the key heads evenly");
-        if (c.head_dim <= 0 || c.head_dim > MAX_HD || c.head_dim % 2 != 0)
-            fail("decoder: head_dim must be even and at most 256");
+        if (c.head_dim <= 0 || c.head_dim > 128 || c.head_dim % 8 != 0)
+            fail("decoder: head_dim must be a multiple of 8 and at most 128");
+        if (c.heads / c.kv_heads > 4) fail("decoder: at most 4 query heads per key/value head");
         auto D = std::make_shared<DecoderImpl>();
         D->c = c;
         const int hd = c.head_dim, qkv_rows = (c.heads + 2 * c.kv_heads) * hd;
@@ -641,6 +921,7 @@ int trit_hip_session_new(const TritHipDecoder* decoder, int max_positions, int f
             s.rope_cos.alloc(cs.size() * 4);
             s.rope_cos.upload(cs.data(), cs.size() * 4);
             s.logits.alloc((size_t)c.vocab * 4);
+            s.partials.alloc((size_t)((c.vocab + CHOOSE_SPAN - 1) / CHOOSE_SPAN) * 8);
             s.state.alloc(sizeof(State));
             ensure_rows(s, 8);
             reset_state(s);
@@ -719,9 +1000,13 @@ int trit_hip_session_generate(TritHipSession* session, int max_new, const int32_
             }
         }
         arm_state(S, max_new, stop, n_stop);
-        build_graph(S);
         hipStream_t s = stream();
-        for (int i = 0; i < max_new; ++i) TRIT_HIP(hipGraphLaunch(S.graph, s));
+        if (use_graph()) {
+            build_graph(S);
+            for (int i = 0; i < max_new; ++i) TRIT_HIP(hipGraphLaunch(S.graph, s));
+        } else {
+            for (int i = 0; i < max_new; ++i) step(S, s);
+        }
         State h{};
         TRIT_HIP(hipMemcpyAsync(&h, S.state.ptr, sizeof(State), hipMemcpyDeviceToHost, s));
         TRIT_HIP(hipStreamSynchronize(s));

@@ -66,6 +66,29 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
            ((uint32_t)(d & 0xff) << 24);
 }
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// A 16-byte load of streamed weights (read once per token): nontemporal,
+// so it does not displace the activations in the caches.
+__device__ __forceinline__ uint4 load_stream(const void* p) {
+    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// DPP lane moves (gfx9 encodings): quad_perm [1,0,3,2] (xor 1), [2,3,0,1]
+// (xor 2), row_half_mirror (lane i <-> 7-i in each 8), row_mirror (i <->
+// 15-i in each 16), row_ror:2 (lane i takes lane i-2 in its row of 16).
+enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140, DPP_ROR2 = 0x122 };
+
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }

@@ -70,6 +70,29 @@ __device__ void quantize_rows(const GemvArgs& a, int k, const Smem& sm) {
     if (a.norm_w) {
         if (a.norm_inv) {
             if (threadIdx.x < m) sm.inv[threadIdx.x] = a.norm_inv[threadIdx.x];
+        } else if (k % 256 == 0) {
+            // A fixed tree: each wave sums 256 values of one row with
+            // shuffles, one thread adds a row's wave sums in order. Every
+            // block gets the same bits.
+            const int per_row = k / 256;
+            for (int base = 0; base < m * per_row; base += THREADS / WAVE) {
+                const int chunk = base + (int)(threadIdx.x / WAVE);
+                float part = 0.0f;
+                if (chunk < m * per_row) {
+                    const int row = chunk / per_row, c = chunk - row * per_row;
+                    const float4 v = *(const float4*)(a.x + (size_t)row * k + c * 256 + (threadIdx.x % WAVE) * 4);
+                    part = (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+                }
+#pragma unroll
+                for (int off = WAVE / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
+                if (threadIdx.x % WAVE == 0 && chunk < m * per_row) sm.red[chunk] = part;
+            }
+            __syncthreads();
+            if (threadIdx.x < m) {
+                float sum = 0.0f;
+                for (int c = 0; c < per_row; ++c) sum += sm.red[threadIdx.x * per_row + c];
+                sm.inv[threadIdx.x] = 1.0f / __builtin_sqrtf(sum / (float)k + a.eps);
+            }
         } else {
             // A fixed tree over the block: every block gets the same bits.
             for (int f = 0; f < m; ++f) {
@@ -125,8 +148,91 @@ __device__ void quantize_rows(const GemvArgs& a, int k, const Smem& sm) {
         if (live) {
             *(uint32_t*)(sm.xq + (size_t)row * k + col) = pack4(c0, c1, c2, c3);
             if (part == 0) {
-                sm.xs[row * groups + g] = W::HALF ? f16_round(scale) : scale;
-                if (W::TERN) sm.xsum[row * groups + g] = sum;
+                sm.xs[row * ((groups + 4) & ~3) + g] = W::HALF ? f16_round(scale) : scale;
+                if (W::TERN) sm.xsum[row * ((groups + 4) & ~3) + g] = sum;
+            }
+        }
+    }
+}
+
+constexpr int XI = 4;  // float4 activation items a thread holds in the one-trip prologue
+
+// The one-trip prologue: the activation rows (and RMSNorm weights) were
+// loaded into registers with the weights, so this only computes. Requires
+// m*k/4 <= XI*THREADS, and k % 256 == 0 when the norm sum is made here.
+template <class W>
+__device__ void quantize_regs(const GemvArgs& a, int k, const Smem& sm, const float4* xv, const float4* nv,
+                              float inv_in) {
+    constexpr int TPG = W::G / 4;
+    const int groups = k / W::G;
+    const int gsx = (groups + 4) & ~3;
+    const int m = a.m;
+    const int items = m * k / 4;
+    const int ipr = k / 4;  // items per row
+    if (a.norm_w) {
+        if (a.norm_inv) {
+            if (threadIdx.x < m) sm.inv[threadIdx.x] = inv_in;
+        } else {
+            // Each wave's 64 items are 256 values of one row: shuffle sums,
+            // then one thread adds a row's wave sums in order.
+#pragma unroll
+            for (int i = 0; i < XI; ++i) {
+                const int item = (int)threadIdx.x + i * THREADS;
+                float part = 0.0f;
+                if (item < items) {
+                    const float4 v = xv[i];
+                    part = (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+                }
+#pragma unroll
+                for (int off = WAVE / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
+                if (threadIdx.x % WAVE == 0 && item < items) sm.red[item / WAVE] = part;
+            }
+            __syncthreads();
+            if (threadIdx.x < m) {
+                const int per_row = ipr / WAVE;
+                float sum = 0.0f;
+                for (int c = 0; c < per_row; ++c) sum += sm.red[threadIdx.x * per_row + c];
+                sm.inv[threadIdx.x] = 1.0f / __builtin_sqrtf(sum / (float)k + a.eps);
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < XI; ++i) {
+        const int base = i * THREADS;
+        if (base >= items) break;  // uniform
+        const int item = base + (int)threadIdx.x;
+        const bool live = item < items;
+        const int row = live ? item / ipr : 0;
+        const int col = (live ? item - row * ipr : 0) * 4;
+        float4 v = xv[i];
+        if (a.norm_w) {
+            const float inv = sm.inv[row];
+            const float4 w = nv[i];
+            v.x = v.x * (inv * w.x);
+            v.y = v.y * (inv * w.y);
+            v.z = v.z * (inv * w.z);
+            v.w = v.w * (inv * w.w);
+        }
+        float peak = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
+                                     __builtin_fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
+#pragma unroll
+        for (int off = TPG / 2; off > 0; off >>= 1) peak = __builtin_fmaxf(peak, __shfl_xor(peak, off));
+        const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+        const float inv = 1.0f / scale;
+        const int c0 = act_code(v.x * inv), c1 = act_code(v.y * inv);
+        const int c2 = act_code(v.z * inv), c3 = act_code(v.w * inv);
+        int sum = c0 + c1 + c2 + c3;
+        if (W::TERN) {
+#pragma unroll
+            for (int off = TPG / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+        }
+        if (live) {
+            *(uint32_t*)(sm.xq + (size_t)row * k + col) = pack4(c0, c1, c2, c3);
+            const int g = col / W::G;
+            if (col % W::G == 0) {
+                sm.xs[row * gsx + g] = W::HALF ? f16_round(scale) : scale;
+                if (W::TERN) sm.xsum[row * gsx + g] = sum;
             }
         }
     }
@@ -158,6 +264,9 @@ __device__ __forceinline__ int chunk_dot(const uint4& w, const int8_t* xq, int k
     }
 }
 
+// Row stride (ints) of a (row, frame) pair's group dots in LDS: 16-byte rows.
+__host__ __device__ __forceinline__ int dot_stride(int groups) { return (groups + 4) & ~3; }
+
 template <class W, int R, int P>
 __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict__ codes,
                                                         const void* __restrict__ scales,
@@ -167,11 +276,14 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
     if (a.skip && *a.skip) return;
     const int m = a.m;
     const int groups = k / W::G;
-    const int rows_tile = P * R;
+    const int gs = dot_stride(groups);
+    constexpr int rows_tile = P * R;
     const int part_rows = n / P;  // rows of one part (the SwiGLU pair's half)
     const int cpr = k / W::KPC;   // chunks per row
     const size_t row_bytes = (size_t)k / W::ROW_DIV;
     const int tiles = part_rows / R;
+    int tile = blockIdx.x;
+    if (tile >= tiles) return;
 
     Smem sm;
     {
@@ -179,45 +291,87 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
         sm.xq = (int8_t*)p;
         p += align16((size_t)m * k);
         sm.xs = (float*)p;
-        p += align16((size_t)m * groups * 4);
+        p += align16((size_t)m * gs * 4);
         sm.xsum = (int*)p;
-        p += align16((size_t)m * groups * 4);
+        p += align16((size_t)m * gs * 4);
         sm.inv = (float*)p;
         p += align16((size_t)MAXF * 4);
         sm.red = (float*)p;
         p += align16((size_t)THREADS * 4);
         sm.dots = (int*)p;
-        p += align16((size_t)rows_tile * m * (groups + 1) * 4);
+        p += align16((size_t)rows_tile * m * gs * 4);
         sm.ws = (float*)p;
-        p += align16((size_t)rows_tile * groups * 4);
+        p += align16((size_t)rows_tile * gs * 4);
         sm.res = (float*)p;
     }
 
-    quantize_rows<W>(a, k, sm);
-    __syncthreads();
-
     const int total = rows_tile * cpr;
-    for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-        const int row0 = tile * R;
-        // Weight scales of the tile into LDS.
+    uint4 w[BATCH];
+    auto load_batch = [&](int t, int base) {
+        const int row0 = t * R;
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) {
+            const int c = base + u * THREADS + (int)threadIdx.x;
+            if (c < total) {
+                const int pr = c / cpr, kc = c - pr * cpr;
+                const int row = (pr / R) * part_rows + row0 + pr % R;
+                w[u] = load_stream(codes + (size_t)row * row_bytes + (size_t)kc * 16);
+            } else {
+                w[u] = make_uint4(0, 0, 0, 0);
+            }
+        }
+    };
+    auto stage_scales = [&](int t) {
+        const int row0 = t * R;
         for (int i = threadIdx.x; i < rows_tile * groups; i += THREADS) {
             const int pr = i / groups, g = i - pr * groups;
             const int row = (pr / R) * part_rows + row0 + pr % R;
-            sm.ws[i] = W::scale(scales, (size_t)row * groups + g);
+            sm.ws[pr * gs + g] = W::scale(scales, (size_t)row * groups + g);
         }
-        for (int base = 0; base < total; base += THREADS * BATCH) {
-            uint4 w[BATCH];
+    };
+
+    // One memory round trip: the first weights, the activations, the norm
+    // weights and the tile's scales are all in flight before any is used.
+    load_batch(tile, 0);
+    const int items = m * k / 4;
+    const bool one_trip = items <= XI * THREADS && (!a.norm_w || a.norm_inv || k % 256 == 0) &&
+                          rows_tile * groups <= XI * THREADS;
+    if (one_trip) {
+        float4 xv[XI], nv[XI];
+        float sv[XI];
 #pragma unroll
-            for (int u = 0; u < BATCH; ++u) {
-                const int c = base + u * THREADS + (int)threadIdx.x;
-                if (c < total) {
-                    const int pr = c / cpr, kc = c - pr * cpr;
-                    const int row = (pr / R) * part_rows + row0 + pr % R;
-                    w[u] = *(const uint4*)(codes + (size_t)row * row_bytes + (size_t)kc * 16);
-                } else {
-                    w[u] = make_uint4(0, 0, 0, 0);
-                }
+        for (int i = 0; i < XI; ++i) {
+            const int item = (int)threadIdx.x + i * THREADS;
+            xv[i] = item < items ? *(const float4*)(a.x + (size_t)item * 4) : make_float4(0, 0, 0, 0);
+            nv[i] = (a.norm_w && item < items) ? *(const float4*)(a.norm_w + (item * 4) % k)
+                                                : make_float4(0, 0, 0, 0);
+            const int si = (int)threadIdx.x + i * THREADS;
+            if (si < rows_tile * groups) {
+                const int pr = si / groups, g = si - pr * groups;
+                const int row = (pr / R) * part_rows + tile * R + pr % R;
+                sv[i] = W::scale(scales, (size_t)row * groups + g);
             }
+        }
+        const float inv_in = (a.norm_w && a.norm_inv && (int)threadIdx.x < m) ? a.norm_inv[threadIdx.x] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < XI; ++i) {
+            const int si = (int)threadIdx.x + i * THREADS;
+            if (si < rows_tile * groups) {
+                const int pr = si / groups, g = si - pr * groups;
+                sm.ws[pr * gs + g] = sv[i];
+            }
+        }
+        quantize_regs<W>(a, k, sm, xv, nv, inv_in);
+    } else {
+        stage_scales(tile);
+        quantize_rows<W>(a, k, sm);
+    }
+    __syncthreads();
+
+    for (;;) {
+        const int row0 = tile * R;
+        for (int base = 0; base < total; base += THREADS * BATCH) {
+            if (base > 0) load_batch(tile, base);
 #pragma unroll
             for (int u = 0; u < BATCH; ++u) {
                 const int c0 = base + u * THREADS;
@@ -231,32 +385,53 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
                     int d = chunk_dot<W>(w[u], sm.xq + (size_t)f * k, kc);
 #pragma unroll
                     for (int off = 1; off < W::LPG; off <<= 1) d += __shfl_xor(d, off);
-                    if (live && (kc % W::LPG) == 0) sm.dots[(pr * m + f) * (groups + 1) + g] = d;
+                    if (live && (kc % W::LPG) == 0) sm.dots[(pr * m + f) * gs + g] = d;
                 }
             }
         }
+        const int next = tile + gridDim.x;
         __syncthreads();
-        // The f32 chain, one thread per (row, frame).
+        // The next tile's weights stream in while this one's chains run.
+        if (next < tiles) load_batch(next, 0);
+        // The f32 chain, one thread per (row, frame), four groups per step.
         for (int t = threadIdx.x; t < rows_tile * m; t += THREADS) {
             const int pr = t / m, f = t - pr * m;
-            const int* dots = sm.dots + (pr * m + f) * (groups + 1);
-            const float* ws = sm.ws + pr * groups;
-            const float* xs = sm.xs + f * groups;
-            float total_f = 0.0f;
-            for (int g = 0; g < groups; ++g) {
+            const int* dots = sm.dots + (pr * m + f) * gs;
+            const float* ws = sm.ws + pr * gs;
+            const float* xs = sm.xs + f * gs;
+            const int* xsum = sm.xsum + f * gs;
+            float acc = 0.0f;
+            int g = 0;
+            for (; g + 4 <= groups; g += 4) {
+                int4 d = *(const int4*)(dots + g);
+                const float4 wv = *(const float4*)(ws + g);
+                const float4 xv = *(const float4*)(xs + g);
+                if (W::TERN) {
+                    const int4 sv = *(const int4*)(xsum + g);
+                    d.x -= sv.x;
+                    d.y -= sv.y;
+                    d.z -= sv.z;
+                    d.w -= sv.w;
+                }
+                acc = __builtin_fmaf((float)d.x, wv.x * xv.x, acc);
+                acc = __builtin_fmaf((float)d.y, wv.y * xv.y, acc);
+                acc = __builtin_fmaf((float)d.z, wv.z * xv.z, acc);
+                acc = __builtin_fmaf((float)d.w, wv.w * xv.w, acc);
+            }
+            for (; g < groups; ++g) {
                 int d = dots[g];
-                if (W::TERN) d -= sm.xsum[f * groups + g];
-                total_f = __builtin_fmaf((float)d, ws[g] * xs[g], total_f);
+                if (W::TERN) d -= xsum[g];
+                acc = __builtin_fmaf((float)d, ws[g] * xs[g], acc);
             }
             const int row = (pr / R) * part_rows + row0 + pr % R;
-            if (bias) total_f = total_f + bias[row];
-            if (a.relu) total_f = __builtin_fmaxf(total_f, 0.0f);
+            if (bias) acc = acc + bias[row];
+            if (a.relu) acc = __builtin_fmaxf(acc, 0.0f);
             if (P == 2) {
-                sm.res[t] = total_f;
+                sm.res[t] = acc;
             } else if (a.epilogue == EPI_RESIDUAL) {
-                a.y[(size_t)f * n + row] = a.residual[(size_t)f * n + row] + total_f;
+                a.y[(size_t)f * n + row] = a.residual[(size_t)f * n + row] + acc;
             } else {
-                a.y[(size_t)f * n + row] = total_f;
+                a.y[(size_t)f * n + row] = acc;
             }
         }
         if (P == 2) {
@@ -269,16 +444,20 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
                 a.y[(size_t)f * part_rows + row0 + r] = silu_trit(gate) * up;
             }
         }
+        if (next >= tiles) break;
+        __syncthreads();
+        tile = next;
+        stage_scales(tile);
         __syncthreads();
     }
 }
 
 size_t smem_bytes(int m, int k, int G, int rows_tile) {
     const int groups = k / G;
+    const int gs = dot_stride(groups);
     auto al = [](size_t v) { return (v + 15) & ~(size_t)15; };
-    return al((size_t)m * k) + 2 * al((size_t)m * groups * 4) + al((size_t)MAXF * 4) + al((size_t)THREADS * 4) +
-           al((size_t)rows_tile * m * (groups + 1) * 4) + al((size_t)rows_tile * groups * 4) +
-           al((size_t)rows_tile * m * 4);
+    return al((size_t)m * k) + 2 * al((size_t)m * gs * 4) + al((size_t)MAXF * 4) + al((size_t)THREADS * 4) +
+           al((size_t)rows_tile * m * gs * 4) + al((size_t)rows_tile * gs * 4) + al((size_t)rows_tile * m * 4);
 }
 
 template <class W, int R, int P>
@@ -319,6 +498,7 @@ void dispatch(const Layer& L, const GemvArgs& a, hipStream_t s) {
 
 void gemv_int(const Layer& L, const GemvArgs& a, hipStream_t s) {
     if (a.m < 1 || a.m > MAXF) fail("gemv: 1 to 8 rows per call");
+    if (gemv_row(L, a, s)) return;
     if (a.epilogue == EPI_SILU_PAIR && (L.n % 2 != 0)) fail("gemv: the SwiGLU pair needs an even row count");
     switch (L.kind) {
         case Q8_0:

@@ -119,6 +119,9 @@ struct GemvArgs {
 
 // Integer products (Q8_0, Q4_K, INT8, TERNARY), m <= 8.
 void gemv_int(const Layer& L, const GemvArgs& a, hipStream_t s);
+// The one-row Q8_0 decode product (k 1024, 2048 or 3072); false when the
+// shape or kind is not one it takes.
+bool gemv_row(const Layer& L, const GemvArgs& a, hipStream_t s);
 // f16 products, m <= 8.
 void gemv_f16(const Layer& L, const GemvArgs& a, hipStream_t s);
 // Any layer kind.

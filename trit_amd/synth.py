@@ -211,27 +211,28 @@ def lm_weights(cfg: dict, config: int = 1, sigma: float = 0.02, norm_jitter: flo
 
     Linears: Q8_0 codes uniform in [-127, 127], block scales N(0, sigma)/127.
     Embeddings (tied head): f16 N(0, sigma). Norm weights 1 (plus optional
-    uniform jitter, so tests see non-unit norms). Layers are generated in
-    `workers` processes (0: up to 8); the bytes do not depend on it.
+    uniform jitter, so tests see non-unit norms). Layers are generated on
+    `workers` threads (0: up to 8; numpy releases the GIL in its array
+    operations); the bytes do not depend on it.
     """
     d = cfg["d"]
     jobs = [(cfg, config, 16 * (i + 1), sigma, norm_jitter) for i in range(cfg["layers"])]
     if workers == 0:
         import os
         workers = min(8, os.cpu_count() or 1) if cfg["layers"] * cfg["d"] >= 8192 else 1
-    import multiprocessing as mp
+    from concurrent.futures import ThreadPoolExecutor
 
     if workers > 1:
-        with mp.get_context("fork").Pool(workers) as pool:
-            layers = pool.map(_layer, jobs)
+        with ThreadPoolExecutor(workers) as pool:
+            layers = list(pool.map(_layer, jobs))
     else:
         layers = [_layer(j) for j in jobs]
     t = 16 * (cfg["layers"] + 1)
     vocab = cfg["vocab"]
     parts = [(seed_for(config, t), r0, min(vocab, r0 + 8192), d, sigma) for r0 in range(0, vocab, 8192)]
     if workers > 1:
-        with mp.get_context("fork").Pool(workers) as pool:
-            embed = np.concatenate(pool.map(_embed_rows, parts))
+        with ThreadPoolExecutor(workers) as pool:
+            embed = np.concatenate(list(pool.map(_embed_rows, parts)))
     else:
         embed = np.concatenate([_embed_rows(p) for p in parts])
     if norm_jitter == 0.0:
