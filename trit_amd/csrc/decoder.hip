@@ -316,67 +316,167 @@ struct Split {
     static constexpr int CH = sizeof(KV) == 2 ? 64 : 32;
 };
 
+// Qwen3's per-head RMSNorm (serial sum of the rounded squares, as
+// src/layers.rs:139) and the rotary halves (src/layers.rs:303-334) of one
+// head held in LDS `v` (hd values), by the block's first hd threads.
+__device__ void norm_rope_head(float* v, float* sq, const float* w, int hd, float eps, const float* sn,
+                               const float* cs, bool norm, bool rope, float* inv_slot) {
+    const int e = threadIdx.x;
+    if (norm) {
+        if (e < hd) sq[e] = v[e] * v[e];
+        __syncthreads();
+        if (e == 0) {
+            float sum = 0.0f;
+            for (int i = 0; i < hd; i += 4) {
+                const float4 q4 = *(const float4*)(sq + i);
+                sum = sum + q4.x;
+                sum = sum + q4.y;
+                sum = sum + q4.z;
+                sum = sum + q4.w;
+            }
+            *inv_slot = 1.0f / __builtin_sqrtf(sum / (float)hd + eps);
+        }
+        __syncthreads();
+        float t = 0.0f;
+        if (e < hd) t = v[e] * (*inv_slot * w[e]);
+        __syncthreads();
+        if (e < hd) v[e] = t;
+        __syncthreads();
+    }
+    if (rope) {
+        const int half = hd / 2;
+        float out = 0.0f;
+        if (e < hd) {
+            const int i = e < half ? e : e - half;
+            const float s_ = sn[i], c = cs[i];
+            if (e < half) {
+                const float ac = v[e] * c, bs = v[e + half] * s_;
+                out = ac - bs;
+            } else {
+                const float bc = v[e] * c, as = v[e - half] * s_;
+                out = bc + as;
+            }
+        }
+        __syncthreads();
+        if (e < hd) v[e] = out;
+        __syncthreads();
+    }
+}
+
 // Fast-mode attention (split over the keys, "flash decoding"): block
 // (g, split, row) stages keys and values [split*CH, split*CH+CH) of
 // key/value head g in LDS with one round of 16-byte loads, scores them
-// against the query heads that share g (16 lanes per dot product), and
-// keeps the chunk's maximum, sum of exp(s - max) and unnormalised p.V. The
-// last block of (row, g) merges the chunks with the usual rescaling. Keys
-// past the row's position get no weight. The sums run in parallel, so the
-// values are within rounding of the exact kernel's, not equal to them.
-template <typename KV>
+// against the query heads that share g (16 lanes per dot product, DPP
+// sums), takes the chunk's softmax with one wave per query head, and keeps
+// the chunk's maximum, sum of exp(s - max) and unnormalised p.V. The last
+// block of (row, g) merges the chunks with the usual rescaling. Keys past
+// the row's position get no weight. The sums run in parallel, so the values
+// are within rounding of the exact kernel's, not equal to them.
+//
+// FUSED (one decode row): the block also does the q/k norm and rotary of
+// its heads from the raw qkv product, and the block whose chunk holds the
+// new position appends that key and value to the caches.
+template <typename KV, bool FUSED>
 __global__ __launch_bounds__(ATT_THREADS) void attention_split_kernel(
-    const float* __restrict__ qkv, int stride, int heads, int kvh, int hd, const KV* __restrict__ kcache,
-    const KV* __restrict__ vcache, int max_pos, int rows, float* __restrict__ out, float* __restrict__ part,
-    unsigned int* __restrict__ arrived, int max_splits, const State* st) {
+    const float* __restrict__ qkv, int stride, int heads, int kvh, int hd, KV* __restrict__ kcache,
+    KV* __restrict__ vcache, int max_pos, int rows, float* __restrict__ out, float* __restrict__ part,
+    unsigned int* __restrict__ arrived, int max_splits, const State* st, int qk_norm,
+    const float* __restrict__ q_norm, const float* __restrict__ k_norm, float eps,
+    const float* __restrict__ rope_sin, const float* __restrict__ rope_cos) {
     constexpr int CH = Split<KV>::CH;
     constexpr int PER = 16 / sizeof(KV);  // cache values per 16-byte load
     if (st->done) return;
     extern __shared__ __align__(16) char smem[];
     KV* Ks = (KV*)smem;
     KV* Vs = Ks + CH * hd;
-    __shared__ float qh[4 * 128];
+    __shared__ __align__(16) float qh[4 * 128];
+    __shared__ __align__(16) float kv_new[2][128];
+    __shared__ __align__(16) float sq[128];
+    __shared__ float inv_slot;
     __shared__ float sc[4][CH];
     __shared__ float mrow[4], lrow[4];
     __shared__ bool last;
     const int g = blockIdx.x, split = blockIdx.y, row = blockIdx.z;
     const int group = heads / kvh;
-    const int tk = st->pos + rows;
-    const int visible = st->pos + row + 1;
+    const int pos = st->pos;
+    const int tk = pos + rows;
+    const int visible = pos + row + 1;
     const int j0 = split * CH;
     const int splits = (tk + CH - 1) / CH;
     if (split >= splits) return;
     const int nk = min(CH, tk - j0);
+    // With FUSED, the new position is not in the cache yet: stage one key less.
+    const int nstage = FUSED && split == splits - 1 ? nk - 1 : nk;
     const uint4* K = (const uint4*)(kcache + ((size_t)g * max_pos + j0) * hd);
     const uint4* V = (const uint4*)(vcache + ((size_t)g * max_pos + j0) * hd);
-    // Stage the chunk: every load is issued before the first store waits.
-    const int units = nk * hd / PER;
-    constexpr int UPT = CH * 128 / (16 / (int)sizeof(KV)) / ATT_THREADS;  // units per thread at hd 128
+    const int units = nstage * hd / PER;
+    constexpr int UPT = CH * 128 / (16 / (int)sizeof(KV)) / ATT_THREADS;
     uint4 kr[UPT], vr[UPT];
 #pragma unroll
     for (int i = 0; i < UPT; ++i) {
-        // Past the chunk, re-read its first unit (in bounds); the store skips it.
+        // Past the staged keys, re-read the first unit (in bounds); the store skips it.
         const int u = (int)threadIdx.x + i * ATT_THREADS;
         const int uc = u < units ? u : 0;
         kr[i] = K[uc];
         vr[i] = V[uc];
     }
     const float scale = 1.0f / __builtin_sqrtf((float)hd);
-    for (int i = threadIdx.x; i < group * hd; i += ATT_THREADS) {
-        const int h = g * group + i / hd;
-        qh[i] = qkv[(size_t)row * stride + (size_t)h * hd + i % hd] * scale;
+    const float* qsrc = qkv + (size_t)row * stride;
+    const bool holds_new = FUSED && split == splits - 1;
+    // The raw q (and new k, v) values this thread needs, fetched with the chunk.
+    const int t = threadIdx.x;
+    float qreg[4] = {0.0f, 0.0f, 0.0f, 0.0f}, kreg = 0.0f, vreg = 0.0f;
+    if (t < hd) {
+#pragma unroll
+        for (int hl = 0; hl < 4; ++hl)
+            if (hl < group) qreg[hl] = qsrc[(size_t)(g * group + hl) * hd + t];
+        if (holds_new) {
+            kreg = qsrc[(size_t)(heads + g) * hd + t];
+            vreg = qsrc[(size_t)(heads + kvh + g) * hd + t];
+        }
     }
 #pragma unroll
     for (int i = 0; i < UPT; ++i) {
-        const int u = (int)threadIdx.x + i * ATT_THREADS;
+        const int u = t + i * ATT_THREADS;
         if (u < units) {
             ((uint4*)Ks)[u] = kr[i];
             ((uint4*)Vs)[u] = vr[i];
         }
     }
-    for (int u = (int)threadIdx.x + UPT * ATT_THREADS; u < units; u += ATT_THREADS) {
+    for (int u = t + UPT * ATT_THREADS; u < units; u += ATT_THREADS) {
         ((uint4*)Ks)[u] = K[u];
         ((uint4*)Vs)[u] = V[u];
+    }
+    if (FUSED) {
+        const float* sn = rope_sin + (size_t)pos * (hd / 2);
+        const float* cs = rope_cos + (size_t)pos * (hd / 2);
+        for (int hl = 0; hl < group; ++hl) {
+            float* v = qh + hl * hd;
+            if (t < hd) v[t] = qreg[hl];
+            __syncthreads();
+            norm_rope_head(v, sq, q_norm, hd, eps, sn, cs, qk_norm != 0, true, &inv_slot);
+        }
+        if (holds_new) {
+            float* kn = kv_new[0];
+            if (t < hd) kn[t] = kreg;
+            __syncthreads();
+            norm_rope_head(kn, sq, k_norm, hd, eps, sn, cs, qk_norm != 0, true, &inv_slot);
+            if (t < hd) {
+                const size_t at = ((size_t)g * max_pos + pos) * hd + t;
+                const KV kq = (KV)kn[t], vq = (KV)vreg;
+                kcache[at] = kq;
+                vcache[at] = vq;
+                // The new key and value, rounded as the cache holds them.
+                Ks[(size_t)nstage * hd + t] = kq;
+                Vs[(size_t)nstage * hd + t] = vq;
+            }
+        }
+        for (int i = t; i < group * hd; i += ATT_THREADS) qh[i] = qh[i] * scale;
+    } else {
+        for (int i = t; i < group * hd; i += ATT_THREADS) {
+            const int h = g * group + i / hd;
+            qh[i] = qsrc[(size_t)h * hd + i % hd] * scale;
+        }
     }
     __syncthreads();
     // Scores: 16 lanes per (head, key), 8 dims per lane and step.
@@ -393,32 +493,60 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_split_kernel(
                 for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(q[e + u], kv[u], acc);
             }
         }
-        acc += __shfl_xor(acc, 8);
-        acc += __shfl_xor(acc, 4);
-        acc += __shfl_xor(acc, 2);
-        acc += __shfl_xor(acc, 1);
+        acc += dpp<DPP_XOR1>(acc);
+        acc += dpp<DPP_XOR2>(acc);
+        acc += dpp<DPP_HALF_MIRROR>(acc);
+        acc += dpp<DPP_MIRROR>(acc);
         if (lane16 == 0) sc[hl][j] = (j < nk && j0 + j < visible) ? acc : -INFINITY;
     }
     __syncthreads();
-    if (threadIdx.x < group) {
-        const int hl = threadIdx.x;
-        float mx = -INFINITY;
-        for (int j = 0; j < nk; ++j) mx = __builtin_fmaxf(mx, sc[hl][j]);
-        float l = 0.0f;
-        for (int j = 0; j < nk; ++j) {
-            const float e = sc[hl][j] == -INFINITY ? 0.0f : exp_trit(sc[hl][j] - mx);
-            sc[hl][j] = e;
-            l += e;
+    // The chunk's softmax, one wave per query head: lane j holds key j (and j+64).
+    {
+        const int w = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+        if (w < group) {
+            const float a = lane < CH ? sc[w][lane] : -INFINITY;
+            const float b = lane + WAVE < CH ? sc[w][lane + WAVE] : -INFINITY;
+            float mx = __builtin_fmaxf(a, b);
+            mx = __builtin_fmaxf(mx, dpp<DPP_XOR1>(mx));
+            mx = __builtin_fmaxf(mx, dpp<DPP_XOR2>(mx));
+            mx = __builtin_fmaxf(mx, dpp<DPP_HALF_MIRROR>(mx));
+            mx = __builtin_fmaxf(mx, dpp<DPP_MIRROR>(mx));
+            mx = __builtin_fmaxf(__builtin_fmaxf(__shfl(mx, 0), __shfl(mx, 16)),
+                                 __builtin_fmaxf(__shfl(mx, 32), __shfl(mx, 48)));
+            const float ea = a == -INFINITY ? 0.0f : exp_trit(a - mx);
+            const float eb = b == -INFINITY ? 0.0f : exp_trit(b - mx);
+            if (lane < CH) sc[w][lane] = ea;
+            if (lane + WAVE < CH) sc[w][lane + WAVE] = eb;
+            float l = ea + eb;
+            l += dpp<DPP_XOR1>(l);
+            l += dpp<DPP_XOR2>(l);
+            l += dpp<DPP_HALF_MIRROR>(l);
+            l += dpp<DPP_MIRROR>(l);
+            l = (__shfl(l, 0) + __shfl(l, 16)) + (__shfl(l, 32) + __shfl(l, 48));
+            if (lane == 0) {
+                mrow[w] = mx;
+                lrow[w] = l;
+            }
         }
-        mrow[hl] = mx;
-        lrow[hl] = l;
     }
     __syncthreads();
     const size_t slot = ((size_t)row * heads + g * group) * max_splits;
     for (int t = threadIdx.x; t < group * hd; t += ATT_THREADS) {
         const int hl = t / hd, e = t % hd;
         float acc = 0.0f;
-        for (int j = 0; j < nk; ++j) acc = __builtin_fmaf(sc[hl][j], kv_load(Vs + (size_t)j * hd + e), acc);
+        int j = 0;
+        for (; j + 8 <= nk; j += 8) {
+            float vv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) vv[u] = kv_load(Vs + (size_t)(j + u) * hd + e);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(sc[hl][j + u], vv[u], acc);
+        }
+        for (; j < nk; ++j) acc = __builtin_fmaf(sc[hl][j], kv_load(Vs + (size_t)j * hd + e), acc);
+        if (splits == 1) {
+            out[(size_t)row * heads * hd + (size_t)(g * group + hl) * hd + e] = acc / lrow[hl];
+            continue;
+        }
         float* p = part + (slot + (size_t)hl * max_splits + split) * (hd + 2);
         p[2 + e] = acc;
         if (e == 0) {
@@ -426,6 +554,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_split_kernel(
             p[1] = lrow[hl];
         }
     }
+    if (splits == 1) return;
     __syncthreads();
     if (threadIdx.x == 0) {
         __threadfence();
@@ -640,6 +769,29 @@ void product(const Layer& L, GemvArgs a, int rows, hipStream_t s, int y_stride) 
     }
 }
 
+template <typename KV>
+void launch_split(SessionImpl& S, int l, int rows, bool fused, hipStream_t s) {
+    const DecoderImpl& D = *S.dec;
+    const auto& c = D.c;
+    const int hd = c.head_dim, stride = (c.heads + 2 * c.kv_heads) * hd;
+    const dim3 grid(c.kv_heads, (S.max_pos + Split<KV>::CH - 1) / Split<KV>::CH, rows);
+    const size_t lds = (size_t)2 * Split<KV>::CH * hd * sizeof(KV);
+    KV* kc = S.kcache.as<KV>() + (size_t)l * c.kv_heads * S.max_pos * hd;
+    KV* vc = S.vcache.as<KV>() + (size_t)l * c.kv_heads * S.max_pos * hd;
+    if (fused)
+        hipLaunchKernelGGL((attention_split_kernel<KV, true>), grid, dim3(ATT_THREADS), lds, s, S.qkv.as<float>(),
+                           stride, c.heads, c.kv_heads, hd, kc, vc, S.max_pos, rows, S.att.as<float>(),
+                           S.att_part.as<float>(), S.att_arrived.as<unsigned int>(), S.max_splits, S.st(),
+                           c.qk_norm, D.q_norm(l), D.k_norm(l), c.eps, S.rope_sin.as<float>(),
+                           S.rope_cos.as<float>());
+    else
+        hipLaunchKernelGGL((attention_split_kernel<KV, false>), grid, dim3(ATT_THREADS), lds, s, S.qkv.as<float>(),
+                           stride, c.heads, c.kv_heads, hd, kc, vc, S.max_pos, rows, S.att.as<float>(),
+                           S.att_part.as<float>(), S.att_arrived.as<unsigned int>(), S.max_splits, S.st(),
+                           c.qk_norm, D.q_norm(l), D.k_norm(l), c.eps, S.rope_sin.as<float>(),
+                           S.rope_cos.as<float>());
+}
+
 // One forward of `rows` rows whose embeddings are in S.x, at positions
 // st->pos.., ending with the logits of the last row.
 void forward(SessionImpl& S, int rows, hipStream_t s) {
@@ -662,23 +814,26 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
         a.norm_w = D.norm_attn(l);
         a.y = S.qkv.as<float>();
         product(*D.qkv[l], a, rows, s, stride);
-        // q/k norm, rotary, cache append.
-        if (S.kv32) {
-            hipLaunchKernelGGL(qk_rope_kernel<float>, dim3(rows * (c.heads + 2 * c.kv_heads)), dim3(hd < 64 ? 64 : hd),
-                               0, s, S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd, c.qk_norm, D.q_norm(l),
-                               D.k_norm(l), c.eps, S.rope_sin.as<float>(), S.rope_cos.as<float>(),
-                               S.kcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd,
-                               S.vcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, st);
-        } else {
-            hipLaunchKernelGGL(qk_rope_kernel<_Float16>, dim3(rows * (c.heads + 2 * c.kv_heads)),
-                               dim3(hd < 64 ? 64 : hd), 0, s, S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
-                               c.qk_norm, D.q_norm(l), D.k_norm(l), c.eps, S.rope_sin.as<float>(),
-                               S.rope_cos.as<float>(),
-                               S.kcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd,
-                               S.vcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, st);
+        // q/k norm, rotary, cache append, attention.
+        const bool fused = !S.exact && rows == 1;
+        if (!fused) {
+            if (S.kv32) {
+                hipLaunchKernelGGL(qk_rope_kernel<float>, dim3(rows * (c.heads + 2 * c.kv_heads)),
+                                   dim3(hd < 64 ? 64 : hd), 0, s, S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
+                                   c.qk_norm, D.q_norm(l), D.k_norm(l), c.eps, S.rope_sin.as<float>(),
+                                   S.rope_cos.as<float>(),
+                                   S.kcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd,
+                                   S.vcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, st);
+            } else {
+                hipLaunchKernelGGL(qk_rope_kernel<_Float16>, dim3(rows * (c.heads + 2 * c.kv_heads)),
+                                   dim3(hd < 64 ? 64 : hd), 0, s, S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
+                                   c.qk_norm, D.q_norm(l), D.k_norm(l), c.eps, S.rope_sin.as<float>(),
+                                   S.rope_cos.as<float>(),
+                                   S.kcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd,
+                                   S.vcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, st);
+            }
+            TRIT_HIP(hipGetLastError());
         }
-        TRIT_HIP(hipGetLastError());
-        // Attention over the caches.
         if (S.exact) {
             // The host sizes shared memory for the largest key count this forward can see.
             const size_t lds = (size_t)(MAX_HD + S.max_pos + ATT_THREADS) * 4;
@@ -687,26 +842,10 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
                                S.kcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd,
                                S.vcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, rows,
                                S.att.as<float>(), 1, st);
+        } else if (S.kv32) {
+            launch_split<float>(S, l, rows, fused, s);
         } else {
-            if (S.kv32) {
-                const dim3 grid(c.kv_heads, (S.max_pos + Split<float>::CH - 1) / Split<float>::CH, rows);
-                const size_t lds = (size_t)2 * Split<float>::CH * hd * 4;
-                hipLaunchKernelGGL(attention_split_kernel<float>, grid, dim3(ATT_THREADS), lds, s, S.qkv.as<float>(),
-                                   stride, c.heads, c.kv_heads, hd,
-                                   S.kcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd,
-                                   S.vcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, rows,
-                                   S.att.as<float>(), S.att_part.as<float>(), S.att_arrived.as<unsigned int>(),
-                                   S.max_splits, st);
-            } else {
-                const dim3 grid(c.kv_heads, (S.max_pos + Split<_Float16>::CH - 1) / Split<_Float16>::CH, rows);
-                const size_t lds = (size_t)2 * Split<_Float16>::CH * hd * 2;
-                hipLaunchKernelGGL(attention_split_kernel<_Float16>, grid, dim3(ATT_THREADS), lds, s,
-                                   S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
-                                   S.kcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd,
-                                   S.vcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos,
-                                   rows, S.att.as<float>(), S.att_part.as<float>(),
-                                   S.att_arrived.as<unsigned int>(), S.max_splits, st);
-            }
+            launch_split<_Float16>(S, l, rows, fused, s);
         }
         TRIT_HIP(hipGetLastError());
         // o with the residual add.
