@@ -97,6 +97,13 @@ int trit_hip_layer_forward(const TritHipLayer *layer, const float *x, int m, int
 int trit_hip_layer_forward_device(const TritHipLayer *layer, const float *x, int m, int relu, float *y,
                                   void *stream);
 
+/* The measurement hook (the counterpart of Trit's kernel bench timing,
+ * src/cpu/v2/bench.rs:42-54): trit_hip_layer_forward_device for 1..8 rows,
+ * which is one kernel launch, stamped with start_event and stop_event
+ * (hipEvent_t, either may be NULL) at the kernel's start and end. */
+int trit_hip_layer_forward_timed(const TritHipLayer *layer, const float *x, int m, int relu, float *y,
+                                 void *stream, void *start_event, void *stop_event);
+
 /* Shape and kind of a layer; device_bytes: the bytes its weights hold. */
 int trit_hip_layer_info(const TritHipLayer *layer, int *n, int *k, int *kind, int64_t *device_bytes);
 

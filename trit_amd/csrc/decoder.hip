@@ -200,6 +200,24 @@ __device__ __forceinline__ void kv_load8(const float* p, float* out) {
     out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
     out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
 }
+template <typename KV>
+__device__ __forceinline__ void kv_unpack8(const uint4* u, float* out);
+template <>
+__device__ __forceinline__ void kv_unpack8<float>(const uint4* u, float* out) {
+    const uint4 a = u[0], b = u[1];
+    out[0] = __uint_as_float(a.x); out[1] = __uint_as_float(a.y); out[2] = __uint_as_float(a.z); out[3] = __uint_as_float(a.w);
+    out[4] = __uint_as_float(b.x); out[5] = __uint_as_float(b.y); out[6] = __uint_as_float(b.z); out[7] = __uint_as_float(b.w);
+}
+template <>
+__device__ __forceinline__ void kv_unpack8<_Float16>(const uint4* u, float* out) {
+    const uint32_t w[4] = {u[0].x, u[0].y, u[0].z, u[0].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        out[2 * i] = f16_to_f32((uint16_t)(w[i] & 0xffff));
+        out[2 * i + 1] = f16_to_f32((uint16_t)(w[i] >> 16));
+    }
+}
+
 __device__ __forceinline__ void kv_load8(const _Float16* p, float* out) {
     const uint4 v = *(const uint4*)p;
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -582,6 +600,230 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_split_kernel(
     }
 }
 
+constexpr int DEC_THREADS = 512;
+constexpr int DEC_GROUPS = DEC_THREADS / 16;  // 16-lane groups, one key row each at a time
+
+// Fast-mode attention of one decode row, one block per key/value head g,
+// every key in one round of loads. 16-lane group G holds keys G, G+32,
+// G+64, ... straight from the caches, lane l16 dims [8*l16, 8*l16+8) of
+// each: the dot products against the query heads of g reduce over the 16
+// lanes by DPP, the softmax and p.V reduce over the block through LDS, so
+// nothing goes back to memory between the scores and the output. The block
+// also does the q/k norm and rotary of its heads and appends the new key
+// and value (src/models/parts/causal_lm.rs:428-446). The sums run in
+// parallel: values within rounding of the exact kernel's.
+template <typename KV, int MAXI, int GROUP>  // MAXI: keys per group (at most 32*MAXI keys); GROUP: q heads per kv head
+__global__ __launch_bounds__(DEC_THREADS) void attention_decode_kernel(
+    const float* __restrict__ qkv, int heads, int kvh, int hd, KV* __restrict__ kcache, KV* __restrict__ vcache,
+    int max_pos, float* __restrict__ out, const State* st, int qk_norm, const float* __restrict__ q_norm,
+    const float* __restrict__ k_norm, float eps, const float* __restrict__ rope_sin,
+    const float* __restrict__ rope_cos) {
+    if (st->done) return;
+    __shared__ __align__(16) float qh[4 * 128];
+    __shared__ __align__(16) float kv_new[2][128];
+    __shared__ __align__(16) float sq[4][128];
+    __shared__ float inv_s[4];
+    __shared__ float red[DEC_THREADS / WAVE][4];
+    __shared__ float stat[2][4];
+    __shared__ __align__(16) float part[DEC_THREADS / WAVE][4 * 128];
+    const int g = blockIdx.x;
+    constexpr int group = GROUP;
+    const int pos = st->pos;
+    const int tk = pos + 1;
+    const int t = threadIdx.x;
+    const int G = t >> 4, l16 = t & 15;
+    const bool dims = l16 * 8 < hd;
+    const KV* K = kcache + (size_t)g * max_pos * hd;
+    const KV* V = vcache + (size_t)g * max_pos * hd;
+    constexpr int PER = 16 / (int)sizeof(KV);  // values per 16 bytes
+    constexpr int U = 8 / PER;                  // 16-byte loads per 8 values
+    // Every key this lane holds, and the raw q / new k, v and norm values.
+    uint4 kr[MAXI][U], vr[MAXI][U];
+#pragma unroll
+    for (int i = 0; i < MAXI; ++i) {
+        const int j = G + DEC_GROUPS * i;
+        const int jc = (j < pos && dims) ? j : 0;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            kr[i][u] = ((const uint4*)(K + (size_t)jc * hd + l16 * 8))[u];
+            vr[i][u] = ((const uint4*)(V + (size_t)jc * hd + l16 * 8))[u];
+        }
+    }
+    const float* src = qkv;
+    const int hh = t / hd, e = t % hd;  // threads [0, (group+1)*hd): q heads, then k
+    float raw = 0.0f, vraw = 0.0f, nw = 1.0f, sn = 0.0f, cs = 1.0f;
+    if (hh < group + 1) {
+        raw = hh < group ? src[(size_t)(g * group + hh) * hd + e] : src[(size_t)(heads + g) * hd + e];
+        if (hh == group) vraw = src[(size_t)(heads + kvh + g) * hd + e];
+        nw = qk_norm ? (hh < group ? q_norm[e] : k_norm[e]) : 1.0f;
+        const int half = hd / 2;
+        sn = rope_sin[(size_t)pos * half + (e % half)];
+        cs = rope_cos[(size_t)pos * half + (e % half)];
+    }
+    // q and k: Trit's per-head norm (serial sum), then the rotary halves.
+    float* vv = hh < group ? qh + hh * hd : kv_new[0];
+    if (hh < group + 1) {
+        vv[e] = raw;
+        sq[hh][e] = raw * raw;
+    }
+    __syncthreads();
+    if (qk_norm && e == 0 && hh < group + 1) {
+        float sum = 0.0f;
+        for (int i = 0; i < hd; i += 4) {
+            const float4 q4 = *(const float4*)(&sq[hh][i]);
+            sum = sum + q4.x;
+            sum = sum + q4.y;
+            sum = sum + q4.z;
+            sum = sum + q4.w;
+        }
+        inv_s[hh] = 1.0f / __builtin_sqrtf(sum / (float)hd + eps);
+    }
+    __syncthreads();
+    float nv = raw;
+    if (hh < group + 1 && qk_norm) nv = raw * (inv_s[hh] * nw);
+    __syncthreads();
+    if (hh < group + 1) vv[e] = nv;
+    __syncthreads();
+    float rot = 0.0f;
+    if (hh < group + 1) {
+        const int half = hd / 2;
+        if (e < half) {
+            const float ac = vv[e] * cs, bs = vv[e + half] * sn;
+            rot = ac - bs;
+        } else {
+            const float bc = vv[e] * cs, as = vv[e - half] * sn;
+            rot = bc + as;
+        }
+    }
+    __syncthreads();
+    const float scale = 1.0f / __builtin_sqrtf((float)hd);
+    if (hh < group) qh[hh * hd + e] = rot * scale;
+    if (hh == group) {
+        const KV kq = (KV)rot, vq = (KV)vraw;
+        kcache[((size_t)g * max_pos + pos) * hd + e] = kq;
+        vcache[((size_t)g * max_pos + pos) * hd + e] = vq;
+        kv_new[0][e] = (float)kq;
+        kv_new[1][e] = (float)vq;
+    }
+    __syncthreads();
+    // The new key and value replace the lane's stale copy of position pos.
+    float q[GROUP][8];
+#pragma unroll
+    for (int hl = 0; hl < GROUP; ++hl)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) q[hl][u] = (dims) ? qh[hl * hd + l16 * 8 + u] : 0.0f;
+    float kn[8], vn[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        kn[u] = dims ? kv_new[0][l16 * 8 + u] : 0.0f;
+        vn[u] = dims ? kv_new[1][l16 * 8 + u] : 0.0f;
+    }
+    // Scores.
+    float sc[MAXI][GROUP];
+    float mx[GROUP];
+#pragma unroll
+    for (int hl = 0; hl < GROUP; ++hl) mx[hl] = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < MAXI; ++i) {
+        const int j = G + DEC_GROUPS * i;
+        float k8[8];
+        if (j == pos) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) k8[u] = kn[u];
+        } else {
+            kv_unpack8<KV>(kr[i], k8);
+        }
+#pragma unroll
+        for (int hl = 0; hl < GROUP; ++hl) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(q[hl][u], k8[u], acc);
+            acc += dpp<DPP_XOR1>(acc);
+            acc += dpp<DPP_XOR2>(acc);
+            acc += dpp<DPP_HALF_MIRROR>(acc);
+            acc += dpp<DPP_MIRROR>(acc);
+            sc[i][hl] = j < tk ? acc : -INFINITY;
+            mx[hl] = __builtin_fmaxf(mx[hl], sc[i][hl]);
+        }
+    }
+    // Block maximum per head: rows of 16 lanes agree; combine the 4 rows of
+    // each wave, then the waves.
+    const int wave = t / WAVE, wl = t % WAVE;
+#pragma unroll
+    for (int hl = 0; hl < GROUP; ++hl) {
+        float m = mx[hl];
+        m = __builtin_fmaxf(__builtin_fmaxf(__shfl(m, 0), __shfl(m, 16)), __builtin_fmaxf(__shfl(m, 32), __shfl(m, 48)));
+        if (wl == 0) red[wave][hl] = m;
+    }
+    __syncthreads();
+    if (t < GROUP) {
+        float m = -INFINITY;
+        for (int w = 0; w < DEC_THREADS / WAVE; ++w) m = __builtin_fmaxf(m, red[w][t]);
+        stat[0][t] = m;
+    }
+    __syncthreads();
+    float l[GROUP];
+#pragma unroll
+    for (int hl = 0; hl < GROUP; ++hl) l[hl] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MAXI; ++i)
+#pragma unroll
+        for (int hl = 0; hl < GROUP; ++hl) {
+            const float p = sc[i][hl] == -INFINITY ? 0.0f : exp_trit(sc[i][hl] - stat[0][hl]);
+            sc[i][hl] = p;
+            l[hl] += p;
+        }
+    // p.V over this lane's keys, then the block sums.
+    float acc[GROUP][8];
+#pragma unroll
+    for (int hl = 0; hl < GROUP; ++hl)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc[hl][u] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MAXI; ++i) {
+        const int j = G + DEC_GROUPS * i;
+        float v8[8];
+        if (j == pos) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v8[u] = vn[u];
+        } else {
+            kv_unpack8<KV>(vr[i], v8);
+        }
+#pragma unroll
+        for (int hl = 0; hl < GROUP; ++hl)
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc[hl][u] = __builtin_fmaf(sc[i][hl], v8[u], acc[hl][u]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int hl = 0; hl < GROUP; ++hl) {
+        // A row's 16 lanes hold the same l: count it from lane 0 of each row.
+        float lw = l[hl];
+        lw = (__shfl(lw, 0) + __shfl(lw, 16)) + (__shfl(lw, 32) + __shfl(lw, 48));
+        if (wl == 0) red[wave][hl] = lw;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            float a = acc[hl][u];
+            a += __shfl_xor(a, 16);
+            a += __shfl_xor(a, 32);
+            if (wl < 16 && dims) part[wave][hl * hd + l16 * 8 + u] = a;
+        }
+    }
+    __syncthreads();
+    if (t < GROUP) {
+        float s2 = 0.0f;
+        for (int w = 0; w < DEC_THREADS / WAVE; ++w) s2 += red[w][t];
+        stat[1][t] = s2;
+    }
+    __syncthreads();
+    if (t < group * hd) {
+        const int hl = t / hd, ee = t % hd;
+        float o = 0.0f;
+        for (int w = 0; w < DEC_THREADS / WAVE; ++w) o += part[w][hl * hd + ee];
+        out[(size_t)(g * group + hl) * hd + ee] = o / stat[1][hl];
+    }
+}
+
 // Greedy choice (CausalLm::greedy, causal_lm.rs:284-302): the first index
 // of the largest logit (src/layers.rs:604-612); a stop token ends the loop
 // without being kept; max_new kept tokens end it too. Each block takes
@@ -769,6 +1011,41 @@ void product(const Layer& L, GemvArgs a, int rows, hipStream_t s, int y_stride) 
     }
 }
 
+template <typename KV, int MAXI, int GROUP>
+void launch_decode_g(SessionImpl& S, int l, hipStream_t s) {
+    const DecoderImpl& D = *S.dec;
+    const auto& c = D.c;
+    const int hd = c.head_dim;
+    KV* kc = S.kcache.as<KV>() + (size_t)l * c.kv_heads * S.max_pos * hd;
+    KV* vc = S.vcache.as<KV>() + (size_t)l * c.kv_heads * S.max_pos * hd;
+    hipLaunchKernelGGL((attention_decode_kernel<KV, MAXI, GROUP>), dim3(c.kv_heads), dim3(DEC_THREADS), 0, s,
+                       S.qkv.as<float>(), c.heads, c.kv_heads, hd, kc, vc, S.max_pos, S.att.as<float>(), S.st(),
+                       c.qk_norm, D.q_norm(l), D.k_norm(l), c.eps, S.rope_sin.as<float>(), S.rope_cos.as<float>());
+}
+
+template <typename KV, int MAXI>
+void launch_decode_i(SessionImpl& S, int l, hipStream_t s) {
+    switch (S.dec->c.heads / S.dec->c.kv_heads) {
+        case 1: return launch_decode_g<KV, MAXI, 1>(S, l, s);
+        case 2: return launch_decode_g<KV, MAXI, 2>(S, l, s);
+        default: return launch_decode_g<KV, MAXI, 4>(S, l, s);
+    }
+}
+
+// Decode attention sized for the session: every key in one round of loads.
+template <typename KV>
+bool launch_decode(SessionImpl& S, int l, hipStream_t s) {
+    const int per_group = (S.max_pos + DEC_GROUPS - 1) / DEC_GROUPS;
+    const int group = S.dec->c.heads / S.dec->c.kv_heads;
+    // The q heads and the new key take one thread per value.
+    if (group != 1 && group != 2 && group != 4) return false;
+    if ((group + 1) * S.dec->c.head_dim > DEC_THREADS) return false;
+    if (per_group <= 4) return launch_decode_i<KV, 4>(S, l, s), true;
+    if (per_group <= 8) return launch_decode_i<KV, 8>(S, l, s), true;
+    if (per_group <= 12) return launch_decode_i<KV, 12>(S, l, s), true;
+    return false;
+}
+
 template <typename KV>
 void launch_split(SessionImpl& S, int l, int rows, bool fused, hipStream_t s) {
     const DecoderImpl& D = *S.dec;
@@ -842,6 +1119,8 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
                                S.kcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd,
                                S.vcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, rows,
                                S.att.as<float>(), 1, st);
+        } else if (fused && (S.kv32 ? launch_decode<float>(S, l, s) : launch_decode<_Float16>(S, l, s))) {
+            // One block per key/value head.
         } else if (S.kv32) {
             launch_split<float>(S, l, rows, fused, s);
         } else {

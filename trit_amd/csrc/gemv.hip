@@ -465,8 +465,8 @@ void launch(const Layer& L, const GemvArgs& a, hipStream_t s) {
     const int tiles = L.n / P / R;
     const size_t lds = smem_bytes(a.m, L.k, W::G, P * R);
     const int grid = tiles < 2048 ? tiles : 2048;
-    hipLaunchKernelGGL((gemv_kernel<W, R, P>), dim3(grid), dim3(THREADS), lds, s, L.codes.as<uint8_t>(),
-                       L.scales.ptr, L.bias.as<float>(), L.n, L.k, a);
+    launch_timed(a, gemv_kernel<W, R, P>, dim3(grid), dim3(THREADS), lds, s, L.codes.as<uint8_t>(),
+                 (const void*)L.scales.ptr, L.bias.as<float>(), L.n, L.k, a);
     TRIT_HIP(hipGetLastError());
 }
 

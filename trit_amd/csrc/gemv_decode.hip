@@ -153,12 +153,13 @@ template <int J>
 void launch_row(const Layer& L, const GemvArgs& a, hipStream_t s) {
     const int P = a.epilogue == EPI_SILU_PAIR ? 2 : 1;
     const int blocks = L.n / P / 4;
+    const uint8_t* c = L.codes.as<uint8_t>();
+    const uint16_t* sc = L.scales.as<uint16_t>();
+    const float* b = L.bias.as<float>();
     if (P == 2)
-        hipLaunchKernelGGL((gemv_row_kernel<J, 2>), dim3(blocks), dim3(LANES), 0, s, L.codes.as<uint8_t>(),
-                           L.scales.as<uint16_t>(), L.bias.as<float>(), L.n, a);
+        launch_timed(a, gemv_row_kernel<J, 2>, dim3(blocks), dim3(LANES), 0, s, c, sc, b, L.n, a);
     else
-        hipLaunchKernelGGL((gemv_row_kernel<J, 1>), dim3(blocks), dim3(LANES), 0, s, L.codes.as<uint8_t>(),
-                           L.scales.as<uint16_t>(), L.bias.as<float>(), L.n, a);
+        launch_timed(a, gemv_row_kernel<J, 1>, dim3(blocks), dim3(LANES), 0, s, c, sc, b, L.n, a);
     TRIT_HIP(hipGetLastError());
 }
 

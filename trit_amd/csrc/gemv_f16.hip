@@ -106,13 +106,13 @@ void gemv_f16(const Layer& L, const GemvArgs& a, hipStream_t s) {
     const float* b = L.bias.as<float>();
     switch (L.k) {
         case 1024:
-            hipLaunchKernelGGL((f16_kernel<8>), dim3(grid), dim3(THREADS), lds, s, w, b, L.n, L.k, a);
+            launch_timed(a, f16_kernel<8>, dim3(grid), dim3(THREADS), lds, s, w, b, L.n, L.k, a);
             break;
         case 2048:
-            hipLaunchKernelGGL((f16_kernel<16>), dim3(grid), dim3(THREADS), lds, s, w, b, L.n, L.k, a);
+            launch_timed(a, f16_kernel<16>, dim3(grid), dim3(THREADS), lds, s, w, b, L.n, L.k, a);
             break;
         default:
-            hipLaunchKernelGGL((f16_kernel<0>), dim3(grid), dim3(THREADS), lds, s, w, b, L.n, L.k, a);
+            launch_timed(a, f16_kernel<0>, dim3(grid), dim3(THREADS), lds, s, w, b, L.n, L.k, a);
             break;
     }
     TRIT_HIP(hipGetLastError());

@@ -1,6 +1,7 @@
 // Internal declarations of the trit_hip library (gfx950).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <atomic>
@@ -115,7 +116,19 @@ struct GemvArgs {
     int relu = 0;
     // Device flag: nonzero skips the launch (a finished decode loop).
     const int* skip = nullptr;
+    // Measurement: events stamped at the product kernel's start and end
+    // (hipExtLaunchKernel), or null.
+    hipEvent_t ev_start = nullptr, ev_stop = nullptr;
 };
+
+// Launches `kernel`, with the start/stop events of `a` when it has them.
+template <typename K, typename... Args>
+void launch_timed(const GemvArgs& a, K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, Args... args) {
+    if (a.ev_start || a.ev_stop)
+        hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, s, a.ev_start, a.ev_stop, 0u, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
+}
 
 // Integer products (Q8_0, Q4_K, INT8, TERNARY), m <= 8.
 void gemv_int(const Layer& L, const GemvArgs& a, hipStream_t s);

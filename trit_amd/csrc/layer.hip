@@ -312,6 +312,23 @@ int trit_hip_layer_forward_device(const TritHipLayer* layer, const float* x, int
     });
 }
 
+int trit_hip_layer_forward_timed(const TritHipLayer* layer, const float* x, int m, int relu, float* y, void* s,
+                                 void* start_event, void* stop_event) {
+    return guard(-1, [&] {
+        if (!layer || !x || !y) fail("layer, x or y is NULL");
+        if (m < 1 || m > 8) fail("timed forward: 1 to 8 rows (one kernel launch)");
+        GemvArgs a;
+        a.x = x;
+        a.m = m;
+        a.y = y;
+        a.relu = relu;
+        a.ev_start = (hipEvent_t)start_event;
+        a.ev_stop = (hipEvent_t)stop_event;
+        layer_forward(*layer->layer, a, s ? (hipStream_t)s : stream());
+        return 0;
+    });
+}
+
 int trit_hip_layer_forward(const TritHipLayer* layer, const float* x, int m, int relu, float* y) {
     return guard(-1, [&] {
         if (!layer || !x || !y) fail("layer, x or y is NULL");
