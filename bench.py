@@ -9,10 +9,11 @@ greedy decode token. `value` is decode tokens/s with every weight resident
 in HBM before the timed region.
 
 The JSON line also carries
-- roofline: the dominant decode kernel (the Q8_0 SwiGLU gate_up product,
-  6144 x 1024) timed with HIP events on its own stream, launch by launch,
-  inside a sweep over all 112 Q8_0 products of a step in decode order (so
-  its weights come from HBM, not the 256 MB Infinity Cache);
+- roofline: the dominant decode product (the Q8_0 gate_up weights, 6144 x
+  1024, one row) timed with HIP events stamped at the kernel's start and
+  end, launch by launch, inside sweeps over all 112 Q8_0 products of a step
+  in decode order (so its weights come from HBM, not the 256 MB Infinity
+  Cache);
 - cpu_baseline: the oracle (a C++ restatement of Trit's AVX-512 VNNI path,
   one pinned thread per core of the largest L3 domain) on the same weights
   and prompt, with the greedy tokens of both compared.
@@ -36,6 +37,11 @@ from trit_amd import hip, model, synth  # noqa: E402
 
 METRIC = "decode tokens/sec + GEMV HBM GB/s (% of peak), Qwen3-0.6B-shape Q8_0, 1 GPU"
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the roofline kernel, from rocprofv3 --pmc runs of
+# `bench.py --profile-pass` (profiles/gemv_row_q8_0_6144x1024_hbm_traffic.md):
+# FETCH_SIZE 3313.1 KiB x 2.0 (the scale a 256 MiB device copy gives) plus
+# WRITE_SIZE 48.0 KiB x 1.0.
+GATE_UP_TRAFFIC_BYTES = round((3313.1 * 2.0 + 48.0) * 1024)
 
 
 class Hip:
@@ -111,7 +117,7 @@ def gemv_roofline(H, linears, cfg, sweeps):
     for sweep in range(sweeps + 1):
         for i, layer in enumerate(linears):
             if i % 4 == 2:
-                # The gate_up product, with the SwiGLU epilogue as in the decode step.
+                # The gate_up weights as a plain layer product (one kernel launch).
                 a, b = events[i // 4]
                 hip.check(timed(layer.h, x, 1, 0, y, stream, a, b))
             else:
@@ -126,7 +132,7 @@ def gemv_roofline(H, linears, cfg, sweeps):
     algo = weight + d * 4 + 2 * ffn * 4
     achieved = algo / (avg_ms * 1e-3) / 1e9
     return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
+                frac=round(achieved / HBM_PEAK_GBS, 4), traffic=GATE_UP_TRAFFIC_BYTES,
                 kernel="gemv_row_kernel<4,1>: Q8_0 one-row product, the 6144x1024 gate_up weights",
                 bytes_per_launch=algo, avg_us=round(avg_ms * 1e3, 3), launches=len(durations),
                 timing="hipExtLaunchKernel start/stop events per launch, inside decode-order sweeps of "
@@ -165,10 +171,13 @@ def main():
     ap.add_argument("--mode", choices=["fast", "exact"], default="fast")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--sweeps", type=int, default=20, help="decode-order GEMV sweeps for the roofline")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="only the roofline sweeps and a 256 MiB device copy (the counter scale for "
+                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(json.dumps({"error": "this build runs on one GPU; Trit's token loop has no multi-GPU path "
-                                   "(see DESIGN.md for how it would shard)", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "the token loop runs on one GPU: Trit's decoder has no multi-GPU path, "
+                                   "so only --gpus 1 is measured", "n_gpus": args.gpus}))
         sys.exit(2)
 
     cfg = dict(synth.QWEN3_06B)
@@ -179,6 +188,14 @@ def main():
 
     hip.init(0)
     lm, linears, embed = build_layers(w)
+    if args.profile_pass:
+        H = Hip()
+        roof = gemv_roofline(H, linears, cfg, args.sweeps)
+        copy_bytes = 256 << 20
+        src, dst = H.malloc(copy_bytes), H.malloc(copy_bytes)
+        H.ok(H.L.hipMemcpy(dst, src, C.c_size_t(copy_bytes), 3), "hipMemcpy")
+        print(json.dumps({"profile_pass": True, "roofline": roof, "copy_bytes": copy_bytes}), flush=True)
+        return
     flags = hip.EXACT if args.mode == "exact" else 0
     max_pos = args.prompt + args.steps
     sess = lm.session(max_pos, flags)

@@ -77,9 +77,10 @@ int trit_hip_layer_ternary_base3(int n, int k, const uint8_t *packed, const floa
                                  TritHipLayer **out);
 
 /* ggml Q4_K weights as stored in GGUF: n*k/256 super-blocks of 144 bytes.
- * Results are Trit's: the values are those of expand-then-Blocks::quantize
- * (reference src/cpu/ggml_quants.rs:168-196, src/cpu/gemm.rs:58-76,
- * src/cpu/tensors.rs:263-286), computed from the 4-bit codes on the fly.
+ * Results are Trit's: the device expands the super-blocks and requantizes
+ * each 32 values to Q8_0 codes at creation, as expand-then-Blocks::quantize
+ * does (reference src/cpu/ggml_quants.rs:168-196, src/cpu/gemm.rs:58-76,
+ * src/cpu/tensors.rs:263-286); products then run on those codes.
  * k % 256 == 0. */
 int trit_hip_layer_q4_k(int n, int k, const void *blocks, TritHipLayer **out);
 
