@@ -37,6 +37,7 @@ from trit_amd import hip, model, synth  # noqa: E402
 
 METRIC = "decode tokens/sec + GEMV HBM GB/s (% of peak), Qwen3-0.6B-shape Q8_0, 1 GPU"
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 # HBM bytes per launch of the roofline kernel, from rocprofv3 --pmc runs of
 # `bench.py --profile-pass` (profiles/gemv_row_q8_0_6144x1024_hbm_traffic.md):
 # FETCH_SIZE 3313.1 KiB x 2.0 (the scale a 256 MiB device copy gives) plus
@@ -139,6 +140,107 @@ def gemv_roofline(H, linears, cfg, sweeps):
                        "all 112 Q8_0 products (468 MB per sweep, past the 256 MB Infinity Cache)")
 
 
+def timed_sweeps(H, stream, layers, x, y, m, sweeps):
+    """Average kernel time (ms) of each product launch, stamped by HIP events
+    at the kernel's start and end, over `sweeps` passes through `layers`
+    (copies of the weights whose total exceeds the Infinity Cache)."""
+    timed = hip.lib().trit_hip_layer_forward_timed
+    events = [(H.event(), H.event()) for _ in layers]
+    durations = []
+    for sweep in range(sweeps + 1):
+        for (a, b), layer in zip(events, layers):
+            hip.check(timed(layer.h, x, m, 0, y, stream, a, b))
+        H.sync(stream)
+        if sweep > 0:
+            durations += [H.elapsed_ms(a, b) for a, b in events]
+    return float(np.mean(durations))
+
+
+def config_lines(H, sweeps=10):
+    """The per-product configurations: C1 Q8_0 GEMV, C3 ternary GEMV, C4
+    Q4_K set, C5 prefill GEMM on the matrix cores."""
+    stream = H.stream()
+    out = {}
+    xbuf = H.malloc(1564 * 8192 * 4)
+    ybuf = H.malloc(1564 * 16384 * 4)
+    H.upload(xbuf, synth.activations(synth.seed_for(0, 77), 64, 8192))
+
+    def gbs(nbytes, ms):
+        return round(nbytes / (ms * 1e-3) / 1e9, 1)
+
+    # C1: Q8_0 2048 x 2048, one row; 64 copies (285 MB) rotate past the caches.
+    n = k = 2048
+    codes, sbits = synth.q8_0_matrix(synth.seed_for(0, 1), n, k)
+    blocks = synth.q8_0_blocks(codes, sbits)
+    copies = [hip.Dense.q8_0(n, k, blocks) for _ in range(64)]
+    ms = timed_sweeps(H, stream, copies, xbuf, ybuf, 1, sweeps)
+    algo = n * k * 34 // 32 + 4 * k + 4 * n
+    out["c1_q8_0_gemv_2048x2048_b1"] = dict(avg_us=round(ms * 1e3, 3), bytes=algo, gb_s=gbs(algo, ms),
+                                            frac=round(gbs(algo, ms) / HBM_PEAK_GBS, 4), copies=64)
+    del copies
+
+    # C3: ternary 4096 x 4096, rows 1 and 8; 64 copies (270 MB).
+    n = k = 4096
+    tcodes, tscales = synth.ternary_matrix(synth.seed_for(0, 3), n, k)
+    copies = [hip.Dense.ternary(tcodes, tscales) for _ in range(64)]
+    for b in (1, 8):
+        ms = timed_sweeps(H, stream, copies, xbuf, ybuf, b, sweeps)
+        algo = n * k // 4 + n * 4 + b * (4 * k + 4 * n)
+        out[f"c3_ternary_gemv_4096x4096_b{b}"] = dict(avg_us=round(ms * 1e3, 3), bytes=algo, gb_s=gbs(algo, ms),
+                                                      frac=round(gbs(algo, ms) / HBM_PEAK_GBS, 4), copies=64)
+    del copies
+
+    # C4: the Q4_K set of a 3B layer (K x N): qkv 3072 x 4096, o 3072 x 3072,
+    # gate/up 3072 x 16384, down 8192 x 3072; 3 copies of the set (311 MB as
+    # the Q8_0 codes the device runs).
+    shapes = [(4096, 3072), (3072, 3072), (16384, 3072), (3072, 8192)]
+    sets = []
+    for rep in range(3):
+        sets += [hip.Dense.q4_k(nn, kk, synth.q4_k_blocks(synth.seed_for(0, 40 + i), nn, kk))
+                 for i, (nn, kk) in enumerate(shapes)]
+    for b in (1, 4):
+        ms = timed_sweeps(H, stream, sets, xbuf, ybuf, b, sweeps)  # average per product
+        q4k = sum(nn * kk * 144 // 256 for nn, kk in shapes)
+        dev = sum(nn * kk * 34 // 32 for nn, kk in shapes)
+        io = sum(b * (nn + kk) * 4 for nn, kk in shapes)
+        set_ms = ms * len(shapes)
+        out[f"c4_q4_k_set_b{b}"] = dict(set_us=round(set_ms * 1e3, 2), q4_k_bytes=q4k + io,
+                                        gb_s_q4_k_bytes=gbs(q4k + io, set_ms),
+                                        frac=round(gbs(q4k + io, set_ms) / HBM_PEAK_GBS, 4),
+                                        device_bytes=dev + io, gb_s_device_bytes=gbs(dev + io, set_ms),
+                                        note="held as Trit's requantized Q8_0 codes (34 B per 32 weights)")
+    del sets
+
+    # C5: prefill contraction, 1564 rows (1500 encoder + 64 text), K 2048.
+    m, k = 1564, 2048
+    H.upload(xbuf, synth.activations(synth.seed_for(0, 5), m, k))
+    fwd = hip.lib().trit_hip_layer_forward_device
+    res = {}
+    total_ops, total_gemm_ms, total_call_ms = 0, 0.0, 0.0
+    for i, n in enumerate((2048, 6144, 2048)):
+        codes, sbits = synth.q8_0_matrix(synth.seed_for(0, 50 + i), n, k)
+        layer = hip.Dense.q8_0(n, k, synth.q8_0_blocks(codes, sbits))
+        gemm_ms = timed_sweeps(H, stream, [layer], xbuf, ybuf, m, sweeps)
+        a, b = H.event(), H.event()
+        H.record(a, stream)
+        for _ in range(sweeps):
+            hip.check(fwd(layer.h, xbuf, m, 0, ybuf, stream))
+        H.record(b, stream)
+        call_ms = H.elapsed_ms(a, b) / sweeps
+        ops = 2 * m * n * k
+        total_ops += ops
+        total_gemm_ms += gemm_ms
+        total_call_ms += call_ms
+        res[f"n{n}"] = dict(gemm_us=round(gemm_ms * 1e3, 2), call_us=round(call_ms * 1e3, 2),
+                            tops=round(ops / (gemm_ms * 1e-3) / 1e12, 1))
+    out["c5_prefill_gemm_1564x2048"] = dict(
+        products=res, ops=total_ops, gemm_us=round(total_gemm_ms * 1e3, 2),
+        call_us=round(total_call_ms * 1e3, 2), tops=round(total_ops / (total_gemm_ms * 1e-3) / 1e12, 1),
+        mfma_frac=round(total_ops / (total_gemm_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4), peak_tops=INT8_PEAK_TOPS,
+        note="gemm_us: the MFMA kernels (event-stamped); call_us adds the activation quantization pass")
+    return out
+
+
 def cpu_baseline(w, prompt, steps):
     from oracle import oracle as O
 
@@ -170,7 +272,10 @@ def main():
     ap.add_argument("--prompt", type=int, default=256)
     ap.add_argument("--mode", choices=["fast", "exact"], default="fast")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-configs", action="store_true", help="skip the per-product configuration lines")
     ap.add_argument("--sweeps", type=int, default=20, help="decode-order GEMV sweeps for the roofline")
+    ap.add_argument("--configs-pass", action="store_true",
+                    help="only the per-product configuration lines (for profiler runs)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="only the roofline sweeps and a 256 MiB device copy (the counter scale for "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs)")
@@ -187,6 +292,9 @@ def main():
     print(f"[bench] weights generated in {time.perf_counter() - t0:.1f}s", file=sys.stderr, flush=True)
 
     hip.init(0)
+    if args.configs_pass:
+        print(json.dumps({"configs_pass": True, "configs": config_lines(Hip(), sweeps=args.sweeps)}), flush=True)
+        return
     lm, linears, embed = build_layers(w)
     if args.profile_pass:
         H = Hip()
@@ -222,6 +330,12 @@ def main():
     roof = gemv_roofline(H, linears, cfg, args.sweeps)
     print(f"[bench] roofline {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}%)", file=sys.stderr, flush=True)
 
+    configs = None
+    if not args.no_configs:
+        print("[bench] product configurations ...", file=sys.stderr, flush=True)
+        configs = config_lines(H)
+        print(f"[bench] configurations: {json.dumps(configs)}", file=sys.stderr, flush=True)
+
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(t_decode / max(len(tokens), 1) * 1e3, 4),
@@ -234,6 +348,8 @@ def main():
         "prefill_tokens_per_s": round(args.prompt / t_prefill, 1),
         "roofline": roof,
     }
+    if configs:
+        out["configs"] = configs
     if not args.no_cpu:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
         cb = cpu_baseline(w, prompt, args.steps)

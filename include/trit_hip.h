@@ -90,18 +90,25 @@ int trit_hip_layer_f16(int n, int k, const uint16_t *weights, const float *bias,
 
 /* y = x * W^T (+ bias, then max(y, 0) when relu): x is m x k f32, y m x n
  * f32, host memory. Replaces Dense::forward / forward_relu
- * (reference src/cpu/gemm.rs:500-542). */
+ * (reference src/cpu/gemm.rs:500-542). Up to 8 rows run on the small-batch
+ * GEMV kernels; more rows of a Q8_0, Q4_K or int8 layer with n % 128 == 0
+ * run on the matrix cores (int8 MFMA), with the same bits. */
 int trit_hip_layer_forward(const TritHipLayer *layer, const float *x, int m, int relu, float *y);
 
 /* The same on device pointers, enqueued on `stream` (a hipStream_t; NULL:
- * the library's stream), without a wait. */
+ * the library's stream), without a wait. A matrix-core product uses a
+ * scratch buffer of the calling thread: calls from one thread must not
+ * overlap on different streams. */
 int trit_hip_layer_forward_device(const TritHipLayer *layer, const float *x, int m, int relu, float *y,
                                   void *stream);
 
 /* The measurement hook (the counterpart of Trit's kernel bench timing,
- * src/cpu/v2/bench.rs:42-54): trit_hip_layer_forward_device for 1..8 rows,
- * which is one kernel launch, stamped with start_event and stop_event
- * (hipEvent_t, either may be NULL) at the kernel's start and end. */
+ * src/cpu/v2/bench.rs:42-54): trit_hip_layer_forward_device with the
+ * product kernel's launch stamped with start_event and stop_event
+ * (hipEvent_t, either may be NULL) at the kernel's start and end. 1..8 rows
+ * are one launch; a matrix-core product stamps its GEMM kernel (the
+ * activation quantization runs before it, unstamped). Fails for more than
+ * 8 rows of a layer the matrix cores do not take. */
 int trit_hip_layer_forward_timed(const TritHipLayer *layer, const float *x, int m, int relu, float *y,
                                  void *stream, void *start_event, void *stop_event);
 

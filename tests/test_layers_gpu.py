@@ -45,7 +45,47 @@ def test_q8_0_bias_relu(gpu):
     assert bits_equal(got, ref)
 
 
-@pytest.mark.parametrize("n,k,m", [(512, 1024, 1), (384, 2048, 4)])
+# More than 8 rows: the matrix-core product (int8 MFMA), same bits.
+@pytest.mark.parametrize("n,k,m", [(256, 512, 9), (384, 1024, 64), (128, 256, 100), (2048, 2048, 257),
+                                   (1024, 3072, 40)])
+def test_q8_0_many_rows(gpu, n, k, m):
+    print(f"case q8_0 matrix cores n={n} k={k} m={m}", flush=True)
+    codes, sbits, blocks = q8_layer(synth.seed_for(2, n + k), n, k)
+    x = synth.activations(synth.seed_for(2, 7 + m), m, k)
+    ref = O.Int8(codes, sbits.view(np.float16).astype(np.float32), 32, True)(x)
+    got = gpu.Dense.q8_0(n, k, blocks).forward(x)
+    assert bits_equal(got, ref), np.max(np.abs(got - ref))
+
+
+def test_q8_0_many_rows_bias_relu(gpu):
+    print("case q8_0 matrix cores bias relu", flush=True)
+    n, k, m = 256, 512, 33
+    codes, sbits, blocks = q8_layer(14, n, k)
+    bias = synth.activations(15, 1, n)[0]
+    x = synth.activations(16, m, k)
+    ref = np.maximum(O.Int8(codes, sbits.view(np.float16).astype(np.float32), 32, True)(x) + bias, 0)
+    got = gpu.Dense.q8_0(n, k, blocks, bias).forward(x, relu=True)
+    assert bits_equal(got, ref)
+
+
+@pytest.mark.parametrize("n", [2048, 6144])
+def test_prefill_gemm_1564_rows(gpu, n):
+    """The audio-LLM prefill contraction: 1500 encoder + 64 text rows, K 2048.
+    The oracle checks a sample of rows (each output row depends on its own
+    input row only), the edges of the 64-row tiles included."""
+    print(f"case q8_0 prefill 1564x2048 n={n}", flush=True)
+    m, k = 1564, 2048
+    codes, sbits, blocks = q8_layer(synth.seed_for(5, n), n, k)
+    x = synth.activations(synth.seed_for(5, 1564), m, k)
+    got = gpu.Dense.q8_0(n, k, blocks).forward(x)
+    rows = sorted(set([0, 1, 31, 32, 63, 64, 127, 1499, 1500, 1535, 1536, 1562, 1563]
+                      + synth.ints(55, (19,), 0, m - 1).tolist()))
+    ref = O.Int8(codes, sbits.view(np.float16).astype(np.float32), 32, True)(x[rows])
+    assert bits_equal(got[rows], ref), np.max(np.abs(got[rows] - ref))
+    assert np.all(np.isfinite(got))
+
+
+@pytest.mark.parametrize("n,k,m", [(512, 1024, 1), (384, 2048, 4), (256, 512, 33), (512, 1024, 70)])
 def test_int8(gpu, n, k, m):
     print(f"case int8 n={n} k={k} m={m}", flush=True)
     codes = synth.ints(21, (n, k), -127, 127).astype(np.int8)
@@ -64,7 +104,7 @@ def ternary_inputs(n, k):
     return codes, scales
 
 
-@pytest.mark.parametrize("m", [1, 8])
+@pytest.mark.parametrize("m", [1, 8, 12])
 def test_ternary_4096(gpu, m):
     print(f"case ternary 4096x4096 m={m}", flush=True)
     n = k = 4096
@@ -90,7 +130,7 @@ def test_ternary_base3(gpu):
     assert bits_equal(got, ref)
 
 
-@pytest.mark.parametrize("n,k,m", [(4096, 3072, 1), (3072, 8192, 4), (256, 512, 3)])
+@pytest.mark.parametrize("n,k,m", [(4096, 3072, 1), (3072, 8192, 4), (256, 512, 3), (256, 512, 20)])
 def test_q4_k(gpu, n, k, m):
     print(f"case q4_k n={n} k={k} m={m}", flush=True)
     blocks = synth.q4_k_blocks(41 + n, n, k)

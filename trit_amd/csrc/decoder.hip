@@ -15,6 +15,7 @@
 // (+ residual). The bracketed kernels run in exact mode only: there the
 // RMSNorm sum is Trit's serial chain; in fast mode each product block
 // computes it with a fixed tree.
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -944,6 +945,7 @@ struct SessionImpl {
     DeviceMemory kcache, vcache, rope_sin, rope_cos;
     DeviceMemory x, qkv, att, hid, inv, normed, logits, state, tokens_in, tokens_out, partials;
     DeviceMemory att_part, att_arrived;  // split attention: chunk partials, per (row, kv head) counters
+    DeviceMemory gemm_scratch;           // quantized rows of the matrix-core products
     int max_splits = 0;
     int host_pos = 0;
     hipGraphExec_t graph = nullptr;
@@ -990,6 +992,8 @@ void ensure_rows(SessionImpl& S, int rows) {
     S.max_splits = (S.max_pos + Split<float>::CH - 1) / Split<float>::CH;
     S.att_part.alloc((size_t)rows * c.heads * S.max_splits * (c.head_dim + 2) * 4);
     S.att_arrived.alloc((size_t)rows * c.kv_heads * 4);
+    const int kmax = std::max(std::max(c.d, qd), c.ffn);
+    S.gemm_scratch.alloc(gemm_scratch_bytes(rows, kmax));
     TRIT_HIP(hipMemset(S.att_arrived.ptr, 0, (size_t)rows * c.kv_heads * 4));
     S.rows_cap = rows;
     if (S.graph) {
@@ -998,8 +1002,11 @@ void ensure_rows(SessionImpl& S, int rows) {
     }
 }
 
-// Integer product of `rows` rows in launches of up to 8.
-void product(const Layer& L, GemvArgs a, int rows, hipStream_t s, int y_stride) {
+// Integer product of `rows` rows: on the matrix cores for more than 8 rows
+// (same bits), else in launches of up to 8.
+void product(SessionImpl& S, const Layer& L, GemvArgs a, int rows, hipStream_t s, int y_stride) {
+    a.m = rows;
+    if (rows > 8 && gemm_supported(L, a)) return gemm_int(L, a, S.gemm_scratch.ptr, s);
     for (int r0 = 0; r0 < rows; r0 += 8) {
         GemvArgs b = a;
         b.m = rows - r0 < 8 ? rows - r0 : 8;
@@ -1090,7 +1097,7 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
         a.x = x;
         a.norm_w = D.norm_attn(l);
         a.y = S.qkv.as<float>();
-        product(*D.qkv[l], a, rows, s, stride);
+        product(S, *D.qkv[l], a, rows, s, stride);
         // q/k norm, rotary, cache append, attention.
         const bool fused = !S.exact && rows == 1;
         if (!fused) {
@@ -1134,7 +1141,7 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
         o.y = x;
         o.residual = x;
         o.epilogue = EPI_RESIDUAL;
-        product(*D.o[l], o, rows, s, c.d);
+        product(S, *D.o[l], o, rows, s, c.d);
         // gate_up with the MLP norm in the prologue and SwiGLU after.
         GemvArgs gu;
         gu.skip = &st->done;
@@ -1148,7 +1155,7 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
         gu.norm_w = D.norm_mlp(l);
         gu.y = S.hid.as<float>();
         gu.epilogue = EPI_SILU_PAIR;
-        product(*D.gate_up[l], gu, rows, s, c.ffn);
+        product(S, *D.gate_up[l], gu, rows, s, c.ffn);
         // down with the residual add.
         GemvArgs dn;
         dn.skip = &st->done;
@@ -1156,7 +1163,7 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
         dn.y = x;
         dn.residual = x;
         dn.epilogue = EPI_RESIDUAL;
-        product(*D.down[l], dn, rows, s, c.d);
+        product(S, *D.down[l], dn, rows, s, c.d);
     }
     // Final norm of the last row, then the head.
     const float* last = x + (size_t)(rows - 1) * c.d;

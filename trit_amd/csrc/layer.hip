@@ -100,11 +100,41 @@ void layer_forward(const Layer& L, const GemvArgs& a, hipStream_t s) {
     return gemv_int(L, a, s);
 }
 
-// Per-thread staging buffers of the host-pointer forward.
+// Per-thread staging buffers of the host-pointer forward, and the scratch
+// of the calling thread's many-row products.
 struct Staging {
-    DeviceMemory x, y;
+    DeviceMemory x, y, scratch;
 };
 thread_local Staging g_staging;
+
+// Rows above this many run on the matrix cores when the layer allows it.
+constexpr int GEMM_MIN_ROWS = 9;
+
+// One product of m rows: the matrix-core product for many rows, else the
+// small-batch kernels in calls of up to 8 rows.
+void forward_rows(const Layer& L, GemvArgs a, int m, hipStream_t s) {
+    a.m = m;
+    if (m >= GEMM_MIN_ROWS && gemm_supported(L, a)) {
+        const size_t need = gemm_scratch_bytes(m, L.k);
+        if (g_staging.scratch.bytes < need) {
+            // Work already queued may still use the old scratch.
+            TRIT_HIP(hipDeviceSynchronize());
+            g_staging.scratch.alloc(need);
+        }
+        return gemm_int(L, a, g_staging.scratch.ptr, s);
+    }
+    if (a.ev_start || a.ev_stop) {
+        if (m > 8) fail("timed forward: more than 8 rows of this layer take several launches");
+    }
+    const float* x = a.x;
+    float* y = a.y;
+    for (int r0 = 0; r0 < m; r0 += 8) {
+        a.x = x + (size_t)r0 * L.k;
+        a.y = y + (size_t)r0 * L.n;
+        a.m = m - r0 < 8 ? m - r0 : 8;
+        layer_forward(L, a, s);
+    }
+}
 
 }  // namespace trit
 
@@ -299,15 +329,8 @@ int trit_hip_layer_forward_device(const TritHipLayer* layer, const float* x, int
         a.m = m;
         a.y = y;
         a.relu = relu;
-        hipStream_t st = s ? (hipStream_t)s : stream();
-        const Layer& L = *layer->layer;
-        // Rows in calls of up to 8.
-        for (int r0 = 0; r0 < m; r0 += 8) {
-            a.x = x + (size_t)r0 * L.k;
-            a.y = y + (size_t)r0 * L.n;
-            a.m = m - r0 < 8 ? m - r0 : 8;
-            layer_forward(L, a, st);
-        }
+        if (m <= 0) fail("m must be positive");
+        forward_rows(*layer->layer, a, m, s ? (hipStream_t)s : stream());
         return 0;
     });
 }
@@ -316,15 +339,14 @@ int trit_hip_layer_forward_timed(const TritHipLayer* layer, const float* x, int 
                                  void* start_event, void* stop_event) {
     return guard(-1, [&] {
         if (!layer || !x || !y) fail("layer, x or y is NULL");
-        if (m < 1 || m > 8) fail("timed forward: 1 to 8 rows (one kernel launch)");
+        if (m <= 0) fail("m must be positive");
         GemvArgs a;
         a.x = x;
-        a.m = m;
         a.y = y;
         a.relu = relu;
         a.ev_start = (hipEvent_t)start_event;
         a.ev_stop = (hipEvent_t)stop_event;
-        layer_forward(*layer->layer, a, s ? (hipStream_t)s : stream());
+        forward_rows(*layer->layer, a, m, s ? (hipStream_t)s : stream());
         return 0;
     });
 }
