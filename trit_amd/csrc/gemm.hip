@@ -19,10 +19,13 @@
 //  2. quantize_kernel: Trit's activation quantizer over all rows into codes
 //     (m x k) and group scales stored group-major (g x mpad), so that a
 //     lane's four consecutive output rows read one 16-byte load;
-//  3. gemm_kernel: 256 threads = 2 x 2 waves; a wave owns 32 rows of x by
-//     two 32-row MFMA tiles of weights (or, for the SwiGLU pair, the gate
-//     tile and its up tile), so every (row, output) total stays in one
-//     lane's registers from the first group to the epilogue.
+//  3. gemm_kernel: 256 threads = 2 x 2 waves over 64 rows of x and 128
+//     weight rows. K runs in 256-byte chunks staged through LDS: 16 threads
+//     read a row's 256 contiguous bytes, and the next chunk's loads are in
+//     flight while this one computes. A wave owns 32 rows of x by two
+//     32-row MFMA tiles of weights (or, for the SwiGLU pair, the gate tile
+//     and its up tile), so every (row, output) total stays in one lane's
+//     registers from the first group to the epilogue.
 #include "device.h"
 #include "internal.h"
 
@@ -92,106 +95,227 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
     if (live && col % G == 0) xs[(size_t)(col / G) * mpad + row] = real ? (HALF ? f16_round(scale) : scale) : 0.0f;
 }
 
-template <bool HALF>
-__device__ __forceinline__ float weight_scale(const void* s, size_t i) {
-    if (HALF) return f16_to_f32(((const uint16_t*)s)[i]);
-    return ((const float*)s)[i];
+constexpr int KC = 256;           // bytes of K per LDS chunk
+constexpr int ROW_LDS = KC + 16;  // padded LDS row: rows 8 apart start 4 banks apart
+constexpr int BN_ROWS = 128;      // weight rows per block
+
+// One K chunk in LDS: the block's 64 x rows and 128 weight rows, and their
+// group scales (weight scales widened to f32).
+template <int G>
+struct alignas(16) Stage {
+    static constexpr int GPC = KC / G;  // groups per chunk
+    alignas(16) int8_t a[BM * ROW_LDS];
+    alignas(16) int8_t b[BN_ROWS * ROW_LDS];
+    alignas(16) float xs[GPC][BM];
+    alignas(16) float ws[GPC][BN_ROWS];
+};
+
+// A group's operand fragments: lane (lr, h) holds bytes [16h, 16h + 16) of
+// each 32-wide step of x row lr and weight rows lr of the two tiles.
+template <int CH>
+struct Frags {
+    v4i a[CH], b0[CH], b1[CH];
+};
+
+template <int G>
+__device__ __forceinline__ void read_frags(const int8_t* la, const int8_t* lb0, const int8_t* lb1, int gi,
+                                           Frags<G / 32>& f) {
+#pragma unroll
+    for (int s = 0; s < G / 32; ++s) {
+        const int off = gi * G + 32 * s;
+        f.a[s] = *(const v4i*)(la + off);
+        f.b0[s] = *(const v4i*)(lb0 + off);
+        f.b1[s] = *(const v4i*)(lb1 + off);
+    }
 }
 
-// One group's operands: per 32-wide step, the x tile's 16 bytes and the
-// two weight tiles'; the x scales of the lane's 16 output rows and the two
-// weight rows' scales.
-template <int CH>
-struct Operands {
-    v4i a[CH], b0[CH], b1[CH];
-    float4 xv[4];
+// The i32 dots of a group for the wave's two weight tiles.
+template <int G>
+__device__ __forceinline__ void mfma_group(const Frags<G / 32>& f, v16i& d0, v16i& d1) {
+#pragma unroll
+    for (int s = 0; s < G / 32; ++s) {
+        d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[s], f.b0[s], d0, 0, 0, 0);
+        d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[s], f.b1[s], d1, 0, 0, 0);
+    }
+}
+
+// A group's scales for the lane: x scales of its 16 output rows (four
+// runs of four), weight scales of its two columns.
+struct Scales {
+    float4 x[4];
     float w0, w1;
 };
 
+__device__ __forceinline__ void read_scales(const float* xs, const float* ws, int xrow, int c0, int c1, Scales& s) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) s.x[q] = *(const float4*)(xs + xrow + 8 * q);
+    s.w0 = ws[c0];
+    s.w1 = ws[c1];
+}
+
 template <int G, bool HALF, int P>
-__global__ __launch_bounds__(GEMM_THREADS) void gemm_kernel(const int8_t* __restrict__ xq,
-                                                            const float* __restrict__ xs, int m, int mpad,
-                                                            const int8_t* __restrict__ codes,
-                                                            const void* __restrict__ scales,
-                                                            const float* __restrict__ bias, int n, int k, int nb,
-                                                            int mb, GemvArgs a) {
-    constexpr int CH = G / 32;  // MFMA steps per group
+__global__ __launch_bounds__(GEMM_THREADS, 2) void gemm_kernel(const int8_t* __restrict__ xq,
+                                                               const float* __restrict__ xs, int m, int mpad,
+                                                               const int8_t* __restrict__ codes,
+                                                               const void* __restrict__ scales,
+                                                               const float* __restrict__ bias, int n, int k,
+                                                               int nb, int mb, GemvArgs a) {
+    constexpr int GPC = KC / G;  // groups per chunk
+    constexpr int CH = G / 32;   // MFMA steps per group
+    __shared__ __align__(16) Stage<G> st;
     if (a.skip && *a.skip) return;
-    const int groups = k / G;
+    const int groups = k / G, chunks = k / KC;
     // Tiles in XCD order: block b runs on XCD b % 8; the blocks of one XCD
     // share weight tiles, which then stay in that XCD's L2.
-    const int b = blockIdx.x;
+    const int blk = blockIdx.x;
     int bn, bm;
     if (nb % 8 == 0) {
-        const int t = b / 8;
-        bn = b % 8 + 8 * (t / mb);
-        bm = t % mb;
+        const int q = blk / 8;
+        bn = blk % 8 + 8 * (q / mb);
+        bm = q % mb;
     } else {
-        bn = b % nb;
-        bm = b / nb;
+        bn = blk % nb;
+        bm = blk / nb;
     }
-    const int lane = threadIdx.x % WAVE, w = threadIdx.x / WAVE;
+    const int t = threadIdx.x;
+    const int lane = t % WAVE, w = t / WAVE;
     const int lr = lane % 32, h = lane / 32;
-    const int m0 = bm * BM + (w % 2) * 32;
-    int r0, r1;  // first weight rows of the wave's two tiles
-    if (P == 1) {
-        r0 = bn * 128 + (w / 2) * 64;
-        r1 = r0 + 32;
-    } else {
-        r0 = bn * 64 + (w / 2) * 32;
-        r1 = n / 2 + r0;
+    const int mbase = bm * BM;
+    // LDS weight row i holds weight row brow(i): 128 rows, or for the
+    // SwiGLU pair 64 gate rows then their 64 up rows.
+    auto brow = [&](int i) { return P == 1 ? bn * 128 + i : (i < 64 ? bn * 64 + i : n / 2 + bn * 64 + (i - 64)); };
+
+    // Global loads of a chunk, 16 bytes a piece, 16 threads a row (256
+    // contiguous bytes): 4 x pieces and 8 weight pieces per thread; threads
+    // [0, 16*GPC) one float4 of x scales, threads [128, 256) one weight row's
+    // GPC scales.
+    // Byte offsets of the thread's pieces in row 0 of the chunk; rows are
+    // k bytes apart (x: at most m*k < 2^31 bytes, weights: n*k).
+    uint32_t ag[4], bg[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int p = t + GEMM_THREADS * i, row = p / 16;
+        const int mrow = mbase + row < m ? mbase + row : m - 1;
+        ag[i] = (uint32_t)mrow * (uint32_t)k + 16 * (p % 16);
     }
-    const int arow = m0 + lr < m ? m0 + lr : m - 1;
-    const int8_t* ap = xq + (size_t)arow * k + 16 * h;
-    const int8_t* bp0 = codes + (size_t)(r0 + lr) * k + 16 * h;
-    const int8_t* bp1 = codes + (size_t)(r1 + lr) * k + 16 * h;
-    const float* xp = xs + m0 + 4 * h;
-    const size_t s0 = (size_t)(r0 + lr) * groups, s1 = (size_t)(r1 + lr) * groups;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int p = t + GEMM_THREADS * i;
+        bg[i] = (uint32_t)brow(p / 16) * (uint32_t)k + 16 * (p % 16);
+    }
+    const bool xs_thread = t < 16 * GPC;
+    const bool ws_thread = t >= 128;
+    const int ws_row = t - 128;
+    const size_t ws_base = ws_thread ? (size_t)brow(ws_row) * groups : 0;
+
+    v4i ra[4], rb[8];
+    float4 rx = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    uint4 rw = make_uint4(0, 0, 0, 0);  // HALF: 8 f16 scales; else 2 f32 in .x .y
+    auto fetch = [&](int c) {
+        const size_t off = (size_t)c * KC;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ra[i] = *(const v4i*)(xq + ag[i] + off);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) rb[i] = *(const v4i*)(codes + bg[i] + off);
+        if (xs_thread) rx = *(const float4*)(xs + (size_t)(c * GPC + t / 16) * mpad + mbase + 4 * (t % 16));
+        if (ws_thread) {
+            if (HALF) {
+                rw = *(const uint4*)((const uint16_t*)scales + ws_base + c * GPC);
+            } else {
+                const float2 f = *(const float2*)((const float*)scales + ws_base + c * GPC);
+                rw.x = __builtin_bit_cast(uint32_t, f.x);
+                rw.y = __builtin_bit_cast(uint32_t, f.y);
+            }
+        }
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int p = t + GEMM_THREADS * i;
+            *(v4i*)(st.a + (p / 16) * ROW_LDS + 16 * (p % 16)) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int p = t + GEMM_THREADS * i;
+            *(v4i*)(st.b + (p / 16) * ROW_LDS + 16 * (p % 16)) = rb[i];
+        }
+        if (xs_thread) *(float4*)(&st.xs[t / 16][4 * (t % 16)]) = rx;
+        if (ws_thread) {
+            if (HALF) {
+                const uint32_t v[4] = {rw.x, rw.y, rw.z, rw.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    st.ws[2 * j][ws_row] = f16_to_f32((uint16_t)(v[j] & 0xffff));
+                    st.ws[2 * j + 1][ws_row] = f16_to_f32((uint16_t)(v[j] >> 16));
+                }
+            } else {
+                st.ws[0][ws_row] = __builtin_bit_cast(float, rw.x);
+                st.ws[1][ws_row] = __builtin_bit_cast(float, rw.y);
+            }
+        }
+    };
+
+    // The wave's tiles: x rows [32 (w % 2), +32) of the block; weight LDS
+    // rows sub0 and sub1 (+32 each).
+    const int wn = w / 2;
+    const int sub0 = P == 1 ? wn * 64 : wn * 32;
+    const int sub1 = P == 1 ? wn * 64 + 32 : 64 + wn * 32;
+    const int8_t* la = st.a + ((w % 2) * 32 + lr) * ROW_LDS + 16 * h;
+    const int8_t* lb0 = st.b + (sub0 + lr) * ROW_LDS + 16 * h;
+    const int8_t* lb1 = st.b + (sub1 + lr) * ROW_LDS + 16 * h;
+    const int xrow = (w % 2) * 32 + 4 * h;
 
     float t0[16], t1[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) t0[r] = t1[r] = 0.0f;
 
-    // Operands of group g: lane (lr, h) holds bytes [16h, 16h + 16) of each
-    // 32-wide step in x row m0 + lr and in weight rows r0 + lr, r1 + lr.
-    // Everything a group needs is loaded one group ahead, so the wait for a
-    // group's loads never waits for the next group's.
-    auto load = [&](int g, Operands<CH>& o) {
-#pragma unroll
-        for (int s = 0; s < CH; ++s) {
-            const size_t off = (size_t)g * G + 32 * s;
-            o.a[s] = *(const v4i*)(ap + off);
-            o.b0[s] = *(const v4i*)(bp0 + off);
-            o.b1[s] = *(const v4i*)(bp1 + off);
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) o.xv[q] = *(const float4*)(xp + (size_t)g * mpad + 8 * q);
-        o.w0 = weight_scale<HALF>(scales, s0 + g);
-        o.w1 = weight_scale<HALF>(scales, s1 + g);
-    };
-    Operands<CH> cur, nxt;
-    load(0, cur);
-    for (int g = 0; g < groups; ++g) {
-        if (g + 1 < groups) load(g + 1, nxt);
+    fetch(0);
+    for (int c = 0; c < chunks; ++c) {
+        __syncthreads();  // the previous chunk's reads are done
+        stash();
+        __syncthreads();
+        if (c + 1 < chunks) fetch(c + 1);  // lands while this chunk computes
+        // Software pipeline over the chunk's groups: at step gi the matrix
+        // cores run group gi + 1 from fragments read one step earlier, LDS
+        // reads for group gi + 2 are in flight, and the vector ALUs run
+        // group gi's f32 chain. Scheduling barriers keep the compiler from
+        // folding the stages back together.
+        Frags<CH> f, fn;
         v16i d0 = {}, d1 = {};
+        read_frags<G>(la, lb0, lb1, 0, f);
+        mfma_group<G>(f, d0, d1);
+        if (GPC > 1) read_frags<G>(la, lb0, lb1, 1, f);
 #pragma unroll
-        for (int s = 0; s < CH; ++s) {
-            d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[s], cur.b0[s], d0, 0, 0, 0);
-            d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[s], cur.b1[s], d1, 0, 0, 0);
-        }
-        // Output (row 8*(r/4) + 4h + r%4, column lr) of a tile is register r.
+        for (int gi = 0; gi < GPC; ++gi) {
+            v16i n0 = {}, n1 = {};
+            if (gi + 1 < GPC) mfma_group<G>(f, n0, n1);
+            if (gi + 2 < GPC) read_frags<G>(la, lb0, lb1, gi + 2, fn);
+            Scales sc;
+            read_scales(st.xs[gi], st.ws[gi], xrow, sub0 + lr, sub1 + lr, sc);
+            __builtin_amdgcn_sched_barrier(0);
+            // Output (row 8*(r/4) + 4h + r%4, column lr) of a tile is register r.
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float4 x4 = cur.xv[r / 4];
-            const float xsv = r % 4 == 0 ? x4.x : r % 4 == 1 ? x4.y : r % 4 == 2 ? x4.z : x4.w;
-            t0[r] = __builtin_fmaf((float)d0[r], cur.w0 * xsv, t0[r]);
-            t1[r] = __builtin_fmaf((float)d1[r], cur.w1 * xsv, t1[r]);
+            for (int q = 0; q < 4; ++q) {
+                const float xv[4] = {sc.x[q].x, sc.x[q].y, sc.x[q].z, sc.x[q].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int r = 4 * q + j;
+                    t0[r] = __builtin_fmaf((float)d0[r], sc.w0 * xv[j], t0[r]);
+                    t1[r] = __builtin_fmaf((float)d1[r], sc.w1 * xv[j], t1[r]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            d0 = n0;
+            d1 = n1;
+            f = fn;
         }
-        cur = nxt;
     }
 
     // Epilogue, as the small-batch kernel's: bias, relu, then the residual
     // add or the SwiGLU pair (src/models/parts/causal_lm.rs:464-473).
+    const int r0 = P == 1 ? bn * 128 + sub0 : bn * 64 + wn * 32;
+    const int r1 = P == 1 ? bn * 128 + sub1 : n / 2 + r0;
+    const int m0 = mbase + (w % 2) * 32;
     const int ldy = n / P;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -256,8 +380,9 @@ void launch_gemm(const Layer& L, const GemvArgs& a, const Scratch& sc, hipStream
 
 bool gemm_supported(const Layer& L, const GemvArgs& a) {
     if (L.kind != Q8_0 && L.kind != Q4_K && L.kind != INT8) return false;
-    if (L.n % 128 != 0 || L.k % group_of(L) != 0) return false;
-    if (a.norm_w && !a.norm_inv && L.k % 256 != 0) return false;
+    if (L.n % 128 != 0 || L.k % KC != 0) return false;
+    // 32-bit byte offsets into the codes of x and of the weights.
+    if ((int64_t)a.m * L.k >= (int64_t)1 << 31 || (int64_t)L.n * L.k >= (int64_t)1 << 32) return false;
     return a.m >= 1;
 }
 

@@ -138,7 +138,7 @@ bool gemv_row(const Layer& L, const GemvArgs& a, hipStream_t s);
 // f16 products, m <= 8.
 void gemv_f16(const Layer& L, const GemvArgs& a, hipStream_t s);
 // Integer products of any row count on the matrix cores (Q8_0, Q4_K, INT8
-// with n % 128 == 0). `scratch` holds gemm_scratch_bytes(m, k) bytes of
+// with n % 128 == 0 and k % 256 == 0). `scratch` holds gemm_scratch_bytes(m, k) bytes of
 // device memory the product may overwrite.
 bool gemm_supported(const Layer& L, const GemvArgs& a);
 size_t gemm_scratch_bytes(int m, int k);
