@@ -215,3 +215,51 @@ def test_generate_long_prompt(small, flags):
         err = rel(logits, want_logits)
         assert err < 5e-2
         check_fast_tokens(got, ref, p, 20, float(np.max(np.abs(logits - want_logits))), least=0 if flags == 0 else 5)
+
+
+def test_mid_step_fast(mid, monkeypatch):
+    """The persistent decode step (fast mode, f16 caches, the default for
+    this model): greedy tokens against the oracle's and the per-kernel
+    loop's, positions, a stop token, and a second generate call that
+    continues the first."""
+    print("case decoder mid persistent step", flush=True)
+    w, ref, lm = mid
+    p = synth.prompt(98, 40, MID["vocab"])
+    s = lm.session(96, 0)
+    logits = s.prefill(p)
+    got = s.generate(24)
+    assert len(got) == 24
+    assert s.position == 40 + 23
+    ref.reset()
+    want_logits = ref.forward(p)
+    assert rel(logits, want_logits) < 5e-2
+    bound = float(np.max(np.abs(logits - want_logits)))
+    check_fast_tokens(got, ref, p, 24, bound, least=0)
+
+    # The per-kernel loop with the same f16 caches: the two differ only in
+    # the order of the attention sums (rounding), so the greedy tokens agree.
+    monkeypatch.setenv("TRIT_HIP_STEP", "0")
+    k = lm.session(96, 0)
+    k.prefill(p)
+    kern = k.generate(24)
+    monkeypatch.delenv("TRIT_HIP_STEP")
+    print(f"step {got.tolist()}\nkernel {kern.tolist()}", flush=True)
+    assert got.tolist() == kern.tolist()
+
+    # A stop token ends the loop without being kept.
+    s2 = lm.session(96, 0)
+    s2.prefill(p)
+    stop = [int(got[5])]
+    cut = got.tolist().index(stop[0])
+    got2 = s2.generate(24, stop=stop)
+    assert got2.tolist() == got.tolist()[:cut]
+    assert s2.position == 40 + cut
+
+    # Two calls: the second starts from the first one's last choice.
+    s3 = lm.session(96, 0)
+    s3.prefill(p)
+    a = s3.generate(10)
+    b = s3.generate(10)
+    assert a.tolist() == got.tolist()[:10]
+    assert b.tolist() == got.tolist()[9:19]
+    assert s3.position == 40 + 18

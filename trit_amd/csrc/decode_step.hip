@@ -1,0 +1,981 @@
+// The persistent decode step: one launch per greedy token runs the choice,
+// every layer and the head (src/models/parts/causal_lm.rs:284-302,410-481)
+// on all CUs at once, one block per CU.
+//
+// Blocks hand activations to each other through exchange words: 8 bytes
+// holding an f32 value and a 32-bit tag, written with one agent-scope store
+// and polled with agent-scope loads until the tag is the one the reader
+// waits for. The tag names the launch and the phase, so a word is never
+// mistaken for an older one, and no barrier, fence or cache flush is
+// needed between phases. A phase's weights do not depend on its inputs:
+// each block issues their loads before it waits, so the weight stream
+// overlaps the hand-over instead of following it.
+//
+// Per layer (tags in order): qkv product -> attention partials (32 key
+// splits per key/value head, one per block) -> combined attention -> o
+// product + residual -> gate_up product + SwiGLU -> down product +
+// residual. Then the final RMSNorm, the f16 head and each block's best
+// logit; the next launch's first act is the greedy choice over those
+// candidates (first maximum wins, src/layers.rs:604-612).
+//
+// Products use the one-row kernel's arithmetic (gemv_decode.hip): Trit's
+// quantizer, exact i32 block dots and the f32 group chain in order, so
+// their values are Trit's bit for bit given the same input. The RMSNorm
+// sums are the one-row kernel's tree; attention sums run in parallel
+// (fast mode). Every wait has a deadline: a block that misses it marks the
+// session's error flag and the launch drains.
+#include "decoder_impl.h"
+#include "device.h"
+
+#include <climits>
+
+namespace trit {
+namespace {
+
+constexpr int T = 512;         // threads per block
+constexpr int NW = T / WAVE;   // waves per block
+constexpr int HD = 128;        // head_dim
+constexpr int MAXC = 4;        // 32-key chunks of a split held in registers
+constexpr int MAXD = 2048;     // largest d
+constexpr int MAXK = 3072;     // largest product input
+constexpr int PH = 6;          // exchange phases per layer
+
+struct LayerPtrs {
+    const uint8_t* codes[4];  // qkv, o, gate_up, down: Q8_0 codes n x k
+    const uint16_t* scales[4];
+    const float* norm_attn;
+    const float* norm_mlp;
+    const float* q_norm;
+    const float* k_norm;
+    _Float16* kcache;  // [kv head][position][HD]
+    _Float16* vcache;
+};
+
+struct StepArgs {
+    const LayerPtrs* layers;
+    int n_layers, d, qd, ffn, heads, kvh, vocab, qk_norm, max_pos;
+    float eps;
+    const uint16_t* embed;  // f16 lane-chain table, vocab x d
+    const uint16_t* head;   // f16 head in 4-row tiles (head_tile_kernel)
+    const float* final_norm;
+    const float* rope_sin;  // [position][HD / 2]
+    const float* rope_cos;
+    uint64_t* X;     // d words: the residual stream after o / down
+    uint64_t* QKV;   // (heads + 2 kvh) * HD words
+    uint64_t* PART;  // heads * splits * (HD + 2) words: max, sum, p.V
+    uint64_t* ATT;   // heads * HD words
+    uint64_t* H;     // ffn words
+    float2* cand;    // per block: best logit, its index (int bits)
+    int* out;
+    State* st;
+    int splits;               // key splits per key/value head (blocks / kvh)
+    int comb;                 // combined attention outputs per block
+    int rq, ro, rgu, rd;      // rows per block (gate_up: pairs), multiples of 4
+    int rh;                   // head rows per block
+    unsigned long long ticks; // wall-clock ticks a block may wait in a launch
+};
+
+struct Smem {
+    alignas(16) float xres[MAXD];  // the residual stream, this phase's copy
+    alignas(16) float xin[MAXK];   // a product's input / gathered partials
+    alignas(16) int8_t xq[MAXK];
+    alignas(16) float xs[MAXK / 32];
+    alignas(16) float qkv[6 * HD];  // a key/value head's q heads, k, v
+    alignas(16) float kvn[2][HD];   // the new key and value, as cached
+    alignas(16) float gpart[32][2 * HD];  // attention: per 16-lane group p.V of two heads
+    float gmax[32][2];
+    float gl[32][2];
+    float bv[T];
+    int bi[T];
+    float inv;
+    int abort;
+    int token;
+};
+
+__device__ __forceinline__ uint32_t tag_of(uint32_t tag0, int layer, int phase) {
+    return tag0 + (uint32_t)(layer * PH + phase + 1);
+}
+
+__device__ __forceinline__ void put(uint64_t* p, float v, uint32_t tag) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t peek(const uint64_t* p) {
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ bool aborted(Smem& sm) {
+    return __hip_atomic_load(&sm.abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0;
+}
+
+// Waits for n exchange words tagged `tag` (word i at src[index(i)]) and
+// stores their values in dst[i]. Ends with a block barrier; false when a
+// word missed the deadline (the block then leaves the launch).
+template <typename Index>
+__device__ bool gather(const uint64_t* src, int n, Index index, uint32_t tag, float* dst, Smem& sm,
+                       unsigned long long deadline, State* st) {
+    constexpr int MAXW = MAXK / T;
+    uint64_t w[MAXW];
+#pragma unroll
+    for (int j = 0; j < MAXW; ++j) w[j] = 0;  // tag 0 is never waited for
+    const int t = threadIdx.x;
+    unsigned spins = 0;
+    while (true) {
+        bool ok = true;
+#pragma unroll
+        for (int j = 0; j < MAXW; ++j) {
+            const int i = t + T * j;
+            if (i < n && (uint32_t)(w[j] >> 32) != tag) w[j] = peek(src + index(i));
+        }
+#pragma unroll
+        for (int j = 0; j < MAXW; ++j) {
+            const int i = t + T * j;
+            if (i < n && (uint32_t)(w[j] >> 32) != tag) ok = false;
+        }
+        if (ok) break;
+        if ((++spins & 31) == 0) {
+            if (aborted(sm)) break;
+            if (wall_clock64() > deadline) {
+                __hip_atomic_store(&sm.abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                atomicOr(&st->err, 1);
+                break;
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < MAXW; ++j) {
+        const int i = t + T * j;
+        if (i < n) dst[i] = __uint_as_float((uint32_t)w[j]);
+    }
+    __syncthreads();
+    return !aborted(sm);
+}
+
+struct Linear {
+    __device__ int operator()(int i) const { return i; }
+};
+
+// ---- products -----------------------------------------------------------
+
+// One wave's four rows (SwiGLU: four gate rows and their up rows): lane l
+// of a row holds 16-byte chunks l + 16j of it and the scales of their
+// blocks, as the one-row kernel loads them.
+template <int J, int P>
+struct Rows {
+    uint4 w[P][J];
+    uint32_t ws[P][(J + 1) / 2];  // f16 scale bits, two a register
+};
+
+template <int J, int P>
+__device__ __forceinline__ void load_rows(const uint8_t* codes, const uint16_t* scales, int part_rows, int row,
+                                          Rows<J, P>& r) {
+    constexpr int K = J * 256, G = K / 32;
+    const int l = threadIdx.x & 15;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const uint8_t* src = codes + (size_t)(p * part_rows + row) * K;
+#pragma unroll
+        for (int j = 0; j < J; ++j) r.w[p][j] = load_stream(src + (size_t)(l + 16 * j) * 16);
+        const uint16_t* sc = scales + (size_t)(p * part_rows + row) * G + (l >> 1);
+#pragma unroll
+        for (int j = 0; j < J; j += 2)
+            r.ws[p][j / 2] = (uint32_t)sc[8 * j] | (j + 1 < J ? (uint32_t)sc[8 * (j + 1)] << 16 : 0u);
+    }
+}
+
+// RMSNorm factor of x (K = 256 J values in LDS) by one wave, the one-row
+// kernel's tree: every block gets the same bits.
+template <int J>
+__device__ __forceinline__ float norm_inv_wave(const float* x, float eps) {
+    constexpr int K = J * 256;
+    const int lane = threadIdx.x % WAVE;
+    float part = 0.0f;
+#pragma unroll
+    for (int i = 0; i < J; ++i) {
+        const float4 v = *(const float4*)(x + (size_t)(lane + WAVE * i) * 4);
+        part += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+    }
+    part += dpp<DPP_XOR1>(part);
+    part += dpp<DPP_XOR2>(part);
+    part += dpp<DPP_HALF_MIRROR>(part);
+    part += dpp<DPP_MIRROR>(part);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, part), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, part), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, part), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, part), 48));
+    const float sum = ((r0 + r1) + r2) + r3;
+    return 1.0f / __builtin_sqrtf(sum / (float)K + eps);
+}
+
+// The RMSNorm weights of the quantizer items a thread takes (item t + T i),
+// loaded ahead of the phase's wait.
+template <int J>
+struct NormRegs {
+    static constexpr int N = (J * 64 + T - 1) / T;
+    float4 w[N];
+};
+
+template <int J>
+__device__ __forceinline__ void load_norm(const float* norm_w, NormRegs<J>& r) {
+#pragma unroll
+    for (int i = 0; i < NormRegs<J>::N; ++i) {
+        const int item = threadIdx.x + T * i;
+        r.w[i] = item < J * 64 ? *(const float4*)(norm_w + (size_t)item * 4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+}
+
+// Trit's activation quantizer over x (K values in LDS), optionally after
+// RMSNorm x * (inv * w), into sm.xq / sm.xs; ends with a block barrier.
+template <int J>
+__device__ void quantize_block(const float* x, const NormRegs<J>* nr, Smem& sm) {
+    constexpr int ITEMS = J * 64;  // float4 items; a multiple of 64: whole waves
+    const float inv = sm.inv;
+#pragma unroll
+    for (int i = 0; i < NormRegs<J>::N; ++i) {
+        const int item = threadIdx.x + T * i;
+        if (item >= ITEMS) break;  // uniform per wave
+        float4 v = *(const float4*)(x + (size_t)item * 4);
+        if (nr) {
+            const float4 nw = nr->w[i];
+            v.x = v.x * (inv * nw.x);
+            v.y = v.y * (inv * nw.y);
+            v.z = v.z * (inv * nw.z);
+            v.w = v.w * (inv * nw.w);
+        }
+        float peak = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
+                                     __builtin_fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
+        peak = __builtin_fmaxf(peak, dpp<DPP_XOR1>(peak));
+        peak = __builtin_fmaxf(peak, dpp<DPP_XOR2>(peak));
+        peak = __builtin_fmaxf(peak, dpp<DPP_HALF_MIRROR>(peak));
+        const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+        const float q = 1.0f / scale;
+        *(uint32_t*)(sm.xq + item * 4) =
+            pack4(act_code(v.x * q), act_code(v.y * q), act_code(v.z * q), act_code(v.w * q));
+        if ((item & 7) == 0) sm.xs[item >> 3] = f16_round(scale);
+    }
+    __syncthreads();
+}
+
+// The one-row kernel's dots and f32 chain for a wave's rows; the total of
+// each row lands in lane 14 of its 16 lanes.
+template <int J, int P>
+__device__ __forceinline__ void row_chain(const Rows<J, P>& r, const Smem& sm, float (&acc)[P]) {
+    const int l = threadIdx.x & 15;
+#pragma unroll
+    for (int p = 0; p < P; ++p) acc[p] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        // Chunk j's dots (the block's two halves meet by DPP), then the
+        // chain's steps over blocks 8j .. 8j + 7.
+        const uint4 xc = *(const uint4*)(sm.xq + (l + 16 * j) * 16);
+        const float sc = sm.xs[(l >> 1) + 8 * j];
+        float df[P], prod[P];
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            int d = sdot4(r.w[p][j].x, xc.x, 0);
+            d = sdot4(r.w[p][j].y, xc.y, d);
+            d = sdot4(r.w[p][j].z, xc.z, d);
+            d = sdot4(r.w[p][j].w, xc.w, d);
+            d += dpp<DPP_XOR1>(d);
+            df[p] = (float)d;
+            prod[p] = f16_to_f32((uint16_t)(r.ws[p][j / 2] >> (16 * (j & 1)))) * sc;
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                const float in = (j == 0 && q == 0) ? 0.0f : dpp<DPP_ROR2>(acc[p]);
+                acc[p] = __builtin_fmaf(df[p], prod[p], in);
+            }
+    }
+}
+
+// ---- attention ------------------------------------------------------------
+
+// The keys of a split this lane holds: 16-lane group G takes keys
+// j0 + G + 32i, lane l16 dims [8 l16, 8 l16 + 8).
+struct KvRegs {
+    uint4 k[MAXC], v[MAXC];
+};
+
+__device__ __forceinline__ void kv_prefetch(const _Float16* K, const _Float16* V, int j0, int j1, int pos,
+                                            KvRegs& kv) {
+    const int G = threadIdx.x >> 4, l16 = threadIdx.x & 15;
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) {
+        kv.k[i] = kv.v[i] = make_uint4(0, 0, 0, 0);
+        if (j0 + 32 * i >= j1) continue;  // past the split's keys (uniform)
+        const int j = j0 + G + 32 * i;
+        const int jc = (j < j1 && j != pos) ? j : 0;  // the new key comes from the qkv product
+        kv.k[i] = *(const uint4*)(K + (size_t)jc * HD + l16 * 8);
+        kv.v[i] = *(const uint4*)(V + (size_t)jc * HD + l16 * 8);
+    }
+}
+
+__device__ __forceinline__ void unpack8(const uint4 r, float (&out)[8]) {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        out[2 * i] = f16_to_f32((uint16_t)(w[i] & 0xffff));
+        out[2 * i + 1] = f16_to_f32((uint16_t)(w[i] >> 16));
+    }
+}
+
+// Block (kv head g, split s): q/k norm and rotary of the heads of g, the
+// cache append (by the split that holds the new position), scores,
+// softmax and p.V over the split's keys, written as partials (max, sum,
+// unnormalised p.V) per query head.
+template <int GROUP>
+__device__ bool attention(const StepArgs& a, const LayerPtrs& L, int pos, uint32_t tag_in, uint32_t tag_out,
+                          Smem& sm, unsigned long long deadline) {
+    const int b = blockIdx.x, g = b / a.splits, s = b % a.splits;
+    const int t = threadIdx.x;
+    const int tk = pos + 1, span = (tk + a.splits - 1) / a.splits;
+    const int j0 = s * span, j1 = min(j0 + span, tk);
+    const int heads = a.heads, kvh = a.kvh;
+    const auto index = [g, heads, kvh](int i) {
+        if (i < GROUP * HD) return g * GROUP * HD + i;
+        if (i < (GROUP + 1) * HD) return (heads + g) * HD + (i - GROUP * HD);
+        return (heads + kvh + g) * HD + (i - (GROUP + 1) * HD);
+    };
+    // The split's cached keys and values, the q/k norm weights and the
+    // rotary values load while the qkv rows arrive.
+    KvRegs kv;
+    kv_prefetch(L.kcache + (size_t)g * a.max_pos * HD, L.vcache + (size_t)g * a.max_pos * HD, j0, j1, pos, kv);
+    const int hh = t / WAVE, i = t % WAVE;
+    float nw0 = 1.0f, nw1 = 1.0f, sn = 0.0f, cs = 1.0f;
+    if (hh <= GROUP) {
+        if (a.qk_norm) {
+            const float* nw = hh < GROUP ? L.q_norm : L.k_norm;
+            nw0 = nw[i];
+            nw1 = nw[i + HD / 2];
+        }
+        sn = a.rope_sin[(size_t)pos * (HD / 2) + i];
+        cs = a.rope_cos[(size_t)pos * (HD / 2) + i];
+    }
+    if (!gather(a.QKV, (GROUP + 2) * HD, index, tag_in, sm.qkv, sm, deadline, a.st)) return false;
+
+    // Wave hh takes head hh (the q heads, then k, then v), lane i its dims
+    // i and i + 64 (a rotary pair): Qwen3's per-head RMSNorm (a shuffle
+    // tree) and the rotary halves run in registers
+    // (src/models/parts/causal_lm.rs:428-446, src/layers.rs:136-144,303-334).
+    if (hh < GROUP + 2) {
+        float x0 = sm.qkv[hh * HD + i], x1 = sm.qkv[hh * HD + i + HD / 2];
+        if (hh <= GROUP) {
+            if (a.qk_norm) {
+                float sum = x0 * x0 + x1 * x1;
+#pragma unroll
+                for (int off = WAVE / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+                const float inv = 1.0f / __builtin_sqrtf(sum / (float)HD + a.eps);
+                x0 = x0 * (inv * nw0);
+                x1 = x1 * (inv * nw1);
+            }
+            const float ac = x0 * cs, bs = x1 * sn, bc = x1 * cs, as = x0 * sn;
+            x0 = ac - bs;
+            x1 = bc + as;
+        }
+        if (hh < GROUP) {
+            const float scale = 1.0f / __builtin_sqrtf((float)HD);
+            sm.qkv[hh * HD + i] = x0 * scale;
+            sm.qkv[hh * HD + i + HD / 2] = x1 * scale;
+        } else {
+            // The new key (wave GROUP) or value (wave GROUP + 1), as cached.
+            const int which = hh - GROUP;
+            const _Float16 c0 = (_Float16)x0, c1 = (_Float16)x1;
+            if (j0 <= pos && pos < j1) {
+                _Float16* cache = (which == 0 ? L.kcache : L.vcache) + ((size_t)g * a.max_pos + pos) * HD;
+                cache[i] = c0;
+                cache[i + HD / 2] = c1;
+            }
+            sm.kvn[which][i] = (float)c0;
+            sm.kvn[which][i + HD / 2] = (float)c1;
+        }
+    }
+    __syncthreads();
+
+    const int G = t >> 4, l16 = t & 15;
+    float q[GROUP][8], kn[8], vn[8];
+#pragma unroll
+    for (int hl = 0; hl < GROUP; ++hl)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) q[hl][u] = sm.qkv[hl * HD + l16 * 8 + u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        kn[u] = sm.kvn[0][l16 * 8 + u];
+        vn[u] = sm.kvn[1][l16 * 8 + u];
+    }
+    // Only the chunks the split's keys reach (uniform over the block).
+    const int chunks = (j1 - j0 + 31) / 32;
+    float sc[MAXC][GROUP], mx[GROUP];
+#pragma unroll
+    for (int hl = 0; hl < GROUP; ++hl) mx[hl] = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) {
+#pragma unroll
+        for (int hl = 0; hl < GROUP; ++hl) sc[i][hl] = -INFINITY;
+        if (i >= chunks) continue;
+        const int j = j0 + G + 32 * i;
+        float k8[8];
+        if (j == pos) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) k8[u] = kn[u];
+        } else {
+            unpack8(kv.k[i], k8);
+        }
+#pragma unroll
+        for (int hl = 0; hl < GROUP; ++hl) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(q[hl][u], k8[u], acc);
+            acc += dpp<DPP_XOR1>(acc);
+            acc += dpp<DPP_XOR2>(acc);
+            acc += dpp<DPP_HALF_MIRROR>(acc);
+            acc += dpp<DPP_MIRROR>(acc);
+            sc[i][hl] = j < j1 ? acc : -INFINITY;
+            mx[hl] = __builtin_fmaxf(mx[hl], sc[i][hl]);
+        }
+    }
+    // 16-lane group G holds keys j0 + G + 32i: the groups' maxima, the
+    // split's maximum, then each group's exp sums and p.V into LDS, summed
+    // over the live groups in order.
+    const int live = min(32, j1 - j0);
+    static_assert(GROUP <= 2, "the group partials hold two query heads");
+    if (l16 == 0)
+#pragma unroll
+        for (int hl = 0; hl < GROUP; ++hl) sm.gmax[G][hl] = mx[hl];
+    __syncthreads();
+    float M[GROUP];
+#pragma unroll
+    for (int hl = 0; hl < GROUP; ++hl) {
+        M[hl] = -INFINITY;
+        for (int q = 0; q < live; ++q) M[hl] = __builtin_fmaxf(M[hl], sm.gmax[q][hl]);
+    }
+    float l[GROUP], acc[GROUP][8];
+#pragma unroll
+    for (int hl = 0; hl < GROUP; ++hl) {
+        l[hl] = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc[hl][u] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) {
+        if (i >= chunks) continue;
+        const int j = j0 + G + 32 * i;
+        float v8[8];
+        if (j == pos) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v8[u] = vn[u];
+        } else {
+            unpack8(kv.v[i], v8);
+        }
+#pragma unroll
+        for (int hl = 0; hl < GROUP; ++hl) {
+            const float p = sc[i][hl] == -INFINITY ? 0.0f : exp_trit(sc[i][hl] - M[hl]);
+            l[hl] += p;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc[hl][u] = __builtin_fmaf(p, v8[u], acc[hl][u]);
+        }
+    }
+    if (G < live) {
+#pragma unroll
+        for (int hl = 0; hl < GROUP; ++hl) {
+            if (l16 == 0) sm.gl[G][hl] = l[hl];
+            *(float4*)(&sm.gpart[G][hl * HD + l16 * 8]) = make_float4(acc[hl][0], acc[hl][1], acc[hl][2], acc[hl][3]);
+            *(float4*)(&sm.gpart[G][hl * HD + l16 * 8 + 4]) = make_float4(acc[hl][4], acc[hl][5], acc[hl][6], acc[hl][7]);
+        }
+    }
+    __syncthreads();
+    if (t < GROUP * HD) {
+        const int hl = t / HD, ee = t % HD;
+        float o = 0.0f;
+        for (int q = 0; q < live; ++q) o += sm.gpart[q][hl * HD + ee];
+        const size_t base = ((size_t)(g * GROUP + hl) * a.splits + s) * (HD + 2);
+        put(a.PART + base + 2 + ee, o, tag_out);
+        if (ee == 0) {
+            float lsum = 0.0f;
+            for (int q = 0; q < live; ++q) lsum += sm.gl[q][hl];
+            put(a.PART + base, M[hl], tag_out);
+            put(a.PART + base + 1, lsum, tag_out);
+        }
+    }
+    return true;
+}
+
+// Block b merges the splits of `comb` attention outputs (one query head's
+// dims [e0, e0 + comb)) with the usual rescaling: wave e takes output e,
+// lane s split s, and the sums are shuffle trees in a fixed order.
+__device__ bool combine(const StepArgs& a, uint32_t tag_in, uint32_t tag_out, Smem& sm,
+                        unsigned long long deadline) {
+    const int o0 = blockIdx.x * a.comb, h = o0 / HD, e0 = o0 % HD, per = 2 + a.comb;
+    const int splits = a.splits;
+    const auto index = [h, e0, per, splits](int i) {
+        const int s = i / per, r = i - s * per;
+        const int base = (h * splits + s) * (HD + 2);
+        return r < 2 ? base + r : base + 2 + e0 + (r - 2);
+    };
+    if (!gather(a.PART, splits * per, index, tag_in, sm.xin, sm, deadline, a.st)) return false;
+    const int e = threadIdx.x / WAVE, s = threadIdx.x % WAVE;
+    if (e < a.comb) {
+        const bool live = s < splits;
+        const float m = live ? sm.xin[s * per] : -INFINITY;
+        float M = m;
+#pragma unroll
+        for (int off = WAVE / 2; off > 0; off >>= 1) M = __builtin_fmaxf(M, __shfl_xor(M, off));
+        const float w = m == -INFINITY ? 0.0f : exp_trit(m - M);
+        float Ls = live ? sm.xin[s * per + 1] * w : 0.0f;
+        float O = live ? sm.xin[s * per + 2 + e] * w : 0.0f;
+#pragma unroll
+        for (int off = WAVE / 2; off > 0; off >>= 1) {
+            Ls += __shfl_xor(Ls, off);
+            O += __shfl_xor(O, off);
+        }
+        if (s == 0) put(a.ATT + o0 + e, O / Ls, tag_out);
+    }
+    return true;
+}
+
+__device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+// The best (value, index) pair of a wave, in every lane: shuffle tree.
+__device__ __forceinline__ void best_of_wave(float& bv, int& bi) {
+#pragma unroll
+    for (int off = WAVE / 2; off > 0; off >>= 1) {
+        const float v = __shfl_xor(bv, off);
+        const int i = __shfl_xor(bi, off);
+        better(bv, bi, v, i);
+    }
+}
+
+template <int JD, int JO, int JF, int GROUP>
+__global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step, int pos, uint32_t tag0) {
+    __shared__ Smem sm;
+    State* st = a.st;
+    if (st->done) return;
+    const int t = threadIdx.x, w = t / WAVE, lane = t % WAVE, b = blockIdx.x;
+    const unsigned long long deadline = wall_clock64() + a.ticks;
+    if (t == 0) sm.abort = 0;
+
+    // The first layer's qkv rows stream in during the choice.
+    Rows<JD, 1> rq{};
+    const bool aq = w < a.rq / 4;
+    const int rowq = b * a.rq + 4 * w + (lane >> 4);
+    if (aq) load_rows<JD, 1>(a.layers[0].codes[0], a.layers[0].scales[0], 0, rowq, rq);
+
+    // ---- the greedy choice over the blocks' candidates -------------------
+    {
+        float best = -INFINITY;
+        int index = INT_MAX;
+        if (t < (int)gridDim.x) {
+            const float2 c = a.cand[t];
+            best = c.x;
+            index = __float_as_int(c.y);
+        }
+        best_of_wave(best, index);
+        if (lane == 0) {
+            sm.bv[w] = best;
+            sm.bi[w] = index;
+        }
+        __syncthreads();
+        float bv = sm.bv[0];
+        int bi = sm.bi[0];
+        for (int q = 1; q < NW; ++q) better(bv, bi, sm.bv[q], sm.bi[q]);
+        const int token = bi == INT_MAX ? 0 : bi;
+        bool stop = false;
+        for (int s = 0; s < st->n_stop; ++s) stop |= st->stop[s] == token;
+        const bool append = !stop && step < st->max_new;
+        const bool forward = append && step + 1 < st->max_new;
+        if (b == 0 && t == 0) {
+            st->token = token;
+            if (append) {
+                a.out[step] = token;
+                st->n_out = step + 1;
+            }
+            if (!forward) st->done = 1;
+        }
+        if (!forward) return;
+        // Dense::row of the token (src/cpu/gemm.rs:412-429) is layer 0's input.
+        const int s_count = a.d / 16;
+        for (int kk = t; kk < a.d; kk += T) {
+            const int s = kk / 16, i = kk % 16;
+            sm.xres[kk] = f16_to_f32(a.embed[((size_t)token * 16 + i) * s_count + s]);
+        }
+        __syncthreads();
+    }
+
+    const bool ao = w < a.ro / 4, agu = w < a.rgu / 4, ad = w < a.rd / 4;
+    const int rowo = b * a.ro + 4 * w + (lane >> 4);
+    const int rowgu = b * a.rgu + 4 * w + (lane >> 4);
+    const int rowd = b * a.rd + 4 * w + (lane >> 4);
+    const Linear lin;
+
+    // Each product's rows are loaded one phase ahead of it: the loads run
+    // while the block waits for that phase's inputs. (Zero-initialised so
+    // that no register stays live across the layer loop.)
+    for (int layer = 0; layer < a.n_layers; ++layer) {
+        Rows<JO, 1> ro{};
+        Rows<JD, 2> rgu{};
+        Rows<JF, 1> rd{};
+        const LayerPtrs& L = a.layers[layer];
+        // qkv: x (gathered, or the embedding) -> RMSNorm -> quantize -> rows.
+        NormRegs<JD> nq;
+        load_norm<JD>(L.norm_attn, nq);
+        if (layer > 0 && !gather(a.X, a.d, lin, tag_of(tag0, layer - 1, 5), sm.xres, sm, deadline, st)) return;
+        if (w == 0) {
+            const float inv = norm_inv_wave<JD>(sm.xres, a.eps);
+            if (lane == 0) sm.inv = inv;
+        }
+        __syncthreads();
+        quantize_block<JD>(sm.xres, &nq, sm);
+        if (aq) {
+            float acc[1];
+            row_chain<JD, 1>(rq, sm, acc);
+            if ((lane & 15) == 14) put(a.QKV + rowq, acc[0], tag_of(tag0, layer, 0));
+        }
+        // attention partials.
+        __syncthreads();
+        if (!attention<GROUP>(a, L, pos, tag_of(tag0, layer, 0), tag_of(tag0, layer, 1), sm, deadline)) return;
+        // combine; the o rows stream in meanwhile.
+        if (ao) load_rows<JO, 1>(L.codes[1], L.scales[1], 0, rowo, ro);
+        __syncthreads();
+        if (!combine(a, tag_of(tag0, layer, 1), tag_of(tag0, layer, 2), sm, deadline)) return;
+        // o + residual; the gate_up rows stream in meanwhile.
+        if (agu) load_rows<JD, 2>(L.codes[2], L.scales[2], a.ffn, rowgu, rgu);
+        __syncthreads();
+        if (!gather(a.ATT, a.qd, lin, tag_of(tag0, layer, 2), sm.xin, sm, deadline, st)) return;
+        quantize_block<JO>(sm.xin, (const NormRegs<JO>*)nullptr, sm);
+        if (ao) {
+            float acc[1];
+            row_chain<JO, 1>(ro, sm, acc);
+            if ((lane & 15) == 14) put(a.X + rowo, sm.xres[rowo] + acc[0], tag_of(tag0, layer, 3));
+        }
+        // gate_up + SwiGLU.
+        NormRegs<JD> ngu;
+        load_norm<JD>(L.norm_mlp, ngu);
+        __syncthreads();
+        if (!gather(a.X, a.d, lin, tag_of(tag0, layer, 3), sm.xres, sm, deadline, st)) return;
+        if (w == 0) {
+            const float inv = norm_inv_wave<JD>(sm.xres, a.eps);
+            if (lane == 0) sm.inv = inv;
+        }
+        __syncthreads();
+        quantize_block<JD>(sm.xres, &ngu, sm);
+        if (agu) {
+            float acc[2];
+            row_chain<JD, 2>(rgu, sm, acc);
+            if ((lane & 15) == 14) put(a.H + rowgu, silu_trit(acc[0]) * acc[1], tag_of(tag0, layer, 4));
+        }
+        // down + residual; the down rows and the next layer's qkv rows
+        // stream in meanwhile.
+        if (ad) load_rows<JF, 1>(L.codes[3], L.scales[3], 0, rowd, rd);
+        if (aq && layer + 1 < a.n_layers)
+            load_rows<JD, 1>(a.layers[layer + 1].codes[0], a.layers[layer + 1].scales[0], 0, rowq, rq);
+        __syncthreads();
+        if (!gather(a.H, a.ffn, lin, tag_of(tag0, layer, 4), sm.xin, sm, deadline, st)) return;
+        quantize_block<JF>(sm.xin, (const NormRegs<JF>*)nullptr, sm);
+        if (ad) {
+            float acc[1];
+            row_chain<JF, 1>(rd, sm, acc);
+            if ((lane & 15) == 14) put(a.X + rowd, sm.xres[rowd] + acc[0], tag_of(tag0, layer, 5));
+        }
+        __syncthreads();
+    }
+
+    // ---- final RMSNorm, the head, the block's best logit ----------------
+    // Pass p of block b covers head rows [32 (p nb + b), +32), 16-lane
+    // group r row 32 (p nb + b) + r: the blocks sweep the table together.
+    // Three passes of weights are in flight at a time, and each lane keeps
+    // the normed x values of its lane chain in registers.
+    constexpr int S8 = JD * 2;  // 16-byte loads per lane chain: d / 128
+    const int l16 = t & 15;
+    const int rows_pass = T / 16, nb = (int)gridDim.x;
+    const int passes = (a.vocab + rows_pass * nb - 1) / (rows_pass * nb);
+    auto row_of = [&](int p) { return (p * nb + b) * rows_pass + (t >> 4); };
+    // Wave w of pass p reads 4-row tile (p nb + b) 8 + w: instruction j
+    // reads the tile's 1 KB run j, in which lane 16g + i finds block j of
+    // lane chain i of the tile's row g.
+    const int tiles = (a.vocab + 3) / 4;
+    auto load_pass = [&](int p, uint4 (&wv)[S8]) {
+        const int tile = (p * nb + b) * (rows_pass / 4) + w;
+        const uint4* src = (const uint4*)(a.head + (size_t)(tile < tiles ? tile : 0) * 4 * a.d);
+#pragma unroll
+        for (int j = 0; j < S8; ++j) wv[j] = load_stream(src + j * WAVE + lane);
+    };
+    uint4 ring[3][S8];
+#pragma unroll
+    for (int q = 0; q < 3; ++q)
+        if (q < passes) load_pass(q, ring[q]);
+    float fn[(MAXD + T - 1) / T];
+#pragma unroll
+    for (int q = 0; q < (MAXD + T - 1) / T; ++q) fn[q] = t + T * q < a.d ? a.final_norm[t + T * q] : 0.0f;
+    if (!gather(a.X, a.d, lin, tag_of(tag0, a.n_layers - 1, 5), sm.xres, sm, deadline, st)) return;
+    if (w == 0) {
+        const float inv = norm_inv_wave<JD>(sm.xres, a.eps);
+        if (lane == 0) sm.inv = inv;
+    }
+    __syncthreads();
+    // RMSNorm as src/layers.rs:136-144: x * (inv * w).
+#pragma unroll
+    for (int q = 0; q < (MAXD + T - 1) / T; ++q)
+        if (t + T * q < a.d) sm.xin[t + T * q] = sm.xres[t + T * q] * (sm.inv * fn[q]);
+    __syncthreads();
+    float xr[S8 * 8];  // lane chain l16 of the normed x
+#pragma unroll
+    for (int s = 0; s < S8 * 8; ++s) xr[s] = sm.xin[16 * s + l16];
+    float best = -INFINITY;
+    int index = INT_MAX;
+    auto head_pass = [&](int p, uint4 (&wv)[S8]) {
+        // Trit's 16-lane f16 order (gemv_f16.hip): lane chain, then the tree.
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < S8; ++j) {
+            const uint32_t words[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+#pragma unroll
+            for (int hh = 0; hh < 8; ++hh) {
+                const float wf = f16_to_f32((uint16_t)(words[hh >> 1] >> ((hh & 1) * 16)));
+                acc = __builtin_fmaf(xr[j * 8 + hh], wf, acc);
+            }
+        }
+        float v = acc;
+        v = v + __shfl_xor(v, 8);
+        v = v + __shfl_xor(v, 4);
+        v = v + __shfl_xor(v, 2);
+        v = v + __shfl_xor(v, 1);
+        const int row = row_of(p);
+        if (row < a.vocab && (index == INT_MAX || v > best)) {
+            best = v;
+            index = row;
+        }
+        if (p + 3 < passes) load_pass(p + 3, wv);
+    };
+    for (int p = 0; p < passes; p += 3) {
+        head_pass(p, ring[0]);
+        if (p + 1 < passes) head_pass(p + 1, ring[1]);
+        if (p + 2 < passes) head_pass(p + 2, ring[2]);
+    }
+    // The block's first maximum: the lanes of a row group agree; waves by
+    // shuffles, then one thread over the waves.
+    best_of_wave(best, index);
+    if (lane == 0) {
+        sm.bv[w] = best;
+        sm.bi[w] = index;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float bv = sm.bv[0];
+        int bi = sm.bi[0];
+        for (int q = 1; q < NW; ++q) better(bv, bi, sm.bv[q], sm.bi[q]);
+        a.cand[b] = make_float2(bv, __int_as_float(bi));
+        if (b == 0) st->pos = pos + 1;
+    }
+}
+
+// The head's tiled layout: rows in tiles of four; in a tile, 16-byte run
+// (j, g, i) holds values 8j .. 8j + 7 of lane chain i of row g (element
+// kk = 16 s + i of the row is value s of chain i), runs ordered j, then g,
+// then i. From the lane-chain layout [row][i][s] of an F16 layer.
+__global__ void head_tile_kernel(const uint16_t* __restrict__ src, int n, int k, uint16_t* __restrict__ dst) {
+    const int s8 = k / 128;  // 8-value runs per chain
+    const size_t chunks = (size_t)n * 16 * s8;
+    for (size_t q = blockIdx.x * (size_t)blockDim.x + threadIdx.x; q < chunks; q += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = q / (16 * s8);
+        const int rem = (int)(q - r * 16 * s8), i = rem / s8, j = rem % s8;
+        const size_t to = (r / 4) * (size_t)(4 * 16 * s8) + (size_t)(j * 4 + (int)(r % 4)) * 16 + i;
+        ((uint4*)dst)[to] = ((const uint4*)src)[q];
+    }
+}
+
+// The blocks' candidates from a logits row (after a prefill), with the
+// head phase's row split.
+__global__ __launch_bounds__(256) void cand_kernel(const float* __restrict__ logits, int vocab, int rh,
+                                                   float2* __restrict__ cand) {
+    __shared__ float bv[256];
+    __shared__ int bi[256];
+    const int r0 = blockIdx.x * rh, r1 = min(r0 + rh, vocab);
+    float best = -INFINITY;
+    int index = INT_MAX;
+    for (int i = r0 + (int)threadIdx.x; i < r1; i += 256) {
+        const float v = logits[i];
+        if (index == INT_MAX || v > best) {
+            best = v;
+            index = i;
+        }
+    }
+    bv[threadIdx.x] = best;
+    bi[threadIdx.x] = index;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) better(bv[threadIdx.x], bi[threadIdx.x], bv[threadIdx.x + s], bi[threadIdx.x + s]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) cand[blockIdx.x] = make_float2(bv[0], __int_as_float(bi[0]));
+}
+
+using StepFn = void (*)(StepArgs, int, int, uint32_t);
+
+// The instantiated shapes: (d/256, heads*hd/256, ffn/256, q heads per kv head).
+StepFn step_fn(int jd, int jo, int jf, int group) {
+    if (jd == 4 && jo == 8 && jf == 12 && group == 2) return step_kernel<4, 8, 12, 2>;  // Qwen3-0.6B
+    if (jd == 4 && jo == 4 && jf == 8 && group == 2) return step_kernel<4, 4, 8, 2>;
+    return nullptr;
+}
+
+int device_blocks() {
+    int dev = 0;
+    TRIT_HIP(hipGetDevice(&dev));
+    int cus = 0;
+    TRIT_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    return cus;
+}
+
+struct Plan {
+    int blocks, splits, comb, rq, ro, rgu, rd, rh;
+    StepFn fn;
+};
+
+bool plan(const SessionImpl& S, Plan& p) {
+    const DecoderImpl& D = *S.dec;
+    const auto& c = D.c;
+    if (S.exact || S.kv32) return false;
+    if (c.head_dim != HD || c.kv_heads <= 0 || c.heads % c.kv_heads != 0) return false;
+    const int group = c.heads / c.kv_heads, qd = c.heads * HD;
+    if (c.d % 256 || qd % 256 || c.ffn % 256 || c.d > MAXD || qd > MAXK || c.ffn > MAXK) return false;
+    if (c.layers <= 0 || c.layers * PH + PH >= 256) return false;
+    p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group);
+    if (!p.fn) return false;
+    auto q8 = [](const LayerRef& L) { return (L->kind == Q8_0 || L->kind == Q4_K) && !L->bias.ptr; };
+    for (int l = 0; l < c.layers; ++l)
+        if (!q8(D.qkv[l]) || !q8(D.o[l]) || !q8(D.gate_up[l]) || !q8(D.down[l])) return false;
+    const Layer& head = D.head ? *D.head : *D.embed;
+    if (head.kind != F16 || head.k != c.d || head.bias.ptr || D.embed->kind != F16) return false;
+    p.blocks = device_blocks();
+    if (p.blocks < c.kv_heads || p.blocks % c.kv_heads) return false;
+    p.splits = p.blocks / c.kv_heads;
+    if (S.max_pos > p.splits * 32 * MAXC) return false;
+    if ((qd % p.blocks) || HD % (qd / p.blocks)) return false;
+    p.comb = qd / p.blocks;
+    if (p.splits > WAVE || p.comb > NW || p.splits * (2 + p.comb) > MAXK) return false;
+    const int nq = (c.heads + 2 * c.kv_heads) * HD;
+    auto rows = [&](int n, int& r) {
+        if (n % (4 * p.blocks)) return false;
+        r = n / p.blocks;
+        return r <= 4 * NW;
+    };
+    if (!rows(nq, p.rq) || !rows(c.d, p.ro) || !rows(c.ffn, p.rgu) || !rows(c.d, p.rd)) return false;
+    p.rh = (c.vocab + p.blocks - 1) / p.blocks;
+    return true;
+}
+
+}  // namespace
+
+bool decode_step_supported(const SessionImpl& S) {
+    Plan p;
+    return plan(S, p);
+}
+
+void decode_step_prepare(SessionImpl& S, hipStream_t s) {
+    Plan p;
+    if (!plan(S, p)) fail("decode step: the session's model does not fit the persistent step");
+    const DecoderImpl& D = *S.dec;
+    const auto& c = D.c;
+    const int nq = (c.heads + 2 * c.kv_heads) * HD, qd = c.heads * HD;
+    const size_t words = (size_t)c.d + nq + (size_t)c.heads * p.splits * (HD + 2) + qd + c.ffn;
+    if (!S.step_words.ptr) {
+        S.step_words.alloc(words * 8);
+        TRIT_HIP(hipMemsetAsync(S.step_words.ptr, 0, words * 8, s));
+        S.step_cand.alloc((size_t)p.blocks * sizeof(float2));
+        std::vector<LayerPtrs> table(c.layers);
+        for (int l = 0; l < c.layers; ++l) {
+            const LayerRef* ls[4] = {&D.qkv[l], &D.o[l], &D.gate_up[l], &D.down[l]};
+            for (int i = 0; i < 4; ++i) {
+                table[l].codes[i] = (*ls[i])->codes.as<uint8_t>();
+                table[l].scales[i] = (*ls[i])->scales.as<uint16_t>();
+            }
+            table[l].norm_attn = D.norm_attn(l);
+            table[l].norm_mlp = D.norm_mlp(l);
+            table[l].q_norm = D.q_norm(l);
+            table[l].k_norm = D.k_norm(l);
+            table[l].kcache = S.kcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * HD;
+            table[l].vcache = S.vcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * HD;
+        }
+        const Layer& head = D.head ? *D.head : *D.embed;
+        std::call_once(D.step_head_once, [&] {
+            const size_t rows = (size_t)(c.vocab + 3) / 4 * 4;
+            D.step_head.alloc(rows * c.d * 2);
+            TRIT_HIP(hipMemsetAsync(D.step_head.ptr, 0, rows * c.d * 2, s));
+            hipLaunchKernelGGL(head_tile_kernel, dim3(4096), dim3(256), 0, s, head.codes.as<uint16_t>(), c.vocab, c.d,
+                               D.step_head.as<uint16_t>());
+            TRIT_HIP(hipGetLastError());
+            TRIT_HIP(hipStreamSynchronize(s));
+        });
+        S.step_table.alloc(table.size() * sizeof(LayerPtrs));
+        TRIT_HIP(hipMemcpy(S.step_table.ptr, table.data(), table.size() * sizeof(LayerPtrs), hipMemcpyHostToDevice));
+        S.step_seq = 0;
+    }
+    if (!S.step_cand_fresh) {
+        hipLaunchKernelGGL(cand_kernel, dim3(p.blocks), dim3(256), 0, s, S.logits.as<float>(), c.vocab, p.rh,
+                           S.step_cand.as<float2>());
+        TRIT_HIP(hipGetLastError());
+    }
+}
+
+void decode_step_launch(SessionImpl& S, int step, int pos, hipStream_t s) {
+    Plan p;
+    if (!plan(S, p)) fail("decode step: the session's model does not fit the persistent step");
+    const DecoderImpl& D = *S.dec;
+    const auto& c = D.c;
+    const int nq = (c.heads + 2 * c.kv_heads) * HD, qd = c.heads * HD;
+    // Tags: launch counter in the high 24 bits, phase in the low 8. When
+    // the counter would wrap, the words start over from zero.
+    if (++S.step_seq >= (1u << 24)) {
+        const size_t words = (size_t)c.d + nq + (size_t)c.heads * p.splits * (HD + 2) + qd + c.ffn;
+        TRIT_HIP(hipMemsetAsync(S.step_words.ptr, 0, words * 8, s));
+        S.step_seq = 1;
+    }
+    const uint32_t tag0 = S.step_seq << 8;
+    StepArgs a{};
+    a.layers = S.step_table.as<LayerPtrs>();
+    a.n_layers = c.layers;
+    a.d = c.d;
+    a.qd = qd;
+    a.ffn = c.ffn;
+    a.heads = c.heads;
+    a.kvh = c.kv_heads;
+    a.vocab = c.vocab;
+    a.qk_norm = c.qk_norm;
+    a.max_pos = S.max_pos;
+    a.eps = c.eps;
+    a.embed = D.embed->codes.as<uint16_t>();
+    a.head = D.step_head.as<uint16_t>();
+    a.final_norm = D.final_norm();
+    a.rope_sin = S.rope_sin.as<float>();
+    a.rope_cos = S.rope_cos.as<float>();
+    uint64_t* w = S.step_words.as<uint64_t>();
+    a.X = w;
+    a.QKV = a.X + c.d;
+    a.PART = a.QKV + nq;
+    a.ATT = a.PART + (size_t)c.heads * p.splits * (HD + 2);
+    a.H = a.ATT + qd;
+    a.cand = S.step_cand.as<float2>();
+    a.out = S.tokens_out.as<int>();
+    a.st = S.st();
+    a.splits = p.splits;
+    a.comb = p.comb;
+    a.rq = p.rq;
+    a.ro = p.ro;
+    a.rgu = p.rgu;
+    a.rd = p.rd;
+    a.rh = p.rh;
+    int rate_khz = 0, dev = 0;
+    TRIT_HIP(hipGetDevice(&dev));
+    TRIT_HIP(hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, dev));
+    a.ticks = (unsigned long long)(rate_khz > 0 ? rate_khz : 100000) * 200ull;  // 200 ms
+    void* args[] = {&a, &step, &pos, (void*)&tag0};
+    TRIT_HIP(hipLaunchCooperativeKernel((const void*)p.fn, dim3(p.blocks), dim3(T), args, 0, s));
+}
+
+}  // namespace trit

@@ -21,27 +21,16 @@
 #include <cstring>
 
 #include "../../include/trit_hip.h"
+#include "decoder_impl.h"
 #include "device.h"
 #include "internal.h"
 
 namespace trit {
 namespace {
 
-constexpr int MAX_STOP = 64;
 constexpr int MAX_HD = 256;
 constexpr int ATT_THREADS = 256;
 
-// Device state of a session.
-struct State {
-    int pos;        // positions in the caches
-    int done;       // nonzero: the decode loop has ended
-    int n_out;      // tokens written by the loop
-    int max_new;    // loop limit
-    int n_stop;     // stop tokens
-    int token;      // the last token chosen
-    unsigned int arrived;  // blocks of the greedy choice that are done (back to 0 after)
-    int stop[MAX_STOP];
-};
 
 constexpr int CHOOSE_THREADS = 256;
 constexpr int CHOOSE_SPAN = CHOOSE_THREADS * 4;  // logits per block
@@ -924,38 +913,6 @@ __global__ void advance_kernel(State* st, int rows) {
 
 // ---- host side ------------------------------------------------------------
 
-struct DecoderImpl {
-    TritHipLmConfig c{};
-    std::vector<LayerRef> qkv, o, gate_up, down;
-    LayerRef embed, head;
-    DeviceMemory norms;  // per layer: attn[d] mlp[d] q[hd] k[hd]; then final[d]
-    size_t layer_norm_stride = 0;
-    const float* norm_attn(int l) const { return norms.as<float>() + l * layer_norm_stride; }
-    const float* norm_mlp(int l) const { return norm_attn(l) + c.d; }
-    const float* q_norm(int l) const { return norm_attn(l) + 2 * c.d; }
-    const float* k_norm(int l) const { return q_norm(l) + c.head_dim; }
-    const float* final_norm() const { return norms.as<float>() + c.layers * layer_norm_stride; }
-};
-
-struct SessionImpl {
-    std::shared_ptr<DecoderImpl> dec;
-    int max_pos = 0, flags = 0;
-    bool exact = false, kv32 = false;
-    int rows_cap = 0;
-    DeviceMemory kcache, vcache, rope_sin, rope_cos;
-    DeviceMemory x, qkv, att, hid, inv, normed, logits, state, tokens_in, tokens_out, partials;
-    DeviceMemory att_part, att_arrived;  // split attention: chunk partials, per (row, kv head) counters
-    DeviceMemory gemm_scratch;           // quantized rows of the matrix-core products
-    int max_splits = 0;
-    int host_pos = 0;
-    hipGraphExec_t graph = nullptr;
-    int graph_out_cap = 0;
-
-    ~SessionImpl() {
-        if (graph) (void)hipGraphExecDestroy(graph);
-    }
-    State* st() const { return state.as<State>(); }
-};
 
 namespace {
 
@@ -1201,6 +1158,7 @@ void arm_state(SessionImpl& S, int max_new, const int32_t* stop, int n_stop) {
     TRIT_HIP(hipMemcpy(&h, S.state.ptr, sizeof(State), hipMemcpyDeviceToHost));
     h.done = 0;
     h.n_out = 0;
+    h.err = 0;
     h.max_new = max_new;
     h.n_stop = n_stop;
     for (int i = 0; i < n_stop; ++i) h.stop[i] = stop[i];
@@ -1222,6 +1180,14 @@ void step(SessionImpl& S, hipStream_t s) {
 bool use_graph() {
     const char* v = getenv("TRIT_HIP_GRAPH");
     return !(v && v[0] == '0');
+}
+
+// Fast-mode sessions whose model fits it decode on the persistent step
+// (decode_step.hip); TRIT_HIP_STEP=0 keeps them on the per-kernel loop.
+bool use_step(const SessionImpl& S) {
+    const char* v = getenv("TRIT_HIP_STEP");
+    if (v && v[0] == '0') return false;
+    return decode_step_supported(S);
 }
 
 void build_graph(SessionImpl& S) {
@@ -1386,6 +1352,7 @@ static int prefill_common(TritHipSession* session, int n, float* logits, const i
     }
     forward(S, n, s);
     S.host_pos += n;
+    S.step_cand_fresh = false;
     read_logits(S, logits);
     return 0;
 }
@@ -1426,7 +1393,11 @@ int trit_hip_session_generate(TritHipSession* session, int max_new, const int32_
         }
         arm_state(S, max_new, stop, n_stop);
         hipStream_t s = stream();
-        if (use_graph()) {
+        if (use_step(S)) {
+            decode_step_prepare(S, s);
+            for (int i = 0; i < max_new; ++i) decode_step_launch(S, i, S.host_pos + i, s);
+            S.step_cand_fresh = true;
+        } else if (use_graph()) {
             build_graph(S);
             for (int i = 0; i < max_new; ++i) TRIT_HIP(hipGraphLaunch(S.graph, s));
         } else {
@@ -1435,6 +1406,7 @@ int trit_hip_session_generate(TritHipSession* session, int max_new, const int32_
         State h{};
         TRIT_HIP(hipMemcpyAsync(&h, S.state.ptr, sizeof(State), hipMemcpyDeviceToHost, s));
         TRIT_HIP(hipStreamSynchronize(s));
+        if (h.err) fail("generate: a decode-step block waited past its deadline (the step was abandoned)");
         TRIT_HIP(hipMemcpy(out, S.tokens_out.ptr, (size_t)h.n_out * 4, hipMemcpyDeviceToHost));
         S.host_pos = h.pos;
         return h.n_out;

@@ -1,0 +1,81 @@
+// Decoder and session structures shared by the per-kernel token loop
+// (decoder.hip) and the persistent decode step (decode_step.hip).
+#pragma once
+
+#include <memory>
+#include <mutex>
+#include <vector>
+
+#include "../../include/trit_hip.h"
+#include "internal.h"
+
+namespace trit {
+
+constexpr int MAX_STOP = 64;
+
+// Device state of a session.
+struct State {
+    int pos;        // positions in the caches
+    int done;       // nonzero: the decode loop has ended
+    int n_out;      // tokens written by the loop
+    int max_new;    // loop limit
+    int n_stop;     // stop tokens
+    int token;      // the last token chosen
+    unsigned int arrived;  // blocks of the greedy choice that are done (back to 0 after)
+    int err;               // nonzero: a decode-step block waited past its deadline
+    int stop[MAX_STOP];
+};
+
+struct DecoderImpl {
+    TritHipLmConfig c{};
+    std::vector<LayerRef> qkv, o, gate_up, down;
+    LayerRef embed, head;
+    DeviceMemory norms;  // per layer: attn[d] mlp[d] q[hd] k[hd]; then final[d]
+    size_t layer_norm_stride = 0;
+    const float* norm_attn(int l) const { return norms.as<float>() + l * layer_norm_stride; }
+    const float* norm_mlp(int l) const { return norm_attn(l) + c.d; }
+    const float* q_norm(int l) const { return norm_attn(l) + 2 * c.d; }
+    const float* k_norm(int l) const { return q_norm(l) + c.head_dim; }
+    const float* final_norm() const { return norms.as<float>() + c.layers * layer_norm_stride; }
+    // The head in the persistent step's tiled f16 layout, made on first use.
+    mutable DeviceMemory step_head;
+    mutable std::once_flag step_head_once;
+};
+
+struct SessionImpl {
+    std::shared_ptr<DecoderImpl> dec;
+    int max_pos = 0, flags = 0;
+    bool exact = false, kv32 = false;
+    int rows_cap = 0;
+    DeviceMemory kcache, vcache, rope_sin, rope_cos;
+    DeviceMemory x, qkv, att, hid, inv, normed, logits, state, tokens_in, tokens_out, partials;
+    DeviceMemory att_part, att_arrived;  // split attention: chunk partials, per (row, kv head) counters
+    DeviceMemory gemm_scratch;           // quantized rows of the matrix-core products
+    int max_splits = 0;
+    int host_pos = 0;
+    hipGraphExec_t graph = nullptr;
+    int graph_out_cap = 0;
+    // The persistent decode step: exchange words, per-block candidates of
+    // the greedy choice, per-layer pointer table; a launch counter makes
+    // each launch's exchange tags unique.
+    DeviceMemory step_words, step_cand, step_table;
+    uint32_t step_seq = 0;
+    bool step_cand_fresh = false;  // candidates newer than `logits`
+
+    ~SessionImpl() {
+        if (graph) (void)hipGraphExecDestroy(graph);
+    }
+    State* st() const { return state.as<State>(); }
+};
+
+// The persistent decode step (decode_step.hip).
+// Whether the session's model and mode run on it.
+bool decode_step_supported(const SessionImpl& S);
+// Prepares the exchange buffers and, when the last logits are newer than
+// the step's candidates, the candidates from the logits.
+void decode_step_prepare(SessionImpl& S, hipStream_t s);
+// One greedy step (choice, forward, head): launch `step` of a generate call
+// at cache position `pos`.
+void decode_step_launch(SessionImpl& S, int step, int pos, hipStream_t s);
+
+}  // namespace trit
