@@ -263,3 +263,29 @@ def test_mid_step_fast(mid, monkeypatch):
     assert a.tolist() == got.tolist()[:10]
     assert b.tolist() == got.tolist()[9:19]
     assert s3.position == 40 + 18
+
+
+def test_mid_flash_prefill(mid, monkeypatch):
+    """Prompt attention on the matrix cores (fast mode, f16 caches): logits
+    against the oracle's and the split kernel's, a 300-row prompt (several
+    64-key tiles, a partial 32-row query tile) at once and in two parts."""
+    print("case decoder mid flash prefill", flush=True)
+    w, ref, lm = mid
+    p = synth.prompt(99, 300, MID["vocab"])
+    ref.reset()
+    want = ref.forward(p)
+    s = lm.session(320, 0)
+    got = s.prefill(p)
+    parts = lm.session(320, 0)
+    parts.prefill(p[:100])
+    got_parts = parts.prefill(p[100:])
+    monkeypatch.setenv("TRIT_HIP_FLASH", "0")
+    k = lm.session(320, 0)
+    split = k.prefill(p)
+    monkeypatch.delenv("TRIT_HIP_FLASH")
+    print(f"flash vs oracle {rel(got, want):.3g}, vs split {rel(got, split):.3g}, parts {rel(got_parts, got):.3g}, "
+          f"split vs oracle {rel(split, want):.3g}", flush=True)
+    assert rel(got, want) < 5e-2
+    assert rel(got, split) < 2e-2
+    assert rel(got_parts, got) < 2e-2
+    assert int(np.argmax(got)) == int(np.argmax(split))

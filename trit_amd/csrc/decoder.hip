@@ -959,6 +959,12 @@ void ensure_rows(SessionImpl& S, int rows) {
     }
 }
 
+// TRIT_HIP_FLASH=0 keeps prompt attention on the split kernel.
+bool use_flash() {
+    const char* v = getenv("TRIT_HIP_FLASH");
+    return !(v && v[0] == '0');
+}
+
 // Integer product of `rows` rows: on the matrix cores for more than 8 rows
 // (same bits), else in launches of up to 8.
 void product(SessionImpl& S, const Layer& L, GemvArgs a, int rows, hipStream_t s, int y_stride) {
@@ -1085,6 +1091,9 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
                                S.att.as<float>(), 1, st);
         } else if (fused && (S.kv32 ? launch_decode<float>(S, l, s) : launch_decode<_Float16>(S, l, s))) {
             // One block per key/value head.
+        } else if (!fused && rows > 1 && flash_prefill_supported(S) && use_flash()) {
+            // Prompt rows (never inside the captured step): positions from the host.
+            flash_prefill(S, l, rows, S.host_pos, s);
         } else if (S.kv32) {
             launch_split<float>(S, l, rows, fused, s);
         } else {

@@ -68,6 +68,11 @@ struct SessionImpl {
     State* st() const { return state.as<State>(); }
 };
 
+// Prefill attention on the matrix cores (attention_mfma.hip): fast mode
+// with f16 caches; rows of the forward at positions pos0.., layer `layer`.
+bool flash_prefill_supported(const SessionImpl& S);
+void flash_prefill(SessionImpl& S, int layer, int rows, int pos0, hipStream_t s);
+
 // The persistent decode step (decode_step.hip).
 // Whether the session's model and mode run on it.
 bool decode_step_supported(const SessionImpl& S);
