@@ -238,6 +238,29 @@ def config_lines(H, sweeps=10):
         call_us=round(total_call_ms * 1e3, 2), tops=round(total_ops / (total_gemm_ms * 1e-3) / 1e12, 1),
         mfma_frac=round(total_ops / (total_gemm_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4), peak_tops=INT8_PEAK_TOPS,
         note="gemm_us: the MFMA kernels (event-stamped); call_us adds the activation quantization pass")
+
+    # C5 end to end: one decoder layer of the prefill's shape (hidden 2048,
+    # 16/8 heads x 128, SwiGLU 3072) over the 1564-row prompt: the MFMA
+    # products, q/k norm + rotary + cache append, causal GQA attention on
+    # the matrix cores, and the (one-row) head of a 1024-token vocabulary.
+    c5 = dict(d=2048, ffn=3072, layers=1, heads=16, kv_heads=8, head_dim=128, vocab=1024, eps=1e-6,
+              rope_base=1e6, qk_norm=1)
+    lm5 = model.build_decoder(synth.lm_weights(c5, config=5))
+    p5 = synth.prompt(5, m, c5["vocab"])
+    sess = lm5.session(m, 0)
+    sess.prefill(p5, want_logits=False)  # warm-up
+    times = []
+    for _ in range(3):
+        sess.reset()
+        t0 = time.perf_counter()
+        sess.prefill(p5, want_logits=False)
+        times.append(time.perf_counter() - t0)
+    t5 = min(times)
+    att_ops = 2 * 2 * c5["heads"] * c5["head_dim"] * (m * (m + 1) // 2)
+    out["c5_prefill_layer_1564"] = dict(
+        layer_ms=round(t5 * 1e3, 3), rows_per_s=round(m / t5, 1), attention_ops=att_ops,
+        note="one layer over 1564 rows, wall clock of the prefill call (host synchronisation included)")
+    del sess, lm5
     return out
 
 

@@ -104,6 +104,34 @@ __device__ __forceinline__ uint64_t peek(const uint64_t* p) {
     return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Reductions over a wave: DPP inside each row of 16 lanes (every lane gets
+// its row's result), then the four rows by readlane (uniform result).
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp<DPP_XOR1>(v);
+    v += dpp<DPP_XOR2>(v);
+    v += dpp<DPP_HALF_MIRROR>(v);
+    v += dpp<DPP_MIRROR>(v);
+    return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = __builtin_fmaxf(v, dpp<DPP_XOR1>(v));
+    v = __builtin_fmaxf(v, dpp<DPP_XOR2>(v));
+    v = __builtin_fmaxf(v, dpp<DPP_HALF_MIRROR>(v));
+    v = __builtin_fmaxf(v, dpp<DPP_MIRROR>(v));
+    return v;
+}
+__device__ __forceinline__ float lane_f(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    return ((lane_f(v, 0) + lane_f(v, 16)) + lane_f(v, 32)) + lane_f(v, 48);
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = row16_max(v);
+    return __builtin_fmaxf(__builtin_fmaxf(lane_f(v, 0), lane_f(v, 16)), __builtin_fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+
 __device__ __forceinline__ bool aborted(Smem& sm) {
     return __hip_atomic_load(&sm.abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0;
 }
@@ -363,9 +391,7 @@ __device__ bool attention(const StepArgs& a, const LayerPtrs& L, int pos, uint32
         float x0 = sm.qkv[hh * HD + i], x1 = sm.qkv[hh * HD + i + HD / 2];
         if (hh <= GROUP) {
             if (a.qk_norm) {
-                float sum = x0 * x0 + x1 * x1;
-#pragma unroll
-                for (int off = WAVE / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+                const float sum = wave_sum(x0 * x0 + x1 * x1);
                 const float inv = 1.0f / __builtin_sqrtf(sum / (float)HD + a.eps);
                 x0 = x0 * (inv * nw0);
                 x1 = x1 * (inv * nw1);
@@ -518,17 +544,10 @@ __device__ bool combine(const StepArgs& a, uint32_t tag_in, uint32_t tag_out, Sm
     if (e < a.comb) {
         const bool live = s < splits;
         const float m = live ? sm.xin[s * per] : -INFINITY;
-        float M = m;
-#pragma unroll
-        for (int off = WAVE / 2; off > 0; off >>= 1) M = __builtin_fmaxf(M, __shfl_xor(M, off));
+        const float M = wave_max(m);
         const float w = m == -INFINITY ? 0.0f : exp_trit(m - M);
-        float Ls = live ? sm.xin[s * per + 1] * w : 0.0f;
-        float O = live ? sm.xin[s * per + 2 + e] * w : 0.0f;
-#pragma unroll
-        for (int off = WAVE / 2; off > 0; off >>= 1) {
-            Ls += __shfl_xor(Ls, off);
-            O += __shfl_xor(O, off);
-        }
+        const float Ls = wave_sum(live ? sm.xin[s * per + 1] * w : 0.0f);
+        const float O = wave_sum(live ? sm.xin[s * per + 2 + e] * w : 0.0f);
         if (s == 0) put(a.ATT + o0 + e, O / Ls, tag_out);
     }
     return true;
@@ -542,13 +561,30 @@ __device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
 }
 
 // The best (value, index) pair of a wave, in every lane: shuffle tree.
+template <int CTRL>
+__device__ __forceinline__ void better_dpp(float& bv, int& bi) {
+    const float v = dpp<CTRL>(bv);
+    const int i = dpp<CTRL>(bi);
+    better(bv, bi, v, i);
+}
+
 __device__ __forceinline__ void best_of_wave(float& bv, int& bi) {
+    better_dpp<DPP_XOR1>(bv, bi);
+    better_dpp<DPP_XOR2>(bv, bi);
+    better_dpp<DPP_HALF_MIRROR>(bv, bi);
+    better_dpp<DPP_MIRROR>(bv, bi);
+    // The four rows' results, read before any is overwritten.
+    float v[4];
+    int i[4];
 #pragma unroll
-    for (int off = WAVE / 2; off > 0; off >>= 1) {
-        const float v = __shfl_xor(bv, off);
-        const int i = __shfl_xor(bi, off);
-        better(bv, bi, v, i);
+    for (int r = 0; r < 4; ++r) {
+        v[r] = lane_f(bv, 16 * r);
+        i[r] = __builtin_amdgcn_readlane(bi, 16 * r);
     }
+    bv = v[0];
+    bi = i[0];
+#pragma unroll
+    for (int r = 1; r < 4; ++r) better(bv, bi, v[r], i[r]);
 }
 
 template <int JD, int JO, int JF, int GROUP>
@@ -740,13 +776,16 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step, int po
                 acc = __builtin_fmaf(xr[j * 8 + hh], wf, acc);
             }
         }
+        // Lane i adds lane i - 8, - 4, - 2, - 1 of its row (rotations): in
+        // lane 0 that is the xor tree of gemv_f16.hip, bit for bit (the
+        // pairs it adds are the same sums with their operands swapped).
         float v = acc;
-        v = v + __shfl_xor(v, 8);
-        v = v + __shfl_xor(v, 4);
-        v = v + __shfl_xor(v, 2);
-        v = v + __shfl_xor(v, 1);
+        v = v + dpp<0x128>(v);
+        v = v + dpp<0x124>(v);
+        v = v + dpp<DPP_ROR2>(v);
+        v = v + dpp<0x121>(v);
         const int row = row_of(p);
-        if (row < a.vocab && (index == INT_MAX || v > best)) {
+        if (l16 == 0 && row < a.vocab && (index == INT_MAX || v > best)) {
             best = v;
             index = row;
         }
