@@ -43,6 +43,10 @@ INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 # FETCH_SIZE 3313.1 KiB x 2.0 (the scale a 256 MiB device copy gives) plus
 # WRITE_SIZE 48.0 KiB x 1.0.
 GATE_UP_TRAFFIC_BYTES = round((3313.1 * 2.0 + 48.0) * 1024)
+# HBM bytes per forward launch of the persistent decode step, from the same
+# kind of runs (profiles/decode_step_qwen3_0.6b_hbm_traffic.md): FETCH_SIZE
+# 432 963 KiB x 2.0 plus WRITE_SIZE 19 608 KiB, at positions 256..270.
+STEP_TRAFFIC_BYTES = round((432963 * 2.0 + 19608) * 1024)
 
 
 class Hip:
@@ -264,6 +268,35 @@ def config_lines(H, sweeps=10):
     return out
 
 
+def step_roofline(cfg, prompt, steps, step_ms, persistent):
+    """The decode loop's kernel: the persistent step (one launch per token)
+    timed with HIP events around its launches. Algorithmic bytes per launch:
+    every Q8_0 weight once (34 B per 32), the f16 head, the f16 keys and
+    values of the positions attended (the average over the timed tokens),
+    the embedding row and the norm weights."""
+    d, ffn, hd, L = cfg["d"], cfg["ffn"], cfg["head_dim"], cfg["layers"]
+    qkv = (cfg["heads"] + 2 * cfg["kv_heads"]) * hd
+    weights = L * (qkv * d + d * cfg["heads"] * hd + 2 * ffn * d + d * ffn) * 34 // 32
+    head = cfg["vocab"] * d * 2
+    # Launch i < steps - 1 forwards a token at position prompt + i over
+    # prompt + i + 1 keys; the last launch only makes the final choice.
+    forwards = steps - 1
+    mean_keys = prompt + (forwards - 1) / 2.0 + 1
+    kv = int(L * cfg["kv_heads"] * hd * 2 * 2 * mean_keys)
+    small = d * 2 + L * (2 * d + 2 * hd) * 4 + d * 4
+    per_launch = (weights + head + kv + small) * forwards // steps
+    launches = steps
+    avg_ms = step_ms / launches
+    achieved = per_launch / (avg_ms * 1e-3) / 1e9
+    return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                frac=round(achieved / HBM_PEAK_GBS, 4), traffic=STEP_TRAFFIC_BYTES if persistent else None,
+                kernel="step_kernel<4,8,12,2>: the persistent decode step (choice, 28 layers, head)" if persistent
+                else "the per-kernel decode step (graph replay)",
+                bytes_per_launch=per_launch, avg_us=round(avg_ms * 1e3, 3), launches=launches,
+                timing="HIP events recorded on the library's stream before the first and after the last step launch "
+                       "(trit_hip_session_generate_timed); launches include the final choice-only step")
+
+
 def cpu_baseline(w, prompt, steps):
     from oracle import oracle as O
 
@@ -338,18 +371,26 @@ def main():
 
     sess.reset()
     print("[bench] timed prefill + decode ...", file=sys.stderr, flush=True)
+    H = Hip()
     t0 = time.perf_counter()
     sess.prefill(prompt, want_logits=False)
     t_prefill = time.perf_counter() - t0
+    ev_a, ev_b = H.event(), H.event()
+    out_tokens = np.empty(args.steps, np.int32)
+    persistent = C.c_int(0)
     t0 = time.perf_counter()
-    tokens = sess.generate(args.steps)
+    n = hip.check(hip.lib().trit_hip_session_generate_timed(sess.h, args.steps, None, 0,
+                                                            out_tokens.ctypes.data_as(C.c_void_p), ev_a, ev_b,
+                                                            C.byref(persistent)))
     t_decode = time.perf_counter() - t0
+    tokens = out_tokens[:n]
+    step_ms = H.elapsed_ms(ev_a, ev_b)
     value = len(tokens) / t_decode
-    print(f"[bench] gpu decode {value:.1f} tok/s, prefill {args.prompt / t_prefill:.1f} tok/s",
-          file=sys.stderr, flush=True)
+    print(f"[bench] gpu decode {value:.1f} tok/s (device {args.steps / step_ms * 1e3:.1f}), "
+          f"prefill {args.prompt / t_prefill:.1f} tok/s", file=sys.stderr, flush=True)
+    step_roof = step_roofline(cfg, args.prompt, args.steps, step_ms, bool(persistent.value))
 
     print("[bench] roofline sweep ...", file=sys.stderr, flush=True)
-    H = Hip()
     roof = gemv_roofline(H, linears, cfg, args.sweeps)
     print(f"[bench] roofline {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}%)", file=sys.stderr, flush=True)
 
@@ -369,7 +410,8 @@ def main():
                    "ffn": 3072, "vocab": 151936, "prompt": args.prompt, "mode": args.mode,
                    "kv_cache": "f32" if args.mode == "exact" else "f16"},
         "prefill_tokens_per_s": round(args.prompt / t_prefill, 1),
-        "roofline": roof,
+        "roofline": step_roof,
+        "gemv_roofline": roof,
     }
     if configs:
         out["configs"] = configs

@@ -1380,45 +1380,59 @@ int trit_hip_session_prefill_rows(TritHipSession* session, const float* rows, in
     });
 }
 
+static int generate_common(TritHipSession* session, int max_new, const int32_t* stop, int n_stop, int32_t* out,
+                           hipEvent_t ev_start, hipEvent_t ev_stop) {
+    if (!session) fail("session is NULL");
+    SessionImpl& S = session->impl;
+    if (S.host_pos == 0) fail("generate: prefill a prompt first");
+    if (max_new <= 0) return 0;
+    if (!out) fail("generate: out is NULL");
+    if (n_stop < 0 || n_stop > MAX_STOP) fail("generate: at most 64 stop tokens");
+    if (n_stop && !stop) fail("generate: stop is NULL");
+    // The loop forwards up to max_new - 1 new tokens.
+    if (S.host_pos + max_new - 1 > S.max_pos)
+        fail("generate: " + std::to_string(max_new) + " tokens exceed the session's positions");
+    if (S.graph_out_cap < max_new) {
+        S.tokens_out.alloc((size_t)max_new * 4);
+        S.graph_out_cap = max_new;
+        if (S.graph) {
+            (void)hipGraphExecDestroy(S.graph);
+            S.graph = nullptr;
+        }
+    }
+    arm_state(S, max_new, stop, n_stop);
+    hipStream_t s = stream();
+    const bool persistent = use_step(S);
+    if (persistent) decode_step_prepare(S, s);
+    else if (use_graph()) build_graph(S);
+    if (ev_start) TRIT_HIP(hipEventRecord(ev_start, s));
+    if (persistent) {
+        for (int i = 0; i < max_new; ++i) decode_step_launch(S, i, S.host_pos + i, s);
+        S.step_cand_fresh = true;
+    } else if (use_graph()) {
+        for (int i = 0; i < max_new; ++i) TRIT_HIP(hipGraphLaunch(S.graph, s));
+    } else {
+        for (int i = 0; i < max_new; ++i) step(S, s);
+    }
+    if (ev_stop) TRIT_HIP(hipEventRecord(ev_stop, s));
+    State h{};
+    TRIT_HIP(hipMemcpyAsync(&h, S.state.ptr, sizeof(State), hipMemcpyDeviceToHost, s));
+    TRIT_HIP(hipStreamSynchronize(s));
+    if (h.err) fail("generate: a decode-step block waited past its deadline (the step was abandoned)");
+    TRIT_HIP(hipMemcpy(out, S.tokens_out.ptr, (size_t)h.n_out * 4, hipMemcpyDeviceToHost));
+    S.host_pos = h.pos;
+    return h.n_out;
+}
+
 int trit_hip_session_generate(TritHipSession* session, int max_new, const int32_t* stop, int n_stop, int32_t* out) {
+    return guard(-1, [&] { return generate_common(session, max_new, stop, n_stop, out, nullptr, nullptr); });
+}
+
+int trit_hip_session_generate_timed(TritHipSession* session, int max_new, const int32_t* stop, int n_stop,
+                                    int32_t* out, void* start_event, void* stop_event, int* persistent) {
     return guard(-1, [&] {
-        if (!session) fail("session is NULL");
-        SessionImpl& S = session->impl;
-        if (S.host_pos == 0) fail("generate: prefill a prompt first");
-        if (max_new <= 0) return 0;
-        if (!out) fail("generate: out is NULL");
-        if (n_stop < 0 || n_stop > MAX_STOP) fail("generate: at most 64 stop tokens");
-        if (n_stop && !stop) fail("generate: stop is NULL");
-        // The loop forwards up to max_new - 1 new tokens.
-        if (S.host_pos + max_new - 1 > S.max_pos)
-            fail("generate: " + std::to_string(max_new) + " tokens exceed the session's positions");
-        if (S.graph_out_cap < max_new) {
-            S.tokens_out.alloc((size_t)max_new * 4);
-            S.graph_out_cap = max_new;
-            if (S.graph) {
-                (void)hipGraphExecDestroy(S.graph);
-                S.graph = nullptr;
-            }
-        }
-        arm_state(S, max_new, stop, n_stop);
-        hipStream_t s = stream();
-        if (use_step(S)) {
-            decode_step_prepare(S, s);
-            for (int i = 0; i < max_new; ++i) decode_step_launch(S, i, S.host_pos + i, s);
-            S.step_cand_fresh = true;
-        } else if (use_graph()) {
-            build_graph(S);
-            for (int i = 0; i < max_new; ++i) TRIT_HIP(hipGraphLaunch(S.graph, s));
-        } else {
-            for (int i = 0; i < max_new; ++i) step(S, s);
-        }
-        State h{};
-        TRIT_HIP(hipMemcpyAsync(&h, S.state.ptr, sizeof(State), hipMemcpyDeviceToHost, s));
-        TRIT_HIP(hipStreamSynchronize(s));
-        if (h.err) fail("generate: a decode-step block waited past its deadline (the step was abandoned)");
-        TRIT_HIP(hipMemcpy(out, S.tokens_out.ptr, (size_t)h.n_out * 4, hipMemcpyDeviceToHost));
-        S.host_pos = h.pos;
-        return h.n_out;
+        if (persistent) *persistent = session && use_step(session->impl) ? 1 : 0;
+        return generate_common(session, max_new, stop, n_stop, out, (hipEvent_t)start_event, (hipEvent_t)stop_event);
     });
 }
 

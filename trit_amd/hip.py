@@ -62,6 +62,7 @@ def lib():
             "trit_hip_session_prefill": (i, [p, p, i, p]),
             "trit_hip_session_prefill_rows": (i, [p, p, i, p]),
             "trit_hip_session_generate": (i, [p, i, p, i, p]),
+            "trit_hip_session_generate_timed": (i, [p, i, p, i, p, p, p, p]),
             "trit_hip_session_reset": (i, [p]),
             "trit_hip_session_position": (i, [p]),
             "trit_hip_session_free": (None, [p]),
