@@ -40,6 +40,8 @@ constexpr int MAXD = 2048;     // largest d
 constexpr int MAXK = 3072;     // largest product input
 constexpr int PH = 6;          // exchange phases per layer
 
+constexpr int cmax(int x, int y) { return x > y ? x : y; }
+
 struct LayerPtrs {
     const uint8_t* codes[4];  // qkv, o, gate_up, down: Q8_0 codes n x k
     const uint16_t* scales[4];
@@ -137,43 +139,51 @@ __device__ __forceinline__ bool aborted(Smem& sm) {
 }
 
 // Waits for n exchange words tagged `tag` (word i at src[index(i)]) and
-// stores their values in dst[i]. Ends with a block barrier; false when a
-// word missed the deadline (the block then leaves the launch).
-template <typename Index>
+// stores their values in dst[i]. Wave p0 + k polls words
+// [k WAVE MW, (k + 1) WAVE MW), lane l word l + WAVE j of them (one base
+// address, constant offsets), so ceil(n / (WAVE MW)) waves from p0 poll
+// and the rest only wait at the barrier. A wave's vector memory operations
+// complete in order, so a wave that has just stored exchange words or
+// issued weight loads sees its polls late: each phase picks p0 and MW to
+// poll from waves without such work in flight (measured on the device).
+// Ends with a block barrier; false when a word missed the deadline (the
+// block then leaves the launch).
+template <int MW, typename Index>
 __device__ bool gather(const uint64_t* src, int n, Index index, uint32_t tag, float* dst, Smem& sm,
-                       unsigned long long deadline, State* st) {
-    constexpr int MAXW = MAXK / T;
-    uint64_t w[MAXW];
+                       unsigned long long deadline, State* st, int p0 = 0) {
+    const int i0 = ((int)(threadIdx.x / WAVE) - p0) * WAVE * MW + (int)(threadIdx.x % WAVE);
+    if (i0 >= 0 && i0 < n) {  // uniform per wave: whether the wave polls
+        uint64_t w[MW];
 #pragma unroll
-    for (int j = 0; j < MAXW; ++j) w[j] = 0;  // tag 0 is never waited for
-    const int t = threadIdx.x;
-    unsigned spins = 0;
-    while (true) {
-        bool ok = true;
+        for (int j = 0; j < MW; ++j) w[j] = 0;  // tag 0 is never waited for
+        unsigned spins = 0;
+        while (true) {
+            bool ok = true;
 #pragma unroll
-        for (int j = 0; j < MAXW; ++j) {
-            const int i = t + T * j;
-            if (i < n && (uint32_t)(w[j] >> 32) != tag) w[j] = peek(src + index(i));
-        }
+            for (int j = 0; j < MW; ++j) {
+                const int i = i0 + WAVE * j;
+                if (i < n && (uint32_t)(w[j] >> 32) != tag) w[j] = peek(src + index(i));
+            }
 #pragma unroll
-        for (int j = 0; j < MAXW; ++j) {
-            const int i = t + T * j;
-            if (i < n && (uint32_t)(w[j] >> 32) != tag) ok = false;
-        }
-        if (ok) break;
-        if ((++spins & 31) == 0) {
-            if (aborted(sm)) break;
-            if (wall_clock64() > deadline) {
-                __hip_atomic_store(&sm.abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                atomicOr(&st->err, 1);
-                break;
+            for (int j = 0; j < MW; ++j) {
+                const int i = i0 + WAVE * j;
+                if (i < n && (uint32_t)(w[j] >> 32) != tag) ok = false;
+            }
+            if (ok) break;
+            if ((++spins & 31) == 0) {
+                if (aborted(sm)) break;
+                if (wall_clock64() > deadline) {
+                    __hip_atomic_store(&sm.abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    atomicOr(&st->err, 1);
+                    break;
+                }
             }
         }
-    }
 #pragma unroll
-    for (int j = 0; j < MAXW; ++j) {
-        const int i = t + T * j;
-        if (i < n) dst[i] = __uint_as_float((uint32_t)w[j]);
+        for (int j = 0; j < MW; ++j) {
+            const int i = i0 + WAVE * j;
+            if (i < n) dst[i] = __uint_as_float((uint32_t)w[j]);
+        }
     }
     __syncthreads();
     return !aborted(sm);
@@ -185,29 +195,34 @@ struct Linear {
 
 // ---- products -----------------------------------------------------------
 
-// One wave's four rows (SwiGLU: four gate rows and their up rows): lane l
-// of a row holds 16-byte chunks l + 16j of it and the scales of their
-// blocks, as the one-row kernel loads them.
-template <int J, int P>
+// A wave's four rows of one product (SwiGLU: four gate rows and their up
+// rows): lane l of a row holds 16-byte chunks l + 16j of it and the scales
+// of their blocks, as the one-row kernel loads them. A wave holds one
+// product's rows at a time, so every product shares one register set:
+// N chunks and NS scale words, product (J, P) using w[p J + j] and
+// ws[p ((J + 1) / 2) + j / 2].
+template <int N, int NS>
 struct Rows {
-    uint4 w[P][J];
-    uint32_t ws[P][(J + 1) / 2];  // f16 scale bits, two a register
+    uint4 w[N];
+    uint32_t ws[NS];  // f16 scale bits, two a register
 };
 
-template <int J, int P>
+template <int J, int P, int N, int NS>
 __device__ __forceinline__ void load_rows(const uint8_t* codes, const uint16_t* scales, int part_rows, int row,
-                                          Rows<J, P>& r) {
+                                          Rows<N, NS>& r) {
+    static_assert(P * J <= N && P * ((J + 1) / 2) <= NS, "the row registers hold the product");
     constexpr int K = J * 256, G = K / 32;
     const int l = threadIdx.x & 15;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
         const uint8_t* src = codes + (size_t)(p * part_rows + row) * K;
 #pragma unroll
-        for (int j = 0; j < J; ++j) r.w[p][j] = load_stream(src + (size_t)(l + 16 * j) * 16);
+        for (int j = 0; j < J; ++j) r.w[p * J + j] = load_stream(src + (size_t)(l + 16 * j) * 16);
         const uint16_t* sc = scales + (size_t)(p * part_rows + row) * G + (l >> 1);
 #pragma unroll
         for (int j = 0; j < J; j += 2)
-            r.ws[p][j / 2] = (uint32_t)sc[8 * j] | (j + 1 < J ? (uint32_t)sc[8 * (j + 1)] << 16 : 0u);
+            r.ws[p * ((J + 1) / 2) + j / 2] =
+                (uint32_t)sc[8 * j] | (j + 1 < J ? (uint32_t)sc[8 * (j + 1)] << 16 : 0u);
     }
 }
 
@@ -286,8 +301,8 @@ __device__ void quantize_block(const float* x, const NormRegs<J>* nr, Smem& sm) 
 
 // The one-row kernel's dots and f32 chain for a wave's rows; the total of
 // each row lands in lane 14 of its 16 lanes.
-template <int J, int P>
-__device__ __forceinline__ void row_chain(const Rows<J, P>& r, const Smem& sm, float (&acc)[P]) {
+template <int J, int P, int N, int NS>
+__device__ __forceinline__ void row_chain(const Rows<N, NS>& r, const Smem& sm, float (&acc)[P]) {
     const int l = threadIdx.x & 15;
 #pragma unroll
     for (int p = 0; p < P; ++p) acc[p] = 0.0f;
@@ -300,13 +315,14 @@ __device__ __forceinline__ void row_chain(const Rows<J, P>& r, const Smem& sm, f
         float df[P], prod[P];
 #pragma unroll
         for (int p = 0; p < P; ++p) {
-            int d = sdot4(r.w[p][j].x, xc.x, 0);
-            d = sdot4(r.w[p][j].y, xc.y, d);
-            d = sdot4(r.w[p][j].z, xc.z, d);
-            d = sdot4(r.w[p][j].w, xc.w, d);
+            const uint4 wc = r.w[p * J + j];
+            int d = sdot4(wc.x, xc.x, 0);
+            d = sdot4(wc.y, xc.y, d);
+            d = sdot4(wc.z, xc.z, d);
+            d = sdot4(wc.w, xc.w, d);
             d += dpp<DPP_XOR1>(d);
             df[p] = (float)d;
-            prod[p] = f16_to_f32((uint16_t)(r.ws[p][j / 2] >> (16 * (j & 1)))) * sc;
+            prod[p] = f16_to_f32((uint16_t)(r.ws[p * ((J + 1) / 2) + j / 2] >> (16 * (j & 1)))) * sc;
         }
 #pragma unroll
         for (int q = 0; q < 8; ++q)
@@ -334,9 +350,10 @@ __device__ __forceinline__ void kv_prefetch(const _Float16* K, const _Float16* V
         kv.k[i] = kv.v[i] = make_uint4(0, 0, 0, 0);
         if (j0 + 32 * i >= j1) continue;  // past the split's keys (uniform)
         const int j = j0 + G + 32 * i;
-        const int jc = (j < j1 && j != pos) ? j : 0;  // the new key comes from the qkv product
-        kv.k[i] = *(const uint4*)(K + (size_t)jc * HD + l16 * 8);
-        kv.v[i] = *(const uint4*)(V + (size_t)jc * HD + l16 * 8);
+        if (j < j1 && j != pos) {  // the new key comes from the qkv product
+            kv.k[i] = *(const uint4*)(K + (size_t)j * HD + l16 * 8);
+            kv.v[i] = *(const uint4*)(V + (size_t)j * HD + l16 * 8);
+        }
     }
 }
 
@@ -381,7 +398,11 @@ __device__ bool attention(const StepArgs& a, const LayerPtrs& L, int pos, uint32
         sn = a.rope_sin[(size_t)pos * (HD / 2) + i];
         cs = a.rope_cos[(size_t)pos * (HD / 2) + i];
     }
-    if (!gather(a.QKV, (GROUP + 2) * HD, index, tag_in, sm.qkv, sm, deadline, a.st)) return false;
+    // One wave polls: the first whose 16-lane groups load no key and that
+    // stored no qkv value (the qkv rows sit in the last a.rq / 4 waves).
+    const int kw = (j1 - j0 + 3) / 4, nqw = a.rq / 4;
+    if (!gather<8>(a.QKV, (GROUP + 2) * HD, index, tag_in, sm.qkv, sm, deadline, a.st, kw < NW - nqw ? kw : 0))
+        return false;
 
     // Wave hh takes head hh (the q heads, then k, then v), lane i its dims
     // i and i + 64 (a rotary pair): Qwen3's per-head RMSNorm (a shuffle
@@ -531,7 +552,7 @@ __device__ bool attention(const StepArgs& a, const LayerPtrs& L, int pos, uint32
 // dims [e0, e0 + comb)) with the usual rescaling: wave e takes output e,
 // lane s split s, and the sums are shuffle trees in a fixed order.
 __device__ bool combine(const StepArgs& a, uint32_t tag_in, uint32_t tag_out, Smem& sm,
-                        unsigned long long deadline) {
+                        unsigned long long deadline, int p0) {
     const int o0 = blockIdx.x * a.comb, h = o0 / HD, e0 = o0 % HD, per = 2 + a.comb;
     const int splits = a.splits;
     const auto index = [h, e0, per, splits](int i) {
@@ -539,7 +560,9 @@ __device__ bool combine(const StepArgs& a, uint32_t tag_in, uint32_t tag_out, Sm
         const int base = (h * splits + s) * (HD + 2);
         return r < 2 ? base + r : base + 2 + e0 + (r - 2);
     };
-    if (!gather(a.PART, splits * per, index, tag_in, sm.xin, sm, deadline, a.st)) return false;
+    // The qkv waves poll: the attention partials were stored by the first
+    // waves, and the o rows are loading into the waves after gate_up's.
+    if (!gather<2>(a.PART, splits * per, index, tag_in, sm.xin, sm, deadline, a.st, NW - a.rq / 4)) return false;
     const int e = threadIdx.x / WAVE, s = threadIdx.x % WAVE;
     if (e < a.comb) {
         const bool live = s < splits;
@@ -596,11 +619,20 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step, int po
     const unsigned long long deadline = wall_clock64() + a.ticks;
     if (t == 0) sm.abort = 0;
 
-    // The first layer's qkv rows stream in during the choice.
-    Rows<JD, 1> rq{};
-    const bool aq = w < a.rq / 4;
-    const int rowq = b * a.rq + 4 * w + (lane >> 4);
-    if (aq) load_rows<JD, 1>(a.layers[0].codes[0], a.layers[0].scales[0], 0, rowq, rq);
+    // Waves by product, four rows a wave: gate_up [0, nu), o [nu, nu + no),
+    // down [nu, nu + nd), qkv [NW - nqw, NW). Each product's rows load one
+    // phase ahead of it (o during the combine's wait, gate_up during o's,
+    // down and the next layer's qkv during down's); a wave holds one
+    // product's rows at a time, so all share one register set.
+    const int nu = a.rgu / 4, no = a.ro / 4, nd = a.rd / 4, nqw = a.rq / 4;
+    // The one row register set (see Rows); the first layer's qkv rows
+    // stream in during the choice.
+    constexpr int RN = cmax(cmax(2 * JD, JO), JF);
+    constexpr int RS = cmax(cmax(2 * ((JD + 1) / 2), (JO + 1) / 2), (JF + 1) / 2);
+    Rows<RN, RS> rr{};
+    const bool aq = w >= NW - nqw;
+    const int rowq = b * a.rq + 4 * (w - (NW - nqw)) + (lane >> 4);
+    if (aq) load_rows<JD, 1>(a.layers[0].codes[0], a.layers[0].scales[0], 0, rowq, rr);
 
     // ---- the greedy choice over the blocks' candidates -------------------
     {
@@ -643,24 +675,23 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step, int po
         __syncthreads();
     }
 
-    const bool ao = w < a.ro / 4, agu = w < a.rgu / 4, ad = w < a.rd / 4;
-    const int rowo = b * a.ro + 4 * w + (lane >> 4);
+    const bool agu = w < nu, ao = w >= nu && w < nu + no, ad = w >= nu && w < nu + nd;
+    const int rowo = b * a.ro + 4 * (w - nu) + (lane >> 4);
     const int rowgu = b * a.rgu + 4 * w + (lane >> 4);
-    const int rowd = b * a.rd + 4 * w + (lane >> 4);
+    const int rowd = b * a.rd + 4 * (w - nu) + (lane >> 4);
     const Linear lin;
 
     // Each product's rows are loaded one phase ahead of it: the loads run
     // while the block waits for that phase's inputs. (Zero-initialised so
     // that no register stays live across the layer loop.)
     for (int layer = 0; layer < a.n_layers; ++layer) {
-        Rows<JO, 1> ro{};
-        Rows<JD, 2> rgu{};
-        Rows<JF, 1> rd{};
         const LayerPtrs& L = a.layers[layer];
         // qkv: x (gathered, or the embedding) -> RMSNorm -> quantize -> rows.
         NormRegs<JD> nq;
         load_norm<JD>(L.norm_attn, nq);
-        if (layer > 0 && !gather(a.X, a.d, lin, tag_of(tag0, layer - 1, 5), sm.xres, sm, deadline, st)) return;
+        // Polled by the first waves (the down rows' wave stored x).
+        if (layer > 0 && !gather<6>(a.X, a.d, lin, tag_of(tag0, layer - 1, 5), sm.xres, sm, deadline, st))
+            return;
         if (w == 0) {
             const float inv = norm_inv_wave<JD>(sm.xres, a.eps);
             if (lane == 0) sm.inv = inv;
@@ -669,31 +700,31 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step, int po
         quantize_block<JD>(sm.xres, &nq, sm);
         if (aq) {
             float acc[1];
-            row_chain<JD, 1>(rq, sm, acc);
+            row_chain<JD, 1>(rr, sm, acc);
             if ((lane & 15) == 14) put(a.QKV + rowq, acc[0], tag_of(tag0, layer, 0));
         }
         // attention partials.
         __syncthreads();
         if (!attention<GROUP>(a, L, pos, tag_of(tag0, layer, 0), tag_of(tag0, layer, 1), sm, deadline)) return;
         // combine; the o rows stream in meanwhile.
-        if (ao) load_rows<JO, 1>(L.codes[1], L.scales[1], 0, rowo, ro);
+        if (ao) load_rows<JO, 1>(L.codes[1], L.scales[1], 0, rowo, rr);
         __syncthreads();
-        if (!combine(a, tag_of(tag0, layer, 1), tag_of(tag0, layer, 2), sm, deadline)) return;
+        if (!combine(a, tag_of(tag0, layer, 1), tag_of(tag0, layer, 2), sm, deadline, nu + no)) return;
         // o + residual; the gate_up rows stream in meanwhile.
-        if (agu) load_rows<JD, 2>(L.codes[2], L.scales[2], a.ffn, rowgu, rgu);
+        if (agu) load_rows<JD, 2>(L.codes[2], L.scales[2], a.ffn, rowgu, rr);
         __syncthreads();
-        if (!gather(a.ATT, a.qd, lin, tag_of(tag0, layer, 2), sm.xin, sm, deadline, st)) return;
+        if (!gather<MAXK / T>(a.ATT, a.qd, lin, tag_of(tag0, layer, 2), sm.xin, sm, deadline, st)) return;
         quantize_block<JO>(sm.xin, (const NormRegs<JO>*)nullptr, sm);
         if (ao) {
             float acc[1];
-            row_chain<JO, 1>(ro, sm, acc);
+            row_chain<JO, 1>(rr, sm, acc);
             if ((lane & 15) == 14) put(a.X + rowo, sm.xres[rowo] + acc[0], tag_of(tag0, layer, 3));
         }
         // gate_up + SwiGLU.
         NormRegs<JD> ngu;
         load_norm<JD>(L.norm_mlp, ngu);
         __syncthreads();
-        if (!gather(a.X, a.d, lin, tag_of(tag0, layer, 3), sm.xres, sm, deadline, st)) return;
+        if (!gather<MAXK / T>(a.X, a.d, lin, tag_of(tag0, layer, 3), sm.xres, sm, deadline, st)) return;
         if (w == 0) {
             const float inv = norm_inv_wave<JD>(sm.xres, a.eps);
             if (lane == 0) sm.inv = inv;
@@ -702,20 +733,19 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step, int po
         quantize_block<JD>(sm.xres, &ngu, sm);
         if (agu) {
             float acc[2];
-            row_chain<JD, 2>(rgu, sm, acc);
+            row_chain<JD, 2>(rr, sm, acc);
             if ((lane & 15) == 14) put(a.H + rowgu, silu_trit(acc[0]) * acc[1], tag_of(tag0, layer, 4));
         }
-        // down + residual; the down rows and the next layer's qkv rows
-        // stream in meanwhile.
-        if (ad) load_rows<JF, 1>(L.codes[3], L.scales[3], 0, rowd, rd);
+        // down + residual.
+        if (ad) load_rows<JF, 1>(L.codes[3], L.scales[3], 0, rowd, rr);
         if (aq && layer + 1 < a.n_layers)
-            load_rows<JD, 1>(a.layers[layer + 1].codes[0], a.layers[layer + 1].scales[0], 0, rowq, rq);
+            load_rows<JD, 1>(a.layers[layer + 1].codes[0], a.layers[layer + 1].scales[0], 0, rowq, rr);
         __syncthreads();
-        if (!gather(a.H, a.ffn, lin, tag_of(tag0, layer, 4), sm.xin, sm, deadline, st)) return;
+        if (!gather<MAXK / T>(a.H, a.ffn, lin, tag_of(tag0, layer, 4), sm.xin, sm, deadline, st)) return;
         quantize_block<JF>(sm.xin, (const NormRegs<JF>*)nullptr, sm);
         if (ad) {
             float acc[1];
-            row_chain<JF, 1>(rd, sm, acc);
+            row_chain<JF, 1>(rr, sm, acc);
             if ((lane & 15) == 14) put(a.X + rowd, sm.xres[rowd] + acc[0], tag_of(tag0, layer, 5));
         }
         __syncthreads();
@@ -748,7 +778,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step, int po
     float fn[(MAXD + T - 1) / T];
 #pragma unroll
     for (int q = 0; q < (MAXD + T - 1) / T; ++q) fn[q] = t + T * q < a.d ? a.final_norm[t + T * q] : 0.0f;
-    if (!gather(a.X, a.d, lin, tag_of(tag0, a.n_layers - 1, 5), sm.xres, sm, deadline, st)) return;
+    if (!gather<MAXD / T>(a.X, a.d, lin, tag_of(tag0, a.n_layers - 1, 5), sm.xres, sm, deadline, st)) return;
     if (w == 0) {
         const float inv = norm_inv_wave<JD>(sm.xres, a.eps);
         if (lane == 0) sm.inv = inv;
@@ -905,6 +935,13 @@ bool plan(const SessionImpl& S, Plan& p) {
         return r <= 4 * NW;
     };
     if (!rows(nq, p.rq) || !rows(c.d, p.ro) || !rows(c.ffn, p.rgu) || !rows(c.d, p.rd)) return false;
+    // The kernel's wave ranges by product (disjoint where rows are live
+    // together) and the waves each gather polls with.
+    const int nu = p.rgu / 4, no = p.ro / 4, nd = p.rd / 4, nqw = p.rq / 4;
+    if (nu + std::max(no, nd) + nqw > NW) return false;
+    auto fits = [](int n, int p0, int mw) { return p0 + (n + WAVE * mw - 1) / (WAVE * mw) <= NW; };
+    if (!fits((group + 2) * HD, NW - nqw - 1, 8) || !fits(p.splits * (2 + p.comb), NW - nqw, 2)) return false;
+    if (!fits(c.d, 0, 6) || !fits(qd, 0, MAXK / T) || !fits(c.ffn, 0, MAXK / T)) return false;
     p.rh = (c.vocab + p.blocks - 1) / p.blocks;
     return true;
 }
