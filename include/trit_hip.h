@@ -96,7 +96,7 @@ int trit_hip_layer_f16(int n, int k, const uint16_t *weights, const float *bias,
 int trit_hip_layer_forward(const TritHipLayer *layer, const float *x, int m, int relu, float *y);
 
 /* The same on device pointers, enqueued on `stream` (a hipStream_t; NULL:
- * the library's stream), without a wait. A matrix-core product uses a
+ * the library's stream), without a wait. Products of 2 or more rows use a
  * scratch buffer of the calling thread: calls from one thread must not
  * overlap on different streams. */
 int trit_hip_layer_forward_device(const TritHipLayer *layer, const float *x, int m, int relu, float *y,
@@ -105,10 +105,13 @@ int trit_hip_layer_forward_device(const TritHipLayer *layer, const float *x, int
 /* The measurement hook (the counterpart of Trit's kernel bench timing,
  * src/cpu/v2/bench.rs:42-54): trit_hip_layer_forward_device with the
  * product kernel's launch stamped with start_event and stop_event
- * (hipEvent_t, either may be NULL) at the kernel's start and end. 1..8 rows
- * are one launch; a matrix-core product stamps its GEMM kernel (the
- * activation quantization runs before it, unstamped). Fails for more than
- * 8 rows of a layer the matrix cores do not take. */
+ * (hipEvent_t, either may be NULL) at the kernel's start and end. One row
+ * (and f16 layers) is one launch; 2..8 rows of an integer layer quantize
+ * their activations in a pass of their own first, and start_event then
+ * stamps that pass's start, so the interval covers the whole call. A
+ * matrix-core product stamps its GEMM kernel (the activation quantization
+ * runs before it, unstamped). Fails for more than 8 rows of a layer the
+ * matrix cores do not take. */
 int trit_hip_layer_forward_timed(const TritHipLayer *layer, const float *x, int m, int relu, float *y,
                                  void *stream, void *start_event, void *stop_event);
 

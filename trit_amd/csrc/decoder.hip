@@ -950,7 +950,7 @@ void ensure_rows(SessionImpl& S, int rows) {
     S.att_part.alloc((size_t)rows * c.heads * S.max_splits * (c.head_dim + 2) * 4);
     S.att_arrived.alloc((size_t)rows * c.kv_heads * 4);
     const int kmax = std::max(std::max(c.d, qd), c.ffn);
-    S.gemm_scratch.alloc(gemm_scratch_bytes(rows, kmax));
+    S.gemm_scratch.alloc(std::max(gemm_scratch_bytes(rows, kmax), gemv_scratch_bytes(8, kmax)));
     TRIT_HIP(hipMemset(S.att_arrived.ptr, 0, (size_t)rows * c.kv_heads * 4));
     S.rows_cap = rows;
     if (S.graph) {
@@ -970,6 +970,8 @@ bool use_flash() {
 void product(SessionImpl& S, const Layer& L, GemvArgs a, int rows, hipStream_t s, int y_stride) {
     a.m = rows;
     if (rows > 8 && gemm_supported(L, a)) return gemm_int(L, a, S.gemm_scratch.ptr, s);
+    a.scratch = S.gemm_scratch.ptr;
+    a.scratch_bytes = S.gemm_scratch.bytes;
     for (int r0 = 0; r0 < rows; r0 += 8) {
         GemvArgs b = a;
         b.m = rows - r0 < 8 ? rows - r0 : 8;

@@ -22,6 +22,10 @@
 #include "device.h"
 #include "internal.h"
 
+#include <algorithm>
+#include <map>
+#include <mutex>
+
 namespace trit {
 namespace {
 
@@ -37,7 +41,7 @@ struct Q8 {
     __device__ static float scale(const void* s, size_t i) { return f16_to_f32(((const uint16_t*)s)[i]); }
 };
 struct I8 {
-    static constexpr int G = 128, KPC = 16, LPG = 8, ROW_DIV = 1;
+    static constexpr int G = 128, KPC = 16, LPG = 8, ROW_DIV = 1;  // LPG: 2 or 8
     static constexpr bool HALF = false, TERN = false;
     __device__ static float scale(const void* s, size_t i) { return ((const float*)s)[i]; }
 };
@@ -58,13 +62,78 @@ struct Smem {
     float* res;    // P*R*m chain results (pair epilogue)
 };
 
-__device__ __forceinline__ size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
+__host__ __device__ __forceinline__ size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
+
+// Maximum and sum over the TPG consecutive lanes of a quantizer group
+// (TPG = 8 or 32): DPP inside rows of 16 lanes, one cross-row shuffle for
+// 32. Order-free (max, integer sums), so any lane order gives Trit's values.
+template <int TPG>
+__device__ __forceinline__ float group_max(float v) {
+    v = __builtin_fmaxf(v, dpp<DPP_XOR1>(v));
+    v = __builtin_fmaxf(v, dpp<DPP_XOR2>(v));
+    v = __builtin_fmaxf(v, dpp<DPP_HALF_MIRROR>(v));
+    if (TPG >= 16) v = __builtin_fmaxf(v, dpp<DPP_MIRROR>(v));
+    if (TPG >= 32) v = __builtin_fmaxf(v, __shfl_xor(v, 16));
+    return v;
+}
+template <int TPG>
+__device__ __forceinline__ int group_sum(int v) {
+    v += dpp<DPP_XOR1>(v);
+    v += dpp<DPP_XOR2>(v);
+    v += dpp<DPP_HALF_MIRROR>(v);
+    if (TPG >= 16) v += dpp<DPP_MIRROR>(v);
+    if (TPG >= 32) v += __shfl_xor(v, 16);
+    return v;
+}
+
+constexpr int QB = 8;  // float4 items a thread has in flight in the prologue
+
+// Where a row's activation code `col` sits in LDS (k codes a row). Ternary
+// products read 64 codes a lane (one 16-byte weight chunk): their codes are
+// stored as four planes of 16-byte pieces, piece j of chunk c at
+// (j k / 64 + c) 16, so the lanes of a wave, holding consecutive chunks,
+// read consecutive 16-byte pieces. Other kinds keep the row order.
+template <class W>
+__device__ __forceinline__ int code_pos(int col, int k) {
+    if constexpr (W::TERN) return ((col >> 4) & 3) * (k >> 2) + (col >> 6) * 16 + (col & 15);
+    return col;
+}
+
+// Trit's quantizer on one float4 item (values col .. col + 3 of a row): the
+// group's TPG lanes (consecutive, aligned) find the peak together; the
+// codes go to xq (at code_pos), and the group's first lane stores its scale
+// (f16 rounded for Q8_0) and code sum at xs[col / G], xsum[col / G]. Every
+// lane of the wave calls it (the DPP steps read neighbours); `live` lanes
+// store.
+template <class W>
+__device__ __forceinline__ void quantize_item(float4 v, bool live, int col, int k, int8_t* xq, float* xs,
+                                              int* xsum) {
+    constexpr int TPG = W::G / 4;
+    float peak = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
+                                 __builtin_fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
+    peak = group_max<TPG>(peak);
+    const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
+    const float qi = 1.0f / scale;
+    const int c0 = act_code(v.x * qi), c1 = act_code(v.y * qi);
+    const int c2 = act_code(v.z * qi), c3 = act_code(v.w * qi);
+    int sum = c0 + c1 + c2 + c3;
+    if (W::TERN) sum = group_sum<TPG>(sum);
+    if (live) {
+        *(uint32_t*)(xq + code_pos<W>(col, k)) = pack4(c0, c1, c2, c3);
+        if (col % W::G == 0) {
+            xs[col / W::G] = W::HALF ? f16_round(scale) : scale;
+            if (W::TERN) xsum[col / W::G] = sum;
+        }
+    }
+}
 
 // Quantizes the m rows of x into LDS with Trit's rule, optionally after
-// RMSNorm: x * (inv * w).
+// RMSNorm: x * (inv * w). Loads go out QB at a time, so a thread waits
+// for the caches once per batch rather than once per item.
 template <class W>
 __device__ void quantize_rows(const GemvArgs& a, int k, const Smem& sm) {
     constexpr int TPG = W::G / 4;
+    static_assert(TPG == 8 || TPG == 32, "group lanes");
     const int groups = k / W::G;
     const int m = a.m;
     if (a.norm_w) {
@@ -74,18 +143,27 @@ __device__ void quantize_rows(const GemvArgs& a, int k, const Smem& sm) {
             // A fixed tree: each wave sums 256 values of one row with
             // shuffles, one thread adds a row's wave sums in order. Every
             // block gets the same bits.
-            const int per_row = k / 256;
-            for (int base = 0; base < m * per_row; base += THREADS / WAVE) {
-                const int chunk = base + (int)(threadIdx.x / WAVE);
-                float part = 0.0f;
-                if (chunk < m * per_row) {
-                    const int row = chunk / per_row, c = chunk - row * per_row;
-                    const float4 v = *(const float4*)(a.x + (size_t)row * k + c * 256 + (threadIdx.x % WAVE) * 4);
-                    part = (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+            const int per_row = k / 256, chunks = m * per_row, nw = THREADS / WAVE;
+            const int lane = threadIdx.x % WAVE;
+            for (int base = (int)(threadIdx.x / WAVE); base < chunks; base += nw * QB) {
+                float4 v[QB];
+#pragma unroll
+                for (int q = 0; q < QB; ++q) {
+                    const int chunk = base + q * nw;
+                    if (chunk < chunks) {
+                        const int row = chunk / per_row, c = chunk - row * per_row;
+                        v[q] = *(const float4*)(a.x + (size_t)row * k + c * 256 + lane * 4);
+                    }
                 }
 #pragma unroll
-                for (int off = WAVE / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
-                if (threadIdx.x % WAVE == 0 && chunk < m * per_row) sm.red[chunk] = part;
+                for (int q = 0; q < QB; ++q) {
+                    const int chunk = base + q * nw;
+                    if (chunk >= chunks) break;  // uniform per wave
+                    float part = (v[q].x * v[q].x + v[q].y * v[q].y) + (v[q].z * v[q].z + v[q].w * v[q].w);
+#pragma unroll
+                    for (int off = WAVE / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
+                    if (lane == 0) sm.red[chunk] = part;
+                }
             }
             __syncthreads();
             if (threadIdx.x < m) {
@@ -114,43 +192,40 @@ __device__ void quantize_rows(const GemvArgs& a, int k, const Smem& sm) {
         }
         __syncthreads();
     }
+    // Items are float4s in row-major order; a group's TPG items are TPG
+    // consecutive lanes (whole waves: k % 256 == 0 is not needed, since
+    // TPG divides 64 and a row's items divide into whole groups).
     const int total = m * groups * TPG;
-    for (int base = 0; base < total; base += THREADS) {
-        const int i = base + (int)threadIdx.x;
-        const bool live = i < total;
-        const int item = live ? i : 0;
-        const int row = item / (groups * TPG);
-        const int rem = item - row * groups * TPG;
-        const int g = rem / TPG, part = rem - g * TPG;
-        const int col = g * W::G + part * 4;
-        float4 v = *(const float4*)(a.x + (size_t)row * k + col);
-        if (a.norm_w) {
-            const float inv = sm.inv[row];
-            const float4 w = *(const float4*)(a.norm_w + col);
-            v.x = v.x * (inv * w.x);
-            v.y = v.y * (inv * w.y);
-            v.z = v.z * (inv * w.z);
-            v.w = v.w * (inv * w.w);
-        }
-        float peak = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
-                                     __builtin_fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
+    const int ipr = k / 4;  // items per row
+    for (int base = 0; base < total; base += THREADS * QB) {
+        float4 v[QB], nv[QB];
 #pragma unroll
-        for (int off = TPG / 2; off > 0; off >>= 1) peak = __builtin_fmaxf(peak, __shfl_xor(peak, off));
-        const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
-        const float inv = 1.0f / scale;
-        const int c0 = act_code(v.x * inv), c1 = act_code(v.y * inv);
-        const int c2 = act_code(v.z * inv), c3 = act_code(v.w * inv);
-        int sum = c0 + c1 + c2 + c3;
-        if (W::TERN) {
-#pragma unroll
-            for (int off = TPG / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-        }
-        if (live) {
-            *(uint32_t*)(sm.xq + (size_t)row * k + col) = pack4(c0, c1, c2, c3);
-            if (part == 0) {
-                sm.xs[row * ((groups + 4) & ~3) + g] = W::HALF ? f16_round(scale) : scale;
-                if (W::TERN) sm.xsum[row * ((groups + 4) & ~3) + g] = sum;
+        for (int q = 0; q < QB; ++q) {
+            const int i = base + q * THREADS + (int)threadIdx.x;
+            v[q] = nv[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (i < total) {
+                v[q] = *(const float4*)(a.x + (size_t)i * 4);
+                if (a.norm_w) nv[q] = *(const float4*)(a.norm_w + (size_t)(i % ipr) * 4);
             }
+        }
+#pragma unroll
+        for (int q = 0; q < QB; ++q) {
+            const int i0 = base + q * THREADS;
+            if (i0 >= total) break;  // uniform across the block
+            const int i = i0 + (int)threadIdx.x;
+            const bool live = i < total;
+            const int row = live ? i / ipr : 0;
+            const int col = (live ? i - row * ipr : 0) * 4;
+            float4 x = v[q];
+            if (a.norm_w) {
+                const float inv = sm.inv[row];
+                x.x = x.x * (inv * nv[q].x);
+                x.y = x.y * (inv * nv[q].y);
+                x.z = x.z * (inv * nv[q].z);
+                x.w = x.w * (inv * nv[q].w);
+            }
+            const int gsx = (groups + 4) & ~3;
+            quantize_item<W>(x, live, col, k, sm.xq + (size_t)row * k, sm.xs + row * gsx, sm.xsum + row * gsx);
         }
     }
 }
@@ -163,7 +238,6 @@ constexpr int XI = 4;  // float4 activation items a thread holds in the one-trip
 template <class W>
 __device__ void quantize_regs(const GemvArgs& a, int k, const Smem& sm, const float4* xv, const float4* nv,
                               float inv_in) {
-    constexpr int TPG = W::G / 4;
     const int groups = k / W::G;
     const int gsx = (groups + 4) & ~3;
     const int m = a.m;
@@ -214,58 +288,152 @@ __device__ void quantize_regs(const GemvArgs& a, int k, const Smem& sm, const fl
             v.z = v.z * (inv * w.z);
             v.w = v.w * (inv * w.w);
         }
-        float peak = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
-                                     __builtin_fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
-#pragma unroll
-        for (int off = TPG / 2; off > 0; off >>= 1) peak = __builtin_fmaxf(peak, __shfl_xor(peak, off));
-        const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
-        const float inv = 1.0f / scale;
-        const int c0 = act_code(v.x * inv), c1 = act_code(v.y * inv);
-        const int c2 = act_code(v.z * inv), c3 = act_code(v.w * inv);
-        int sum = c0 + c1 + c2 + c3;
-        if (W::TERN) {
-#pragma unroll
-            for (int off = TPG / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-        }
-        if (live) {
-            *(uint32_t*)(sm.xq + (size_t)row * k + col) = pack4(c0, c1, c2, c3);
-            const int g = col / W::G;
-            if (col % W::G == 0) {
-                sm.xs[row * gsx + g] = W::HALF ? f16_round(scale) : scale;
-                if (W::TERN) sm.xsum[row * gsx + g] = sum;
-            }
-        }
+        quantize_item<W>(v, live, col, k, sm.xq + (size_t)row * k, sm.xs + row * gsx, sm.xsum + row * gsx);
     }
 }
 
+// A 16-byte weight chunk ready for its dots: ternary chunks unpacked once
+// into 16 words of four codes (word 4j + s holds the codes of inputs
+// 16j + 4s .. +3: (word j >> 2s) & 0x03030303 of the stored chunk), other
+// kinds as stored.
 template <class W>
-__device__ __forceinline__ int chunk_dot(const uint4& w, const int8_t* xq, int kc) {
+struct Chunk {
+    uint32_t v[W::TERN ? 16 : 4];
+};
+
+template <class W>
+__device__ __forceinline__ Chunk<W> chunk_codes(const uint4& w) {
+    Chunk<W> c;
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
     if constexpr (W::TERN) {
-        // 64 codes: word j holds 16 codes; (word >> 2s) & 0x03030303 are the
-        // codes of inputs 16j + 4s .. 16j + 4s + 3.
-        const uint4* xp = (const uint4*)(xq + (size_t)kc * 64);
-        int d = 0;
-        const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) c.v[4 * j + s] = (words[j] >> (2 * s)) & 0x03030303u;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c.v[j] = words[j];
+    }
+    return c;
+}
+
+// The exact i32 dot of chunk kc with one row of activation codes (xq, k
+// codes, laid out by code_pos).
+template <class W>
+__device__ __forceinline__ int chunk_dot(const Chunk<W>& c, const int8_t* xq, int kc, int k) {
+    int d = 0;
+    if constexpr (W::TERN) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint4 xv = xp[j];
-            const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-            for (int s = 0; s < 4; ++s) d = sdot4((words[j] >> (2 * s)) & 0x03030303u, xs[s], d);
+            const uint4 xv = *(const uint4*)(xq + (size_t)j * (k >> 2) + (size_t)kc * 16);
+            d = sdot4(c.v[4 * j], xv.x, d);
+            d = sdot4(c.v[4 * j + 1], xv.y, d);
+            d = sdot4(c.v[4 * j + 2], xv.z, d);
+            d = sdot4(c.v[4 * j + 3], xv.w, d);
         }
-        return d;
     } else {
         const uint4 xv = *(const uint4*)(xq + (size_t)kc * 16);
-        int d = sdot4(w.x, xv.x, 0);
-        d = sdot4(w.y, xv.y, d);
-        d = sdot4(w.z, xv.z, d);
-        d = sdot4(w.w, xv.w, d);
-        return d;
+        d = sdot4(c.v[0], xv.x, d);
+        d = sdot4(c.v[1], xv.y, d);
+        d = sdot4(c.v[2], xv.z, d);
+        d = sdot4(c.v[3], xv.w, d);
     }
+    return d;
 }
 
 // Row stride (ints) of a (row, frame) pair's group dots in LDS: 16-byte rows.
 __host__ __device__ __forceinline__ int dot_stride(int groups) { return (groups + 4) & ~3; }
+
+// Bytes of the quantized rows' image: codes m x k, then f32 scales and i32
+// code sums m x dot_stride(k / G) each, every part 16-byte aligned -- the
+// first bytes of the product kernel's LDS, in the same layout.
+__host__ __device__ __forceinline__ size_t pre_bytes(int m, int k, int G) {
+    const size_t gs = (size_t)dot_stride(k / G);
+    return align16((size_t)m * k) + 2 * align16((size_t)m * gs * 4);
+}
+
+// RMSNorm factor of one row by the whole block, with the sum trees of
+// quantize_rows (so both paths give a row the same bits); every thread
+// returns it.
+__device__ float row_inv_block(const float* x, int k, float eps, float* red) {
+    float sum = 0.0f;
+    if (k % 256 == 0) {
+        const int per_row = k / 256, nw = THREADS / WAVE, lane = threadIdx.x % WAVE;
+        for (int base = (int)(threadIdx.x / WAVE); base < per_row; base += nw * QB) {
+            float4 v[QB];
+#pragma unroll
+            for (int q = 0; q < QB; ++q)
+                if (base + q * nw < per_row) v[q] = *(const float4*)(x + (size_t)(base + q * nw) * 256 + lane * 4);
+#pragma unroll
+            for (int q = 0; q < QB; ++q) {
+                if (base + q * nw >= per_row) break;  // uniform per wave
+                float part = (v[q].x * v[q].x + v[q].y * v[q].y) + (v[q].z * v[q].z + v[q].w * v[q].w);
+#pragma unroll
+                for (int off = WAVE / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
+                if (lane == 0) red[base + q * nw] = part;
+            }
+        }
+        __syncthreads();
+        for (int c = 0; c < per_row; ++c) sum += red[c];
+    } else {
+        float part = 0.0f;
+        for (int i = threadIdx.x; i < k; i += THREADS) {
+            const float v = x[i];
+            part += v * v;
+        }
+        red[threadIdx.x] = part;
+        __syncthreads();
+        for (int st = THREADS / 2; st > 0; st >>= 1) {
+            if ((int)threadIdx.x < st) red[threadIdx.x] += red[threadIdx.x + st];
+            __syncthreads();
+        }
+        sum = red[0];
+    }
+    return 1.0f / __builtin_sqrtf(sum / (float)k + eps);
+}
+
+constexpr int PRE_ITEMS = 2;  // float4 items a thread quantizes in the quantization pass
+
+// The quantization pass for 2..8 rows: Trit's quantizer (after RMSNorm when
+// the product has one) runs once per call instead of once per product
+// block. Block (row, slice) writes items [slice THREADS PRE_ITEMS, ...) of
+// the row into the image (pre_bytes) the product kernel copies into LDS.
+template <class W>
+__global__ __launch_bounds__(THREADS) void prequant_kernel(GemvArgs a, int k, uint8_t* __restrict__ img) {
+    __shared__ float red[THREADS];
+    if (a.skip && *a.skip) return;
+    const int m = a.m, row = blockIdx.x, gs = dot_stride(k / W::G);
+    int8_t* xq = (int8_t*)img + (size_t)row * k;
+    float* xs = (float*)(img + align16((size_t)m * k)) + (size_t)row * gs;
+    int* xsum = (int*)(img + align16((size_t)m * k) + align16((size_t)m * gs * 4)) + (size_t)row * gs;
+    const float* x = a.x + (size_t)row * k;
+    const int ipr = k / 4, base = blockIdx.y * THREADS * PRE_ITEMS;
+    float4 v[PRE_ITEMS], nv[PRE_ITEMS];
+#pragma unroll
+    for (int q = 0; q < PRE_ITEMS; ++q) {
+        const int i = base + q * THREADS + (int)threadIdx.x;
+        v[q] = nv[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (i < ipr) {
+            v[q] = *(const float4*)(x + (size_t)i * 4);
+            if (a.norm_w) nv[q] = *(const float4*)(a.norm_w + (size_t)i * 4);
+        }
+    }
+    float inv = 1.0f;
+    if (a.norm_w) inv = a.norm_inv ? a.norm_inv[row] : row_inv_block(x, k, a.eps, red);
+#pragma unroll
+    for (int q = 0; q < PRE_ITEMS; ++q) {
+        if (base + q * THREADS >= ipr) break;  // uniform across the block
+        const int i = base + q * THREADS + (int)threadIdx.x;
+        float4 xv = v[q];
+        if (a.norm_w) {
+            xv.x = xv.x * (inv * nv[q].x);
+            xv.y = xv.y * (inv * nv[q].y);
+            xv.z = xv.z * (inv * nv[q].z);
+            xv.w = xv.w * (inv * nv[q].w);
+        }
+        quantize_item<W>(xv, i < ipr, i * 4, k, xq, xs, xsum);
+    }
+}
 
 template <class W, int R, int P>
 __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict__ codes,
@@ -307,7 +475,8 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
 
     const int total = rows_tile * cpr;
     uint4 w[BATCH];
-    auto load_batch = [&](int t, int base) {
+    uint4 wn[BATCH];  // the next batch, in flight while this one computes
+    auto load_into = [&](uint4 (&dst)[BATCH], int t, int base) {
         const int row0 = t * R;
 #pragma unroll
         for (int u = 0; u < BATCH; ++u) {
@@ -315,12 +484,13 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
             if (c < total) {
                 const int pr = c / cpr, kc = c - pr * cpr;
                 const int row = (pr / R) * part_rows + row0 + pr % R;
-                w[u] = load_stream(codes + (size_t)row * row_bytes + (size_t)kc * 16);
+                dst[u] = load_stream(codes + (size_t)row * row_bytes + (size_t)kc * 16);
             } else {
-                w[u] = make_uint4(0, 0, 0, 0);
+                dst[u] = make_uint4(0, 0, 0, 0);
             }
         }
     };
+    auto load_batch = [&](int t, int base) { load_into(w, t, base); };
     auto stage_scales = [&](int t) {
         const int row0 = t * R;
         for (int i = threadIdx.x; i < rows_tile * groups; i += THREADS) {
@@ -334,9 +504,32 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
     // weights and the tile's scales are all in flight before any is used.
     load_batch(tile, 0);
     const int items = m * k / 4;
-    const bool one_trip = items <= XI * THREADS && (!a.norm_w || a.norm_inv || k % 256 == 0) &&
+    const bool one_trip = !a.pre && items <= XI * THREADS && (!a.norm_w || a.norm_inv || k % 256 == 0) &&
                           rows_tile * groups <= XI * THREADS;
-    if (one_trip) {
+    if (a.pre) {
+        // The rows were quantized by the quantization pass: one copy of
+        // its image into the first bytes of LDS.
+        // Up to IB pieces a thread are in flight at once (with the tile's
+        // weight scales), so most images take one memory round trip.
+        constexpr int IB = 12;
+        const int n16 = (int)(pre_bytes(m, k, W::G) / 16);
+        const uint4* src = (const uint4*)a.pre;
+        uint4* dst = (uint4*)smem_raw;
+        for (int base = 0; base < n16; base += THREADS * IB) {
+            uint4 v[IB];
+#pragma unroll
+            for (int q = 0; q < IB; ++q) {
+                const int i = base + q * THREADS + (int)threadIdx.x;
+                if (i < n16) v[q] = src[i];
+            }
+            if (base == 0) stage_scales(tile);
+#pragma unroll
+            for (int q = 0; q < IB; ++q) {
+                const int i = base + q * THREADS + (int)threadIdx.x;
+                if (i < n16) dst[i] = v[q];
+            }
+        }
+    } else if (one_trip) {
         float4 xv[XI], nv[XI];
         float sv[XI];
 #pragma unroll
@@ -371,7 +564,8 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
     for (;;) {
         const int row0 = tile * R;
         for (int base = 0; base < total; base += THREADS * BATCH) {
-            if (base > 0) load_batch(tile, base);
+            const bool more = base + THREADS * BATCH < total;  // uniform
+            if (more) load_into(wn, tile, base + THREADS * BATCH);
 #pragma unroll
             for (int u = 0; u < BATCH; ++u) {
                 const int c0 = base + u * THREADS;
@@ -381,12 +575,19 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
                 const int cc = live ? c : 0;
                 const int pr = cc / cpr, kc = cc - pr * cpr;
                 const int g = kc / W::LPG;
+                const Chunk<W> ch = chunk_codes<W>(w[u]);
                 for (int f = 0; f < m; ++f) {
-                    int d = chunk_dot<W>(w[u], sm.xq + (size_t)f * k, kc);
-#pragma unroll
-                    for (int off = 1; off < W::LPG; off <<= 1) d += __shfl_xor(d, off);
+                    int d = chunk_dot<W>(ch, sm.xq + (size_t)f * k, kc, k);
+                    // The group's LPG lanes (2 or 8, aligned) add their dots.
+                    d += dpp<DPP_XOR1>(d);
+                    if (W::LPG >= 4) d += dpp<DPP_XOR2>(d);
+                    if (W::LPG >= 8) d += dpp<DPP_HALF_MIRROR>(d);
                     if (live && (kc % W::LPG) == 0) sm.dots[(pr * m + f) * gs + g] = d;
                 }
+            }
+            if (more) {
+#pragma unroll
+                for (int u = 0; u < BATCH; ++u) w[u] = wn[u];
             }
         }
         const int next = tile + gridDim.x;
@@ -402,6 +603,9 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
             const int* xsum = sm.xsum + f * gs;
             float acc = 0.0f;
             int g = 0;
+            // Unrolled so that later groups' loads issue ahead of the
+            // dependent FMAs (the chain itself is serial).
+#pragma unroll 4
             for (; g + 4 <= groups; g += 4) {
                 int4 d = *(const int4*)(dots + g);
                 const float4 wv = *(const float4*)(ws + g);
@@ -460,11 +664,32 @@ size_t smem_bytes(int m, int k, int G, int rows_tile) {
            al((size_t)rows_tile * m * gs * 4) + al((size_t)rows_tile * gs * 4) + al((size_t)rows_tile * m * 4);
 }
 
+// Blocks of `kernel` the device holds at once (cached per kernel and LDS
+// size).
+int resident_blocks(const void* kernel, int threads, size_t lds) {
+    static std::mutex mu;
+    static std::map<std::pair<const void*, size_t>, int> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    const auto key = std::make_pair(kernel, lds);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int per_cu = 0, dev = 0, cus = 0;
+    TRIT_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds));
+    TRIT_HIP(hipGetDevice(&dev));
+    TRIT_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    const int n = std::max(1, per_cu) * std::max(1, cus);
+    cache[key] = n;
+    return n;
+}
+
 template <class W, int R, int P>
 void launch(const Layer& L, const GemvArgs& a, hipStream_t s) {
     const int tiles = L.n / P / R;
     const size_t lds = smem_bytes(a.m, L.k, W::G, P * R);
-    const int grid = tiles < 2048 ? tiles : 2048;
+    int grid = tiles < 2048 ? tiles : 2048;
+    // With the rows quantized ahead, each block copies their image once:
+    // no more blocks than are resident together, looping over the tiles.
+    if (a.pre) grid = std::min(grid, resident_blocks((const void*)gemv_kernel<W, R, P>, THREADS, lds));
     launch_timed(a, gemv_kernel<W, R, P>, dim3(grid), dim3(THREADS), lds, s, L.codes.as<uint8_t>(),
                  (const void*)L.scales.ptr, L.bias.as<float>(), L.n, L.k, a);
     TRIT_HIP(hipGetLastError());
@@ -489,12 +714,27 @@ void dispatch_rows(const Layer& L, const GemvArgs& a, hipStream_t s) {
 }
 
 template <class W>
-void dispatch(const Layer& L, const GemvArgs& a, hipStream_t s) {
+void dispatch(const Layer& L, const GemvArgs& a0, hipStream_t s) {
+    GemvArgs a = a0;
+    // Two or more rows: quantize once in a pass of its own when the caller
+    // gave scratch for the image (a timed call then starts its interval at
+    // that pass's start).
+    if (a.m >= 2 && !a.pre && a.scratch && a.scratch_bytes >= pre_bytes(a.m, L.k, W::G)) {
+        const dim3 grid(a.m, (L.k / 4 + THREADS * PRE_ITEMS - 1) / (THREADS * PRE_ITEMS));
+        GemvArgs t = a;
+        t.ev_stop = nullptr;  // the start event, if any, stamps this pass's start
+        launch_timed(t, prequant_kernel<W>, grid, dim3(THREADS), 0, s, a, L.k, (uint8_t*)a.scratch);
+        TRIT_HIP(hipGetLastError());
+        a.pre = (const uint8_t*)a.scratch;
+        a.ev_start = nullptr;
+    }
     if (a.epilogue == EPI_SILU_PAIR) return dispatch_rows<W, 2>(L, a, s);
     return dispatch_rows<W, 1>(L, a, s);
 }
 
 }  // namespace
+
+size_t gemv_scratch_bytes(int m, int k) { return pre_bytes(m, k, 32) > pre_bytes(m, k, 128) ? pre_bytes(m, k, 32) : pre_bytes(m, k, 128); }
 
 void gemv_int(const Layer& L, const GemvArgs& a, hipStream_t s) {
     if (a.m < 1 || a.m > MAXF) fail("gemv: 1 to 8 rows per call");

@@ -119,6 +119,13 @@ struct GemvArgs {
     // Measurement: events stamped at the product kernel's start and end
     // (hipExtLaunchKernel), or null.
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
+    // Device memory the product may overwrite (scratch_bytes of it), or
+    // null: 2..8 rows then quantize in one pass of their own
+    // (gemv_scratch_bytes) instead of in every product block.
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
+    // Set by the integer products: the quantized rows' image.
+    const uint8_t* pre = nullptr;
 };
 
 // Launches `kernel`, with the start/stop events of `a` when it has them.
@@ -132,6 +139,8 @@ void launch_timed(const GemvArgs& a, K kernel, dim3 grid, dim3 block, size_t lds
 
 // Integer products (Q8_0, Q4_K, INT8, TERNARY), m <= 8.
 void gemv_int(const Layer& L, const GemvArgs& a, hipStream_t s);
+// Scratch bytes that let gemv_int quantize m rows of k inputs once.
+size_t gemv_scratch_bytes(int m, int k);
 // The one-row Q8_0 decode product (k 1024, 2048 or 3072); false when the
 // shape or kind is not one it takes.
 bool gemv_row(const Layer& L, const GemvArgs& a, hipStream_t s);

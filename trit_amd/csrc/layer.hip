@@ -110,18 +110,25 @@ thread_local Staging g_staging;
 // Rows above this many run on the matrix cores when the layer allows it.
 constexpr int GEMM_MIN_ROWS = 9;
 
+// Grows the calling thread's scratch to `need` bytes.
+void* staging_scratch(size_t need) {
+    if (g_staging.scratch.bytes < need) {
+        // Work already queued may still use the old scratch.
+        TRIT_HIP(hipDeviceSynchronize());
+        g_staging.scratch.alloc(need);
+    }
+    return g_staging.scratch.ptr;
+}
+
 // One product of m rows: the matrix-core product for many rows, else the
-// small-batch kernels in calls of up to 8 rows.
+// small-batch kernels in calls of up to 8 rows (2..8 rows of an integer
+// layer with their activations quantized once, in the scratch).
 void forward_rows(const Layer& L, GemvArgs a, int m, hipStream_t s) {
     a.m = m;
-    if (m >= GEMM_MIN_ROWS && gemm_supported(L, a)) {
-        const size_t need = gemm_scratch_bytes(m, L.k);
-        if (g_staging.scratch.bytes < need) {
-            // Work already queued may still use the old scratch.
-            TRIT_HIP(hipDeviceSynchronize());
-            g_staging.scratch.alloc(need);
-        }
-        return gemm_int(L, a, g_staging.scratch.ptr, s);
+    if (m >= GEMM_MIN_ROWS && gemm_supported(L, a)) return gemm_int(L, a, staging_scratch(gemm_scratch_bytes(m, L.k)), s);
+    if (m >= 2 && L.kind != F16) {
+        a.scratch_bytes = gemv_scratch_bytes(m < 8 ? m : 8, L.k);
+        a.scratch = staging_scratch(a.scratch_bytes);
     }
     if (a.ev_start || a.ev_stop) {
         if (m > 8) fail("timed forward: more than 8 rows of this layer take several launches");
