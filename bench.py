@@ -38,6 +38,9 @@ from trit_amd import hip, model, synth  # noqa: E402
 METRIC = "decode tokens/sec + GEMV HBM GB/s (% of peak), Qwen3-0.6B-shape Q8_0, 1 GPU"
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+# Vector ALU lane operations per second without packed math: 256 CUs x 4
+# SIMDs x 16 lanes x 2.4 GHz (one wave64 instruction per 4 cycles a SIMD).
+VALU_PEAK_TOPS = 39.32
 # HBM bytes per launch of the roofline kernel, from rocprofv3 --pmc runs of
 # `bench.py --profile-pass` (profiles/gemv_row_q8_0_6144x1024_hbm_traffic.md):
 # FETCH_SIZE 3313.1 KiB x 2.0 (the scale a 256 MiB device copy gives) plus
@@ -45,8 +48,8 @@ INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 GATE_UP_TRAFFIC_BYTES = round((3313.1 * 2.0 + 48.0) * 1024)
 # HBM bytes per forward launch of the persistent decode step, from the same
 # kind of runs (profiles/decode_step_qwen3_0.6b_hbm_traffic.md): FETCH_SIZE
-# 432 963 KiB x 2.0 plus WRITE_SIZE 19 608 KiB, at positions 256..270.
-STEP_TRAFFIC_BYTES = round((432963 * 2.0 + 19608) * 1024)
+# 432 070 KiB x 2.0 plus WRITE_SIZE 19 608 KiB, at positions 256..270.
+STEP_TRAFFIC_BYTES = round((432070 * 2.0 + 19608) * 1024)
 
 
 class Hip:
@@ -237,11 +240,18 @@ def config_lines(H, sweeps=10):
         total_call_ms += call_ms
         res[f"n{n}"] = dict(gemm_us=round(gemm_ms * 1e3, 2), call_us=round(call_ms * 1e3, 2),
                             tops=round(ops / (gemm_ms * 1e-3) / 1e12, 1))
+    # The exact group chain costs three vector operations per (row, output,
+    # 32-group): convert the i32 dot, scale product, FMA -- the bound of
+    # this bit-exact GEMM is the vector ALUs, not the matrix cores.
+    valu_ops = 3 * m * sum((2048, 6144, 2048)) * (k // 32)
     out["c5_prefill_gemm_1564x2048"] = dict(
         products=res, ops=total_ops, gemm_us=round(total_gemm_ms * 1e3, 2),
         call_us=round(total_call_ms * 1e3, 2), tops=round(total_ops / (total_gemm_ms * 1e-3) / 1e12, 1),
         mfma_frac=round(total_ops / (total_gemm_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4), peak_tops=INT8_PEAK_TOPS,
-        note="gemm_us: the MFMA kernels (event-stamped); call_us adds the activation quantization pass")
+        valu_ops=valu_ops, valu_bound_us=round(valu_ops / (VALU_PEAK_TOPS * 1e12) * 1e6, 1),
+        valu_frac=round(valu_ops / (total_gemm_ms * 1e-3) / (VALU_PEAK_TOPS * 1e12), 4),
+        note="gemm_us: the MFMA kernels (event-stamped); call_us adds the activation quantization pass; "
+             "valu_frac: the exact f32 group chain's vector operations against the vector ALU peak")
 
     # C5 end to end: one decoder layer of the prefill's shape (hidden 2048,
     # 16/8 heads x 128, SwiGLU 3072) over the 1564-row prompt: the MFMA
