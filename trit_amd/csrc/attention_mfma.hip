@@ -1,16 +1,26 @@
 // Prefill attention on the matrix cores (fast mode, f16 key/value caches):
 // causal GQA over the caches after the prompt rows were appended
-// (src/layers.rs:343-504 for the mathematics; the sums run in other orders,
-// so the values are within rounding of the exact kernel's).
+// (src/layers.rs:343-504 for the mathematics; the sums run in other orders
+// and exp is the hardware exp2, so the values are within rounding of the
+// exact kernel's).
 //
 // Block (key/value head g, query tile qt) takes query rows
 // [32 qt, 32 qt + 32) of every query head that shares g: wave 2 hl + half
 // holds 16 rows of head g*GROUP + hl. Keys stream through LDS in tiles of
-// 64 (K row-major, V transposed); per tile a wave makes its 16 x 64 scores
-// with v_mfma_f32_16x16x32_f16 (q in f16, scaled by 1/sqrt(hd)), masks the
-// keys past each row's position, updates the running max and sum
-// (flash-attention rescaling, Trit's Cephes exp) and adds P.V, P through
-// LDS in f16, with the same instruction. The output is O / sum in f32.
+// 64 (K row-major, V transposed), each tile loaded into registers while
+// the previous one computes; the blocks with the longest causal rows start
+// first.
+//
+// The wave works on transposed products, so that the probabilities never
+// leave registers: S^T = K Q^T (v_mfma_f32_16x16x32_f16 with the keys as
+// rows) gives lane l the scores of query l % 16 for keys 4 (l / 16) + r of
+// each 16-key subtile; after the mask and the online softmax (running max
+// and sum per query, q pre-scaled by log2(e) / sqrt(hd)) those values,
+// converted to f16, are already the B operand of O^T = V^T P^T for a K
+// step of 32 keys taken in the order
+//   slot 8 j + i -> key 4 j + i (i < 4), 16 + 4 j + (i - 4) (i >= 4),
+// and the A operand reads V^T rows in that same order (two 8-byte pieces).
+// Lane l ends with O^T[16 n + 4 (l / 16) + r][query l % 16].
 //
 // Lane layouts of the 16x16x32 f16 instruction (checked on the device): an
 // operand lane l holds row (or column) l % 16, elements 8 (l / 16) .. +7 of
@@ -22,6 +32,7 @@ namespace trit {
 namespace {
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int HD = 128;
@@ -29,7 +40,6 @@ constexpr int QT = 32;      // query rows per block and head
 constexpr int KT = 64;      // keys per tile
 constexpr int KS = HD + 8;  // LDS row stride of K, in halves
 constexpr int VS = KT + 8;  // LDS row stride of V^T
-constexpr int PS = KT + 8;  // LDS row stride of P
 
 template <int GROUP>
 __global__ __launch_bounds__(GROUP * 128) void flash_prefill_kernel(const float* __restrict__ qkv, int stride,
@@ -38,47 +48,44 @@ __global__ __launch_bounds__(GROUP * 128) void flash_prefill_kernel(const float*
                                                                     const _Float16* __restrict__ vcache, int max_pos,
                                                                     float* __restrict__ out, int qd) {
     constexpr int NT = GROUP * 128;
+    constexpr int KP = KT * HD / 8;          // 16-byte pieces of a K tile
+    constexpr int KPT = (KP + NT - 1) / NT;  // a thread's K pieces
+    constexpr int VI = (KT / 4) * (HD / 8);  // V items: 4 keys x 8 dims
+    constexpr int VPT = (VI + NT - 1) / NT;  // a thread's V items
     __shared__ __align__(16) _Float16 Ks[KT * KS];
     __shared__ __align__(16) _Float16 Vt[HD * VS];
-    __shared__ __align__(16) _Float16 Ps[GROUP * 2][16 * PS];
-    const int g = blockIdx.x, qt = blockIdx.y;
+    const int g = blockIdx.x, qt = gridDim.y - 1 - blockIdx.y;
     const int t = threadIdx.x, w = t / WAVE, l = t % WAVE;
     const int hl = w / 2, half = w % 2, h = g * GROUP + hl;
     const int r0 = qt * QT + half * 16;  // the wave's first query row
     const int lr = l % 16, lq = l / 16;
+    const int row = r0 + lr;                        // this lane's query
+    const int seen = row < rows ? pos0 + row : -1;  // the last key it sees
 
-    // Q fragments: row r0 + lr, dims 32 ks + 8 lq + i.
-    const float scale = 1.0f / __builtin_sqrtf((float)HD);
+    // Q^T fragments (B operand): query lr, dims 32 ks + 8 lq + i, scaled by
+    // log2(e) / sqrt(hd) so that the scores are exp2 exponents.
+    const float scale = 1.4426950408889634f / __builtin_sqrtf((float)HD);
     v8h qf[4];
-    {
-        const int row = r0 + lr;
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), b = a;
-            if (row < rows) {
-                const float* src = qkv + (size_t)row * stride + (size_t)h * HD + 32 * ks + 8 * lq;
-                a = *(const float4*)src;
-                b = *(const float4*)(src + 4);
-            }
-            qf[ks][0] = (_Float16)(a.x * scale);
-            qf[ks][1] = (_Float16)(a.y * scale);
-            qf[ks][2] = (_Float16)(a.z * scale);
-            qf[ks][3] = (_Float16)(a.w * scale);
-            qf[ks][4] = (_Float16)(b.x * scale);
-            qf[ks][5] = (_Float16)(b.y * scale);
-            qf[ks][6] = (_Float16)(b.z * scale);
-            qf[ks][7] = (_Float16)(b.w * scale);
+    for (int ks = 0; ks < 4; ++ks) {
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), b = a;
+        if (row < rows) {
+            const float* src = qkv + (size_t)row * stride + (size_t)h * HD + 32 * ks + 8 * lq;
+            a = *(const float4*)src;
+            b = *(const float4*)(src + 4);
         }
+        qf[ks][0] = (_Float16)(a.x * scale);
+        qf[ks][1] = (_Float16)(a.y * scale);
+        qf[ks][2] = (_Float16)(a.z * scale);
+        qf[ks][3] = (_Float16)(a.w * scale);
+        qf[ks][4] = (_Float16)(b.x * scale);
+        qf[ks][5] = (_Float16)(b.y * scale);
+        qf[ks][6] = (_Float16)(b.z * scale);
+        qf[ks][7] = (_Float16)(b.w * scale);
     }
 
-    // Running max and sum of rows 4 lq + r; output columns n*16 + lr.
-    float m[4], lsum[4];
-    v4f o[8];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        m[r] = -INFINITY;
-        lsum[r] = 0.0f;
-    }
+    float m = -INFINITY, lsum = 0.0f;  // of query lr (the same in its 4 lanes)
+    v4f o[8];                          // O^T rows 16 n + 4 lq + r, column lr
 #pragma unroll
     for (int n = 0; n < 8; ++n) o[n] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
@@ -87,101 +94,134 @@ __global__ __launch_bounds__(GROUP * 128) void flash_prefill_kernel(const float*
     const int tiles = (kend + KT - 1) / KT;
     const _Float16* K = kcache + (size_t)g * max_pos * HD;
     const _Float16* V = vcache + (size_t)g * max_pos * HD;
+
+    // Tile loads, one tile ahead: K piece u = key u / 16, dims 8 (u % 16)..;
+    // V item u = keys 4 (u / 16) .. +3, dims 8 (u % 16) .. (keys past kend
+    // read key 0: in bounds, masked in the scores).
+    uint4 kr[KPT], vr[VPT][4];
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) kr[i] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) vr[i][q] = make_uint4(0, 0, 0, 0);
+#define TRIT_FETCH(KT_)                                                                                     \
+    do {                                                                                                    \
+        _Pragma("unroll") for (int i = 0; i < KPT; ++i) {                                                   \
+            const int u = t + NT * i;                                                                       \
+            if (u < KP) {                                                                                   \
+                const int j = (KT_) * KT + u / (HD / 8);                                                    \
+                kr[i] = *(const uint4*)(K + (size_t)(j < kend ? j : 0) * HD + (u % (HD / 8)) * 8);          \
+            }                                                                                               \
+        }                                                                                                   \
+        _Pragma("unroll") for (int i = 0; i < VPT; ++i) {                                                   \
+            const int u = t + NT * i;                                                                       \
+            if (u < VI) {                                                                                   \
+                _Pragma("unroll") for (int q = 0; q < 4; ++q) {                                             \
+                    const int j = (KT_) * KT + 4 * (u / (HD / 8)) + q;                                      \
+                    vr[i][q] = *(const uint4*)(V + (size_t)(j < kend ? j : 0) * HD + (u % (HD / 8)) * 8);   \
+                }                                                                                           \
+            }                                                                                               \
+        }                                                                                                   \
+    } while (0)
+
+    TRIT_FETCH(0);
     for (int kt = 0; kt < tiles; ++kt) {
         __syncthreads();  // the previous tile's K, V^T reads are done
-        // K: 16 threads a key (coalesced 256-byte rows).
-        for (int u = t; u < KT * HD / 8; u += NT) {
-            const int key = u / (HD / 8), c8 = u % (HD / 8);
-            const int j = kt * KT + key;
-            const uint4 kv = *(const uint4*)(K + (size_t)(j < kend ? j : 0) * HD + c8 * 8);
-            *(uint4*)(Ks + key * KS + c8 * 8) = kv;
-        }
-        // V^T: 64 threads a chunk column (consecutive keys write consecutive halves).
-        for (int u = t; u < KT * HD / 8; u += NT) {
-            const int key = u % KT, c8 = u / KT;
-            const int j = kt * KT + key;
-            const uint4 vv = *(const uint4*)(V + (size_t)(j < kend ? j : 0) * HD + c8 * 8);
-            const uint32_t wds[4] = {vv.x, vv.y, vv.z, vv.w};
+        // K row-major; V transposed: a thread's four keys' halves of dim d
+        // go to Vt[d][4 kq ..] as one 8-byte store (halves paired by byte
+        // perms: low halves of word d / 2 for even d, high for odd).
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint16_t bits = (uint16_t)(wds[i >> 1] >> ((i & 1) * 16));
-                Vt[(c8 * 8 + i) * VS + key] = __builtin_bit_cast(_Float16, bits);
+        for (int i = 0; i < KPT; ++i) {
+            const int u = t + NT * i;
+            if (u < KP) *(uint4*)(Ks + (u / (HD / 8)) * KS + (u % (HD / 8)) * 8) = kr[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int u = t + NT * i;
+            if (u < VI) {
+                const int kq = u / (HD / 8), c8 = u % (HD / 8);
+                const uint32_t k0[4] = {vr[i][0].x, vr[i][0].y, vr[i][0].z, vr[i][0].w};
+                const uint32_t k1[4] = {vr[i][1].x, vr[i][1].y, vr[i][1].z, vr[i][1].w};
+                const uint32_t k2[4] = {vr[i][2].x, vr[i][2].y, vr[i][2].z, vr[i][2].w};
+                const uint32_t k3[4] = {vr[i][3].x, vr[i][3].y, vr[i][3].z, vr[i][3].w};
+#pragma unroll
+                for (int d = 0; d < 8; ++d) {
+                    const uint32_t sel = (d & 1) ? 0x07060302u : 0x05040100u;
+                    uint2 v;
+                    v.x = __builtin_amdgcn_perm(k1[d / 2], k0[d / 2], sel);
+                    v.y = __builtin_amdgcn_perm(k3[d / 2], k2[d / 2], sel);
+                    *(uint2*)(Vt + (c8 * 8 + d) * VS + 4 * kq) = v;
+                }
             }
         }
         __syncthreads();
+        if (kt + 1 < tiles) TRIT_FETCH(kt + 1);  // lands while this tile computes
 
-        // Scores: 4 key subtiles of 16.
+        // S^T for 4 subtiles of 16 keys: lane holds keys 16 sub + 4 lq + r.
         v4f s[4];
 #pragma unroll
         for (int sub = 0; sub < 4; ++sub) {
             s[sub] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const v8h kb = *(const v8h*)(Ks + (sub * 16 + lr) * KS + 32 * ks + 8 * lq);
-                s[sub] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qf[ks], kb, s[sub], 0, 0, 0);
+                const v8h ka = *(const v8h*)(Ks + (sub * 16 + lr) * KS + 32 * ks + 8 * lq);
+                s[sub] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qf[ks], s[sub], 0, 0, 0);
             }
         }
-        // Mask, running max, exp, running sum, rescale.
-        float p[4][4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = r0 + 4 * lq + r;
-            const int seen = row < rows ? pos0 + row : -1;  // last key the row sees
-            float mt = -INFINITY;
-#pragma unroll
-            for (int sub = 0; sub < 4; ++sub) {
-                const int key = kt * KT + sub * 16 + lr;
-                if (key > seen) s[sub][r] = -INFINITY;
-                mt = __builtin_fmaxf(mt, s[sub][r]);
-            }
-            mt = __builtin_fmaxf(mt, __shfl_xor(mt, 1));
-            mt = __builtin_fmaxf(mt, __shfl_xor(mt, 2));
-            mt = __builtin_fmaxf(mt, __shfl_xor(mt, 4));
-            mt = __builtin_fmaxf(mt, __shfl_xor(mt, 8));
-            const float mn = __builtin_fmaxf(m[r], mt);
-            const float alpha = (m[r] == -INFINITY) ? 0.0f : exp_trit(m[r] - mn);
-            float rs = 0.0f;
-#pragma unroll
-            for (int sub = 0; sub < 4; ++sub) {
-                p[sub][r] = s[sub][r] == -INFINITY ? 0.0f : exp_trit(s[sub][r] - mn);
-                rs += p[sub][r];
-            }
-            rs += __shfl_xor(rs, 1);
-            rs += __shfl_xor(rs, 2);
-            rs += __shfl_xor(rs, 4);
-            rs += __shfl_xor(rs, 8);
-            lsum[r] = __builtin_fmaf(lsum[r], alpha, rs);
-            m[r] = mn;
-#pragma unroll
-            for (int n = 0; n < 8; ++n) o[n][r] *= alpha;
-        }
-        // P (16 x 64, f16) through this wave's LDS rows, read back as A fragments.
-        _Float16* P = Ps[w];
+        // Mask, the tile's maximum for the query (its 16 values here, then
+        // the lanes lr + 16 j), the running max and sum, rescale.
+        float mt = -INFINITY;
 #pragma unroll
         for (int sub = 0; sub < 4; ++sub)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) P[(4 * lq + r) * PS + sub * 16 + lr] = (_Float16)p[sub][r];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            for (int r = 0; r < 4; ++r) {
+                const int key = kt * KT + sub * 16 + 4 * lq + r;
+                if (key > seen) s[sub][r] = -INFINITY;
+                mt = __builtin_fmaxf(mt, s[sub][r]);
+            }
+        mt = __builtin_fmaxf(mt, __shfl_xor(mt, 16));
+        mt = __builtin_fmaxf(mt, __shfl_xor(mt, 32));
+        const float mn = __builtin_fmaxf(m, mt);
+        const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first tile (m = -inf)
+        float rs = 0.0f;
+        v4h pk[4];  // exp2(s - mn) in f16, per subtile
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const v8h pa = *(const v8h*)(P + lr * PS + 32 * ks + 8 * lq);
+        for (int sub = 0; sub < 4; ++sub)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float p = __builtin_amdgcn_exp2f(s[sub][r] - mn);  // masked: exp2(-inf) = 0
+                rs += p;
+                pk[sub][r] = (_Float16)p;
+            }
+        rs += __shfl_xor(rs, 16);
+        rs += __shfl_xor(rs, 32);
+        lsum = __builtin_fmaf(lsum, alpha, rs);
+        m = mn;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) o[n] *= alpha;
+        // O^T += V^T P^T over two K steps of 32 keys (subtiles 2c, 2c + 1).
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const v8h pb = {pk[2 * c][0], pk[2 * c][1], pk[2 * c][2], pk[2 * c][3],
+                            pk[2 * c + 1][0], pk[2 * c + 1][1], pk[2 * c + 1][2], pk[2 * c + 1][3]};
 #pragma unroll
             for (int n = 0; n < 8; ++n) {
-                const v8h vb = *(const v8h*)(Vt + (n * 16 + lr) * VS + 32 * ks + 8 * lq);
-                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[n], 0, 0, 0);
+                const _Float16* vrow = Vt + (n * 16 + lr) * VS + 32 * c + 4 * lq;
+                const v4h lo = *(const v4h*)vrow, hi = *(const v4h*)(vrow + 16);
+                const v8h va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, o[n], 0, 0, 0);
             }
         }
     }
+#undef TRIT_FETCH
 
+    if (row < rows) {
+        const float inv = 1.0f / lsum;
+        float* dst = out + (size_t)row * qd + (size_t)h * HD + 4 * lq;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int row = r0 + 4 * lq + r;
-        if (row >= rows) continue;
-        const float inv = 1.0f / lsum[r];
-#pragma unroll
-        for (int n = 0; n < 8; ++n) out[(size_t)row * qd + (size_t)h * HD + n * 16 + lr] = o[n][r] * inv;
+        for (int n = 0; n < 8; ++n)
+            *(float4*)(dst + 16 * n) = make_float4(o[n][0] * inv, o[n][1] * inv, o[n][2] * inv, o[n][3] * inv);
     }
 }
 

@@ -150,6 +150,7 @@ __device__ void quantize_rows(const GemvArgs& a, int k, const Smem& sm) {
 #pragma unroll
                 for (int q = 0; q < QB; ++q) {
                     const int chunk = base + q * nw;
+                    v[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                     if (chunk < chunks) {
                         const int row = chunk / per_row, c = chunk - row * per_row;
                         v[q] = *(const float4*)(a.x + (size_t)row * k + c * 256 + lane * 4);
@@ -363,7 +364,8 @@ __device__ float row_inv_block(const float* x, int k, float eps, float* red) {
             float4 v[QB];
 #pragma unroll
             for (int q = 0; q < QB; ++q)
-                if (base + q * nw < per_row) v[q] = *(const float4*)(x + (size_t)(base + q * nw) * 256 + lane * 4);
+                v[q] = base + q * nw < per_row ? *(const float4*)(x + (size_t)(base + q * nw) * 256 + lane * 4)
+                                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
             for (int q = 0; q < QB; ++q) {
                 if (base + q * nw >= per_row) break;  // uniform per wave
@@ -520,7 +522,7 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const uint8_t* __restrict
 #pragma unroll
             for (int q = 0; q < IB; ++q) {
                 const int i = base + q * THREADS + (int)threadIdx.x;
-                if (i < n16) v[q] = src[i];
+                v[q] = i < n16 ? src[i] : make_uint4(0, 0, 0, 0);
             }
             if (base == 0) stage_scales(tile);
 #pragma unroll
