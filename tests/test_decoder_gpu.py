@@ -289,3 +289,29 @@ def test_mid_flash_prefill(mid, monkeypatch):
     assert rel(got, split) < 2e-2
     assert rel(got_parts, got) < 2e-2
     assert int(np.argmax(got)) == int(np.argmax(split))
+
+
+def test_mid_flash_prefill_long_rows(mid, monkeypatch):
+    """Prompt attention over long rows (up to 1100 keys, 18 key tiles of 64):
+    1100 rows at once and as 700 + 400 (a continuation whose query tiles
+    start mid-way through the keys), against the oracle and the split
+    kernel; every value finite."""
+    print("case decoder mid flash prefill long rows", flush=True)
+    w, ref, lm = mid
+    p = synth.prompt(98, 1100, MID["vocab"])
+    ref.reset()
+    want = ref.forward(p)
+    got = lm.session(1152, 0).prefill(p)
+    parts = lm.session(1152, 0)
+    parts.prefill(p[:700])
+    got_parts = parts.prefill(p[700:])
+    monkeypatch.setenv("TRIT_HIP_FLASH", "0")
+    split = lm.session(1152, 0).prefill(p)
+    monkeypatch.delenv("TRIT_HIP_FLASH")
+    print(f"flash vs oracle {rel(got, want):.3g}, vs split {rel(got, split):.3g}, parts {rel(got_parts, got):.3g}",
+          flush=True)
+    assert np.all(np.isfinite(got)) and np.all(np.isfinite(got_parts))
+    assert rel(got, want) < 5e-2
+    assert rel(got, split) < 2e-2
+    assert rel(got_parts, got) < 2e-2
+    assert int(np.argmax(got)) == int(np.argmax(split))

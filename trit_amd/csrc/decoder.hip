@@ -181,6 +181,57 @@ __global__ void qk_rope_kernel(float* __restrict__ qkv, int stride, int heads, i
     }
 }
 
+// Fast mode, head_dim 128: the same step with one wave per (row, head),
+// lane i holding dims i and i + 64 (a rotary pair), the norm's sum a DPP
+// tree (fast mode: tree sums) -- four heads a 256-thread block instead of
+// a block a head with a serial sum.
+template <typename KV>
+__global__ __launch_bounds__(256) void qk_rope_wave_kernel(float* __restrict__ qkv, int stride, int rows, int heads,
+                                                            int kvh, int qk_norm, const float* __restrict__ q_norm,
+                                                            const float* __restrict__ k_norm, float eps,
+                                                            const float* __restrict__ rope_sin,
+                                                            const float* __restrict__ rope_cos,
+                                                            KV* __restrict__ kcache, KV* __restrict__ vcache,
+                                                            int max_pos, const State* st) {
+    constexpr int HD = 128, HALF = 64;
+    if (st->done) return;
+    const int per_row = heads + 2 * kvh;
+    const int item = (int)(blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE);
+    if (item >= rows * per_row) return;  // a whole wave
+    const int row = item / per_row, head = item % per_row, lane = threadIdx.x % WAVE;
+    const int pos = st->pos + row;
+    float* src = qkv + (size_t)row * stride + (size_t)head * HD;
+    const bool is_q = head < heads, is_k = !is_q && head < heads + kvh;
+    float x0 = src[lane], x1 = src[lane + HALF];
+    if (is_q || is_k) {
+        if (qk_norm) {
+            float sq = x0 * x0 + x1 * x1;
+            sq += dpp<DPP_XOR1>(sq);
+            sq += dpp<DPP_XOR2>(sq);
+            sq += dpp<DPP_HALF_MIRROR>(sq);
+            sq += dpp<DPP_MIRROR>(sq);
+            const float sum = (__shfl(sq, 0) + __shfl(sq, 16)) + (__shfl(sq, 32) + __shfl(sq, 48));
+            const float inv = 1.0f / __builtin_sqrtf(sum / (float)HD + eps);
+            const float* w = is_q ? q_norm : k_norm;
+            x0 = x0 * (inv * w[lane]);
+            x1 = x1 * (inv * w[lane + HALF]);
+        }
+        const float sn = rope_sin[(size_t)pos * HALF + lane], cs = rope_cos[(size_t)pos * HALF + lane];
+        const float a = x0, b = x1;
+        x0 = a * cs - b * sn;
+        x1 = b * cs + a * sn;
+    }
+    if (is_q) {
+        src[lane] = x0;
+        src[lane + HALF] = x1;
+    } else {
+        const int g = is_k ? head - heads : head - heads - kvh;
+        KV* cache = (is_k ? kcache : vcache) + ((size_t)g * max_pos + pos) * HD;
+        cache[lane] = (KV)x0;
+        cache[lane + HALF] = (KV)x1;
+    }
+}
+
 __device__ __forceinline__ float kv_load(const float* p) { return *p; }
 __device__ __forceinline__ float kv_load(const _Float16* p) { return (float)*p; }
 
@@ -1073,6 +1124,13 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
                                    S.rope_cos.as<float>(),
                                    S.kcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd,
                                    S.vcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, st);
+            } else if (hd == 128) {
+                const int items = rows * (c.heads + 2 * c.kv_heads);
+                hipLaunchKernelGGL(qk_rope_wave_kernel<_Float16>, dim3((items + 3) / 4), dim3(256), 0, s,
+                                   S.qkv.as<float>(), stride, rows, c.heads, c.kv_heads, c.qk_norm, D.q_norm(l),
+                                   D.k_norm(l), c.eps, S.rope_sin.as<float>(), S.rope_cos.as<float>(),
+                                   S.kcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd,
+                                   S.vcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, st);
             } else {
                 hipLaunchKernelGGL(qk_rope_kernel<_Float16>, dim3(rows * (c.heads + 2 * c.kv_heads)),
                                    dim3(hd < 64 ? 64 : hd), 0, s, S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
