@@ -307,6 +307,69 @@ def step_roofline(cfg, prompt, steps, step_ms, persistent):
                        "(trit_hip_session_generate_timed); launches include the final choice-only step")
 
 
+def cpu_configs(configs, min_s=0.3):
+    """The oracle (Trit's AVX-512 VNNI path, restated; the pinned team of
+    cpu_baseline) on the same product shapes and seeds as config_lines:
+    cpu_us per call (or per set) beside each GPU line, and the ratio. Each
+    product runs repeatedly for at least min_s seconds; C5 times the three
+    1564-row products once each."""
+    from oracle import oracle as O
+
+    isa = O.isa_best()
+
+    def timed(fn):
+        fn()  # warm
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            dt = time.perf_counter() - t0
+            if dt >= min_s:
+                return dt / n * 1e6
+
+    def q8(codes, sbits):
+        return O.Int8(codes, sbits.view(np.float16).astype(np.float32), 32, True, isa)
+
+    def note(key, cpu_us, gpu_us, sample):
+        if key in configs:
+            configs[key].update(cpu_us=round(cpu_us, 1), gpu_vs_cpu=round(cpu_us / gpu_us, 1), cpu_sample=sample)
+
+    x = synth.activations(synth.seed_for(0, 77), 64, 8192)
+    codes, sbits = synth.q8_0_matrix(synth.seed_for(0, 1), 2048, 2048)
+    L = q8(codes, sbits)
+    key = "c1_q8_0_gemv_2048x2048_b1"
+    if key in configs:
+        note(key, timed(lambda: L(x[:1, :2048])), configs[key]["avg_us"], "one row, the same weights repeated for 0.3 s (held in the CPU caches where they fit)")
+    tcodes, tscales = synth.ternary_matrix(synth.seed_for(0, 3), 4096, 4096)
+    T = O.Ternary(tcodes, tscales, isa)
+    for b in (1, 8):
+        key = f"c3_ternary_gemv_4096x4096_b{b}"
+        if key in configs:
+            note(key, timed(lambda: T(x[:b, :4096])), configs[key]["avg_us"], f"{b} rows, the same weights repeated for 0.3 s")
+    shapes = [(4096, 3072), (3072, 3072), (16384, 3072), (3072, 8192)]
+    set4 = []
+    for i, (nn, kk) in enumerate(shapes):
+        c, sc = O.q8_0_quantize(O.q4_k_expand(synth.q4_k_blocks(synth.seed_for(0, 40 + i), nn, kk)))
+        set4.append((O.Int8(c.reshape(nn, kk), sc.reshape(nn, kk // 32), 32, True, isa), kk))
+    for b in (1, 4):
+        key = f"c4_q4_k_set_b{b}"
+        if key in configs:
+            note(key, timed(lambda: [layer(x[:b, :kk]) for layer, kk in set4]), configs[key]["set_us"],
+                 f"the four products at {b} rows (Q4_K expanded and requantized as Trit does), repeated for 0.3 s")
+    key = "c5_prefill_gemm_1564x2048"
+    if key in configs:
+        xa = synth.activations(synth.seed_for(0, 5), 1564, 2048)
+        total = 0.0
+        for i, n in enumerate((2048, 6144, 2048)):
+            c, sb = synth.q8_0_matrix(synth.seed_for(0, 50 + i), n, 2048)
+            layer = q8(c, sb)
+            layer(xa[:64])
+            t0 = time.perf_counter()
+            layer(xa)
+            total += time.perf_counter() - t0
+        note(key, total * 1e6, configs[key]["gemm_us"], "the three 1564-row products, once each")
+
+
 def cpu_baseline(w, prompt, steps):
     from oracle import oracle as O
 
@@ -435,6 +498,9 @@ def main():
                       f"{args.steps} greedy steps ({cb['t_decode']:.2f} s), {cb['isa']} path"}
         out["tokens_identical"] = [int(t) for t in tokens] == cb["tokens"]
         out["gpu_vs_cpu"] = round(value / cpu_value, 2)
+        if configs:
+            print("[bench] cpu configurations ...", file=sys.stderr, flush=True)
+            cpu_configs(configs)
     print(json.dumps(out), flush=True)
 
 
