@@ -310,19 +310,23 @@ def step_roofline(cfg, prompt, steps, step_ms, persistent):
 def cpu_configs(configs, min_s=0.3):
     """The oracle (Trit's AVX-512 VNNI path, restated; the pinned team of
     cpu_baseline) on the same product shapes and seeds as config_lines:
-    cpu_us per call (or per set) beside each GPU line, and the ratio. Each
-    product runs repeatedly for at least min_s seconds; C5 times the three
-    1564-row products once each."""
+    cpu_us per call (or per set) beside each GPU line, and the ratio. As on
+    the GPU, C1 and C3 rotate 64 copies of the weights and C4 three copies
+    of the set, so the weights come from DRAM rather than the CPU caches;
+    each runs for at least min_s seconds. C5 times the three 1564-row
+    products once each."""
     from oracle import oracle as O
 
     isa = O.isa_best()
 
-    def timed(fn):
-        fn()  # warm
+    def timed(fns):
+        for fn in fns:
+            fn()  # warm
         n, t0 = 0, time.perf_counter()
         while True:
-            fn()
-            n += 1
+            for fn in fns:
+                fn()
+            n += len(fns)
             dt = time.perf_counter() - t0
             if dt >= min_s:
                 return dt / n * 1e6
@@ -335,27 +339,35 @@ def cpu_configs(configs, min_s=0.3):
             configs[key].update(cpu_us=round(cpu_us, 1), gpu_vs_cpu=round(cpu_us / gpu_us, 1), cpu_sample=sample)
 
     x = synth.activations(synth.seed_for(0, 77), 64, 8192)
-    codes, sbits = synth.q8_0_matrix(synth.seed_for(0, 1), 2048, 2048)
-    L = q8(codes, sbits)
     key = "c1_q8_0_gemv_2048x2048_b1"
     if key in configs:
-        note(key, timed(lambda: L(x[:1, :2048])), configs[key]["avg_us"], "one row, the same weights repeated for 0.3 s (held in the CPU caches where they fit)")
+        codes, sbits = synth.q8_0_matrix(synth.seed_for(0, 1), 2048, 2048)
+        Ls = [q8(codes, sbits) for _ in range(64)]
+        note(key, timed([lambda L=L: L(x[:1, :2048]) for L in Ls]), configs[key]["avg_us"],
+             "one row over 64 copies of the weights (285 MB), for 0.3 s")
+        del Ls
     tcodes, tscales = synth.ternary_matrix(synth.seed_for(0, 3), 4096, 4096)
-    T = O.Ternary(tcodes, tscales, isa)
+    Ts = [O.Ternary(tcodes, tscales, isa) for _ in range(64)]
     for b in (1, 8):
         key = f"c3_ternary_gemv_4096x4096_b{b}"
         if key in configs:
-            note(key, timed(lambda: T(x[:b, :4096])), configs[key]["avg_us"], f"{b} rows, the same weights repeated for 0.3 s")
+            note(key, timed([lambda T=T: T(x[:b, :4096]) for T in Ts]), configs[key]["avg_us"],
+                 f"{b} rows over 64 copies of the weights, for 0.3 s")
+    del Ts
     shapes = [(4096, 3072), (3072, 3072), (16384, 3072), (3072, 8192)]
     set4 = []
     for i, (nn, kk) in enumerate(shapes):
         c, sc = O.q8_0_quantize(O.q4_k_expand(synth.q4_k_blocks(synth.seed_for(0, 40 + i), nn, kk)))
-        set4.append((O.Int8(c.reshape(nn, kk), sc.reshape(nn, kk // 32), 32, True, isa), kk))
+        for _ in range(3):
+            set4.append((O.Int8(c.reshape(nn, kk), sc.reshape(nn, kk // 32), 32, True, isa), kk))
     for b in (1, 4):
         key = f"c4_q4_k_set_b{b}"
         if key in configs:
-            note(key, timed(lambda: [layer(x[:b, :kk]) for layer, kk in set4]), configs[key]["set_us"],
-                 f"the four products at {b} rows (Q4_K expanded and requantized as Trit does), repeated for 0.3 s")
+            per_set = timed([lambda L=L, kk=kk: L(x[:b, :kk]) for L, kk in set4]) * len(shapes)
+            note(key, per_set, configs[key]["set_us"],
+                 f"the four products at {b} rows (Q4_K expanded and requantized as Trit does), "
+                 f"three copies of the set, for 0.3 s")
+    del set4
     key = "c5_prefill_gemm_1564x2048"
     if key in configs:
         xa = synth.activations(synth.seed_for(0, 5), 1564, 2048)
