@@ -713,7 +713,9 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step, int po
         // o + residual; the gate_up rows stream in meanwhile.
         if (agu) load_rows<JD, 2>(L.codes[2], L.scales[2], a.ffn, rowgu, rr);
         __syncthreads();
-        if (!gather<MAXK / T>(a.ATT, a.qd, lin, tag_of(tag0, layer, 2), sm.xin, sm, deadline, st)) return;
+        // Polled from the first o wave on: the gate_up waves' loads are in
+        // flight.
+        if (!gather<8>(a.ATT, a.qd, lin, tag_of(tag0, layer, 2), sm.xin, sm, deadline, st, nu)) return;
         quantize_block<JO>(sm.xin, (const NormRegs<JO>*)nullptr, sm);
         if (ao) {
             float acc[1];
@@ -941,7 +943,7 @@ bool plan(const SessionImpl& S, Plan& p) {
     if (nu + std::max(no, nd) + nqw > NW) return false;
     auto fits = [](int n, int p0, int mw) { return p0 + (n + WAVE * mw - 1) / (WAVE * mw) <= NW; };
     if (!fits((group + 2) * HD, NW - nqw - 1, 8) || !fits(p.splits * (2 + p.comb), NW - nqw, 2)) return false;
-    if (!fits(c.d, 0, 6) || !fits(qd, 0, MAXK / T) || !fits(c.ffn, 0, MAXK / T)) return false;
+    if (!fits(c.d, 0, 6) || !fits(qd, nu, 8) || !fits(c.ffn, 0, MAXK / T)) return false;
     p.rh = (c.vocab + p.blocks - 1) / p.blocks;
     return true;
 }
