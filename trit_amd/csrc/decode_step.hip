@@ -495,7 +495,12 @@ __device__ bool attention(const StepArgs& a, const LayerPtrs& L, int pos, uint32
 #pragma unroll
     for (int hl = 0; hl < GROUP; ++hl) {
         M[hl] = -INFINITY;
-        for (int q = 0; q < live; ++q) M[hl] = __builtin_fmaxf(M[hl], sm.gmax[q][hl]);
+        int q = 0;
+        for (; q + 4 <= live; q += 4) {
+            const float a0 = sm.gmax[q][hl], a1 = sm.gmax[q + 1][hl], a2 = sm.gmax[q + 2][hl], a3 = sm.gmax[q + 3][hl];
+            M[hl] = __builtin_fmaxf(__builtin_fmaxf(M[hl], __builtin_fmaxf(a0, a1)), __builtin_fmaxf(a2, a3));
+        }
+        for (; q < live; ++q) M[hl] = __builtin_fmaxf(M[hl], sm.gmax[q][hl]);
     }
     float l[GROUP], acc[GROUP][8];
 #pragma unroll
@@ -535,12 +540,22 @@ __device__ bool attention(const StepArgs& a, const LayerPtrs& L, int pos, uint32
     if (t < GROUP * HD) {
         const int hl = t / HD, ee = t % HD;
         float o = 0.0f;
-        for (int q = 0; q < live; ++q) o += sm.gpart[q][hl * HD + ee];
+        // In group order; four loads issued ahead of their adds.
+        int q = 0;
+        for (; q + 4 <= live; q += 4) {
+            const float a0 = sm.gpart[q][hl * HD + ee], a1 = sm.gpart[q + 1][hl * HD + ee];
+            const float a2 = sm.gpart[q + 2][hl * HD + ee], a3 = sm.gpart[q + 3][hl * HD + ee];
+            o += a0;
+            o += a1;
+            o += a2;
+            o += a3;
+        }
+        for (; q < live; ++q) o += sm.gpart[q][hl * HD + ee];
         const size_t base = ((size_t)(g * GROUP + hl) * a.splits + s) * (HD + 2);
         put(a.PART + base + 2 + ee, o, tag_out);
         if (ee == 0) {
             float lsum = 0.0f;
-            for (int q = 0; q < live; ++q) lsum += sm.gl[q][hl];
+            for (int q2 = 0; q2 < live; ++q2) lsum += sm.gl[q2][hl];
             put(a.PART + base, M[hl], tag_out);
             put(a.PART + base + 1, lsum, tag_out);
         }
