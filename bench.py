@@ -46,10 +46,12 @@ VALU_PEAK_TOPS = 39.32
 # FETCH_SIZE 3313.1 KiB x 2.0 (the scale a 256 MiB device copy gives) plus
 # WRITE_SIZE 48.0 KiB x 1.0.
 GATE_UP_TRAFFIC_BYTES = round((3313.1 * 2.0 + 48.0) * 1024)
-# HBM bytes per forward launch of the persistent decode step, from the same
-# kind of runs (profiles/decode_step_qwen3_0.6b_hbm_traffic.md): FETCH_SIZE
-# 432 070 KiB x 2.0 plus WRITE_SIZE 19 608 KiB, at positions 256..270.
-STEP_TRAFFIC_BYTES = round((432070 * 2.0 + 19608) * 1024)
+# HBM bytes per forward of the persistent decode step, from the same kind of
+# runs (profiles/decode_step_qwen3_0.6b_hbm_traffic.md): FETCH_SIZE and
+# WRITE_SIZE of one launch of 128 steps (127 forwards, positions 256..382)
+# over the forwards, FETCH_SIZE x 2.0 plus WRITE_SIZE x 1.0.
+STEP_FETCH_KIB, STEP_WRITE_KIB = 434748.3, 19624.1
+STEP_TRAFFIC_BYTES = round((STEP_FETCH_KIB * 2.0 + STEP_WRITE_KIB) * 1024)
 
 
 class Hip:
@@ -279,32 +281,38 @@ def config_lines(H, sweeps=10):
 
 
 def step_roofline(cfg, prompt, steps, step_ms, persistent):
-    """The decode loop's kernel: the persistent step (one launch per token)
-    timed with HIP events around its launches. Algorithmic bytes per launch:
-    every Q8_0 weight once (34 B per 32), the f16 head, the f16 keys and
-    values of the positions attended (the average over the timed tokens),
-    the embedding row and the norm weights."""
+    """The decode loop's kernel: the persistent step (one launch runs every
+    step of a generate call) timed with HIP events around it. Algorithmic
+    bytes per forward: every Q8_0 weight once (34 B per 32), the f16 head,
+    the f16 keys and values of the positions attended (the average over the
+    timed tokens), the embedding row and the norm weights; one launch holds
+    steps - 1 forwards. The per-kernel fallback is one graph replay a
+    step."""
     d, ffn, hd, L = cfg["d"], cfg["ffn"], cfg["head_dim"], cfg["layers"]
     qkv = (cfg["heads"] + 2 * cfg["kv_heads"]) * hd
     weights = L * (qkv * d + d * cfg["heads"] * hd + 2 * ffn * d + d * ffn) * 34 // 32
     head = cfg["vocab"] * d * 2
-    # Launch i < steps - 1 forwards a token at position prompt + i over
-    # prompt + i + 1 keys; the last launch only makes the final choice.
+    # Step i < steps - 1 forwards a token at position prompt + i over
+    # prompt + i + 1 keys; the last step only makes the final choice.
     forwards = steps - 1
     mean_keys = prompt + (forwards - 1) / 2.0 + 1
     kv = int(L * cfg["kv_heads"] * hd * 2 * 2 * mean_keys)
     small = d * 2 + L * (2 * d + 2 * hd) * 4 + d * 4
-    per_launch = (weights + head + kv + small) * forwards // steps
-    launches = steps
+    per_forward = weights + head + kv + small
+    launches = 1 if persistent else steps
+    per_launch = per_forward * forwards // launches
     avg_ms = step_ms / launches
     achieved = per_launch / (avg_ms * 1e-3) / 1e9
     return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                frac=round(achieved / HBM_PEAK_GBS, 4), traffic=STEP_TRAFFIC_BYTES if persistent else None,
-                kernel="step_kernel<4,8,12,2>: the persistent decode step (choice, 28 layers, head)" if persistent
-                else "the per-kernel decode step (graph replay)",
-                bytes_per_launch=per_launch, avg_us=round(avg_ms * 1e3, 3), launches=launches,
-                timing="HIP events recorded on the library's stream before the first and after the last step launch "
-                       "(trit_hip_session_generate_timed); launches include the final choice-only step")
+                frac=round(achieved / HBM_PEAK_GBS, 4),
+                traffic=STEP_TRAFFIC_BYTES * forwards if persistent else None,
+                kernel=f"step_kernel<4,8,12,2>: the persistent decode step, {steps} steps (choice, 28 layers, "
+                       "head) in one launch" if persistent else "the per-kernel decode step (graph replay)",
+                bytes_per_launch=per_launch, bytes_per_forward=per_forward, forwards=forwards,
+                avg_us=round(avg_ms * 1e3, 3), us_per_forward=round(step_ms * 1e3 / forwards, 3),
+                traffic_per_forward=STEP_TRAFFIC_BYTES if persistent else None, launches=launches,
+                timing="HIP events recorded on the library's stream before and after the step launch "
+                       "(trit_hip_session_generate_timed); the launch includes the final choice-only step")
 
 
 def cpu_configs(configs, min_s=0.3):

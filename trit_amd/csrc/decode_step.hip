@@ -1,11 +1,12 @@
-// The persistent decode step: one launch per greedy token runs the choice,
-// every layer and the head (src/models/parts/causal_lm.rs:284-302,410-481)
-// on all CUs at once, one block per CU.
+// The persistent decode step: one launch runs a generate call's greedy
+// tokens, each its choice, every layer and the head
+// (src/models/parts/causal_lm.rs:284-302,410-481), on all CUs at once, one
+// block per CU.
 //
 // Blocks hand activations to each other through exchange words: 8 bytes
 // holding an f32 value and a 32-bit tag, written with one agent-scope store
 // and polled with agent-scope loads until the tag is the one the reader
-// waits for. The tag names the launch and the phase, so a word is never
+// waits for. The tag names the token step and the phase, so a word is never
 // mistaken for an older one, and no barrier, fence or cache flush is
 // needed between phases. A phase's weights do not depend on its inputs:
 // each block issues their loads before it waits, so the weight stream
@@ -15,8 +16,10 @@
 // splits per key/value head, one per block) -> combined attention -> o
 // product + residual -> gate_up product + SwiGLU -> down product +
 // residual. Then the final RMSNorm, the f16 head and each block's best
-// logit; the next launch's first act is the greedy choice over those
-// candidates (first maximum wins, src/layers.rs:604-612).
+// logit, published as two more exchange words; the next step's first act
+// is the greedy choice over those candidates (first maximum wins,
+// src/layers.rs:604-612). The first step of a launch takes them from where
+// the previous launch, or the prompt's logits, left them.
 //
 // Products use the one-row kernel's arithmetic (gemv_decode.hip): Trit's
 // quantizer, exact i32 block dots and the f32 group chain in order, so
@@ -67,6 +70,7 @@ struct StepArgs {
     uint64_t* PART;  // heads * splits * (HD + 2) words: max, sum, p.V
     uint64_t* ATT;   // heads * HD words
     uint64_t* H;     // ffn words
+    uint64_t* CAND;  // 2 words per block: its best logit and that row's index
     float2* cand;    // per block: best logit, its index (int bits)
     int* out;
     State* st;
@@ -74,7 +78,7 @@ struct StepArgs {
     int comb;                 // combined attention outputs per block
     int rq, ro, rgu, rd;      // rows per block (gate_up: pairs), multiples of 4
     int rh;                   // head rows per block
-    unsigned long long ticks; // wall-clock ticks a block may wait in a launch
+    unsigned long long ticks; // wall-clock ticks a block may wait in a step
 };
 
 struct Smem {
@@ -149,9 +153,9 @@ __device__ __forceinline__ bool aborted(Smem& sm) {
 // Ends with a block barrier; false when a word missed the deadline (the
 // block then leaves the launch).
 template <int MW, typename Index>
-__device__ bool gather(const uint64_t* src, int n, Index index, uint32_t tag, float* dst, Smem& sm,
+__device__ bool gather(int t, const uint64_t* src, int n, Index index, uint32_t tag, float* dst, Smem& sm,
                        unsigned long long deadline, State* st, int p0 = 0) {
-    const int i0 = ((int)(threadIdx.x / WAVE) - p0) * WAVE * MW + (int)(threadIdx.x % WAVE);
+    const int i0 = (t / WAVE - p0) * WAVE * MW + t % WAVE;
     if (i0 >= 0 && i0 < n) {  // uniform per wave: whether the wave polls
         uint64_t w[MW];
 #pragma unroll
@@ -208,11 +212,11 @@ struct Rows {
 };
 
 template <int J, int P, int N, int NS>
-__device__ __forceinline__ void load_rows(const uint8_t* codes, const uint16_t* scales, int part_rows, int row,
+__device__ __forceinline__ void load_rows(int t, const uint8_t* codes, const uint16_t* scales, int part_rows, int row,
                                           Rows<N, NS>& r) {
     static_assert(P * J <= N && P * ((J + 1) / 2) <= NS, "the row registers hold the product");
     constexpr int K = J * 256, G = K / 32;
-    const int l = threadIdx.x & 15;
+    const int l = t & 15;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
         const uint8_t* src = codes + (size_t)(p * part_rows + row) * K;
@@ -229,9 +233,9 @@ __device__ __forceinline__ void load_rows(const uint8_t* codes, const uint16_t* 
 // RMSNorm factor of x (K = 256 J values in LDS) by one wave, the one-row
 // kernel's tree: every block gets the same bits.
 template <int J>
-__device__ __forceinline__ float norm_inv_wave(const float* x, float eps) {
+__device__ __forceinline__ float norm_inv_wave(int t, const float* x, float eps) {
     constexpr int K = J * 256;
-    const int lane = threadIdx.x % WAVE;
+    const int lane = t % WAVE;
     float part = 0.0f;
 #pragma unroll
     for (int i = 0; i < J; ++i) {
@@ -259,10 +263,10 @@ struct NormRegs {
 };
 
 template <int J>
-__device__ __forceinline__ void load_norm(const float* norm_w, NormRegs<J>& r) {
+__device__ __forceinline__ void load_norm(int t, const float* norm_w, NormRegs<J>& r) {
 #pragma unroll
     for (int i = 0; i < NormRegs<J>::N; ++i) {
-        const int item = threadIdx.x + T * i;
+        const int item = t + T * i;
         r.w[i] = item < J * 64 ? *(const float4*)(norm_w + (size_t)item * 4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
 }
@@ -270,12 +274,12 @@ __device__ __forceinline__ void load_norm(const float* norm_w, NormRegs<J>& r) {
 // Trit's activation quantizer over x (K values in LDS), optionally after
 // RMSNorm x * (inv * w), into sm.xq / sm.xs; ends with a block barrier.
 template <int J>
-__device__ void quantize_block(const float* x, const NormRegs<J>* nr, Smem& sm) {
+__device__ void quantize_block(int t, const float* x, const NormRegs<J>* nr, Smem& sm) {
     constexpr int ITEMS = J * 64;  // float4 items; a multiple of 64: whole waves
     const float inv = sm.inv;
 #pragma unroll
     for (int i = 0; i < NormRegs<J>::N; ++i) {
-        const int item = threadIdx.x + T * i;
+        const int item = t + T * i;
         if (item >= ITEMS) break;  // uniform per wave
         float4 v = *(const float4*)(x + (size_t)item * 4);
         if (nr) {
@@ -302,8 +306,8 @@ __device__ void quantize_block(const float* x, const NormRegs<J>* nr, Smem& sm) 
 // The one-row kernel's dots and f32 chain for a wave's rows; the total of
 // each row lands in lane 14 of its 16 lanes.
 template <int J, int P, int N, int NS>
-__device__ __forceinline__ void row_chain(const Rows<N, NS>& r, const Smem& sm, float (&acc)[P]) {
-    const int l = threadIdx.x & 15;
+__device__ __forceinline__ void row_chain(int t, const Rows<N, NS>& r, const Smem& sm, float (&acc)[P]) {
+    const int l = t & 15;
 #pragma unroll
     for (int p = 0; p < P; ++p) acc[p] = 0.0f;
 #pragma unroll
@@ -342,9 +346,9 @@ struct KvRegs {
     uint4 k[MAXC], v[MAXC];
 };
 
-__device__ __forceinline__ void kv_prefetch(const _Float16* K, const _Float16* V, int j0, int j1, int pos,
+__device__ __forceinline__ void kv_prefetch(int t, const _Float16* K, const _Float16* V, int j0, int j1, int pos,
                                             KvRegs& kv) {
-    const int G = threadIdx.x >> 4, l16 = threadIdx.x & 15;
+    const int G = t >> 4, l16 = t & 15;
 #pragma unroll
     for (int i = 0; i < MAXC; ++i) {
         kv.k[i] = kv.v[i] = make_uint4(0, 0, 0, 0);
@@ -371,10 +375,9 @@ __device__ __forceinline__ void unpack8(const uint4 r, float (&out)[8]) {
 // softmax and p.V over the split's keys, written as partials (max, sum,
 // unnormalised p.V) per query head.
 template <int GROUP>
-__device__ bool attention(const StepArgs& a, const LayerPtrs& L, int pos, uint32_t tag_in, uint32_t tag_out,
+__device__ bool attention(int t, const StepArgs& a, const LayerPtrs& L, int pos, uint32_t tag_in, uint32_t tag_out,
                           Smem& sm, unsigned long long deadline) {
     const int b = blockIdx.x, g = b / a.splits, s = b % a.splits;
-    const int t = threadIdx.x;
     const int tk = pos + 1, span = (tk + a.splits - 1) / a.splits;
     const int j0 = s * span, j1 = min(j0 + span, tk);
     const int heads = a.heads, kvh = a.kvh;
@@ -386,7 +389,7 @@ __device__ bool attention(const StepArgs& a, const LayerPtrs& L, int pos, uint32
     // The split's cached keys and values, the q/k norm weights and the
     // rotary values load while the qkv rows arrive.
     KvRegs kv;
-    kv_prefetch(L.kcache + (size_t)g * a.max_pos * HD, L.vcache + (size_t)g * a.max_pos * HD, j0, j1, pos, kv);
+    kv_prefetch(t, L.kcache + (size_t)g * a.max_pos * HD, L.vcache + (size_t)g * a.max_pos * HD, j0, j1, pos, kv);
     const int hh = t / WAVE, i = t % WAVE;
     float nw0 = 1.0f, nw1 = 1.0f, sn = 0.0f, cs = 1.0f;
     if (hh <= GROUP) {
@@ -401,7 +404,7 @@ __device__ bool attention(const StepArgs& a, const LayerPtrs& L, int pos, uint32
     // One wave polls: the first whose 16-lane groups load no key and that
     // stored no qkv value (the qkv rows sit in the last a.rq / 4 waves).
     const int kw = (j1 - j0 + 3) / 4, nqw = a.rq / 4;
-    if (!gather<8>(a.QKV, (GROUP + 2) * HD, index, tag_in, sm.qkv, sm, deadline, a.st, kw < NW - nqw ? kw : 0))
+    if (!gather<8>(t, a.QKV, (GROUP + 2) * HD, index, tag_in, sm.qkv, sm, deadline, a.st, kw < NW - nqw ? kw : 0))
         return false;
 
     // Wave hh takes head hh (the q heads, then k, then v), lane i its dims
@@ -566,7 +569,7 @@ __device__ bool attention(const StepArgs& a, const LayerPtrs& L, int pos, uint32
 // Block b merges the splits of `comb` attention outputs (one query head's
 // dims [e0, e0 + comb)) with the usual rescaling: wave e takes output e,
 // lane s split s, and the sums are shuffle trees in a fixed order.
-__device__ bool combine(const StepArgs& a, uint32_t tag_in, uint32_t tag_out, Smem& sm,
+__device__ bool combine(int t, const StepArgs& a, uint32_t tag_in, uint32_t tag_out, Smem& sm,
                         unsigned long long deadline, int p0) {
     const int o0 = blockIdx.x * a.comb, h = o0 / HD, e0 = o0 % HD, per = 2 + a.comb;
     const int splits = a.splits;
@@ -577,8 +580,8 @@ __device__ bool combine(const StepArgs& a, uint32_t tag_in, uint32_t tag_out, Sm
     };
     // The qkv waves poll: the attention partials were stored by the first
     // waves, and the o rows are loading into the waves after gate_up's.
-    if (!gather<2>(a.PART, splits * per, index, tag_in, sm.xin, sm, deadline, a.st, NW - a.rq / 4)) return false;
-    const int e = threadIdx.x / WAVE, s = threadIdx.x % WAVE;
+    if (!gather<2>(t, a.PART, splits * per, index, tag_in, sm.xin, sm, deadline, a.st, NW - a.rq / 4)) return false;
+    const int e = t / WAVE, s = t % WAVE;
     if (e < a.comb) {
         const bool live = s < splits;
         const float m = live ? sm.xin[s * per] : -INFINITY;
@@ -626,13 +629,12 @@ __device__ __forceinline__ void best_of_wave(float& bv, int& bi) {
 }
 
 template <int JD, int JO, int JF, int GROUP>
-__global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step, int pos, uint32_t tag0) {
+__global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int pos0, uint32_t seq0, int nsteps) {
     __shared__ Smem sm;
     State* st = a.st;
     if (st->done) return;
-    const int t = threadIdx.x, w = t / WAVE, lane = t % WAVE, b = blockIdx.x;
-    const unsigned long long deadline = wall_clock64() + a.ticks;
-    if (t == 0) sm.abort = 0;
+    const int b = blockIdx.x;
+    if (threadIdx.x == 0) sm.abort = 0;
 
     // Waves by product, four rows a wave: gate_up [0, nu), o [nu, nu + no),
     // down [nu, nu + nd), qkv [NW - nqw, NW). Each product's rows load one
@@ -644,16 +646,56 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step, int po
     // stream in during the choice.
     constexpr int RN = cmax(cmax(2 * JD, JO), JF);
     constexpr int RS = cmax(cmax(2 * ((JD + 1) / 2), (JO + 1) / 2), (JF + 1) / 2);
+    const Linear lin;
+
+    // Token steps: step it forwards the token chosen from step it - 1's
+    // candidates (exchange words) -- the first from the candidates the
+    // previous launch or the prompt's logits left in a.cand.
+    for (int it = 0; it < nsteps; ++it) {
+    const int step = step0 + it, pos = pos0 + it;
+    const uint32_t tag0 = (seq0 + (uint32_t)it) << 8;
+    const unsigned long long deadline = wall_clock64() + a.ticks;
+    // The thread index, made opaque to the optimizer at the top of the step,
+    // of each layer and of the head: what derives from it (the wave's
+    // product, a lane's rows) is computed within that part, rather than
+    // hoisted out of the loops and held in registers through the others
+    // (the head needs them).
+    int t, w, lane, rowq, rowo, rowgu, rowd;
+    bool aq, agu, ao, ad;
+    auto fresh = [&] {
+        t = threadIdx.x;
+        asm volatile("" : "+v"(t));
+        t &= T - 1;  // its range, for the arithmetic derived from it
+        w = t / WAVE;
+        lane = t % WAVE;
+        aq = w >= NW - nqw;
+        agu = w < nu;
+        ao = w >= nu && w < nu + no;
+        ad = w >= nu && w < nu + nd;
+        rowq = b * a.rq + 4 * (w - (NW - nqw)) + (lane >> 4);
+        rowo = b * a.ro + 4 * (w - nu) + (lane >> 4);
+        rowgu = b * a.rgu + 4 * w + (lane >> 4);
+        rowd = b * a.rd + 4 * (w - nu) + (lane >> 4);
+    };
+    fresh();
+
+    // The first layer's qkv rows stream in during the choice. (Declared per
+    // step so that nothing of it stays live through the head.)
     Rows<RN, RS> rr{};
-    const bool aq = w >= NW - nqw;
-    const int rowq = b * a.rq + 4 * (w - (NW - nqw)) + (lane >> 4);
-    if (aq) load_rows<JD, 1>(a.layers[0].codes[0], a.layers[0].scales[0], 0, rowq, rr);
+    if (aq) load_rows<JD, 1>(t, a.layers[0].codes[0], a.layers[0].scales[0], 0, rowq, rr);
 
     // ---- the greedy choice over the blocks' candidates -------------------
     {
         float best = -INFINITY;
         int index = INT_MAX;
-        if (t < (int)gridDim.x) {
+        if (it > 0) {
+            const uint32_t tag_c = ((seq0 + (uint32_t)it - 1) << 8) + (uint32_t)(a.n_layers * PH + 1);
+            if (!gather<MAXD / T>(t, a.CAND, 2 * (int)gridDim.x, lin, tag_c, sm.xin, sm, deadline, st)) return;
+            if (t < (int)gridDim.x) {
+                best = sm.xin[2 * t];
+                index = __float_as_int(sm.xin[2 * t + 1]);
+            }
+        } else if (t < (int)gridDim.x) {
             const float2 c = a.cand[t];
             best = c.x;
             index = __float_as_int(c.y);
@@ -690,79 +732,74 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step, int po
         __syncthreads();
     }
 
-    const bool agu = w < nu, ao = w >= nu && w < nu + no, ad = w >= nu && w < nu + nd;
-    const int rowo = b * a.ro + 4 * (w - nu) + (lane >> 4);
-    const int rowgu = b * a.rgu + 4 * w + (lane >> 4);
-    const int rowd = b * a.rd + 4 * (w - nu) + (lane >> 4);
-    const Linear lin;
-
     // Each product's rows are loaded one phase ahead of it: the loads run
     // while the block waits for that phase's inputs. (Zero-initialised so
     // that no register stays live across the layer loop.)
     for (int layer = 0; layer < a.n_layers; ++layer) {
+        fresh();
         const LayerPtrs& L = a.layers[layer];
         // qkv: x (gathered, or the embedding) -> RMSNorm -> quantize -> rows.
         NormRegs<JD> nq;
-        load_norm<JD>(L.norm_attn, nq);
+        load_norm<JD>(t, L.norm_attn, nq);
         // Polled by the first waves (the down rows' wave stored x).
-        if (layer > 0 && !gather<6>(a.X, a.d, lin, tag_of(tag0, layer - 1, 5), sm.xres, sm, deadline, st))
+        if (layer > 0 && !gather<6>(t, a.X, a.d, lin, tag_of(tag0, layer - 1, 5), sm.xres, sm, deadline, st))
             return;
         if (w == 0) {
-            const float inv = norm_inv_wave<JD>(sm.xres, a.eps);
+            const float inv = norm_inv_wave<JD>(t, sm.xres, a.eps);
             if (lane == 0) sm.inv = inv;
         }
         __syncthreads();
-        quantize_block<JD>(sm.xres, &nq, sm);
+        quantize_block<JD>(t, sm.xres, &nq, sm);
         if (aq) {
             float acc[1];
-            row_chain<JD, 1>(rr, sm, acc);
+            row_chain<JD, 1>(t, rr, sm, acc);
             if ((lane & 15) == 14) put(a.QKV + rowq, acc[0], tag_of(tag0, layer, 0));
         }
         // attention partials.
         __syncthreads();
-        if (!attention<GROUP>(a, L, pos, tag_of(tag0, layer, 0), tag_of(tag0, layer, 1), sm, deadline)) return;
+        if (!attention<GROUP>(t, a, L, pos, tag_of(tag0, layer, 0), tag_of(tag0, layer, 1), sm, deadline)) return;
         // combine; the o rows stream in meanwhile.
-        if (ao) load_rows<JO, 1>(L.codes[1], L.scales[1], 0, rowo, rr);
+        if (ao) load_rows<JO, 1>(t, L.codes[1], L.scales[1], 0, rowo, rr);
         __syncthreads();
-        if (!combine(a, tag_of(tag0, layer, 1), tag_of(tag0, layer, 2), sm, deadline, nu + no)) return;
+        if (!combine(t, a, tag_of(tag0, layer, 1), tag_of(tag0, layer, 2), sm, deadline, nu + no)) return;
         // o + residual; the gate_up rows stream in meanwhile.
-        if (agu) load_rows<JD, 2>(L.codes[2], L.scales[2], a.ffn, rowgu, rr);
+        if (agu) load_rows<JD, 2>(t, L.codes[2], L.scales[2], a.ffn, rowgu, rr);
         __syncthreads();
         // Polled from the first o wave on: the gate_up waves' loads are in
         // flight.
-        if (!gather<8>(a.ATT, a.qd, lin, tag_of(tag0, layer, 2), sm.xin, sm, deadline, st, nu)) return;
-        quantize_block<JO>(sm.xin, (const NormRegs<JO>*)nullptr, sm);
+        if (!gather<8>(t, a.ATT, a.qd, lin, tag_of(tag0, layer, 2), sm.xin, sm, deadline, st, nu)) return;
+        quantize_block<JO>(t, sm.xin, (const NormRegs<JO>*)nullptr, sm);
         if (ao) {
             float acc[1];
-            row_chain<JO, 1>(rr, sm, acc);
+            row_chain<JO, 1>(t, rr, sm, acc);
             if ((lane & 15) == 14) put(a.X + rowo, sm.xres[rowo] + acc[0], tag_of(tag0, layer, 3));
         }
         // gate_up + SwiGLU.
         NormRegs<JD> ngu;
-        load_norm<JD>(L.norm_mlp, ngu);
+        load_norm<JD>(t, L.norm_mlp, ngu);
         __syncthreads();
-        if (!gather<MAXK / T>(a.X, a.d, lin, tag_of(tag0, layer, 3), sm.xres, sm, deadline, st)) return;
+        if (!gather<MAXK / T>(t, a.X, a.d, lin, tag_of(tag0, layer, 3), sm.xres, sm, deadline, st)) return;
         if (w == 0) {
-            const float inv = norm_inv_wave<JD>(sm.xres, a.eps);
+            const float inv = norm_inv_wave<JD>(t, sm.xres, a.eps);
             if (lane == 0) sm.inv = inv;
         }
         __syncthreads();
-        quantize_block<JD>(sm.xres, &ngu, sm);
+        quantize_block<JD>(t, sm.xres, &ngu, sm);
         if (agu) {
             float acc[2];
-            row_chain<JD, 2>(rr, sm, acc);
+            row_chain<JD, 2>(t, rr, sm, acc);
             if ((lane & 15) == 14) put(a.H + rowgu, silu_trit(acc[0]) * acc[1], tag_of(tag0, layer, 4));
         }
         // down + residual.
-        if (ad) load_rows<JF, 1>(L.codes[3], L.scales[3], 0, rowd, rr);
+        if (ad) load_rows<JF, 1>(t, L.codes[3], L.scales[3], 0, rowd, rr);
         if (aq && layer + 1 < a.n_layers)
-            load_rows<JD, 1>(a.layers[layer + 1].codes[0], a.layers[layer + 1].scales[0], 0, rowq, rr);
+            load_rows<JD, 1>(t, a.layers[layer + 1].codes[0], a.layers[layer + 1].scales[0], 0, rowq, rr);
         __syncthreads();
-        if (!gather<MAXK / T>(a.H, a.ffn, lin, tag_of(tag0, layer, 4), sm.xin, sm, deadline, st)) return;
-        quantize_block<JF>(sm.xin, (const NormRegs<JF>*)nullptr, sm);
+        if (!gather<MAXK / T>(t, a.H, a.ffn, lin, tag_of(tag0, layer, 4), sm.xin, sm, deadline, st)) return;
+        quantize_block<JF>(t, sm.xin, (const NormRegs<JF>*)nullptr, sm);
         if (ad) {
             float acc[1];
-            row_chain<JF, 1>(rr, sm, acc);
+            row_chain<JF, 1>(t, rr, sm, acc);
             if ((lane & 15) == 14) put(a.X + rowd, sm.xres[rowd] + acc[0], tag_of(tag0, layer, 5));
         }
         __syncthreads();
@@ -774,6 +811,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step, int po
     // Three passes of weights are in flight at a time, and each lane keeps
     // the normed x values of its lane chain in registers.
     constexpr int S8 = JD * 2;  // 16-byte loads per lane chain: d / 128
+    fresh();
     const int l16 = t & 15;
     const int rows_pass = T / 16, nb = (int)gridDim.x;
     const int passes = (a.vocab + rows_pass * nb - 1) / (rows_pass * nb);
@@ -795,9 +833,9 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step, int po
     float fn[(MAXD + T - 1) / T];
 #pragma unroll
     for (int q = 0; q < (MAXD + T - 1) / T; ++q) fn[q] = t + T * q < a.d ? a.final_norm[t + T * q] : 0.0f;
-    if (!gather<MAXD / T>(a.X, a.d, lin, tag_of(tag0, a.n_layers - 1, 5), sm.xres, sm, deadline, st)) return;
+    if (!gather<MAXD / T>(t, a.X, a.d, lin, tag_of(tag0, a.n_layers - 1, 5), sm.xres, sm, deadline, st)) return;
     if (w == 0) {
-        const float inv = norm_inv_wave<JD>(sm.xres, a.eps);
+        const float inv = norm_inv_wave<JD>(t, sm.xres, a.eps);
         if (lane == 0) sm.inv = inv;
     }
     __syncthreads();
@@ -856,7 +894,12 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step, int po
         int bi = sm.bi[0];
         for (int q = 1; q < NW; ++q) better(bv, bi, sm.bv[q], sm.bi[q]);
         a.cand[b] = make_float2(bv, __int_as_float(bi));
+        const uint32_t tag_c = tag0 + (uint32_t)(a.n_layers * PH + 1);
+        put(a.CAND + 2 * b, bv, tag_c);
+        put(a.CAND + 2 * b + 1, __int_as_float(bi), tag_c);
         if (b == 0) st->pos = pos + 1;
+    }
+    __syncthreads();  // sm.bv / sm.bi are the next choice's
     }
 }
 
@@ -901,7 +944,7 @@ __global__ __launch_bounds__(256) void cand_kernel(const float* __restrict__ log
     if (threadIdx.x == 0) cand[blockIdx.x] = make_float2(bv[0], __int_as_float(bi[0]));
 }
 
-using StepFn = void (*)(StepArgs, int, int, uint32_t);
+using StepFn = void (*)(StepArgs, int, int, uint32_t, int);
 
 // The instantiated shapes: (d/256, heads*hd/256, ffn/256, q heads per kv head).
 StepFn step_fn(int jd, int jo, int jf, int group) {
@@ -959,6 +1002,7 @@ bool plan(const SessionImpl& S, Plan& p) {
     auto fits = [](int n, int p0, int mw) { return p0 + (n + WAVE * mw - 1) / (WAVE * mw) <= NW; };
     if (!fits((group + 2) * HD, NW - nqw - 1, 8) || !fits(p.splits * (2 + p.comb), NW - nqw, 2)) return false;
     if (!fits(c.d, 0, 6) || !fits(qd, nu, 8) || !fits(c.ffn, 0, MAXK / T)) return false;
+    if (!fits(2 * p.blocks, 0, MAXD / T)) return false;  // the candidates' words
     p.rh = (c.vocab + p.blocks - 1) / p.blocks;
     return true;
 }
@@ -976,7 +1020,7 @@ void decode_step_prepare(SessionImpl& S, hipStream_t s) {
     const DecoderImpl& D = *S.dec;
     const auto& c = D.c;
     const int nq = (c.heads + 2 * c.kv_heads) * HD, qd = c.heads * HD;
-    const size_t words = (size_t)c.d + nq + (size_t)c.heads * p.splits * (HD + 2) + qd + c.ffn;
+    const size_t words = (size_t)c.d + nq + (size_t)c.heads * p.splits * (HD + 2) + qd + c.ffn + 2 * (size_t)p.blocks;
     if (!S.step_words.ptr) {
         S.step_words.alloc(words * 8);
         TRIT_HIP(hipMemsetAsync(S.step_words.ptr, 0, words * 8, s));
@@ -1016,20 +1060,23 @@ void decode_step_prepare(SessionImpl& S, hipStream_t s) {
     }
 }
 
-void decode_step_launch(SessionImpl& S, int step, int pos, hipStream_t s) {
+void decode_step_launch(SessionImpl& S, int step, int pos, int nsteps, hipStream_t s) {
     Plan p;
     if (!plan(S, p)) fail("decode step: the session's model does not fit the persistent step");
+    if (nsteps < 1 || nsteps >= (1 << 20)) fail("decode step: 1 to 2^20 - 1 steps a launch");
     const DecoderImpl& D = *S.dec;
     const auto& c = D.c;
     const int nq = (c.heads + 2 * c.kv_heads) * HD, qd = c.heads * HD;
-    // Tags: launch counter in the high 24 bits, phase in the low 8. When
-    // the counter would wrap, the words start over from zero.
-    if (++S.step_seq >= (1u << 24)) {
-        const size_t words = (size_t)c.d + nq + (size_t)c.heads * p.splits * (HD + 2) + qd + c.ffn;
+    // Tags: step counter in the high 24 bits, phase in the low 8. When the
+    // counter would wrap, the words start over from zero.
+    if (S.step_seq + (uint32_t)nsteps >= (1u << 24)) {
+        const size_t words =
+            (size_t)c.d + nq + (size_t)c.heads * p.splits * (HD + 2) + qd + c.ffn + 2 * (size_t)p.blocks;
         TRIT_HIP(hipMemsetAsync(S.step_words.ptr, 0, words * 8, s));
-        S.step_seq = 1;
+        S.step_seq = 0;
     }
-    const uint32_t tag0 = S.step_seq << 8;
+    const uint32_t seq0 = S.step_seq + 1;
+    S.step_seq += (uint32_t)nsteps;
     StepArgs a{};
     a.layers = S.step_table.as<LayerPtrs>();
     a.n_layers = c.layers;
@@ -1053,6 +1100,7 @@ void decode_step_launch(SessionImpl& S, int step, int pos, hipStream_t s) {
     a.PART = a.QKV + nq;
     a.ATT = a.PART + (size_t)c.heads * p.splits * (HD + 2);
     a.H = a.ATT + qd;
+    a.CAND = a.H + c.ffn;
     a.cand = S.step_cand.as<float2>();
     a.out = S.tokens_out.as<int>();
     a.st = S.st();
@@ -1067,7 +1115,7 @@ void decode_step_launch(SessionImpl& S, int step, int pos, hipStream_t s) {
     TRIT_HIP(hipGetDevice(&dev));
     TRIT_HIP(hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, dev));
     a.ticks = (unsigned long long)(rate_khz > 0 ? rate_khz : 100000) * 200ull;  // 200 ms
-    void* args[] = {&a, &step, &pos, (void*)&tag0};
+    void* args[] = {&a, &step, &pos, (void*)&seq0, &nsteps};
     TRIT_HIP(hipLaunchCooperativeKernel((const void*)p.fn, dim3(p.blocks), dim3(T), args, 0, s));
 }
 

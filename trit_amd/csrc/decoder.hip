@@ -1467,7 +1467,7 @@ static int generate_common(TritHipSession* session, int max_new, const int32_t* 
     else if (use_graph()) build_graph(S);
     if (ev_start) TRIT_HIP(hipEventRecord(ev_start, s));
     if (persistent) {
-        for (int i = 0; i < max_new; ++i) decode_step_launch(S, i, S.host_pos + i, s);
+        decode_step_launch(S, 0, S.host_pos, max_new, s);
         S.step_cand_fresh = true;
     } else if (use_graph()) {
         for (int i = 0; i < max_new; ++i) TRIT_HIP(hipGraphLaunch(S.graph, s));

@@ -79,8 +79,8 @@ bool decode_step_supported(const SessionImpl& S);
 // Prepares the exchange buffers and, when the last logits are newer than
 // the step's candidates, the candidates from the logits.
 void decode_step_prepare(SessionImpl& S, hipStream_t s);
-// One greedy step (choice, forward, head): launch `step` of a generate call
-// at cache position `pos`.
-void decode_step_launch(SessionImpl& S, int step, int pos, hipStream_t s);
+// Greedy steps `step` .. `step + nsteps - 1` of a generate call (choice,
+// forward, head each) in one launch, the first at cache position `pos`.
+void decode_step_launch(SessionImpl& S, int step, int pos, int nsteps, hipStream_t s);
 
 }  // namespace trit
