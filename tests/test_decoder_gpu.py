@@ -36,6 +36,17 @@ def mid(gpu):
     return w, O.Lm(MID, w, O.isa_best()), model.build_decoder(w)
 
 
+QS = dict(d=1024, ffn=3072, layers=2, heads=16, kv_heads=8, head_dim=128, vocab=3000, eps=1e-6, rope_base=1e6,
+          qk_norm=1)
+
+
+@pytest.fixture(scope="module")
+def qshape(gpu):
+    """Qwen3-0.6B's layer shapes with two layers: fits the persistent step."""
+    w = synth.lm_weights(QS, config=95, sigma=0.1, norm_jitter=0.2)
+    return w, O.Lm(QS, w, O.isa_best()), model.build_decoder(w)
+
+
 def test_mid_generate_exact(mid):
     print("case decoder mid exact", flush=True)
     w, ref, lm = mid
@@ -217,17 +228,16 @@ def test_generate_long_prompt(small, flags):
         check_fast_tokens(got, ref, p, 20, float(np.max(np.abs(logits - want_logits))), least=0 if flags == 0 else 5)
 
 
-def test_mid_step_fast(mid, monkeypatch):
-    """The persistent decode step (fast mode, f16 caches, the default for
-    this model): greedy tokens against the oracle's and the per-kernel
-    loop's, positions, a stop token, and a second generate call that
-    continues the first."""
-    print("case decoder mid persistent step", flush=True)
-    w, ref, lm = mid
-    p = synth.prompt(98, 40, MID["vocab"])
+def check_generate_fast(w, ref, lm, cfg, monkeypatch, persistent):
+    """Fast-mode greedy tokens (f16 caches, the default) against the
+    oracle's and the per-kernel loop's, positions, a stop token, a second
+    generate call that continues the first, and the caches the steps
+    wrote."""
+    p = synth.prompt(98, 40, cfg["vocab"])
     s = lm.session(96, 0)
     logits = s.prefill(p)
     got = s.generate(24)
+    assert s.persistent == persistent
     assert len(got) == 24
     assert s.position == 40 + 23
     ref.reset()
@@ -242,9 +252,26 @@ def test_mid_step_fast(mid, monkeypatch):
     k = lm.session(96, 0)
     k.prefill(p)
     kern = k.generate(24)
+    assert not k.persistent
     monkeypatch.delenv("TRIT_HIP_STEP")
     print(f"step {got.tolist()}\nkernel {kern.tolist()}", flush=True)
     assert got.tolist() == kern.tolist()
+
+    # The caches the steps wrote (every layer's keys and values of the 23
+    # forwarded tokens carry the steps' activations): one more token through
+    # the prompt path over them, against the per-kernel loop's caches and
+    # the oracle fed the same tokens.
+    nxt = np.array([int(got[-1])])
+    after_step = s.prefill(nxt)
+    after_kern = k.prefill(nxt)
+    ref.reset()
+    ref.forward(np.concatenate([p, got[:-1]]))
+    want_after = ref.forward(nxt)
+    print(f"after the steps: vs the per-kernel loop {rel(after_step, after_kern):.3g}, "
+          f"vs the oracle {rel(after_step, want_after):.3g} (loop vs oracle {rel(after_kern, want_after):.3g})",
+          flush=True)
+    assert rel(after_step, after_kern) < 2e-2
+    assert rel(after_step, want_after) < 5e-2
 
     # A stop token ends the loop without being kept.
     s2 = lm.session(96, 0)
@@ -263,6 +290,21 @@ def test_mid_step_fast(mid, monkeypatch):
     assert a.tolist() == got.tolist()[:10]
     assert b.tolist() == got.tolist()[9:19]
     assert s3.position == 40 + 18
+
+
+def test_step_fast(qshape, monkeypatch):
+    """The persistent decode step on Qwen3-0.6B's layer shapes."""
+    print("case decoder persistent step (qwen3 shapes)", flush=True)
+    w, ref, lm = qshape
+    check_generate_fast(w, ref, lm, QS, monkeypatch, persistent=True)
+
+
+def test_mid_generate_fast_f16(mid, monkeypatch):
+    """A model the persistent step's plan does not take (its combine would
+    poll from too few waves): the per-kernel loop, with the same checks."""
+    print("case decoder mid fast f16 caches", flush=True)
+    w, ref, lm = mid
+    check_generate_fast(w, ref, lm, MID, monkeypatch, persistent=False)
 
 
 def test_mid_flash_prefill(mid, monkeypatch):

@@ -433,9 +433,15 @@ __device__ bool attention(int t, const StepArgs& a, const LayerPtrs& L, int pos,
             const int which = hh - GROUP;
             const _Float16 c0 = (_Float16)x0, c1 = (_Float16)x1;
             if (j0 <= pos && pos < j1) {
-                _Float16* cache = (which == 0 ? L.kcache : L.vcache) + ((size_t)g * a.max_pos + pos) * HD;
-                cache[i] = c0;
-                cache[i + HD / 2] = c1;
+                // Later steps of this launch read them from other CUs: the
+                // stores are agent-scope (written through to where every CU
+                // reads).
+                uint16_t* cache =
+                    (uint16_t*)(which == 0 ? L.kcache : L.vcache) + ((size_t)g * a.max_pos + pos) * HD;
+                __hip_atomic_store(cache + i, __builtin_bit_cast(uint16_t, c0), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(cache + i + HD / 2, __builtin_bit_cast(uint16_t, c1), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
             }
             sm.kvn[which][i] = (float)c0;
             sm.kvn[which][i + HD / 2] = (float)c1;

@@ -234,10 +234,14 @@ class Session:
         return logits
 
     def generate(self, max_new, stop=()):
+        """Greedy tokens (trit_hip_session_generate); `self.persistent` then
+        tells whether they ran on the persistent decode step."""
         stop = np.ascontiguousarray(np.array(stop, np.int32).reshape(-1))
         out = np.empty(max(max_new, 1), np.int32)
-        n = check(lib().trit_hip_session_generate(self.h, max_new, ptr(stop) if stop.size else None, stop.size,
-                                                  ptr(out)))
+        persistent = C.c_int(0)
+        n = check(lib().trit_hip_session_generate_timed(self.h, max_new, ptr(stop) if stop.size else None,
+                                                        stop.size, ptr(out), None, None, C.byref(persistent)))
+        self.persistent = bool(persistent.value)
         return out[:n].copy()
 
     def reset(self):
