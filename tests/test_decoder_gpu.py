@@ -292,19 +292,28 @@ def check_generate_fast(w, ref, lm, cfg, monkeypatch, persistent):
     assert s3.position == 40 + 18
 
 
-def test_step_fast(qshape, monkeypatch):
-    """The persistent decode step on Qwen3-0.6B's layer shapes."""
-    print("case decoder persistent step (qwen3 shapes)", flush=True)
+@pytest.mark.parametrize("attention", ["one-pass", "split"])
+def test_step_fast(qshape, monkeypatch, attention):
+    """The persistent decode step on Qwen3-0.6B's layer shapes, with each
+    attention form: every key in one pass (up to 384 positions), or key
+    splits and their combine."""
+    print(f"case decoder persistent step (qwen3 shapes, {attention} attention)", flush=True)
     w, ref, lm = qshape
+    if attention == "split":
+        monkeypatch.setenv("TRIT_HIP_STEP_SPLIT", "1")
     check_generate_fast(w, ref, lm, QS, monkeypatch, persistent=True)
 
 
-def test_mid_generate_fast_f16(mid, monkeypatch):
-    """A model the persistent step's plan does not take (its combine would
-    poll from too few waves): the per-kernel loop, with the same checks."""
-    print("case decoder mid fast f16 caches", flush=True)
+@pytest.mark.parametrize("attention", ["one-pass", "split"])
+def test_mid_step_fast(mid, monkeypatch, attention):
+    """Two dims a block in the one-pass attention; the split form's combine
+    would poll from too few waves for this model, so it runs the per-kernel
+    loop (with the same checks)."""
+    print(f"case decoder mid fast f16 caches ({attention})", flush=True)
     w, ref, lm = mid
-    check_generate_fast(w, ref, lm, MID, monkeypatch, persistent=False)
+    if attention == "split":
+        monkeypatch.setenv("TRIT_HIP_STEP_SPLIT", "1")
+    check_generate_fast(w, ref, lm, MID, monkeypatch, persistent=attention == "one-pass")
 
 
 def test_mid_flash_prefill(mid, monkeypatch):

@@ -31,6 +31,7 @@
 #include "device.h"
 
 #include <climits>
+#include <type_traits>
 
 namespace trit {
 namespace {
@@ -39,6 +40,7 @@ constexpr int T = 512;         // threads per block
 constexpr int NW = T / WAVE;   // waves per block
 constexpr int HD = 128;        // head_dim
 constexpr int MAXC = 4;        // 32-key chunks of a split held in registers
+constexpr int MAXF = 12;       // 32-key chunks of the one-pass attention (384 positions)
 constexpr int MAXD = 2048;     // largest d
 constexpr int MAXK = 3072;     // largest product input
 constexpr int PH = 6;          // exchange phases per layer
@@ -228,6 +230,22 @@ __device__ __forceinline__ void load_rows(int t, const uint8_t* codes, const uin
             r.ws[p * ((J + 1) / 2) + j / 2] =
                 (uint32_t)sc[8 * j] | (j + 1 < J ? (uint32_t)sc[8 * (j + 1)] << 16 : 0u);
     }
+    // The rest of the set is zeroed: after any load no earlier rows stay live.
+#pragma unroll
+    for (int i = P * J; i < N; ++i) r.w[i] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int i = P * ((J + 1) / 2); i < NS; ++i) r.ws[i] = 0;
+}
+
+// The row set zeroed, in the waves that load no rows in a phase: every path
+// then writes the whole set before a product reads it, so no earlier rows
+// stay live through the phases in between (the attention needs the room).
+template <int N, int NS>
+__device__ __forceinline__ void zero_rows(Rows<N, NS>& r) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) r.w[i] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < NS; ++i) r.ws[i] = 0;
 }
 
 // RMSNorm factor of x (K = 256 J values in LDS) by one wave, the one-row
@@ -600,6 +618,183 @@ __device__ bool combine(int t, const StepArgs& a, uint32_t tag_in, uint32_t tag_
     return true;
 }
 
+// One pass over every key (sessions of up to 32 MAXF positions): block b
+// takes key/value head g = b % kvh -- so a head's blocks share an XCD and its
+// L2 -- and, of query head h = (b / kvh) % GROUP of that group, output dims
+// [DPB s, DPB s + DPB), s = b / (kvh GROUP). Every block scores all the
+// head's keys for its query head (16-lane group G the keys G + 32 i, lane
+// l16 dims [8 l16, 8 l16 + 8)), so it finishes the softmax itself and
+// stores its outputs as the o product's input: no partials and no combine
+// hand-over. Lane l16 of a group takes the probability and value of the
+// group's chunk l16; the groups' own maxima, sums and p.V meet in LDS, and
+// the first wave rescales them. (Measured: sparing the polling wave the key
+// loads, with 28 key groups, was slower; so was giving a head's blocks
+// consecutive indices, spread over the XCDs.)
+template <int GROUP, int DPB>
+__device__ bool attention_all(int t, const StepArgs& a, const LayerPtrs& L, int pos, uint32_t tag_in,
+                              uint32_t tag_out, Smem& sm, unsigned long long deadline) {
+    static_assert(DPB == 4 || DPB == 8, "4 or 8 dims a block");
+    const int b = blockIdx.x, kvh = a.kvh, g = b % kvh, hq = (b / kvh) % GROUP, e0 = DPB * (b / (kvh * GROUP));
+    const int tk = pos + 1, chunks = (tk + 31) / 32;
+    const int heads = a.heads;
+    const auto index = [g, heads, kvh](int i) {
+        if (i < GROUP * HD) return g * GROUP * HD + i;
+        if (i < (GROUP + 1) * HD) return (heads + g) * HD + (i - GROUP * HD);
+        return (heads + kvh + g) * HD + (i - (GROUP + 1) * HD);
+    };
+    // Every cached key and this block's value dims load while the qkv rows
+    // arrive; so do the q/k norm weights and the rotary values.
+    const _Float16* K = L.kcache + (size_t)g * a.max_pos * HD;
+    const _Float16* V = L.vcache + (size_t)g * a.max_pos * HD;
+    const int G = t >> 4, l16 = t & 15;
+    uint4 kr[MAXF];
+#pragma unroll
+    for (int i = 0; i < MAXF; ++i) {
+        kr[i] = make_uint4(0, 0, 0, 0);
+        if (i >= chunks) continue;  // uniform
+        const int j = G + 32 * i;
+        if (j < tk && j != pos) kr[i] = *(const uint4*)(K + (size_t)j * HD + l16 * 8);
+    }
+    using VT = typename std::conditional<DPB == 8, uint4, uint2>::type;
+    VT vr{};
+    const int jv = G + 32 * l16;  // the key of this lane's probability
+    if (l16 < chunks && jv < tk && jv != pos) vr = *(const VT*)(V + (size_t)jv * HD + e0);
+    const int hh = t / WAVE, i = t % WAVE;
+    float nw0 = 1.0f, nw1 = 1.0f, sn = 0.0f, cs = 1.0f;
+    if (hh <= GROUP) {
+        if (a.qk_norm) {
+            const float* nw = hh < GROUP ? L.q_norm : L.k_norm;
+            nw0 = nw[i];
+            nw1 = nw[i + HD / 2];
+        }
+        sn = a.rope_sin[(size_t)pos * (HD / 2) + i];
+        cs = a.rope_cos[(size_t)pos * (HD / 2) + i];
+    }
+    if (!gather<8>(t, a.QKV, (GROUP + 2) * HD, index, tag_in, sm.qkv, sm, deadline, a.st, NW - a.rq / 4 - 1))
+        return false;
+
+    // Qwen3's per-head RMSNorm and the rotary halves, wave hh head hh, lane
+    // i dims i and i + 64 (src/models/parts/causal_lm.rs:428-446,
+    // src/layers.rs:136-144,303-334); the first block of the head appends
+    // the new key and value (agent scope: later steps read them elsewhere).
+    if (hh < GROUP + 2) {
+        float x0 = sm.qkv[hh * HD + i], x1 = sm.qkv[hh * HD + i + HD / 2];
+        if (hh <= GROUP) {
+            if (a.qk_norm) {
+                const float sum = wave_sum(x0 * x0 + x1 * x1);
+                const float inv = 1.0f / __builtin_sqrtf(sum / (float)HD + a.eps);
+                x0 = x0 * (inv * nw0);
+                x1 = x1 * (inv * nw1);
+            }
+            const float ac = x0 * cs, bs = x1 * sn, bc = x1 * cs, as = x0 * sn;
+            x0 = ac - bs;
+            x1 = bc + as;
+        }
+        if (hh < GROUP) {
+            const float scale = 1.0f / __builtin_sqrtf((float)HD);
+            sm.qkv[hh * HD + i] = x0 * scale;
+            sm.qkv[hh * HD + i + HD / 2] = x1 * scale;
+        } else {
+            const int which = hh - GROUP;
+            const _Float16 c0 = (_Float16)x0, c1 = (_Float16)x1;
+            if (b < kvh) {
+                uint16_t* cache =
+                    (uint16_t*)(which == 0 ? L.kcache : L.vcache) + ((size_t)g * a.max_pos + pos) * HD;
+                __hip_atomic_store(cache + i, __builtin_bit_cast(uint16_t, c0), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(cache + i + HD / 2, __builtin_bit_cast(uint16_t, c1), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
+            sm.kvn[which][i] = (float)c0;
+            sm.kvn[which][i + HD / 2] = (float)c1;
+        }
+    }
+    __syncthreads();
+
+    // Scores of the group's keys for query head hq, and their maximum.
+    float q[8], kn[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        q[u] = sm.qkv[hq * HD + l16 * 8 + u];
+        kn[u] = sm.kvn[0][l16 * 8 + u];
+    }
+    float sc[MAXF], mx = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < MAXF; ++c) {
+        sc[c] = -INFINITY;
+        if (c >= chunks) continue;
+        const int j = G + 32 * c;
+        float k8[8];
+        if (j == pos) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) k8[u] = kn[u];
+        } else {
+            unpack8(kr[c], k8);
+        }
+        float acc = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(q[u], k8[u], acc);
+        acc = row16_sum(acc);
+        sc[c] = j < tk ? acc : -INFINITY;
+        mx = __builtin_fmaxf(mx, sc[c]);
+    }
+    // Lane l16: the probability of chunk l16's key against the group's
+    // maximum, times its value dims; then the group's sums.
+    float vv[DPB];
+    if (jv == pos) {
+#pragma unroll
+        for (int d = 0; d < DPB; ++d) vv[d] = sm.kvn[1][e0 + d];
+    } else {
+        const uint32_t* vw = (const uint32_t*)&vr;
+#pragma unroll
+        for (int d = 0; d < DPB; ++d) vv[d] = f16_to_f32((uint16_t)(vw[d / 2] >> (16 * (d & 1))));
+    }
+    float mine = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < MAXF; ++c)
+        if (c == l16) mine = sc[c];
+    const float p = mine == -INFINITY ? 0.0f : exp_trit(mine - mx);
+    float part[DPB + 1];
+#pragma unroll
+    for (int d = 0; d < DPB; ++d) part[d] = row16_sum(p * vv[d]);
+    part[DPB] = row16_sum(p);
+    if (l16 == 0) {
+        sm.gmax[G][0] = mx;
+        sm.gl[G][0] = part[DPB];
+#pragma unroll
+        for (int d = 0; d < DPB; ++d) sm.gpart[G][d] = part[d];
+    }
+    __syncthreads();
+
+    // The first wave: lane G rescales group G by exp(max_G - max) (lanes 32
+    // and up repeat lanes 0-31); the sums are shuffle trees; o / l is the
+    // output.
+    if (t < WAVE) {
+        const int gg = t & 31;
+        const float m = sm.gmax[gg][0];
+        float M = m;
+        M = __builtin_fmaxf(M, dpp<DPP_XOR1>(M));
+        M = __builtin_fmaxf(M, dpp<DPP_XOR2>(M));
+        M = __builtin_fmaxf(M, dpp<DPP_HALF_MIRROR>(M));
+        M = __builtin_fmaxf(M, dpp<DPP_MIRROR>(M));
+        M = __builtin_fmaxf(M, __shfl_xor(M, 16));
+        const float f = m == -INFINITY ? 0.0f : exp_trit(m - M);
+        float l = row16_sum(f * sm.gl[gg][0]);
+        l += __shfl_xor(l, 16);
+        float o[DPB];
+#pragma unroll
+        for (int d = 0; d < DPB; ++d) {
+            o[d] = row16_sum(f * sm.gpart[gg][d]);
+            o[d] += __shfl_xor(o[d], 16);
+        }
+        if (t == 0) {
+#pragma unroll
+            for (int d = 0; d < DPB; ++d) put(a.ATT + (size_t)(g * GROUP + hq) * HD + e0 + d, o[d] / l, tag_out);
+        }
+    }
+    return true;
+}
+
 __device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
     if (v > bv || (v == bv && i < bi)) {
         bv = v;
@@ -634,7 +829,7 @@ __device__ __forceinline__ void best_of_wave(float& bv, int& bi) {
     for (int r = 1; r < 4; ++r) better(bv, bi, v[r], i[r]);
 }
 
-template <int JD, int JO, int JF, int GROUP>
+template <int JD, int JO, int JF, int GROUP, int DPB>
 __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int pos0, uint32_t seq0, int nsteps) {
     __shared__ Smem sm;
     State* st = a.st;
@@ -761,19 +956,43 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             row_chain<JD, 1>(t, rr, sm, acc);
             if ((lane & 15) == 14) put(a.QKV + rowq, acc[0], tag_of(tag0, layer, 0));
         }
-        // attention partials.
         __syncthreads();
-        if (!attention<GROUP>(t, a, L, pos, tag_of(tag0, layer, 0), tag_of(tag0, layer, 1), sm, deadline)) return;
-        // combine; the o rows stream in meanwhile.
-        if (ao) load_rows<JO, 1>(t, L.codes[1], L.scales[1], 0, rowo, rr);
-        __syncthreads();
-        if (!combine(t, a, tag_of(tag0, layer, 1), tag_of(tag0, layer, 2), sm, deadline, nu + no)) return;
-        // o + residual; the gate_up rows stream in meanwhile.
-        if (agu) load_rows<JD, 2>(t, L.codes[2], L.scales[2], a.ffn, rowgu, rr);
-        __syncthreads();
-        // Polled from the first o wave on: the gate_up waves' loads are in
-        // flight.
-        if (!gather<8>(t, a.ATT, a.qd, lin, tag_of(tag0, layer, 2), sm.xin, sm, deadline, st, nu)) return;
+        if constexpr (DPB > 0) {
+            // attention in one pass: its outputs are the o product's input.
+            if (!attention_all<GROUP, DPB>(t, a, L, pos, tag_of(tag0, layer, 0), tag_of(tag0, layer, 2), sm,
+                                           deadline))
+                return;
+            // o + residual; the o and gate_up rows stream in meanwhile, and
+            // the qkv waves (nothing in flight) poll.
+            if (ao)
+                load_rows<JO, 1>(t, L.codes[1], L.scales[1], 0, rowo, rr);
+            else
+                zero_rows(rr);
+            if (agu) load_rows<JD, 2>(t, L.codes[2], L.scales[2], a.ffn, rowgu, rr);
+            __syncthreads();
+            if (!gather<8>(t, a.ATT, a.qd, lin, tag_of(tag0, layer, 2), sm.xin, sm, deadline, st, NW - nqw))
+                return;
+        } else {
+            // attention partials.
+            if (!attention<GROUP>(t, a, L, pos, tag_of(tag0, layer, 0), tag_of(tag0, layer, 1), sm, deadline))
+                return;
+            // combine; the o rows stream in meanwhile.
+            if (ao)
+                load_rows<JO, 1>(t, L.codes[1], L.scales[1], 0, rowo, rr);
+            else
+                zero_rows(rr);
+            __syncthreads();
+            if (!combine(t, a, tag_of(tag0, layer, 1), tag_of(tag0, layer, 2), sm, deadline, nu + no)) return;
+            // o + residual; the gate_up rows stream in meanwhile.
+            if (agu)
+                load_rows<JD, 2>(t, L.codes[2], L.scales[2], a.ffn, rowgu, rr);
+            else if (!ao)  // the o rows are still to be used
+                zero_rows(rr);
+            __syncthreads();
+            // Polled from the first o wave on: the gate_up waves' loads are
+            // in flight.
+            if (!gather<8>(t, a.ATT, a.qd, lin, tag_of(tag0, layer, 2), sm.xin, sm, deadline, st, nu)) return;
+        }
         quantize_block<JO>(t, sm.xin, (const NormRegs<JO>*)nullptr, sm);
         if (ao) {
             float acc[1];
@@ -797,7 +1016,10 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             if ((lane & 15) == 14) put(a.H + rowgu, silu_trit(acc[0]) * acc[1], tag_of(tag0, layer, 4));
         }
         // down + residual.
-        if (ad) load_rows<JF, 1>(t, L.codes[3], L.scales[3], 0, rowd, rr);
+        if (ad)
+            load_rows<JF, 1>(t, L.codes[3], L.scales[3], 0, rowd, rr);
+        else
+            zero_rows(rr);
         if (aq && layer + 1 < a.n_layers)
             load_rows<JD, 1>(t, a.layers[layer + 1].codes[0], a.layers[layer + 1].scales[0], 0, rowq, rr);
         __syncthreads();
@@ -953,9 +1175,17 @@ __global__ __launch_bounds__(256) void cand_kernel(const float* __restrict__ log
 using StepFn = void (*)(StepArgs, int, int, uint32_t, int);
 
 // The instantiated shapes: (d/256, heads*hd/256, ffn/256, q heads per kv head).
-StepFn step_fn(int jd, int jo, int jf, int group) {
-    if (jd == 4 && jo == 8 && jf == 12 && group == 2) return step_kernel<4, 8, 12, 2>;  // Qwen3-0.6B
-    if (jd == 4 && jo == 4 && jf == 8 && group == 2) return step_kernel<4, 4, 8, 2>;
+// dpb: output dims of one query head a block takes in the one-pass
+// attention, 0 for the split attention and its combine.
+StepFn step_fn(int jd, int jo, int jf, int group, int dpb) {
+    if (jd == 4 && jo == 8 && jf == 12 && group == 2) {  // Qwen3-0.6B
+        if (dpb == 0) return step_kernel<4, 8, 12, 2, 0>;
+        if (dpb == 8) return step_kernel<4, 8, 12, 2, 8>;
+    }
+    if (jd == 4 && jo == 4 && jf == 8 && group == 2) {
+        if (dpb == 0) return step_kernel<4, 4, 8, 2, 0>;
+        if (dpb == 4) return step_kernel<4, 4, 8, 2, 4>;
+    }
     return nullptr;
 }
 
@@ -968,9 +1198,16 @@ int device_blocks() {
 }
 
 struct Plan {
-    int blocks, splits, comb, rq, ro, rgu, rd, rh;
+    int blocks, splits, comb, dpb, rq, ro, rgu, rd, rh;
     StepFn fn;
 };
+
+// The one-pass attention unless TRIT_HIP_STEP_SPLIT=1 asks for the split
+// attention and its combine (which also serve longer sessions).
+bool split_forced() {
+    const char* v = getenv("TRIT_HIP_STEP_SPLIT");
+    return v && v[0] == '1';
+}
 
 bool plan(const SessionImpl& S, Plan& p) {
     const DecoderImpl& D = *S.dec;
@@ -980,8 +1217,6 @@ bool plan(const SessionImpl& S, Plan& p) {
     const int group = c.heads / c.kv_heads, qd = c.heads * HD;
     if (c.d % 256 || qd % 256 || c.ffn % 256 || c.d > MAXD || qd > MAXK || c.ffn > MAXK) return false;
     if (c.layers <= 0 || c.layers * PH + PH >= 256) return false;
-    p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group);
-    if (!p.fn) return false;
     auto q8 = [](const LayerRef& L) { return (L->kind == Q8_0 || L->kind == Q4_K) && !L->bias.ptr; };
     for (int l = 0; l < c.layers; ++l)
         if (!q8(D.qkv[l]) || !q8(D.o[l]) || !q8(D.gate_up[l]) || !q8(D.down[l])) return false;
@@ -989,11 +1224,6 @@ bool plan(const SessionImpl& S, Plan& p) {
     if (head.kind != F16 || head.k != c.d || head.bias.ptr || D.embed->kind != F16) return false;
     p.blocks = device_blocks();
     if (p.blocks < c.kv_heads || p.blocks % c.kv_heads) return false;
-    p.splits = p.blocks / c.kv_heads;
-    if (S.max_pos > p.splits * 32 * MAXC) return false;
-    if ((qd % p.blocks) || HD % (qd / p.blocks)) return false;
-    p.comb = qd / p.blocks;
-    if (p.splits > WAVE || p.comb > NW || p.splits * (2 + p.comb) > MAXK) return false;
     const int nq = (c.heads + 2 * c.kv_heads) * HD;
     auto rows = [&](int n, int& r) {
         if (n % (4 * p.blocks)) return false;
@@ -1006,9 +1236,27 @@ bool plan(const SessionImpl& S, Plan& p) {
     const int nu = p.rgu / 4, no = p.ro / 4, nd = p.rd / 4, nqw = p.rq / 4;
     if (nu + std::max(no, nd) + nqw > NW) return false;
     auto fits = [](int n, int p0, int mw) { return p0 + (n + WAVE * mw - 1) / (WAVE * mw) <= NW; };
-    if (!fits((group + 2) * HD, NW - nqw - 1, 8) || !fits(p.splits * (2 + p.comb), NW - nqw, 2)) return false;
-    if (!fits(c.d, 0, 6) || !fits(qd, nu, 8) || !fits(c.ffn, 0, MAXK / T)) return false;
+    if (!fits((group + 2) * HD, NW - nqw - 1, 8)) return false;
+    if (!fits(c.d, 0, 6) || !fits(c.ffn, 0, MAXK / T)) return false;
     if (!fits(2 * p.blocks, 0, MAXD / T)) return false;  // the candidates' words
+    p.splits = p.blocks / c.kv_heads;
+    p.comb = qd / p.blocks;
+    // The one-pass attention: every key of the session in registers, each
+    // block dpb dims of one query head.
+    p.dpb = (qd % p.blocks) ? 0 : qd / p.blocks;
+    const bool one_pass = !split_forced() && S.max_pos <= 32 * MAXF && (p.dpb == 4 || p.dpb == 8) &&
+                          p.blocks % (c.kv_heads * group) == 0 && fits(qd, NW - nqw, 8);
+    if (one_pass) {
+        p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group, p.dpb);
+    } else {
+        p.dpb = 0;
+        if (S.max_pos > p.splits * 32 * MAXC) return false;
+        if ((qd % p.blocks) || HD % p.comb) return false;
+        if (p.splits > WAVE || p.comb > NW || p.splits * (2 + p.comb) > MAXK) return false;
+        if (!fits(p.splits * (2 + p.comb), NW - nqw, 2) || !fits(qd, nu, 8)) return false;
+        p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group, 0);
+    }
+    if (!p.fn) return false;
     p.rh = (c.vocab + p.blocks - 1) / p.blocks;
     return true;
 }
