@@ -50,7 +50,7 @@ GATE_UP_TRAFFIC_BYTES = round((3313.1 * 2.0 + 48.0) * 1024)
 # runs (profiles/decode_step_qwen3_0.6b_hbm_traffic.md): FETCH_SIZE and
 # WRITE_SIZE of one launch of 128 steps (127 forwards, positions 256..382)
 # over the forwards, FETCH_SIZE x 2.0 plus WRITE_SIZE x 1.0.
-STEP_FETCH_KIB, STEP_WRITE_KIB = 434748.3, 19624.1
+STEP_FETCH_KIB, STEP_WRITE_KIB = 406372.0, 3944.1
 STEP_TRAFFIC_BYTES = round((STEP_FETCH_KIB * 2.0 + STEP_WRITE_KIB) * 1024)
 
 
@@ -306,8 +306,8 @@ def step_roofline(cfg, prompt, steps, step_ms, persistent):
     return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                 frac=round(achieved / HBM_PEAK_GBS, 4),
                 traffic=STEP_TRAFFIC_BYTES * forwards if persistent else None,
-                kernel=f"step_kernel<4,8,12,2>: the persistent decode step, {steps} steps (choice, 28 layers, "
-                       "head) in one launch" if persistent else "the per-kernel decode step (graph replay)",
+                kernel=f"step_kernel<4,8,12,2,8>: the persistent decode step (one-pass attention), {steps} steps "
+                       "(choice, 28 layers, head) in one launch" if persistent else "the per-kernel decode step (graph replay)",
                 bytes_per_launch=per_launch, bytes_per_forward=per_forward, forwards=forwards,
                 avg_us=round(avg_ms * 1e3, 3), us_per_forward=round(step_ms * 1e3 / forwards, 3),
                 traffic_per_forward=STEP_TRAFFIC_BYTES if persistent else None, launches=launches,
