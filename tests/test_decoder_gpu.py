@@ -306,9 +306,9 @@ def test_step_fast(qshape, monkeypatch, attention):
 
 @pytest.mark.parametrize("attention", ["one-pass", "split"])
 def test_mid_step_fast(mid, monkeypatch, attention):
-    """Two dims a block in the one-pass attention; the split form's combine
-    would poll from too few waves for this model, so it runs the per-kernel
-    loop (with the same checks)."""
+    """Four KV heads: four dims of one query head a block in the one-pass
+    attention; the split form's combine would poll from too few waves for
+    this model, so it runs the per-kernel loop (with the same checks)."""
     print(f"case decoder mid fast f16 caches ({attention})", flush=True)
     w, ref, lm = mid
     if attention == "split":
