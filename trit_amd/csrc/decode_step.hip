@@ -712,25 +712,27 @@ __device__ bool attention_all(int t, const StepArgs& a, const LayerPtrs& L, int 
     __syncthreads();
 
     // Scores of the group's keys for query head hq, and their maximum.
-    float q[8], kn[8];
+    // The new key (the key at pos, in one group's last chunk) is taken as
+    // cached, f16 bits selected in place of the loaded ones: no branches.
+    float q[8];
+    uint32_t knb[4];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-        q[u] = sm.qkv[hq * HD + l16 * 8 + u];
-        kn[u] = sm.kvn[0][l16 * 8 + u];
-    }
+    for (int u = 0; u < 8; ++u) q[u] = sm.qkv[hq * HD + l16 * 8 + u];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+        knb[u] = (uint32_t)f32_to_f16(sm.kvn[0][l16 * 8 + 2 * u]) |
+                 ((uint32_t)f32_to_f16(sm.kvn[0][l16 * 8 + 2 * u + 1]) << 16);
     float sc[MAXF], mx = -INFINITY;
 #pragma unroll
     for (int c = 0; c < MAXF; ++c) {
         sc[c] = -INFINITY;
         if (c >= chunks) continue;
         const int j = G + 32 * c;
+        const bool fresh_key = j == pos;
+        const uint4 kb = make_uint4(fresh_key ? knb[0] : kr[c].x, fresh_key ? knb[1] : kr[c].y,
+                                    fresh_key ? knb[2] : kr[c].z, fresh_key ? knb[3] : kr[c].w);
         float k8[8];
-        if (j == pos) {
-#pragma unroll
-            for (int u = 0; u < 8; ++u) k8[u] = kn[u];
-        } else {
-            unpack8(kr[c], k8);
-        }
+        unpack8(kb, k8);
         float acc = 0.0f;
 #pragma unroll
         for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(q[u], k8[u], acc);
@@ -741,13 +743,14 @@ __device__ bool attention_all(int t, const StepArgs& a, const LayerPtrs& L, int 
     // Lane l16: the probability of chunk l16's key against the group's
     // maximum, times its value dims; then the group's sums.
     float vv[DPB];
-    if (jv == pos) {
-#pragma unroll
-        for (int d = 0; d < DPB; ++d) vv[d] = sm.kvn[1][e0 + d];
-    } else {
+    {
         const uint32_t* vw = (const uint32_t*)&vr;
+        const bool fresh_value = jv == pos;
 #pragma unroll
-        for (int d = 0; d < DPB; ++d) vv[d] = f16_to_f32((uint16_t)(vw[d / 2] >> (16 * (d & 1))));
+        for (int d = 0; d < DPB; ++d) {
+            const float loaded = f16_to_f32((uint16_t)(vw[d / 2] >> (16 * (d & 1))));
+            vv[d] = fresh_value ? sm.kvn[1][e0 + d] : loaded;
+        }
     }
     float mine = -INFINITY;
 #pragma unroll
@@ -766,11 +769,12 @@ __device__ bool attention_all(int t, const StepArgs& a, const LayerPtrs& L, int 
     }
     __syncthreads();
 
-    // The first wave: lane G rescales group G by exp(max_G - max) (lanes 32
-    // and up repeat lanes 0-31); the sums are shuffle trees; o / l is the
-    // output.
+    // The first wave: lane G of each half rescales group G by
+    // exp(max_G - max); the sums are shuffle trees over the half's 32 lanes,
+    // the first half the first DPB / 2 outputs, the second the rest; o / l
+    // is the output.
     if (t < WAVE) {
-        const int gg = t & 31;
+        const int gg = t & 31, half = t >> 5;
         const float m = sm.gmax[gg][0];
         float M = m;
         M = __builtin_fmaxf(M, dpp<DPP_XOR1>(M));
@@ -781,15 +785,17 @@ __device__ bool attention_all(int t, const StepArgs& a, const LayerPtrs& L, int 
         const float f = m == -INFINITY ? 0.0f : exp_trit(m - M);
         float l = row16_sum(f * sm.gl[gg][0]);
         l += __shfl_xor(l, 16);
-        float o[DPB];
+        constexpr int DH = DPB / 2;
+        float o[DH];
 #pragma unroll
-        for (int d = 0; d < DPB; ++d) {
-            o[d] = row16_sum(f * sm.gpart[gg][d]);
+        for (int d = 0; d < DH; ++d) {
+            o[d] = row16_sum(f * sm.gpart[gg][DH * half + d]);
             o[d] += __shfl_xor(o[d], 16);
         }
-        if (t == 0) {
+        if (gg == 0) {
 #pragma unroll
-            for (int d = 0; d < DPB; ++d) put(a.ATT + (size_t)(g * GROUP + hq) * HD + e0 + d, o[d] / l, tag_out);
+            for (int d = 0; d < DH; ++d)
+                put(a.ATT + (size_t)(g * GROUP + hq) * HD + e0 + DH * half + d, o[d] / l, tag_out);
         }
     }
     return true;
