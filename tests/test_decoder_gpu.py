@@ -304,6 +304,33 @@ def test_step_fast(qshape, monkeypatch, attention):
     check_generate_fast(w, ref, lm, QS, monkeypatch, persistent=True)
 
 
+@pytest.mark.parametrize("prompt,steps,max_pos", [(330, 54, 384), (700, 40, 760)])
+def test_step_fast_long(qshape, prompt, steps, max_pos):
+    """Sessions at the one-pass attention's limit (384 positions: all 12
+    chunks of 32 keys) and past it (the split attention takes over): the
+    step's tokens against the oracle's up to the first near-tie, and the
+    caches it wrote against the prompt path's fed the same tokens (so that
+    a near-tie choice cannot make the two diverge)."""
+    print(f"case decoder persistent step long (prompt {prompt}, {steps} steps, {max_pos} positions)", flush=True)
+    w, ref, lm = qshape
+    p = synth.prompt(97, prompt, QS["vocab"])
+    s = lm.session(max_pos, 0)
+    logits = s.prefill(p)
+    got = s.generate(steps)
+    assert s.persistent
+    assert len(got) == steps and s.position == prompt + steps - 1
+    ref.reset()
+    want_logits = ref.forward(p)
+    assert rel(logits, want_logits) < 5e-2
+    check_fast_tokens(got, ref, p, steps, float(np.max(np.abs(logits - want_logits))), least=0)
+    k = lm.session(max_pos, 0)
+    k.prefill(np.concatenate([p, got[:-1]]), want_logits=False)
+    nxt = np.array([int(got[-1])])
+    after_step, after_prompt = s.prefill(nxt), k.prefill(nxt)
+    print(f"after the steps: vs the prompt path {rel(after_step, after_prompt):.3g}", flush=True)
+    assert rel(after_step, after_prompt) < 2e-2
+
+
 @pytest.mark.parametrize("attention", ["one-pass", "split"])
 def test_mid_step_fast(mid, monkeypatch, attention):
     """Four KV heads: four dims of one query head a block in the one-pass
