@@ -189,6 +189,48 @@ int trit_hip_session_position(const TritHipSession *session);
 
 void trit_hip_session_free(TritHipSession *session);
 
+/* ---- GGUF files (reference src/models/gguf/mod.rs:130-300) ------------- */
+
+typedef struct TritHipGguf TritHipGguf;
+
+/* Opens and checks a GGUF v2/v3 file: the magic, the version, the metadata
+ * (strings and arrays of at most 2^24 entries, arrays nested at most 4
+ * deep), a tensor count the file can hold, general.alignment (32 when
+ * absent, never 0), and every tensor's byte range for its ggml type (F32,
+ * F16, BF16, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K, Q6_K). Replaces
+ * Gguf::open (gguf/mod.rs:155-226) with ggml_quants::layout
+ * (src/cpu/ggml_quants.rs:51-75); the error texts are the reference's,
+ * prefixed by the path. Host only: needs no device. */
+int trit_hip_gguf_open(const char *path, TritHipGguf **out);
+void trit_hip_gguf_free(TritHipGguf *gguf);
+int trit_hip_gguf_tensor_count(const TritHipGguf *gguf);
+
+/* Tensor `index` in file order: its name, ggml type name, dims (ne0 first,
+ * up to 4 written), and byte range [start, end) of the file. Any output
+ * may be NULL; the strings live as long as the handle. */
+int trit_hip_gguf_tensor(const TritHipGguf *gguf, int index, const char **name, const char **dtype, int *n_dims,
+                         int64_t *dims, int64_t *start, int64_t *end);
+
+/* Metadata of `key`: an integer (unsigned, or signed and not negative), a
+ * number, or a string (living as long as the handle). -1 when the key is
+ * absent or of another kind (Gguf::get / num, gguf/mod.rs:242-249). */
+int trit_hip_gguf_meta_u64(const TritHipGguf *gguf, const char *key, uint64_t *out);
+int trit_hip_gguf_meta_f64(const TritHipGguf *gguf, const char *key, double *out);
+int trit_hip_gguf_meta_str(const TritHipGguf *gguf, const char *key, const char **out);
+
+/* A decoder from the language model of a GGUF file as transcribe.cpp
+ * writes it: the shape under `prefix` (NULL: from general.architecture,
+ * `stt.qwen3_asr.decoder` for qwen3_asr; keys hidden_size,
+ * intermediate_size, n_layers, n_heads, n_kv_heads, head_dim, vocab_size,
+ * rms_norm_eps, rope_theta, tie_word_embeddings, gguf/blocks.rs:25-45) and
+ * the `dec.*` tensors (gguf/qwen3_asr.rs:103-136; qk_norm when
+ * attn.q_norm is there). Q8_0 and Q4_K linears (q, k, v stacked; gate, up
+ * stacked), F32/F16 norms, an F16 or F32 token table; output.weight only
+ * when the head is untied. The config read is written to *config (may be
+ * NULL). Replaces the GGUF branch of CausalLm::from_tensors
+ * (causal_lm.rs:141-198) for these files. */
+int trit_hip_decoder_from_gguf(const char *path, const char *prefix, TritHipLmConfig *config, TritHipDecoder **out);
+
 #ifdef __cplusplus
 }
 #endif

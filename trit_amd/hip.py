@@ -66,6 +66,15 @@ def lib():
             "trit_hip_session_reset": (i, [p]),
             "trit_hip_session_position": (i, [p]),
             "trit_hip_session_free": (None, [p]),
+            "trit_hip_gguf_open": (i, [C.c_char_p, pp]),
+            "trit_hip_gguf_free": (None, [p]),
+            "trit_hip_gguf_tensor_count": (i, [p]),
+            "trit_hip_gguf_tensor": (i, [p, i, C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), C.POINTER(i),
+                                         C.POINTER(C.c_int64), C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
+            "trit_hip_gguf_meta_u64": (i, [p, C.c_char_p, C.POINTER(C.c_uint64)]),
+            "trit_hip_gguf_meta_f64": (i, [p, C.c_char_p, C.POINTER(C.c_double)]),
+            "trit_hip_gguf_meta_str": (i, [p, C.c_char_p, C.POINTER(C.c_char_p)]),
+            "trit_hip_decoder_from_gguf": (i, [C.c_char_p, C.c_char_p, C.POINTER(LmConfig), pp]),
         }
         for name, (res, args) in sig.items():
             if not hasattr(L, name):
@@ -190,6 +199,19 @@ class CausalLm:
                                          C.byref(out)))
         self.h = out
 
+    @classmethod
+    def from_gguf(cls, path, prefix=None):
+        """The decoder of a GGUF file (trit_hip_decoder_from_gguf)."""
+        self = cls.__new__(cls)
+        c = LmConfig()
+        out = C.c_void_p()
+        check(lib().trit_hip_decoder_from_gguf(str(path).encode(), prefix.encode() if prefix else None,
+                                               C.byref(c), C.byref(out)))
+        self.h = out
+        self.cfg = dict(d=c.d, ffn=c.ffn, layers=c.layers, heads=c.heads, kv_heads=c.kv_heads,
+                        head_dim=c.head_dim, vocab=c.vocab, eps=c.eps, rope_base=c.rope_base, qk_norm=c.qk_norm)
+        return self
+
     def session(self, max_positions, flags=0):
         return Session(self, max_positions, flags)
 
@@ -205,6 +227,55 @@ class CausalLm:
     def free(self):
         if self.h:
             lib().trit_hip_decoder_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Gguf:
+    """A checked GGUF file (trit_hip_gguf_open; Gguf::open,
+    src/models/gguf/mod.rs:155-226). Host only."""
+
+    def __init__(self, path):
+        out = C.c_void_p()
+        check(lib().trit_hip_gguf_open(str(path).encode(), C.byref(out)))
+        self.h = out
+
+    def tensors(self):
+        """[(name, ggml type name, dims (ne0 first), start, end)] in file order."""
+        res = []
+        for i in range(check(lib().trit_hip_gguf_tensor_count(self.h))):
+            name, dtype, nd = C.c_char_p(), C.c_char_p(), C.c_int()
+            dims = (C.c_int64 * 4)()
+            start, end = C.c_int64(), C.c_int64()
+            check(lib().trit_hip_gguf_tensor(self.h, i, C.byref(name), C.byref(dtype), C.byref(nd), dims,
+                                             C.byref(start), C.byref(end)))
+            res.append((name.value.decode(), dtype.value.decode(), list(dims[: min(nd.value, 4)]), start.value,
+                        end.value))
+        return res
+
+    def u64(self, key):
+        v = C.c_uint64()
+        check(lib().trit_hip_gguf_meta_u64(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def f64(self, key):
+        v = C.c_double()
+        check(lib().trit_hip_gguf_meta_f64(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def str(self, key):
+        v = C.c_char_p()
+        check(lib().trit_hip_gguf_meta_str(self.h, key.encode(), C.byref(v)))
+        return v.value.decode()
+
+    def free(self):
+        if self.h:
+            lib().trit_hip_gguf_free(self.h)
             self.h = None
 
     def __del__(self):
