@@ -34,6 +34,31 @@ def test_q8_0(gpu, n, k, m):
     assert bits_equal(got, ref), np.max(np.abs(got - ref))
 
 
+# Products of a few tens of MB and 2..8 rows run on the streaming kernel
+# (persistent waves, segments of 1024 inputs); same bits.
+@pytest.mark.parametrize("n,k,m", [(16384, 3072, 1), (3072, 8192, 1), (4096, 3072, 4), (4096, 4096, 7),
+                                   (8192, 2048, 8), (12288, 1024, 3)])
+def test_q8_0_stream(gpu, n, k, m):
+    print(f"case q8_0 stream n={n} k={k} m={m}", flush=True)
+    codes, sbits, blocks = q8_layer(synth.seed_for(3, n + k), n, k)
+    x = synth.activations(synth.seed_for(3, 7 + m), m, k)
+    ref = O.Int8(codes, sbits.view(np.float16).astype(np.float32), 32, True)(x)
+    got = gpu.Dense.q8_0(n, k, blocks).forward(x)
+    assert bits_equal(got, ref), np.max(np.abs(got - ref))
+
+
+def test_q8_0_stream_bias_relu(gpu):
+    n, k = 2048, 4096
+    codes, sbits, blocks = q8_layer(14, n, k)
+    bias = synth.activations(15, 1, n)[0]
+    for m in (1, 3):
+        print(f"case q8_0 stream bias relu m={m}", flush=True)
+        x = synth.activations(16 + m, m, k)
+        ref = np.maximum(O.Int8(codes, sbits.view(np.float16).astype(np.float32), 32, True)(x) + bias, 0)
+        got = gpu.Dense.q8_0(n, k, blocks, bias).forward(x, relu=True)
+        assert bits_equal(got, ref)
+
+
 def test_q8_0_bias_relu(gpu):
     n, k = 256, 512
     codes, sbits, blocks = q8_layer(11, n, k)

@@ -23,6 +23,7 @@
 #include "internal.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <map>
 #include <mutex>
 
@@ -62,7 +63,6 @@ struct Smem {
     float* res;    // P*R*m chain results (pair epilogue)
 };
 
-__host__ __device__ __forceinline__ size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
 
 // Maximum and sum over the TPG consecutive lanes of a quantizer group
 // (TPG = 8 or 32): DPP inside rows of 16 lanes, one cross-row shuffle for
@@ -342,16 +342,7 @@ __device__ __forceinline__ int chunk_dot(const Chunk<W>& c, const int8_t* xq, in
     return d;
 }
 
-// Row stride (ints) of a (row, frame) pair's group dots in LDS: 16-byte rows.
-__host__ __device__ __forceinline__ int dot_stride(int groups) { return (groups + 4) & ~3; }
 
-// Bytes of the quantized rows' image: codes m x k, then f32 scales and i32
-// code sums m x dot_stride(k / G) each, every part 16-byte aligned -- the
-// first bytes of the product kernel's LDS, in the same layout.
-__host__ __device__ __forceinline__ size_t pre_bytes(int m, int k, int G) {
-    const size_t gs = (size_t)dot_stride(k / G);
-    return align16((size_t)m * k) + 2 * align16((size_t)m * gs * 4);
-}
 
 // RMSNorm factor of one row by the whole block, with the sum trees of
 // quantize_rows (so both paths give a row the same bits); every thread
@@ -730,6 +721,7 @@ void dispatch(const Layer& L, const GemvArgs& a0, hipStream_t s) {
         a.pre = (const uint8_t*)a.scratch;
         a.ev_start = nullptr;
     }
+    if (std::is_same<W, Q8>::value && gemv_stream(L, a, s)) return;
     if (a.epilogue == EPI_SILU_PAIR) return dispatch_rows<W, 2>(L, a, s);
     return dispatch_rows<W, 1>(L, a, s);
 }
@@ -740,6 +732,7 @@ size_t gemv_scratch_bytes(int m, int k) { return pre_bytes(m, k, 32) > pre_bytes
 
 void gemv_int(const Layer& L, const GemvArgs& a, hipStream_t s) {
     if (a.m < 1 || a.m > MAXF) fail("gemv: 1 to 8 rows per call");
+    if (a.m == 1 && gemv_stream(L, a, s)) return;
     if (gemv_row(L, a, s)) return;
     if (a.epilogue == EPI_SILU_PAIR && (L.n % 2 != 0)) fail("gemv: the SwiGLU pair needs an even row count");
     switch (L.kind) {

@@ -137,10 +137,25 @@ void launch_timed(const GemvArgs& a, K kernel, dim3 grid, dim3 block, size_t lds
         hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
 }
 
+__host__ __device__ __forceinline__ size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
+// Row stride (ints) of a (row, frame) pair's group dots in LDS: 16-byte rows.
+__host__ __device__ __forceinline__ int dot_stride(int groups) { return (groups + 4) & ~3; }
+// Bytes of the quantized rows' image: codes m x k, then f32 scales and i32
+// code sums m x dot_stride(k / G) each, every part 16-byte aligned -- the
+// first bytes of the product kernel's LDS, in the same layout.
+__host__ __device__ __forceinline__ size_t pre_bytes(int m, int k, int G) {
+    const size_t gs = (size_t)dot_stride(k / G);
+    return align16((size_t)m * k) + 2 * align16((size_t)m * gs * 4);
+}
+
 // Integer products (Q8_0, Q4_K, INT8, TERNARY), m <= 8.
 void gemv_int(const Layer& L, const GemvArgs& a, hipStream_t s);
 // Scratch bytes that let gemv_int quantize m rows of k inputs once.
 size_t gemv_scratch_bytes(int m, int k);
+// Q8_0 / Q4_K products of 1..8 rows over large weights by persistent
+// streaming waves; false when the shape, the kind or the size is not one it
+// takes. Two or more rows need the quantization pass's image in a.pre.
+bool gemv_stream(const Layer& L, const GemvArgs& a, hipStream_t s);
 // The one-row Q8_0 decode product (k 1024, 2048 or 3072); false when the
 // shape or kind is not one it takes.
 bool gemv_row(const Layer& L, const GemvArgs& a, hipStream_t s);
