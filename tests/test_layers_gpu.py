@@ -140,6 +140,19 @@ def test_ternary_4096(gpu, m):
     assert bits_equal(got, ref)
 
 
+# The streaming kernel's ternary form (k a multiple of 2048), 1..8 rows.
+@pytest.mark.parametrize("n,k,m", [(2048, 2048, 1), (8192, 4096, 3), (1024, 6144, 8), (4096, 2048, 2)])
+def test_ternary_stream(gpu, n, k, m):
+    print(f"case ternary stream n={n} k={k} m={m}", flush=True)
+    codes, scales = ternary_inputs(n, k)
+    # A scale per (row, 128-group), so that a wrong group index shows.
+    scales = (scales * (0.5 + synth.uniform(37, scales.shape))).astype(np.float32)
+    x = synth.activations(36 + m, m, k)
+    ref = O.Ternary(codes, scales)(x)
+    got = gpu.Dense.ternary(codes, scales).forward(x)
+    assert bits_equal(got, ref)
+
+
 def test_ternary_base3(gpu):
     n, k = 64, 640
     codes, scales = ternary_inputs(n, k)

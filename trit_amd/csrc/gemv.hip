@@ -721,7 +721,7 @@ void dispatch(const Layer& L, const GemvArgs& a0, hipStream_t s) {
         a.pre = (const uint8_t*)a.scratch;
         a.ev_start = nullptr;
     }
-    if (std::is_same<W, Q8>::value && gemv_stream(L, a, s)) return;
+    if ((std::is_same<W, Q8>::value || std::is_same<W, T2>::value) && gemv_stream(L, a, s)) return;
     if (a.epilogue == EPI_SILU_PAIR) return dispatch_rows<W, 2>(L, a, s);
     return dispatch_rows<W, 1>(L, a, s);
 }
@@ -732,7 +732,7 @@ size_t gemv_scratch_bytes(int m, int k) { return pre_bytes(m, k, 32) > pre_bytes
 
 void gemv_int(const Layer& L, const GemvArgs& a, hipStream_t s) {
     if (a.m < 1 || a.m > MAXF) fail("gemv: 1 to 8 rows per call");
-    if (a.m == 1 && gemv_stream(L, a, s)) return;
+    if (gemv_stream(L, a, s)) return;  // rows quantized in the block
     if (gemv_row(L, a, s)) return;
     if (a.epilogue == EPI_SILU_PAIR && (L.n % 2 != 0)) fail("gemv: the SwiGLU pair needs an even row count");
     switch (L.kind) {

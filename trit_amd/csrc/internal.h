@@ -152,9 +152,10 @@ __host__ __device__ __forceinline__ size_t pre_bytes(int m, int k, int G) {
 void gemv_int(const Layer& L, const GemvArgs& a, hipStream_t s);
 // Scratch bytes that let gemv_int quantize m rows of k inputs once.
 size_t gemv_scratch_bytes(int m, int k);
-// Q8_0 / Q4_K products of 1..8 rows over large weights by persistent
-// streaming waves; false when the shape, the kind or the size is not one it
-// takes. Two or more rows need the quantization pass's image in a.pre.
+// Q8_0 / Q4_K / ternary products of 1..8 rows by persistent streaming
+// waves; false when the shape, the kind or the size is not one it takes.
+// Rows of more than 16384 inputs in all, and RMSNorm without the caller's
+// factors, need the quantization pass's image in a.pre.
 bool gemv_stream(const Layer& L, const GemvArgs& a, hipStream_t s);
 // The one-row Q8_0 decode product (k 1024, 2048 or 3072); false when the
 // shape or kind is not one it takes.
