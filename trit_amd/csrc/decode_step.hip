@@ -121,6 +121,12 @@ __device__ __forceinline__ float row16_sum(float v) {
     v += dpp<DPP_MIRROR>(v);
     return v;
 }
+__device__ __forceinline__ float row8_sum(float v) {
+    v += dpp<DPP_XOR1>(v);
+    v += dpp<DPP_XOR2>(v);
+    v += dpp<DPP_HALF_MIRROR>(v);
+    return v;
+}
 __device__ __forceinline__ float row16_max(float v) {
     v = __builtin_fmaxf(v, dpp<DPP_XOR1>(v));
     v = __builtin_fmaxf(v, dpp<DPP_XOR2>(v));
@@ -622,12 +628,14 @@ __device__ bool combine(int t, const StepArgs& a, uint32_t tag_in, uint32_t tag_
 // takes key/value head g = b % kvh -- so a head's blocks share an XCD and its
 // L2 -- and, of query head h = (b / kvh) % GROUP of that group, output dims
 // [DPB s, DPB s + DPB), s = b / (kvh GROUP). Every block scores all the
-// head's keys for its query head (16-lane group G the keys G + 32 i, lane
-// l16 dims [8 l16, 8 l16 + 8)), so it finishes the softmax itself and
+// head's keys for its query head (8-lane group G the keys G + 64 i, lane
+// l8 dims [16 l8, 16 l8 + 16)), so it finishes the softmax itself and
 // stores its outputs as the o product's input: no partials and no combine
-// hand-over. Lane l16 of a group takes the probability and value of the
-// group's chunk l16; the groups' own maxima, sums and p.V meet in LDS, and
-// the first wave rescales them. (Measured: sparing the polling wave the key
+// hand-over. Lane l8 of a group takes the probability and value of the
+// group's round l8; the 64 groups' own maxima, sums and p.V meet in LDS,
+// and the first two waves rescale them (Measured: 8-lane groups score in
+// half the instructions of 16-lane ones, whose 8-dim pieces spent as many
+// lane moves on each key's sum as multiplies.) (Measured: sparing the polling wave the key
 // loads, with 28 key groups, was slower; so was giving a head's blocks
 // consecutive indices, spread over the XCDs.)
 template <int GROUP, int DPB>
@@ -635,7 +643,7 @@ __device__ bool attention_all(int t, const StepArgs& a, const LayerPtrs& L, int 
                               uint32_t tag_out, Smem& sm, unsigned long long deadline) {
     static_assert(DPB == 4 || DPB == 8, "4 or 8 dims a block");
     const int b = blockIdx.x, kvh = a.kvh, g = b % kvh, hq = (b / kvh) % GROUP, e0 = DPB * (b / (kvh * GROUP));
-    const int tk = pos + 1, chunks = (tk + 31) / 32;
+    const int tk = pos + 1;
     const int heads = a.heads;
     const auto index = [g, heads, kvh](int i) {
         if (i < GROUP * HD) return g * GROUP * HD + i;
@@ -646,19 +654,25 @@ __device__ bool attention_all(int t, const StepArgs& a, const LayerPtrs& L, int 
     // arrive; so do the q/k norm weights and the rotary values.
     const _Float16* K = L.kcache + (size_t)g * a.max_pos * HD;
     const _Float16* V = L.vcache + (size_t)g * a.max_pos * HD;
-    const int G = t >> 4, l16 = t & 15;
-    uint4 kr[MAXF];
+    // 64 groups of 8 lanes: group G takes keys G + 64 i, lane l8 dims
+    // 16 l8 .. 16 l8 + 15 of each.
+    const int G = t >> 3, l8 = t & 7, rounds = (tk + 63) / 64;
+    uint4 kr[MAXF / 2][2];
 #pragma unroll
-    for (int i = 0; i < MAXF; ++i) {
-        kr[i] = make_uint4(0, 0, 0, 0);
-        if (i >= chunks) continue;  // uniform
-        const int j = G + 32 * i;
-        if (j < tk && j != pos) kr[i] = *(const uint4*)(K + (size_t)j * HD + l16 * 8);
+    for (int i = 0; i < MAXF / 2; ++i) {
+        kr[i][0] = kr[i][1] = make_uint4(0, 0, 0, 0);
+        if (i >= rounds) continue;  // uniform
+        const int j = G + 64 * i;
+        if (j < tk && j != pos) {
+            const uint4* src = (const uint4*)(K + (size_t)j * HD + l8 * 16);
+            kr[i][0] = src[0];
+            kr[i][1] = src[1];
+        }
     }
     using VT = typename std::conditional<DPB == 8, uint4, uint2>::type;
     VT vr{};
-    const int jv = G + 32 * l16;  // the key of this lane's probability
-    if (l16 < chunks && jv < tk && jv != pos) vr = *(const VT*)(V + (size_t)jv * HD + e0);
+    const int jv = G + 64 * l8;  // the key of this lane's probability
+    if (l8 < rounds && jv < tk && jv != pos) vr = *(const VT*)(V + (size_t)jv * HD + e0);
     const int hh = t / WAVE, i = t % WAVE;
     float nw0 = 1.0f, nw1 = 1.0f, sn = 0.0f, cs = 1.0f;
     if (hh <= GROUP) {
@@ -712,35 +726,49 @@ __device__ bool attention_all(int t, const StepArgs& a, const LayerPtrs& L, int 
     __syncthreads();
 
     // Scores of the group's keys for query head hq, and their maximum.
-    // The new key (the key at pos, in one group's last chunk) is taken as
-    // cached, f16 bits selected in place of the loaded ones: no branches.
-    float q[8];
-    uint32_t knb[4];
+    // The new key (the key at pos: group pos % 64, round pos / 64, a round
+    // the block knows) is taken as cached, its f16 bits selected into that
+    // round's registers.
+    float q[16];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) q[u] = sm.qkv[hq * HD + l16 * 8 + u];
+    for (int u = 0; u < 16; ++u) q[u] = sm.qkv[hq * HD + l8 * 16 + u];
+    {
+        const bool gf = G == (pos & 63);
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-        knb[u] = (uint32_t)f32_to_f16(sm.kvn[0][l16 * 8 + 2 * u]) |
-                 ((uint32_t)f32_to_f16(sm.kvn[0][l16 * 8 + 2 * u + 1]) << 16);
-    float sc[MAXF], mx = -INFINITY;
+        for (int c = 0; c < MAXF / 2; ++c) {
+            if (c != (pos >> 6)) continue;  // uniform
 #pragma unroll
-    for (int c = 0; c < MAXF; ++c) {
+            for (int h = 0; h < 2; ++h) {
+                uint32_t nb[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int d = l8 * 16 + 8 * h + 2 * u;
+                    nb[u] = (uint32_t)f32_to_f16(sm.kvn[0][d]) | ((uint32_t)f32_to_f16(sm.kvn[0][d + 1]) << 16);
+                }
+                kr[c][h] = make_uint4(gf ? nb[0] : kr[c][h].x, gf ? nb[1] : kr[c][h].y, gf ? nb[2] : kr[c][h].z,
+                                      gf ? nb[3] : kr[c][h].w);
+            }
+        }
+    }
+    float sc[MAXF / 2], mx = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < MAXF / 2; ++c) {
         sc[c] = -INFINITY;
-        if (c >= chunks) continue;
-        const int j = G + 32 * c;
-        const bool fresh_key = j == pos;
-        const uint4 kb = make_uint4(fresh_key ? knb[0] : kr[c].x, fresh_key ? knb[1] : kr[c].y,
-                                    fresh_key ? knb[2] : kr[c].z, fresh_key ? knb[3] : kr[c].w);
-        float k8[8];
-        unpack8(kb, k8);
+        if (c >= rounds) continue;
+        const int j = G + 64 * c;
         float acc = 0.0f;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(q[u], k8[u], acc);
-        acc = row16_sum(acc);
+        for (int h = 0; h < 2; ++h) {
+            float k8[8];
+            unpack8(kr[c][h], k8);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(q[8 * h + u], k8[u], acc);
+        }
+        acc = row8_sum(acc);
         sc[c] = j < tk ? acc : -INFINITY;
         mx = __builtin_fmaxf(mx, sc[c]);
     }
-    // Lane l16: the probability of chunk l16's key against the group's
+    // Lane l8: the probability of round l8's key against the group's
     // maximum, times its value dims; then the group's sums.
     float vv[DPB];
     {
@@ -754,44 +782,37 @@ __device__ bool attention_all(int t, const StepArgs& a, const LayerPtrs& L, int 
     }
     float mine = -INFINITY;
 #pragma unroll
-    for (int c = 0; c < MAXF; ++c)
-        if (c == l16) mine = sc[c];
+    for (int c = 0; c < MAXF / 2; ++c)
+        if (c == l8) mine = sc[c];
     const float p = mine == -INFINITY ? 0.0f : exp_trit(mine - mx);
     float part[DPB + 1];
 #pragma unroll
-    for (int d = 0; d < DPB; ++d) part[d] = row16_sum(p * vv[d]);
-    part[DPB] = row16_sum(p);
-    if (l16 == 0) {
-        sm.gmax[G][0] = mx;
-        sm.gl[G][0] = part[DPB];
+    for (int d = 0; d < DPB; ++d) part[d] = row8_sum(p * vv[d]);
+    part[DPB] = row8_sum(p);
+    // Group G's maximum, sum and p.V, flat in the attention scratch.
+    float* gmax = &sm.gmax[0][0];
+    float* gl = &sm.gl[0][0];
+    float* gpart = &sm.gpart[0][0];
+    if (l8 == 0) {
+        gmax[G] = mx;
+        gl[G] = part[DPB];
 #pragma unroll
-        for (int d = 0; d < DPB; ++d) sm.gpart[G][d] = part[d];
+        for (int d = 0; d < DPB; ++d) gpart[G * DPB + d] = part[d];
     }
     __syncthreads();
 
-    // The first wave: lane G of each half rescales group G by
-    // exp(max_G - max); the sums are shuffle trees over the half's 32 lanes,
-    // the first half the first DPB / 2 outputs, the second the rest; o / l
-    // is the output.
-    if (t < WAVE) {
-        const int gg = t & 31, half = t >> 5;
-        const float m = sm.gmax[gg][0];
-        float M = m;
-        M = __builtin_fmaxf(M, dpp<DPP_XOR1>(M));
-        M = __builtin_fmaxf(M, dpp<DPP_XOR2>(M));
-        M = __builtin_fmaxf(M, dpp<DPP_HALF_MIRROR>(M));
-        M = __builtin_fmaxf(M, dpp<DPP_MIRROR>(M));
-        M = __builtin_fmaxf(M, __shfl_xor(M, 16));
+    // The first two waves, DPB / 2 outputs each: lane G rescales group G by
+    // exp(max_G - max); the sums are wave trees; o / l is the output.
+    if (t < 2 * WAVE) {
+        const int gg = t & (WAVE - 1), half = t / WAVE;
+        const float m = gmax[gg];
+        const float M = wave_max(m);
         const float f = m == -INFINITY ? 0.0f : exp_trit(m - M);
-        float l = row16_sum(f * sm.gl[gg][0]);
-        l += __shfl_xor(l, 16);
+        const float l = wave_sum(f * gl[gg]);
         constexpr int DH = DPB / 2;
         float o[DH];
 #pragma unroll
-        for (int d = 0; d < DH; ++d) {
-            o[d] = row16_sum(f * sm.gpart[gg][DH * half + d]);
-            o[d] += __shfl_xor(o[d], 16);
-        }
+        for (int d = 0; d < DH; ++d) o[d] = wave_sum(f * gpart[gg * DPB + DH * half + d]);
         if (gg == 0) {
 #pragma unroll
             for (int d = 0; d < DH; ++d)
