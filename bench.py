@@ -42,15 +42,15 @@ INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 # SIMDs x 16 lanes x 2.4 GHz (one wave64 instruction per 4 cycles a SIMD).
 VALU_PEAK_TOPS = 39.32
 # HBM bytes per launch of the roofline kernel, from rocprofv3 --pmc runs of
-# `bench.py --profile-pass` (profiles/gemv_row_q8_0_6144x1024_hbm_traffic.md):
-# FETCH_SIZE 3313.1 KiB x 2.0 (the scale a 256 MiB device copy gives) plus
-# WRITE_SIZE 48.0 KiB x 1.0.
-GATE_UP_TRAFFIC_BYTES = round((3313.1 * 2.0 + 48.0) * 1024)
+# `bench.py --profile-pass` (profiles/gemv_stream_q8_0_6144x1024_hbm_traffic.md):
+# FETCH_SIZE 3353.1 KiB x 2.0 (the scale a 256 MiB device copy gives) plus
+# WRITE_SIZE 24.0 KiB x 1.0.
+GATE_UP_TRAFFIC_BYTES = round((3353.1 * 2.0 + 24.0) * 1024)
 # HBM bytes per forward of the persistent decode step, from the same kind of
 # runs (profiles/decode_step_qwen3_0.6b_hbm_traffic.md): FETCH_SIZE and
 # WRITE_SIZE of one launch of 128 steps (127 forwards, positions 256..382)
 # over the forwards, FETCH_SIZE x 2.0 plus WRITE_SIZE x 1.0.
-STEP_FETCH_KIB, STEP_WRITE_KIB = 406468.5, 3944.1
+STEP_FETCH_KIB, STEP_WRITE_KIB = 406388.96, 3944.06
 STEP_TRAFFIC_BYTES = round((STEP_FETCH_KIB * 2.0 + STEP_WRITE_KIB) * 1024)
 
 
@@ -143,7 +143,7 @@ def gemv_roofline(H, linears, cfg, sweeps):
     achieved = algo / (avg_ms * 1e-3) / 1e9
     return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                 frac=round(achieved / HBM_PEAK_GBS, 4), traffic=GATE_UP_TRAFFIC_BYTES,
-                kernel="gemv_row_kernel<4,1>: Q8_0 one-row product, the 6144x1024 gate_up weights",
+                kernel="gemv_stream_kernel<Q8S,1,1,4>: Q8_0 one-row product, the 6144x1024 gate_up weights",
                 bytes_per_launch=algo, avg_us=round(avg_ms * 1e3, 3), launches=len(durations),
                 timing="hipExtLaunchKernel start/stop events per launch, inside decode-order sweeps of "
                        "all 112 Q8_0 products (468 MB per sweep, past the 256 MB Infinity Cache)")
