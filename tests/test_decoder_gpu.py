@@ -304,6 +304,28 @@ def test_step_fast(qshape, monkeypatch, attention):
     check_generate_fast(w, ref, lm, QS, monkeypatch, persistent=True)
 
 
+@pytest.mark.parametrize("m", [2, 4, 7])
+def test_short_prompt(qshape, m):
+    """Prompts of 2..8 rows run the few-row products (on Qwen3-0.6B's layer
+    shapes: the streaming kernel with the SwiGLU pair and the residual
+    epilogue, the rows quantized in the block or by the quantization pass):
+    exact mode bit for bit against the oracle, fast mode within its bound."""
+    print(f"case decoder short prompt ({m} rows)", flush=True)
+    w, ref, lm = qshape
+    p = synth.prompt(80 + m, m, QS["vocab"])
+    ref.reset()
+    want = ref.forward(p)
+    s = lm.session(64, hip.EXACT)
+    got = s.prefill(p)
+    s.free()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), rel(got, want)
+    f = lm.session(64, 0)
+    fast = f.prefill(p)
+    f.free()
+    print(f"fast vs oracle {rel(fast, want):.3g}", flush=True)
+    assert rel(fast, want) < 5e-2
+
+
 @pytest.mark.parametrize("prompt,steps,max_pos", [(330, 54, 384), (700, 40, 760)])
 def test_step_fast_long(qshape, prompt, steps, max_pos):
     """Sessions at the one-pass attention's limit (384 positions: all 12
