@@ -189,6 +189,21 @@ int trit_hip_session_position(const TritHipSession *session);
 
 void trit_hip_session_free(TritHipSession *session);
 
+/* ---- Attention (reference src/layers.rs:343-504) ---------------------- */
+
+/* Grouped-query attention of tq query rows over tk keys, host memory:
+ * layers::attention (src/layers.rs:343-504,571-587). q rows have stride qs
+ * floats (heads * hd values each), k and v rows stride kvs (kv_heads * hd);
+ * query head h reads key head h / (heads / kv_heads); out is tq rows of
+ * heads * hd floats. causal: row i sees keys 0 .. tk - tq + i; else every
+ * key. flags TRIT_HIP_EXACT: Trit's order and sums with f32 keys and
+ * values, bit for bit (head_dim up to 256, tk up to 16000); 0: the fast
+ * form of the prompt path, keys and values rounded to f16 as the f16 caches
+ * hold them and the products on the matrix cores (head_dim 128; 1, 2 or 4
+ * query heads per key head). */
+int trit_hip_attention(const float *q, int qs, const float *k, const float *v, int kvs, int tq, int tk, int heads,
+                       int kv_heads, int hd, int causal, int flags, float *out);
+
 /* ---- GGUF files (reference src/models/gguf/mod.rs:130-300) ------------- */
 
 typedef struct TritHipGguf TritHipGguf;

@@ -35,7 +35,12 @@ def lib():
 
 class LmConfig(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("d", "ffn", "layers", "heads", "kv_heads", "head_dim", "vocab")] + [
-        ("eps", C.c_float), ("rope_base", C.c_float), ("qk_norm", C.c_int)]
+        ("eps", C.c_float), ("rope_base", C.c_float), ("qk_norm", C.c_int), ("kv_f16", C.c_int),
+        ("embedding_multiplier", C.c_float), ("attention_multiplier", C.c_float),
+        ("residual_multiplier", C.c_float), ("logits_scaling", C.c_float)]
+
+
+TABLE_F16, TABLE_F32, TABLE_Q8 = 0, 1, 2
 
 
 def _bind(L):
@@ -44,6 +49,7 @@ def _bind(L):
         "or_isa_best": (i, []),
         "or_team_start": (i, [i, i]),
         "or_team_size": (i, []),
+        "or_vnni_peak": (C.c_double, [i64]),
         "or_f32_to_f16": (C.c_uint16, [f]),
         "or_f16_to_f32": (f, [C.c_uint16]),
         "or_exp": (f, [f]),
@@ -69,6 +75,14 @@ def _bind(L):
         "or_lm_new": (p, [i, C.POINTER(LmConfig)]),
         "or_lm_set_layer": (i, [p, i, p, p, p, p, p, p, p, p]),
         "or_lm_set_embed": (i, [p, p, p]),
+        "or_lm_set_linear_int8": (i, [p, i, i, p, p]),
+        "or_lm_set_linear_float": (i, [p, i, i, i, p]),
+        "or_lm_set_table": (i, [p, i, i, p, p]),
+        "or_lm_set_ffn_scales": (i, [p, p]),
+        "or_lm_forward_rows": (i, [p, p, i, p]),
+        "or_lm_truncate": (i, [p, i]),
+        "or_lm_position": (i, [p]),
+        "or_lm_embed_row": (i, [p, i, p]),
         "or_lm_generate": (i, [p, p, i, i, p, i, p, p]),
         "or_lm_forward": (i, [p, p, i, p]),
         "or_lm_reset": (None, [p]),
@@ -92,6 +106,12 @@ def isa_best() -> int:
 
 def team_start(spread: int = 0, threads: int = 0) -> int:
     return lib().or_team_start(spread, threads)
+
+
+def vnni_peak(iters: int = 20_000_000) -> float:
+    """int8 multiply-adds per second of the team on register-resident
+    vpdpbusd chains (0 without AVX-512 VNNI)."""
+    return lib().or_vnni_peak(iters)
 
 
 def quantize(x: np.ndarray, group: int, half_scales: bool, isa: int = SCALAR):
@@ -227,11 +247,17 @@ def argmax(v) -> int:
 
 
 class Lm:
-    """CausalLm with Q8_0 linears and a tied f16 table."""
+    """CausalLm (src/models/parts/causal_lm.rs:93-481) with Q8_0 linears and
+    a tied f16 table; kv_f16 rounds each appended key and value through f16
+    (the device's f16 caches). Granite's multipliers come from cfg
+    (embedding_multiplier, attention_multiplier, residual_multiplier,
+    logits_scaling); other linear and table kinds are set afterwards."""
 
-    def __init__(self, cfg: dict, weights, isa: int = SCALAR):
+    def __init__(self, cfg: dict, weights, isa: int = SCALAR, kv_f16: bool = False):
         c = LmConfig(cfg["d"], cfg["ffn"], cfg["layers"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"],
-                     cfg["vocab"], cfg["eps"], cfg["rope_base"], int(cfg.get("qk_norm", 1)))
+                     cfg["vocab"], cfg["eps"], cfg["rope_base"], int(cfg.get("qk_norm", 1)), int(kv_f16),
+                     cfg.get("embedding_multiplier", 1.0), cfg.get("attention_multiplier") or 0.0,
+                     cfg.get("residual_multiplier", 1.0), cfg.get("logits_scaling", 1.0))
         self.cfg = cfg
         self.h = lib().or_lm_new(isa, C.byref(c))
         assert self.h
@@ -240,6 +266,38 @@ class Lm:
                                        ptr(L.norm_attn), ptr(L.norm_mlp), ptr(L.q_norm), ptr(L.k_norm))
             assert rc == 0
         assert lib().or_lm_set_embed(self.h, ptr(weights.embed), ptr(weights.final_norm)) == 0
+
+    def set_linear_int8(self, layer, which, codes, scales):
+        """Linear `which` (0 qkv, 1 o, 2 gate_up, 3 down) as Trit's int8
+        weights (one f32 scale per row and 128 inputs)."""
+        codes = np.ascontiguousarray(codes, np.int8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        assert lib().or_lm_set_linear_int8(self.h, layer, which, ptr(codes), ptr(scales)) == 0
+
+    def set_linear_float(self, layer, which, weights):
+        """Linear `which` as f32 or f16-bits (uint16) weights, f32 math."""
+        w = np.ascontiguousarray(weights)
+        kind = TABLE_F16 if w.dtype == np.uint16 else TABLE_F32
+        w = np.ascontiguousarray(w, np.uint16 if kind == TABLE_F16 else np.float32)
+        assert lib().or_lm_set_linear_float(self.h, layer, which, kind, ptr(w)) == 0
+
+    def set_table(self, which, kind, data, scales=None):
+        """Table 0 (the embedding) or 1 (the untied head; None ties it)."""
+        if data is None:
+            assert lib().or_lm_set_table(self.h, which, kind, None, None) == 0
+            return
+        dt = {TABLE_F16: np.uint16, TABLE_F32: np.float32, TABLE_Q8: np.int8}[kind]
+        data = np.ascontiguousarray(data, dt)
+        sc = None if scales is None else np.ascontiguousarray(scales, np.float32)
+        assert lib().or_lm_set_table(self.h, which, kind, ptr(data), ptr(sc) if sc is not None else None) == 0
+        self._keep = getattr(self, "_keep", []) + [data]
+
+    def set_ffn_scales(self, scales):
+        if scales is None:
+            assert lib().or_lm_set_ffn_scales(self.h, None) == 0
+            return
+        s = np.ascontiguousarray(scales, np.float32)
+        assert lib().or_lm_set_ffn_scales(self.h, ptr(s)) == 0
 
     def generate(self, prompt, max_new, stop=()):
         prompt = np.ascontiguousarray(prompt, np.int32)
@@ -254,11 +312,29 @@ class Lm:
     def reset(self):
         lib().or_lm_reset(self.h)
 
+    def truncate(self, position):
+        assert lib().or_lm_truncate(self.h, position) == 0
+
+    @property
+    def position(self):
+        return lib().or_lm_position(self.h)
+
     def forward(self, tokens):
         tokens = np.ascontiguousarray(tokens, np.int32)
         logits = np.empty(self.cfg["vocab"], np.float32)
         assert lib().or_lm_forward(self.h, ptr(tokens), tokens.size, ptr(logits)) == 0
         return logits
+
+    def forward_rows(self, rows):
+        rows = np.ascontiguousarray(rows, np.float32).reshape(-1, self.cfg["d"])
+        logits = np.empty(self.cfg["vocab"], np.float32)
+        assert lib().or_lm_forward_rows(self.h, ptr(rows), rows.shape[0], ptr(logits)) == 0
+        return logits
+
+    def embed_row(self, token):
+        out = np.empty(self.cfg["d"], np.float32)
+        assert lib().or_lm_embed_row(self.h, int(token), ptr(out)) == 0
+        return out
 
     def __del__(self):
         if getattr(self, "h", None):

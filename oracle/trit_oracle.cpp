@@ -22,6 +22,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -1015,16 +1016,91 @@ int argmax(const float* v, int n) {
 }
 
 // ------------------------------------------------------------- decoder ---
+// A token table (Dense::table / Dense::row, src/cpu/gemm.rs:383-429): f16
+// bits, f32, or int8 storage with one f32 scale per 32 values (Q8,
+// :37-44,117-187), always with f32 math in the 16-lane order.
+struct Table {
+    int kind = OR_TABLE_F16, rows = 0, cols = 0;
+    std::vector<uint16_t> f16;
+    std::vector<float> f32;
+    std::vector<int8_t> codes;
+    std::vector<float> scales;  // rows x cols/32
+
+    // widen_q8 (src/cpu/gemm.rs:171-179): f32(code) * scale, one rounding.
+    void widen_rows(int r0, int r1, float* out) const {
+        const int g = cols / 32;
+        for (int r = r0; r < r1; ++r)
+            for (int kk = 0; kk < cols; ++kk)
+                out[(size_t)(r - r0) * cols + kk] =
+                    (float)codes[(size_t)r * cols + kk] * scales[(size_t)r * g + kk / 32];
+    }
+    void row(int index, float* out) const {
+        if (kind == OR_TABLE_F16) {
+            for (int i = 0; i < cols; ++i) out[i] = f16_to_f32(f16[(size_t)index * cols + i]);
+        } else if (kind == OR_TABLE_F32) {
+            std::memcpy(out, f32.data() + (size_t)index * cols, (size_t)cols * 4);
+        } else {
+            widen_rows(index, index + 1, out);
+        }
+    }
+    // out = x * table^T for one row x (Dense::forward of a table,
+    // src/cpu/gemm.rs:522-525; Q8::matmul widens panels of rows and runs the
+    // f32 product, fgemm.rs:263-295, so each value is the f32 product's).
+    void product(int isa, const float* x, float* out) const {
+        if (kind == OR_TABLE_F16) return matmul<uint16_t>(isa, x, 1, cols, f16.data(), rows, out);
+        if (kind == OR_TABLE_F32) return matmul<float>(isa, x, 1, cols, f32.data(), rows, out);
+        const int P = 4096;
+        std::vector<float> panel((size_t)P * cols);
+        for (int r0 = 0; r0 < rows; r0 += P) {
+            const int r1 = std::min(rows, r0 + P);
+            widen_rows(r0, r1, panel.data());
+            matmul<float>(isa, x, 1, cols, panel.data(), r1 - r0, out + r0);
+        }
+    }
+};
+
+// A decoder linear (Dense, src/cpu/gemm.rs:15-35): int8 activations
+// (Q8_0 or Trit's int8), or f16 / f32 weights with f32 math (matmul,
+// fgemm.rs:213-246).
+struct Linear {
+    Int8Layer* int8 = nullptr;
+    int fkind = -1, n = 0, k = 0;  // OR_TABLE_F16 / OR_TABLE_F32 without int8
+    std::vector<uint16_t> f16;
+    std::vector<float> f32;
+    Linear() = default;
+    Linear(const Linear&) = delete;
+    Linear& operator=(const Linear&) = delete;
+    Linear(Linear&& o) noexcept
+        : int8(o.int8), fkind(o.fkind), n(o.n), k(o.k), f16(std::move(o.f16)), f32(std::move(o.f32)) {
+        o.int8 = nullptr;
+    }
+    ~Linear() { delete int8; }
+    void set_int8(Int8Layer* L) {
+        delete int8;
+        int8 = L;
+        fkind = -1;
+        f16.clear();
+        f32.clear();
+    }
+    void forward(int isa, const float* x, int m, float* out) const {
+        if (int8) return int8_forward(*int8, x, m, out);
+        if (fkind == OR_TABLE_F16) return matmul<uint16_t>(isa, x, m, k, f16.data(), n, out);
+        return matmul<float>(isa, x, m, k, f32.data(), n, out);
+    }
+};
+
 struct Lm {
     int isa;
     or_lm_config c;
     struct Layer {
-        Int8Layer *qkv = nullptr, *o = nullptr, *gate_up = nullptr, *down = nullptr;
+        Linear qkv, o, gate_up, down;
         std::vector<float> norm_attn, norm_mlp, q_norm, k_norm;
     };
     std::vector<Layer> layers;
-    std::vector<uint16_t> embed;
+    Table embed;
+    Table head;  // rows == 0: tied to embed
     std::vector<float> final_norm;
+    std::vector<std::vector<float>> ffn_scales;  // empty, or layers x d
     std::vector<float> rope_sin, rope_cos;
     int rope_positions = 0;
     // Session: f32 caches per layer, positions x (kv_heads*hd).
@@ -1041,14 +1117,6 @@ struct Lm {
         rope_positions = n;
     }
 
-    ~Lm() {
-        for (auto& L : layers) {
-            delete L.qkv;
-            delete L.o;
-            delete L.gate_up;
-            delete L.down;
-        }
-    }
 };
 
 Int8Layer* q8_layer(int isa, int n, int k, const uint8_t* blocks) {
@@ -1059,19 +1127,41 @@ Int8Layer* q8_layer(int isa, int n, int k, const uint8_t* blocks) {
     return int8_new(isa, n, k, 32, true, codes.data(), scales.data());
 }
 
-// src/models/parts/causal_lm.rs:374-389,410-481 for rows of embeddings x.
+// add_scaled_into (src/layers.rs:224-236): x += y, or x += w * y (no fused
+// multiply-add) for a multiplier other than 1.
+void add_scaled(float* x, const float* y, size_t n, float w) {
+    if (w == 1.0f) {
+        for (size_t i = 0; i < n; ++i) x[i] += y[i];
+    } else {
+        for (size_t i = 0; i < n; ++i) x[i] += w * y[i];
+    }
+}
+
+// scale_all (src/layers.rs:218-222): nothing for 1.
+void scale_all(float* x, size_t n, float w) {
+    if (w != 1.0f)
+        for (size_t i = 0; i < n; ++i) x[i] *= w;
+}
+
+// src/models/parts/causal_lm.rs:374-389,410-481 for rows of embeddings x:
+// CausalLm::hidden, the final norm of the last row, the head and the
+// logits scaling.
 void lm_forward_rows(Lm& lm, std::vector<float>& x, int m, float* logits) {
     const auto& c = lm.c;
     int d = c.d, hd = c.head_dim, qd = c.heads * hd, kv = c.kv_heads * hd, stride = qd + 2 * kv;
     int first = lm.position;
     lm.ensure_rope(first + m);
+    scale_all(x.data(), x.size(), c.embedding_multiplier);
+    // Granite's attention multiplier replaces 1/sqrt(head_dim)
+    // (causal_lm.rs:419-424): q is scaled by multiplier * sqrt(hd) first.
+    const float q_scale = c.attention_multiplier != 0.0f ? c.attention_multiplier * std::sqrt((float)hd) : 1.0f;
     std::vector<float> normed((size_t)m * d), qkv((size_t)m * stride), att((size_t)m * qd), y((size_t)m * d);
     std::vector<float> wide((size_t)m * 2 * c.ffn), hidden((size_t)m * c.ffn);
     for (int l = 0; l < c.layers; ++l) {
         auto& L = lm.layers[l];
         normed = x;
         parallel(m, [&](int r) { rmsnorm_row(L.norm_attn.data(), d, c.eps, normed.data() + (size_t)r * d); });
-        int8_forward(*L.qkv, normed.data(), m, qkv.data());
+        L.qkv.forward(lm.isa, normed.data(), m, qkv.data());
         if (c.qk_norm) {
             parallel(m, [&](int r) {
                 float* row = qkv.data() + (size_t)r * stride;
@@ -1082,41 +1172,76 @@ void lm_forward_rows(Lm& lm, std::vector<float>& x, int m, float* logits) {
         }
         rope_apply(qkv.data(), m, stride, c.heads, hd, first, lm.rope_sin.data(), lm.rope_cos.data());
         rope_apply(qkv.data() + qd, m, stride, c.kv_heads, hd, first, lm.rope_sin.data(), lm.rope_cos.data());
+        if (q_scale != 1.0f)
+            for (int r = 0; r < m; ++r)
+                for (int i = 0; i < qd; ++i) qkv[(size_t)r * stride + i] *= q_scale;
         auto& K = lm.keys[l];
         auto& V = lm.values[l];
         for (int r = 0; r < m; ++r) {
             const float* row = qkv.data() + (size_t)r * stride;
             K.insert(K.end(), row + qd, row + qd + kv);
             V.insert(V.end(), row + qd + kv, row + stride);
+            if (c.kv_f16) {
+                // The f16 cache: each appended key and value rounded through
+                // binary16 (round to nearest even) where it is stored.
+                for (size_t i = K.size() - kv; i < K.size(); ++i) K[i] = f16r(K[i]);
+                for (size_t i = V.size() - kv; i < V.size(); ++i) V[i] = f16r(V[i]);
+            }
         }
         int seen = first + m;
         attention(lm.isa, qkv.data(), stride, K.data(), V.data(), kv, m, seen, c.heads, c.kv_heads, hd, true,
                   att.data());
-        int8_forward(*L.o, att.data(), m, y.data());
-        for (size_t i = 0; i < (size_t)m * d; ++i) x[i] += y[i];
+        L.o.forward(lm.isa, att.data(), m, y.data());
+        add_scaled(x.data(), y.data(), (size_t)m * d, c.residual_multiplier);
         normed = x;
         parallel(m, [&](int r) { rmsnorm_row(L.norm_mlp.data(), d, c.eps, normed.data() + (size_t)r * d); });
-        int8_forward(*L.gate_up, normed.data(), m, wide.data());
+        if (!lm.ffn_scales.empty()) {
+            const float* s = lm.ffn_scales[l].data();
+            for (int r = 0; r < m; ++r)
+                for (int i = 0; i < d; ++i) normed[(size_t)r * d + i] *= s[i];
+        }
+        L.gate_up.forward(lm.isa, normed.data(), m, wide.data());
         parallel(m, [&](int r) {
             const float* row = wide.data() + (size_t)r * 2 * c.ffn;
             float* h = hidden.data() + (size_t)r * c.ffn;
             for (int i = 0; i < c.ffn; ++i) h[i] = silu_one(row[i]) * row[c.ffn + i];
         });
-        int8_forward(*L.down, hidden.data(), m, y.data());
-        for (size_t i = 0; i < (size_t)m * d; ++i) x[i] += y[i];
+        L.down.forward(lm.isa, hidden.data(), m, y.data());
+        add_scaled(x.data(), y.data(), (size_t)m * d, c.residual_multiplier);
     }
     lm.position += m;
     std::vector<float> last(x.begin() + (size_t)(m - 1) * d, x.begin() + (size_t)m * d);
     rmsnorm_row(lm.final_norm.data(), d, c.eps, last.data());
-    matmul<uint16_t>(lm.isa, last.data(), 1, d, lm.embed.data(), c.vocab, logits);
+    (lm.head.rows ? lm.head : lm.embed).product(lm.isa, last.data(), logits);
+    scale_all(logits, (size_t)c.vocab, 1.0f / c.logits_scaling);
 }
 
 void lm_forward_tokens(Lm& lm, const int32_t* tokens, int n, float* logits) {
     int d = lm.c.d;
     std::vector<float> x((size_t)n * d);
-    for (int r = 0; r < n; ++r)
-        for (int i = 0; i < d; ++i) x[(size_t)r * d + i] = f16_to_f32(lm.embed[(size_t)tokens[r] * d + i]);
+    for (int r = 0; r < n; ++r) lm.embed.row(tokens[r], x.data() + (size_t)r * d);
     lm_forward_rows(lm, x, n, logits);
+}
+
+bool fill_table(Table& t, int kind, int rows, int cols, const void* data, const float* scales) {
+    if (!data || rows <= 0 || cols <= 0) return false;
+    t = Table();
+    t.kind = kind;
+    t.rows = rows;
+    t.cols = cols;
+    const size_t n = (size_t)rows * cols;
+    if (kind == OR_TABLE_F16) {
+        t.f16.assign((const uint16_t*)data, (const uint16_t*)data + n);
+    } else if (kind == OR_TABLE_F32) {
+        t.f32.assign((const float*)data, (const float*)data + n);
+    } else if (kind == OR_TABLE_Q8) {
+        if (cols % 32 || !scales) return false;
+        t.codes.assign((const int8_t*)data, (const int8_t*)data + n);
+        t.scales.assign(scales, scales + n / 32);
+    } else {
+        return false;
+    }
+    return true;
 }
 
 }  // namespace
@@ -1169,6 +1294,38 @@ int or_team_start(int spread, int threads) {
 }
 
 int or_team_size(void) { return team_threads(); }
+
+// The host's int8 dot-product peak as the team reaches it: each thread runs
+// 12 independent chains of vpdpbusd (64 multiply-adds each) for `iters`
+// rounds; no memory traffic. The yardstick of the baseline's fairness check
+// (a compute-bound int8 product should reach about 90 % of it).
+}  // extern "C"
+namespace {
+AVX512 int64_t vnni_spin(int64_t iters) {
+    __m512i acc[12];
+    for (int i = 0; i < 12; ++i) acc[i] = _mm512_set1_epi32(i);
+    const __m512i a = _mm512_set1_epi32(0x01020304), b = _mm512_set1_epi32(0x05060708);
+    for (int64_t it = 0; it < iters; ++it)
+        for (int i = 0; i < 12; ++i) acc[i] = _mm512_dpbusd_epi32(acc[i], a, b);
+    __m512i t = acc[0];
+    for (int i = 1; i < 12; ++i) t = _mm512_add_epi32(t, acc[i]);
+    return _mm512_reduce_add_epi32(t);
+}
+}  // namespace
+extern "C" {
+
+double or_vnni_peak(int64_t iters) {
+    if (or_isa_best() != OR_AVX512) return 0.0;
+    const int n = team_threads();
+    std::vector<int64_t> sink(n);
+    const auto t0 = std::chrono::steady_clock::now();
+    parallel(n, [&](int t) { sink[t] = vnni_spin(iters); });
+    const double s = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    volatile int64_t keep = 0;
+    for (int64_t v : sink) keep = keep + v;
+    (void)keep;
+    return (double)n * (double)iters * 12.0 * 64.0 / s;
+}
 
 uint16_t or_f32_to_f16(float value) { return f32_to_f16(value); }
 float or_f16_to_f32(uint16_t half) { return f16_to_f32(half); }
@@ -1317,6 +1474,7 @@ void* or_lm_new(int isa, const or_lm_config* cfg) {
     auto* lm = new Lm();
     lm->isa = isa;
     lm->c = *cfg;
+    if (lm->c.logits_scaling == 0.0f) lm->c.logits_scaling = 1.0f;
     lm->layers.resize(cfg->layers);
     lm->keys.resize(cfg->layers);
     lm->values.resize(cfg->layers);
@@ -1331,10 +1489,10 @@ int or_lm_set_layer(void* p, int layer, const uint8_t* qkv, const uint8_t* o, co
     if (layer < 0 || layer >= c.layers) return -1;
     int hd = c.head_dim, d = c.d;
     auto& L = lm->layers[layer];
-    L.qkv = q8_layer(lm->isa, (c.heads + 2 * c.kv_heads) * hd, d, qkv);
-    L.o = q8_layer(lm->isa, d, c.heads * hd, o);
-    L.gate_up = q8_layer(lm->isa, 2 * c.ffn, d, gate_up);
-    L.down = q8_layer(lm->isa, d, c.ffn, down);
+    L.qkv.set_int8(q8_layer(lm->isa, (c.heads + 2 * c.kv_heads) * hd, d, qkv));
+    L.o.set_int8(q8_layer(lm->isa, d, c.heads * hd, o));
+    L.gate_up.set_int8(q8_layer(lm->isa, 2 * c.ffn, d, gate_up));
+    L.down.set_int8(q8_layer(lm->isa, d, c.ffn, down));
     L.norm_attn.assign(norm_attn, norm_attn + d);
     L.norm_mlp.assign(norm_mlp, norm_mlp + d);
     if (c.qk_norm) {
@@ -1344,10 +1502,64 @@ int or_lm_set_layer(void* p, int layer, const uint8_t* qkv, const uint8_t* o, co
     return 0;
 }
 
+int or_lm_set_linear_int8(void* p, int layer, int which, const int8_t* codes, const float* scales) {
+    auto* lm = (Lm*)p;
+    const auto& c = lm->c;
+    if (layer < 0 || layer >= c.layers || which < 0 || which > 3 || !codes || !scales) return -1;
+    const int hd = c.head_dim;
+    const int n[4] = {(c.heads + 2 * c.kv_heads) * hd, c.d, 2 * c.ffn, c.d};
+    const int k[4] = {c.d, c.heads * hd, c.d, c.ffn};
+    if (k[which] % 128) return -1;
+    auto& L = lm->layers[layer];
+    Linear* slot[4] = {&L.qkv, &L.o, &L.gate_up, &L.down};
+    slot[which]->set_int8(int8_new(lm->isa, n[which], k[which], 128, false, codes, scales));
+    return 0;
+}
+
+int or_lm_set_linear_float(void* p, int layer, int which, int kind, const void* weights) {
+    auto* lm = (Lm*)p;
+    const auto& c = lm->c;
+    if (layer < 0 || layer >= c.layers || which < 0 || which > 3 || !weights) return -1;
+    if (kind != OR_TABLE_F16 && kind != OR_TABLE_F32) return -1;
+    const int hd = c.head_dim;
+    const int n[4] = {(c.heads + 2 * c.kv_heads) * hd, c.d, 2 * c.ffn, c.d};
+    const int k[4] = {c.d, c.heads * hd, c.d, c.ffn};
+    auto& L = lm->layers[layer];
+    Linear* slot[4] = {&L.qkv, &L.o, &L.gate_up, &L.down};
+    Linear& q = *slot[which];
+    q.set_int8(nullptr);
+    q.fkind = kind;
+    q.n = n[which];
+    q.k = k[which];
+    const size_t count = (size_t)q.n * q.k;
+    if (kind == OR_TABLE_F16) q.f16.assign((const uint16_t*)weights, (const uint16_t*)weights + count);
+    else q.f32.assign((const float*)weights, (const float*)weights + count);
+    return 0;
+}
+
 int or_lm_set_embed(void* p, const uint16_t* embed, const float* final_norm) {
     auto* lm = (Lm*)p;
-    lm->embed.assign(embed, embed + (size_t)lm->c.vocab * lm->c.d);
+    if (!fill_table(lm->embed, OR_TABLE_F16, lm->c.vocab, lm->c.d, embed, nullptr)) return -1;
     lm->final_norm.assign(final_norm, final_norm + lm->c.d);
+    return 0;
+}
+
+int or_lm_set_table(void* p, int which, int kind, const void* data, const float* scales) {
+    auto* lm = (Lm*)p;
+    if (which == 1 && !data) {
+        lm->head = Table();
+        return 0;
+    }
+    if (which != 0 && which != 1) return -1;
+    return fill_table(which == 0 ? lm->embed : lm->head, kind, lm->c.vocab, lm->c.d, data, scales) ? 0 : -1;
+}
+
+int or_lm_set_ffn_scales(void* p, const float* scales) {
+    auto* lm = (Lm*)p;
+    lm->ffn_scales.clear();
+    if (!scales) return 0;
+    for (int l = 0; l < lm->c.layers; ++l)
+        lm->ffn_scales.emplace_back(scales + (size_t)l * lm->c.d, scales + (size_t)(l + 1) * lm->c.d);
     return 0;
 }
 
@@ -1358,12 +1570,39 @@ void or_lm_reset(void* p) {
     lm->position = 0;
 }
 
+int or_lm_truncate(void* p, int position) {
+    auto* lm = (Lm*)p;
+    if (position < 0 || position > lm->position) return -1;
+    const size_t kv = (size_t)lm->c.kv_heads * lm->c.head_dim;
+    for (auto& k : lm->keys) k.resize((size_t)position * kv);
+    for (auto& v : lm->values) v.resize((size_t)position * kv);
+    lm->position = position;
+    return 0;
+}
+
+int or_lm_position(void* p) { return ((Lm*)p)->position; }
+
+int or_lm_embed_row(void* p, int token, float* out) {
+    auto* lm = (Lm*)p;
+    if (token < 0 || token >= lm->c.vocab) return -1;
+    lm->embed.row(token, out);
+    return 0;
+}
+
 int or_lm_forward(void* p, const int32_t* tokens, int n, float* logits) {
     auto* lm = (Lm*)p;
     if (n <= 0) return -1;
     for (int i = 0; i < n; ++i)
         if (tokens[i] < 0 || tokens[i] >= lm->c.vocab) return -1;
     lm_forward_tokens(*lm, tokens, n, logits);
+    return 0;
+}
+
+int or_lm_forward_rows(void* p, const float* rows, int n, float* logits) {
+    auto* lm = (Lm*)p;
+    if (n <= 0 || !rows) return -1;
+    std::vector<float> x(rows, rows + (size_t)n * lm->c.d);
+    lm_forward_rows(*lm, x, n, logits);
     return 0;
 }
 

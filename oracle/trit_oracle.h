@@ -32,6 +32,10 @@ int or_isa_best(void);
  * Returns the team size. */
 int or_team_start(int spread, int threads);
 int or_team_size(void);
+/* int8 multiply-adds per second of the team on independent vpdpbusd chains
+ * (no memory traffic), `iters` rounds of 12 x 64 per thread; 0 without
+ * AVX-512 VNNI. The yardstick of the baseline's fairness check. */
+double or_vnni_peak(int64_t iters);
 
 /* src/cpu/tensors.rs:542-573 and :575-595. */
 uint16_t or_f32_to_f16(float value);
@@ -99,14 +103,22 @@ void or_attention(const float* q, int qs, const float* k, const float* v, int kv
 /* First index of the largest value (src/layers.rs:604-612). */
 int or_argmax(const float* values, int n);
 
-/* Decoder of the Llama plan with Qwen3 q/k norms
- * (src/models/parts/causal_lm.rs:17-481). Linears are GGUF Q8_0 blocks,
- * the tied embedding/head is an f16 table. */
+/* Decoder of the Llama plan with Qwen3 q/k norms and Granite's multipliers
+ * (src/models/parts/causal_lm.rs:17-481). Linears are GGUF Q8_0 blocks or
+ * Trit's int8 weights; the embedding and the head are token tables. */
 typedef struct {
     int d, ffn, layers, heads, kv_heads, head_dim, vocab;
     float eps, rope_base;
     int qk_norm;
+    /* Keys and values rounded through f16 where they are appended (the
+     * device's f16 caches); 0 keeps Trit's f32 caches. */
+    int kv_f16;
+    /* Granite's multipliers (causal_lm.rs:17-78): 1 (attention: 0) is none. */
+    float embedding_multiplier, attention_multiplier, residual_multiplier, logits_scaling;
 } or_lm_config;
+
+/* Token table kinds (Dense::table, src/cpu/gemm.rs:383-409). */
+enum { OR_TABLE_F16 = 0, OR_TABLE_F32 = 1, OR_TABLE_Q8 = 2 };
 
 void* or_lm_new(int isa, const or_lm_config* cfg);
 /* One layer. qkv: (heads+2*kv_heads)*hd rows of d; o: d rows of heads*hd;
@@ -115,6 +127,29 @@ int or_lm_set_layer(void* lm, int layer, const uint8_t* qkv, const uint8_t* o,
                     const uint8_t* gate_up, const uint8_t* down, const float* norm_attn,
                     const float* norm_mlp, const float* q_norm, const float* k_norm);
 int or_lm_set_embed(void* lm, const uint16_t* embed_f16, const float* final_norm);
+/* Linear `which` (0 qkv, 1 o, 2 gate_up, 3 down) of `layer` as Trit's int8
+ * weights: codes row-major, one f32 scale per row and 128 inputs
+ * (Int8::quantize's layer, src/cpu/int8.rs:292-369). */
+int or_lm_set_linear_int8(void* lm, int layer, int which, const int8_t* codes, const float* scales);
+/* Linear `which` as f16 bits (OR_TABLE_F16) or f32 (OR_TABLE_F32) weights,
+ * row-major, with f32 math in the 16-lane order (Dense::half / Dense::new,
+ * src/cpu/gemm.rs:189-221,500-525). */
+int or_lm_set_linear_float(void* lm, int layer, int which, int kind, const void* weights);
+/* Table `which` (0 the embedding, 1 the untied head) of kind OR_TABLE_*:
+ * f16 bits, f32, or int8 codes with an f32 scale per 32 values (`scales`).
+ * A head with data NULL is tied to the embedding again. */
+int or_lm_set_table(void* lm, int which, int kind, const void* data, const float* scales);
+/* Per-layer scales on the normed MLP input, layers x d, or NULL for none
+ * (CausalLm::set_ffn_scales, causal_lm.rs:303-306,456-462). */
+int or_lm_set_ffn_scales(void* lm, const float* scales);
+/* Logits after rows of embeddings (n x d) at the next positions
+ * (CausalLm::forward_rows, causal_lm.rs:374-389). */
+int or_lm_forward_rows(void* lm, const float* rows, int n, float* logits);
+/* Keeps the first `position` positions of the caches. */
+int or_lm_truncate(void* lm, int position);
+int or_lm_position(void* lm);
+/* Embedding row of `token` as f32 (Dense::row, gemm.rs:412-429). */
+int or_lm_embed_row(void* lm, int token, float* out);
 /* Greedy tokens after `prompt` (CausalLm::generate with no prefix,
  * causal_lm.rs:217-249,284-302). Writes up to max_new tokens to out and
  * returns their count; logits (optional) receives the logits after the

@@ -141,7 +141,9 @@ def test_ternary_4096(gpu, m):
 
 
 # The streaming kernel's ternary form (k a multiple of 2048), 1..8 rows.
-@pytest.mark.parametrize("n,k,m", [(2048, 2048, 1), (8192, 4096, 3), (1024, 6144, 8), (4096, 2048, 2)])
+# (2048, 2048, 8): 8 rows of 2048 inputs quantize inside each block.
+@pytest.mark.parametrize("n,k,m", [(2048, 2048, 1), (8192, 4096, 3), (1024, 6144, 8), (4096, 2048, 2),
+                                   (2048, 2048, 8), (4096, 2048, 5)])
 def test_ternary_stream(gpu, n, k, m):
     print(f"case ternary stream n={n} k={k} m={m}", flush=True)
     codes, scales = ternary_inputs(n, k)
@@ -151,6 +153,21 @@ def test_ternary_stream(gpu, n, k, m):
     ref = O.Ternary(codes, scales)(x)
     got = gpu.Dense.ternary(codes, scales).forward(x)
     assert bits_equal(got, ref)
+
+
+@pytest.mark.parametrize("n,k,m", [(1024, 4096, 6), (2048, 4096, 8), (4096, 2048, 8)])
+def test_stream_after_quantization_pass(gpu, monkeypatch, n, k, m):
+    """TRIT_HIP_GEMV_STREAM=1: 5..8 rows too many to quantize in the block
+    run on the streaming kernel from the quantization pass's image (below
+    the size where it is chosen by itself), ternary and Q8_0."""
+    print(f"case stream after the quantization pass n={n} k={k} m={m}", flush=True)
+    monkeypatch.setenv("TRIT_HIP_GEMV_STREAM", "1")
+    codes, scales = ternary_inputs(n, k)
+    x = synth.activations(38 + m, m, k)
+    assert bits_equal(gpu.Dense.ternary(codes, scales).forward(x), O.Ternary(codes, scales, O.isa_best())(x))
+    qc, sbits, blocks = q8_layer(synth.seed_for(6, n + k), n, k)
+    ref = O.Int8(qc, sbits.view(np.float16).astype(np.float32), 32, True, O.isa_best())(x)
+    assert bits_equal(gpu.Dense.q8_0(n, k, blocks).forward(x), ref)
 
 
 def test_ternary_base3(gpu):
@@ -168,14 +185,19 @@ def test_ternary_base3(gpu):
     assert bits_equal(got, ref)
 
 
-@pytest.mark.parametrize("n,k,m", [(4096, 3072, 1), (3072, 8192, 4), (256, 512, 3), (256, 512, 20)])
+# The 3B layer set of the Q4_K configuration (Wqkv 3072 -> 4096, Wo 3072 ->
+# 3072, gate/up 3072 -> 16384, down 8192 -> 3072) at 1 and 4 rows, and small
+# shapes through the tiled and matrix-core kernels.
+@pytest.mark.parametrize("n,k,m", [(4096, 3072, 1), (4096, 3072, 4), (3072, 3072, 1), (3072, 3072, 4),
+                                   (16384, 3072, 1), (16384, 3072, 4), (3072, 8192, 1), (3072, 8192, 4),
+                                   (256, 512, 3), (256, 512, 20)])
 def test_q4_k(gpu, n, k, m):
     print(f"case q4_k n={n} k={k} m={m}", flush=True)
     blocks = synth.q4_k_blocks(41 + n, n, k)
     vals = O.q4_k_expand(blocks)
     codes, scales = O.q8_0_quantize(vals)
     x = synth.activations(42 + m, m, k)
-    ref = O.Int8(codes.reshape(n, k), scales.reshape(n, k // 32), 32, True)(x)
+    ref = O.Int8(codes.reshape(n, k), scales.reshape(n, k // 32), 32, True, O.isa_best())(x)
     got = gpu.Dense.q4_k(n, k, blocks).forward(x)
     assert bits_equal(got, ref)
 

@@ -29,19 +29,24 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = False) -> str:
+def build(verbose: bool = False, jobs: int = 0) -> str:
+    """Compiles the sources in parallel (`jobs` at a time; 0: up to 8), then links."""
+    from concurrent.futures import ThreadPoolExecutor
+
     os.makedirs(os.path.dirname(OUT), exist_ok=True)
-    objs = []
+    cmds, objs = [], []
     for src in SOURCES:
         path = os.path.join(CSRC, src)
         if not os.path.exists(path):
             continue
         obj = os.path.join(HERE, "lib", src.replace(".hip", ".o"))
-        cmd = [HIPCC, *FLAGS, "-c", path, "-o", obj]
-        if verbose:
-            print(" ".join(cmd), flush=True)
-        run(cmd)
+        cmds.append([HIPCC, *FLAGS, "-c", path, "-o", obj])
         objs.append(obj)
+    if verbose:
+        for cmd in cmds:
+            print(" ".join(cmd), flush=True)
+    with ThreadPoolExecutor(jobs or min(8, os.cpu_count() or 1)) as pool:
+        list(pool.map(run, cmds))
     tmp = OUT + ".tmp"
     run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, OUT)

@@ -22,6 +22,13 @@
 // and the A operand reads V^T rows in that same order (two 8-byte pieces).
 // Lane l ends with O^T[16 n + 4 (l / 16) + r][query l % 16].
 //
+// The keys and values are f16 as cached, so only q and p are rounded to
+// reach the f16 products: each is carried as two f16 parts, hi = f16(v)
+// and lo = f16(v - hi), and each product runs twice (lo, then hi) into the
+// f32 accumulator. The parts hold v to about 2^-22 of its size, so the
+// scores and outputs are those of f32 q and p against the cached keys and
+// values up to f32 rounding of the sums.
+//
 // Lane layouts of the 16x16x32 f16 instruction (checked on the device): an
 // operand lane l holds row (or column) l % 16, elements 8 (l / 16) .. +7 of
 // the 32-wide K step; result lane l holds column l % 16, rows 4 (l / 16) + r.
@@ -46,7 +53,7 @@ __global__ __launch_bounds__(GROUP * 128) void flash_prefill_kernel(const float*
                                                                     int rows, int pos0,
                                                                     const _Float16* __restrict__ kcache,
                                                                     const _Float16* __restrict__ vcache, int max_pos,
-                                                                    float* __restrict__ out, int qd) {
+                                                                    float* __restrict__ out, int qd, int tk_all) {
     constexpr int NT = GROUP * 128;
     constexpr int KP = KT * HD / 8;          // 16-byte pieces of a K tile
     constexpr int KPT = (KP + NT - 1) / NT;  // a thread's K pieces
@@ -59,13 +66,15 @@ __global__ __launch_bounds__(GROUP * 128) void flash_prefill_kernel(const float*
     const int hl = w / 2, half = w % 2, h = g * GROUP + hl;
     const int r0 = qt * QT + half * 16;  // the wave's first query row
     const int lr = l % 16, lq = l / 16;
-    const int row = r0 + lr;                        // this lane's query
-    const int seen = row < rows ? pos0 + row : -1;  // the last key it sees
+    const int row = r0 + lr;  // this lane's query
+    // The last key it sees: causal, its own position; with tk_all > 0
+    // (attention without a mask), every one of the tk_all keys.
+    const int seen = row < rows ? (tk_all > 0 ? tk_all - 1 : pos0 + row) : -1;
 
     // Q^T fragments (B operand): query lr, dims 32 ks + 8 lq + i, scaled by
     // log2(e) / sqrt(hd) so that the scores are exp2 exponents.
     const float scale = 1.4426950408889634f / __builtin_sqrtf((float)HD);
-    v8h qf[4];
+    v8h qf[4], ql[4];  // hi and lo parts
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
         float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), b = a;
@@ -74,14 +83,14 @@ __global__ __launch_bounds__(GROUP * 128) void flash_prefill_kernel(const float*
             a = *(const float4*)src;
             b = *(const float4*)(src + 4);
         }
-        qf[ks][0] = (_Float16)(a.x * scale);
-        qf[ks][1] = (_Float16)(a.y * scale);
-        qf[ks][2] = (_Float16)(a.z * scale);
-        qf[ks][3] = (_Float16)(a.w * scale);
-        qf[ks][4] = (_Float16)(b.x * scale);
-        qf[ks][5] = (_Float16)(b.y * scale);
-        qf[ks][6] = (_Float16)(b.z * scale);
-        qf[ks][7] = (_Float16)(b.w * scale);
+        const float v[8] = {a.x * scale, a.y * scale, a.z * scale, a.w * scale,
+                            b.x * scale, b.y * scale, b.z * scale, b.w * scale};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const _Float16 hi = (_Float16)v[i];
+            qf[ks][i] = hi;
+            ql[ks][i] = (_Float16)(v[i] - (float)hi);
+        }
     }
 
     float m = -INFINITY, lsum = 0.0f;  // of query lr (the same in its 4 lanes)
@@ -90,7 +99,7 @@ __global__ __launch_bounds__(GROUP * 128) void flash_prefill_kernel(const float*
     for (int n = 0; n < 8; ++n) o[n] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
     const int last_row = min(qt * QT + QT, rows) - 1;
-    const int kend = pos0 + last_row + 1;  // keys the block's last row sees
+    const int kend = tk_all > 0 ? tk_all : pos0 + last_row + 1;  // keys the block's last row sees
     const int tiles = (kend + KT - 1) / KT;
     const _Float16* K = kcache + (size_t)g * max_pos * HD;
     const _Float16* V = vcache + (size_t)g * max_pos * HD;
@@ -166,6 +175,7 @@ __global__ __launch_bounds__(GROUP * 128) void flash_prefill_kernel(const float*
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
                 const v8h ka = *(const v8h*)(Ks + (sub * 16 + lr) * KS + 32 * ks + 8 * lq);
+                s[sub] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[ks], s[sub], 0, 0, 0);
                 s[sub] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qf[ks], s[sub], 0, 0, 0);
             }
         }
@@ -185,14 +195,16 @@ __global__ __launch_bounds__(GROUP * 128) void flash_prefill_kernel(const float*
         const float mn = __builtin_fmaxf(m, mt);
         const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first tile (m = -inf)
         float rs = 0.0f;
-        v4h pk[4];  // exp2(s - mn) in f16, per subtile
+        v4h pk[4], pl[4];  // exp2(s - mn) as hi and lo f16 parts, per subtile
 #pragma unroll
         for (int sub = 0; sub < 4; ++sub)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float p = __builtin_amdgcn_exp2f(s[sub][r] - mn);  // masked: exp2(-inf) = 0
                 rs += p;
-                pk[sub][r] = (_Float16)p;
+                const _Float16 hi = (_Float16)p;
+                pk[sub][r] = hi;
+                pl[sub][r] = (_Float16)(p - (float)hi);
             }
         rs += __shfl_xor(rs, 16);
         rs += __shfl_xor(rs, 32);
@@ -205,11 +217,14 @@ __global__ __launch_bounds__(GROUP * 128) void flash_prefill_kernel(const float*
         for (int c = 0; c < 2; ++c) {
             const v8h pb = {pk[2 * c][0], pk[2 * c][1], pk[2 * c][2], pk[2 * c][3],
                             pk[2 * c + 1][0], pk[2 * c + 1][1], pk[2 * c + 1][2], pk[2 * c + 1][3]};
+            const v8h plb = {pl[2 * c][0], pl[2 * c][1], pl[2 * c][2], pl[2 * c][3],
+                             pl[2 * c + 1][0], pl[2 * c + 1][1], pl[2 * c + 1][2], pl[2 * c + 1][3]};
 #pragma unroll
             for (int n = 0; n < 8; ++n) {
                 const _Float16* vrow = Vt + (n * 16 + lr) * VS + 32 * c + 4 * lq;
                 const v4h lo = *(const v4h*)vrow, hi = *(const v4h*)(vrow + 16);
                 const v8h va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, plb, o[n], 0, 0, 0);
                 o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, o[n], 0, 0, 0);
             }
         }
@@ -234,27 +249,34 @@ bool flash_prefill_supported(const SessionImpl& S) {
     return group == 1 || group == 2 || group == 4;
 }
 
-void flash_prefill(SessionImpl& S, int layer, int rows, int pos0, hipStream_t s) {
-    const auto& c = S.dec->c;
-    const int group = c.heads / c.kv_heads, stride = (c.heads + 2 * c.kv_heads) * HD, qd = c.heads * HD;
-    const _Float16* kc = S.kcache.as<_Float16>() + (size_t)layer * c.kv_heads * S.max_pos * HD;
-    const _Float16* vc = S.vcache.as<_Float16>() + (size_t)layer * c.kv_heads * S.max_pos * HD;
-    const dim3 grid(c.kv_heads, (rows + QT - 1) / QT);
+void flash_attention(const float* q, int qs, const _Float16* kc, const _Float16* vc, int max_pos, int heads,
+                     int kv_heads, int rows, int pos0, int tk, int causal, float* out, hipStream_t s) {
+    const int group = heads / kv_heads, qd = heads * HD, tk_all = causal ? 0 : tk;
+    const dim3 grid(kv_heads, (rows + QT - 1) / QT);
     switch (group) {
         case 1:
-            hipLaunchKernelGGL(flash_prefill_kernel<1>, grid, dim3(128), 0, s, S.qkv.as<float>(), stride, rows, pos0,
-                               kc, vc, S.max_pos, S.att.as<float>(), qd);
+            hipLaunchKernelGGL(flash_prefill_kernel<1>, grid, dim3(128), 0, s, q, qs, rows, pos0, kc, vc, max_pos, out,
+                               qd, tk_all);
             break;
         case 2:
-            hipLaunchKernelGGL(flash_prefill_kernel<2>, grid, dim3(256), 0, s, S.qkv.as<float>(), stride, rows, pos0,
-                               kc, vc, S.max_pos, S.att.as<float>(), qd);
+            hipLaunchKernelGGL(flash_prefill_kernel<2>, grid, dim3(256), 0, s, q, qs, rows, pos0, kc, vc, max_pos, out,
+                               qd, tk_all);
             break;
         default:
-            hipLaunchKernelGGL(flash_prefill_kernel<4>, grid, dim3(512), 0, s, S.qkv.as<float>(), stride, rows, pos0,
-                               kc, vc, S.max_pos, S.att.as<float>(), qd);
+            hipLaunchKernelGGL(flash_prefill_kernel<4>, grid, dim3(512), 0, s, q, qs, rows, pos0, kc, vc, max_pos, out,
+                               qd, tk_all);
             break;
     }
     TRIT_HIP(hipGetLastError());
+}
+
+void flash_prefill(SessionImpl& S, int layer, int rows, int pos0, hipStream_t s) {
+    const auto& c = S.dec->c;
+    const int stride = (c.heads + 2 * c.kv_heads) * HD;
+    const _Float16* kc = S.kcache.as<_Float16>() + (size_t)layer * c.kv_heads * S.max_pos * HD;
+    const _Float16* vc = S.vcache.as<_Float16>() + (size_t)layer * c.kv_heads * S.max_pos * HD;
+    flash_attention(S.qkv.as<float>(), stride, kc, vc, S.max_pos, c.heads, c.kv_heads, rows, pos0, pos0 + rows, 1,
+                    S.att.as<float>(), s);
 }
 
 }  // namespace trit

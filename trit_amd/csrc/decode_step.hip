@@ -169,7 +169,13 @@ __device__ bool gather(int t, const uint64_t* src, int n, Index index, uint32_t 
 #pragma unroll
         for (int j = 0; j < MW; ++j) w[j] = 0;  // tag 0 is never waited for
         unsigned spins = 0;
-        while (true) {
+        if (deadline == 0) {
+            // A deadline of zero ticks (set only by the host's test override)
+            // has passed before the first poll.
+            __hip_atomic_store(&sm.abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            atomicOr(&st->err, 1);
+        }
+        while (deadline != 0) {
             bool ok = true;
 #pragma unroll
             for (int j = 0; j < MW; ++j) {
@@ -882,7 +888,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     for (int it = 0; it < nsteps; ++it) {
     const int step = step0 + it, pos = pos0 + it;
     const uint32_t tag0 = (seq0 + (uint32_t)it) << 8;
-    const unsigned long long deadline = wall_clock64() + a.ticks;
+    const unsigned long long deadline = a.ticks ? wall_clock64() + a.ticks : 0ull;
     // The thread index, made opaque to the optimizer at the top of the step,
     // of each layer and of the head: what derives from it (the wave's
     // product, a lane's rows) is computed within that part, rather than
@@ -1396,6 +1402,10 @@ void decode_step_launch(SessionImpl& S, int step, int pos, int nsteps, hipStream
     TRIT_HIP(hipGetDevice(&dev));
     TRIT_HIP(hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, dev));
     a.ticks = (unsigned long long)(rate_khz > 0 ? rate_khz : 100000) * 200ull;  // 200 ms
+    // TRIT_HIP_STEP_DEADLINE_US overrides the deadline (tests of the abort
+    // path: 0 makes every block's first wait give up, and the launch drains).
+    if (const char* v = getenv("TRIT_HIP_STEP_DEADLINE_US"))
+        a.ticks = (unsigned long long)(rate_khz > 0 ? rate_khz : 100000) * strtoull(v, nullptr, 10) / 1000ull;
     void* args[] = {&a, &step, &pos, (void*)&seq0, &nsteps};
     TRIT_HIP(hipLaunchCooperativeKernel((const void*)p.fn, dim3(p.blocks), dim3(T), args, 0, s));
 }

@@ -278,14 +278,15 @@ __device__ __forceinline__ void kv_load8(const _Float16* p, float* out) {
 template <typename KV>
 __global__ __launch_bounds__(ATT_THREADS) void attention_kernel(
     const float* __restrict__ qkv, int stride, int heads, int kvh, int hd, const KV* __restrict__ kcache,
-    const KV* __restrict__ vcache, int max_pos, int rows, float* __restrict__ out, int exact, const State* st) {
+    const KV* __restrict__ vcache, int max_pos, int rows, float* __restrict__ out, int exact, const State* st,
+    int causal = 1) {
     if (st->done) return;
     extern __shared__ float sm[];  // qh[hd] | probs[tk] | red[ATT_THREADS]
     const int h = blockIdx.x;
     const int row = blockIdx.y;
     const int g = h / (heads / kvh);
     const int tk = st->pos + rows;       // keys in the caches for this forward
-    const int visible = st->pos + row + 1;
+    const int visible = causal ? st->pos + row + 1 : tk;
     float* qh = sm;
     float* probs = sm + MAX_HD;
     float* red = probs + tk;
@@ -960,6 +961,22 @@ __global__ void advance_kernel(State* st, int rows) {
     st->pos += rows;
 }
 
+// Rows of keys and values (tk x kvs floats each, head g at g * hd) into the
+// cache layout [g][position][hd] of type KV.
+template <typename KV>
+__global__ void rows_to_cache_kernel(const float* __restrict__ k, const float* __restrict__ v, int kvs, int tk,
+                                     int kvh, int hd, KV* __restrict__ kc, KV* __restrict__ vc) {
+    const size_t total = (size_t)tk * kvh * hd;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const int e = (int)(i % hd);
+        const size_t jg = i / hd;
+        const int g = (int)(jg % kvh), j = (int)(jg / kvh);
+        const size_t to = ((size_t)g * tk + j) * hd + e;
+        kc[to] = (KV)k[(size_t)j * kvs + (size_t)g * hd + e];
+        vc[to] = (KV)v[(size_t)j * kvs + (size_t)g * hd + e];
+    }
+}
+
 }  // namespace
 
 // ---- host side ------------------------------------------------------------
@@ -1219,6 +1236,12 @@ void reset_state(SessionImpl& S) {
     State init{};
     TRIT_HIP(hipMemcpy(S.state.ptr, &init, sizeof(State), hipMemcpyHostToDevice));
     S.host_pos = 0;
+    S.broken = false;
+    S.step_cand_fresh = false;
+}
+
+void check_usable(const SessionImpl& S) {
+    if (S.broken) fail("session: a decode step was abandoned at its deadline; reset the session before using it");
 }
 
 // Clears `done` and sets the loop limits for a generate call, keeping pos.
@@ -1398,6 +1421,7 @@ static int prefill_common(TritHipSession* session, int n, float* logits, const i
     if (!session) fail("session is NULL");
     if (n <= 0) fail("prefill: no rows");
     SessionImpl& S = session->impl;
+    check_usable(S);
     const auto& c = S.dec->c;
     if (S.host_pos + n > S.max_pos)
         fail("prefill: " + std::to_string(S.host_pos + n) + " positions exceed the session's " +
@@ -1444,6 +1468,7 @@ static int generate_common(TritHipSession* session, int max_new, const int32_t* 
                            hipEvent_t ev_start, hipEvent_t ev_stop) {
     if (!session) fail("session is NULL");
     SessionImpl& S = session->impl;
+    check_usable(S);
     if (S.host_pos == 0) fail("generate: prefill a prompt first");
     if (max_new <= 0) return 0;
     if (!out) fail("generate: out is NULL");
@@ -1478,7 +1503,14 @@ static int generate_common(TritHipSession* session, int max_new, const int32_t* 
     State h{};
     TRIT_HIP(hipMemcpyAsync(&h, S.state.ptr, sizeof(State), hipMemcpyDeviceToHost, s));
     TRIT_HIP(hipStreamSynchronize(s));
-    if (h.err) fail("generate: a decode-step block waited past its deadline (the step was abandoned)");
+    if (h.err) {
+        // Blocks left the launch at different points: the caches may hold a
+        // partial step and the device position may have moved.
+        S.broken = true;
+        S.host_pos = h.pos;
+        S.step_cand_fresh = false;
+        fail("generate: a decode-step block waited past its deadline (the step was abandoned; reset the session)");
+    }
     TRIT_HIP(hipMemcpy(out, S.tokens_out.ptr, (size_t)h.n_out * 4, hipMemcpyDeviceToHost));
     S.host_pos = h.pos;
     return h.n_out;
@@ -1512,5 +1544,52 @@ int trit_hip_session_position(const TritHipSession* session) {
 }
 
 void trit_hip_session_free(TritHipSession* session) { delete session; }
+
+int trit_hip_attention(const float* q, int qs, const float* k, const float* v, int kvs, int tq, int tk, int heads,
+                       int kv_heads, int hd, int causal, int flags, float* out) {
+    return guard(-1, [&] {
+        if (!q || !k || !v || !out) fail("attention: q, k, v or out is NULL");
+        if (tq <= 0 || tk <= 0) fail("attention: no rows");
+        if (heads <= 0 || kv_heads <= 0 || heads % kv_heads)
+            fail("attention: the query heads do not share the key heads evenly");
+        if (hd <= 0 || hd > MAX_HD || hd % 8) fail("attention: head_dim must be a multiple of 8 and at most 256");
+        if (qs < heads * hd || kvs < kv_heads * hd) fail("attention: a row stride is shorter than its heads");
+        if (causal && tq > tk) fail("attention: causal attention with more queries than keys");
+        const bool exact = (flags & TRIT_HIP_EXACT) != 0;
+        const int group = heads / kv_heads;
+        if (!exact && (hd != 128 || (group != 1 && group != 2 && group != 4)))
+            fail("attention: the fast form takes head_dim 128 and 1, 2 or 4 query heads per key head");
+        if (exact && (size_t)(MAX_HD + tk + ATT_THREADS) * 4 > 64 * 1024)
+            fail("attention: more keys than the exact kernel's shared memory holds (16000)");
+        hipStream_t s = stream();
+        const size_t qb = (size_t)tq * qs * 4, kb = (size_t)tk * kvs * 4, ob = (size_t)tq * heads * hd * 4;
+        const size_t cache = (size_t)kv_heads * tk * hd * (exact ? 4 : 2);
+        DeviceMemory dq(qb), dk(kb), dv(kb), dkc(cache), dvc(cache), dout(ob), dst(sizeof(State));
+        TRIT_HIP(hipMemcpyAsync(dq.ptr, q, qb, hipMemcpyHostToDevice, s));
+        TRIT_HIP(hipMemcpyAsync(dk.ptr, k, kb, hipMemcpyHostToDevice, s));
+        TRIT_HIP(hipMemcpyAsync(dv.ptr, v, kb, hipMemcpyHostToDevice, s));
+        const int grid = (int)std::min<size_t>(4096, ((size_t)tk * kv_heads * hd + 255) / 256);
+        if (exact) {
+            State st{};
+            st.pos = tk - tq;
+            TRIT_HIP(hipMemcpyAsync(dst.ptr, &st, sizeof(State), hipMemcpyHostToDevice, s));
+            hipLaunchKernelGGL(rows_to_cache_kernel<float>, dim3(grid), dim3(256), 0, s, dk.as<float>(),
+                               dv.as<float>(), kvs, tk, kv_heads, hd, dkc.as<float>(), dvc.as<float>());
+            const size_t lds = (size_t)(MAX_HD + tk + ATT_THREADS) * 4;
+            hipLaunchKernelGGL(attention_kernel<float>, dim3(heads, tq), dim3(ATT_THREADS), lds, s, dq.as<float>(),
+                               qs, heads, kv_heads, hd, dkc.as<float>(), dvc.as<float>(), tk, tq, dout.as<float>(), 1,
+                               dst.as<State>(), causal);
+        } else {
+            hipLaunchKernelGGL(rows_to_cache_kernel<_Float16>, dim3(grid), dim3(256), 0, s, dk.as<float>(),
+                               dv.as<float>(), kvs, tk, kv_heads, hd, dkc.as<_Float16>(), dvc.as<_Float16>());
+            flash_attention(dq.as<float>(), qs, dkc.as<_Float16>(), dvc.as<_Float16>(), tk, heads, kv_heads, tq,
+                            tk - tq, tk, causal, dout.as<float>(), s);
+        }
+        TRIT_HIP(hipGetLastError());
+        TRIT_HIP(hipMemcpyAsync(out, dout.ptr, ob, hipMemcpyDeviceToHost, s));
+        TRIT_HIP(hipStreamSynchronize(s));
+        return 0;
+    });
+}
 
 }  // extern "C"

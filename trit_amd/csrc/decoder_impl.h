@@ -61,6 +61,9 @@ struct SessionImpl {
     DeviceMemory step_words, step_cand, step_table;
     uint32_t step_seq = 0;
     bool step_cand_fresh = false;  // candidates newer than `logits`
+    // A decode step missed its deadline: the caches and the device state
+    // hold a partial step, so the session refuses work until it is reset.
+    bool broken = false;
 
     ~SessionImpl() {
         if (graph) (void)hipGraphExecDestroy(graph);
@@ -72,6 +75,11 @@ struct SessionImpl {
 // with f16 caches; rows of the forward at positions pos0.., layer `layer`.
 bool flash_prefill_supported(const SessionImpl& S);
 void flash_prefill(SessionImpl& S, int layer, int rows, int pos0, hipStream_t s);
+// The same kernel on any queries and f16 caches ([kv head][max_pos][128]):
+// rows query rows (stride qs floats) at positions pos0.., over tk keys;
+// causal, or every key for every row; out rows of heads * 128 floats.
+void flash_attention(const float* q, int qs, const _Float16* kc, const _Float16* vc, int max_pos, int heads,
+                     int kv_heads, int rows, int pos0, int tk, int causal, float* out, hipStream_t s);
 
 // The persistent decode step (decode_step.hip).
 // Whether the session's model and mode run on it.

@@ -337,13 +337,11 @@ void launch_rows(const Layer& L, const GemvArgs& a, hipStream_t s) {
     }
 }
 
-// TRIT_HIP_GEMV_STREAM: 0 never, 1 whenever the shape fits, unset: by size.
+// TRIT_HIP_GEMV_STREAM: 0 never, 1 whenever the shape fits, unset: by size
+// (read at each call, so that tests can switch it).
 int stream_mode() {
-    static const int mode = [] {
-        const char* v = getenv("TRIT_HIP_GEMV_STREAM");
-        return v && *v ? atoi(v) : -1;
-    }();
-    return mode;
+    const char* v = getenv("TRIT_HIP_GEMV_STREAM");
+    return v && *v ? atoi(v) : -1;
 }
 
 template <class W>

@@ -101,23 +101,76 @@ void layer_forward(const Layer& L, const GemvArgs& a, hipStream_t s) {
 }
 
 // Per-thread staging buffers of the host-pointer forward, and the scratch
-// of the calling thread's many-row products.
+// of the calling thread's many-row products. A thread holds one set from a
+// pool; when the thread ends, its set goes back to the pool (no HIP call)
+// and the next thread to need one takes it after a device synchronisation.
+// Nothing frees device memory from a destructor: the main thread's
+// thread-local destructors run inside exit(), where the HIP runtime (or a
+// profiler wrapped around it) may already have shut down.
 struct Staging {
+    int device = -1;
     DeviceMemory x, y, scratch;
 };
-thread_local Staging g_staging;
+
+struct StagingPool {
+    std::mutex mu;
+    std::vector<Staging*> idle;
+};
+
+StagingPool& staging_pool() {
+    static StagingPool* pool = new StagingPool();  // never destroyed
+    return *pool;
+}
+
+struct StagingSlot {
+    Staging* set = nullptr;
+    ~StagingSlot() {
+        if (!set) return;
+        StagingPool& p = staging_pool();
+        std::lock_guard<std::mutex> lock(p.mu);
+        p.idle.push_back(set);
+    }
+};
+thread_local StagingSlot g_slot;
+
+Staging& staging() {
+    if (!g_slot.set) {
+        const int dev = device_id();
+        Staging* got = nullptr;
+        {
+            StagingPool& p = staging_pool();
+            std::lock_guard<std::mutex> lock(p.mu);
+            for (size_t i = 0; i < p.idle.size(); ++i)
+                if (p.idle[i]->device == dev) {
+                    got = p.idle[i];
+                    p.idle.erase(p.idle.begin() + (ptrdiff_t)i);
+                    break;
+                }
+        }
+        if (got) {
+            // Work its previous thread queued may still use it.
+            TRIT_HIP(hipDeviceSynchronize());
+        } else {
+            got = new Staging();
+            got->device = dev;
+        }
+        g_slot.set = got;
+    }
+    return *g_slot.set;
+}
 
 // Rows above this many run on the matrix cores when the layer allows it.
 constexpr int GEMM_MIN_ROWS = 9;
 
 // Grows the calling thread's scratch to `need` bytes.
 void* staging_scratch(size_t need) {
-    if (g_staging.scratch.bytes < need) {
+    Staging& g = staging();
+    if (g.scratch.bytes < need) {
         // Work already queued may still use the old scratch.
         TRIT_HIP(hipDeviceSynchronize());
-        g_staging.scratch.alloc(need);
+        g.scratch.alloc(need);
     }
-    return g_staging.scratch.ptr;
+    return g.scratch.ptr;
 }
 
 // One product of m rows: the matrix-core product for many rows, else the
@@ -364,13 +417,14 @@ int trit_hip_layer_forward(const TritHipLayer* layer, const float* x, int m, int
         if (m <= 0) fail("m must be positive");
         const Layer& L = *layer->layer;
         const size_t xb = (size_t)m * L.k * 4, yb = (size_t)m * L.n * 4;
-        if (g_staging.x.bytes < xb) g_staging.x.alloc(xb);
-        if (g_staging.y.bytes < yb) g_staging.y.alloc(yb);
+        Staging& g = staging();
+        if (g.x.bytes < xb) g.x.alloc(xb);
+        if (g.y.bytes < yb) g.y.alloc(yb);
         hipStream_t st = stream();
-        TRIT_HIP(hipMemcpyAsync(g_staging.x.ptr, x, xb, hipMemcpyHostToDevice, st));
-        if (trit_hip_layer_forward_device(layer, g_staging.x.as<float>(), m, relu, g_staging.y.as<float>(), st) != 0)
+        TRIT_HIP(hipMemcpyAsync(g.x.ptr, x, xb, hipMemcpyHostToDevice, st));
+        if (trit_hip_layer_forward_device(layer, g.x.as<float>(), m, relu, g.y.as<float>(), st) != 0)
             fail(g_error);
-        TRIT_HIP(hipMemcpyAsync(y, g_staging.y.ptr, yb, hipMemcpyDeviceToHost, st));
+        TRIT_HIP(hipMemcpyAsync(y, g.y.ptr, yb, hipMemcpyDeviceToHost, st));
         TRIT_HIP(hipStreamSynchronize(st));
         return 0;
     });

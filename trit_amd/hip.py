@@ -75,6 +75,7 @@ def lib():
             "trit_hip_gguf_meta_f64": (i, [p, C.c_char_p, C.POINTER(C.c_double)]),
             "trit_hip_gguf_meta_str": (i, [p, C.c_char_p, C.POINTER(C.c_char_p)]),
             "trit_hip_decoder_from_gguf": (i, [C.c_char_p, C.c_char_p, C.POINTER(LmConfig), pp]),
+            "trit_hip_attention": (i, [p, i, p, p, i, i, i, i, i, i, i, i, p]),
         }
         for name, (res, args) in sig.items():
             if not hasattr(L, name):
@@ -101,6 +102,18 @@ def ptr(a):
 
 def init(device: int = 0):
     check(lib().trit_hip_init(device))
+
+
+def attention(q, k, v, heads, kv_heads, hd, causal=True, flags=0):
+    """layers::attention (src/layers.rs:343-504) on the device: q tq x qs,
+    k and v tk x kvs f32 rows; returns tq x (heads * hd)."""
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    out = np.empty((q.shape[0], heads * hd), np.float32)
+    check(lib().trit_hip_attention(ptr(q), q.shape[1], ptr(k), ptr(v), k.shape[1], q.shape[0], k.shape[0], heads,
+                                   kv_heads, hd, int(causal), flags, ptr(out)))
+    return out
 
 
 class Dense:
