@@ -280,7 +280,7 @@ def config_lines(H, sweeps=10):
     return out
 
 
-def step_roofline(cfg, prompt, steps, step_ms, persistent):
+def step_roofline(cfg, prompt, steps, step_ms, persistent, mode):
     """The decode loop's kernel: the persistent step (one launch runs every
     step of a generate call) timed with HIP events around it. Algorithmic
     bytes per forward: every Q8_0 weight once (34 B per 32), the f16 head,
@@ -306,8 +306,10 @@ def step_roofline(cfg, prompt, steps, step_ms, persistent):
     return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                 frac=round(achieved / HBM_PEAK_GBS, 4),
                 traffic=STEP_TRAFFIC_BYTES * forwards if persistent else None,
-                kernel=f"step_kernel<4,8,12,2,8>: the persistent decode step (one-pass attention), {steps} steps "
-                       "(choice, 28 layers, head) in one launch" if persistent else "the per-kernel decode step (graph replay)",
+                kernel=(f"step_kernel<4,8,12,2,8,{'false' if mode == 'tree' else 'true'}>: the persistent decode "
+                        f"step ({'tree sums' if mode == 'tree' else 'Trit sum orders'}, one-pass attention), {steps} "
+                        "steps (choice, 28 layers, head) in one launch") if persistent
+                       else "the per-kernel decode step (graph replay)",
                 bytes_per_launch=per_launch, bytes_per_forward=per_forward, forwards=forwards,
                 avg_us=round(avg_ms * 1e3, 3), us_per_forward=round(step_ms * 1e3 / forwards, 3),
                 traffic_per_forward=STEP_TRAFFIC_BYTES if persistent else None, launches=launches,
@@ -466,7 +468,9 @@ def main():
     ap.add_argument("--steps", type=int, default=128, help="greedy decode tokens timed")
     ap.add_argument("--warmup", type=int, default=1, help="untimed prefill + decode runs")
     ap.add_argument("--prompt", type=int, default=256)
-    ap.add_argument("--mode", choices=["fast", "exact"], default="fast")
+    ap.add_argument("--mode", choices=["default", "exact", "tree"], default="default",
+                    help="default: Trit's sums with f16 keys and values; exact: f32 keys and values; "
+                         "tree: tree sums (not Trit's bits)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-configs", action="store_true", help="skip the per-product configuration lines")
     ap.add_argument("--sweeps", type=int, default=20, help="decode-order GEMV sweeps for the roofline")
@@ -501,7 +505,7 @@ def main():
         H.ok(H.L.hipMemcpy(dst, src, C.c_size_t(copy_bytes), 3), "hipMemcpy")
         print(json.dumps({"profile_pass": True, "roofline": roof, "copy_bytes": copy_bytes}), flush=True)
         return
-    flags = hip.EXACT if args.mode == "exact" else 0
+    flags = {"default": 0, "exact": hip.EXACT, "tree": hip.TREE_SUMS}[args.mode]
     max_pos = args.prompt + args.steps
     sess = lm.session(max_pos, flags)
     for _ in range(args.warmup):
@@ -534,7 +538,7 @@ def main():
     value = forwards / t_decode
     print(f"[bench] gpu decode {value:.1f} tok/s (device {forwards / step_ms * 1e3:.1f}), "
           f"prefill {args.prompt / t_prefill:.1f} tok/s", file=sys.stderr, flush=True)
-    step_roof = step_roofline(cfg, args.prompt, args.steps, step_ms, bool(persistent.value))
+    step_roof = step_roofline(cfg, args.prompt, args.steps, step_ms, bool(persistent.value), args.mode)
 
     print("[bench] roofline sweep ...", file=sys.stderr, flush=True)
     roof = gemv_roofline(H, linears, cfg, args.sweeps)
@@ -556,7 +560,8 @@ def main():
                                f"greedy decode steps ({forwards} forwards; tokens/s = forwards/s), batch 1, "
                                "tied f16 head", "layers": 28, "d": 1024, "heads": "16/8x128",
                    "ffn": 3072, "vocab": 151936, "prompt": args.prompt, "mode": args.mode,
-                   "kv_cache": "f32" if args.mode == "exact" else "f16"},
+                   "kv_cache": "f32" if args.mode == "exact" else "f16",
+                   "sums": "tree" if args.mode == "tree" else "trit order (bit-exact)"},
         "prefill_tokens_per_s": round(args.prompt / t_prefill, 1),
         "roofline": step_roof,
         "gemv_roofline": roof,

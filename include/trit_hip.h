@@ -144,9 +144,16 @@ int trit_hip_decoder_new(const TritHipLmConfig *config, const TritHipLayer *cons
                          TritHipDecoder **out);
 void trit_hip_decoder_free(TritHipDecoder *decoder);
 
+/* Session flags. Every sum runs in Trit's order unless TRIT_HIP_TREE_SUMS
+ * is given: the default (0) is Trit's arithmetic with f16 keys and values
+ * (each appended key and value rounded through f16), bit for bit. */
 enum {
-    TRIT_HIP_EXACT = 1, /* every sum in Trit's order, f32 keys and values    */
-    TRIT_HIP_KV_F32 = 2 /* f32 keys and values without the rest of EXACT     */
+    TRIT_HIP_EXACT = 1,     /* Trit's arithmetic throughout: f32 keys and values */
+    TRIT_HIP_KV_F32 = 2,    /* f32 keys and values                              */
+    TRIT_HIP_TREE_SUMS = 4  /* RMSNorm, q/k norm and attention sums as parallel
+                               trees (faster; the int8 activation codes then
+                               differ from Trit's where a value lies within
+                               rounding of a code boundary)                     */
 };
 
 /* Per-call state: the key/value caches of up to max_positions positions

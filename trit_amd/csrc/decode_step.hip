@@ -284,6 +284,44 @@ __device__ __forceinline__ float norm_inv_wave(int t, const float* x, float eps)
     return 1.0f / __builtin_sqrtf(sum / (float)K + eps);
 }
 
+// The serial chain of a wave's values in lane order: lane L holds values
+// N L .. N L + N - 1 of the chain in v[]; returns (in every lane) the sum
+// ((c0 + v_0) + v_1) + ... in that order, for `lanes` lanes. Each round
+// every lane runs the chain of its own values from the same carry, and the
+// carry becomes lane L's result: the chain after lanes 0..L, bit for bit,
+// with every operand in registers (a dependent add per value).
+template <int N>
+__device__ __forceinline__ float lane_chain(const float (&v)[N], float c0, int lanes) {
+    float carry = c0;
+    for (int L = 0; L < lanes; ++L) {
+        float s = carry;
+#pragma unroll
+        for (int i = 0; i < N; ++i) s = s + v[i];
+        carry = lane_f(s, L);
+    }
+    return carry;
+}
+
+// RMSNorm factor of x (K = 256 J values in LDS) in Trit's order: the
+// squares added one after another from 0 (src/layers.rs:138-139), by one
+// wave (lane L holds values [4J L, 4J L + 4J)).
+template <int J>
+__device__ __forceinline__ float norm_inv_serial(int t, const float* x, float eps) {
+    constexpr int K = J * 256, N = K / WAVE;
+    const int lane = t % WAVE;
+    float sq[N];
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+        const float4 v = *(const float4*)(x + (size_t)lane * N + i);
+        sq[i] = v.x * v.x;
+        sq[i + 1] = v.y * v.y;
+        sq[i + 2] = v.z * v.z;
+        sq[i + 3] = v.w * v.w;
+    }
+    const float sum = lane_chain<N>(sq, 0.0f, WAVE);
+    return 1.0f / __builtin_sqrtf(sum / (float)K + eps);
+}
+
 // The RMSNorm weights of the quantizer items a thread takes (item t + T i),
 // loaded ahead of the phase's wait.
 template <int J>
@@ -828,6 +866,169 @@ __device__ bool attention_all(int t, const StepArgs& a, const LayerPtrs& L, int 
     return true;
 }
 
+// One pass over every key in Trit's order (src/layers.rs:442-504,571-587;
+// the orders of src/cpu/fgemm.rs:665-793 and src/cpu/activation.rs
+// exp_sums): the block's query head and output dims as in attention_all,
+// but thread j scores key j (up to T keys) as one fused chain over the 128
+// dims of q * (1/sqrt(hd)); the maximum (order-free); e_j = exp(s_j - max);
+// their sum added in key order from 0; p_j = e_j * (1/sum); and each output
+// dim a fused chain of p_j * v_j over the keys in order -- wave w the dim
+// e0 + w. The q/k norm sums are serial too. The values are Trit's with the
+// f16 caches, bit for bit.
+template <int GROUP, int DPB>
+__device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, int pos, uint32_t tag_in,
+                                uint32_t tag_out, Smem& sm, unsigned long long deadline) {
+    static_assert(DPB == 4 || DPB == 8, "4 or 8 dims a block");
+    constexpr int PK = T / WAVE;  // keys a lane holds in the sum and p.V chains
+    const int b = blockIdx.x, kvh = a.kvh, g = b % kvh, hq = (b / kvh) % GROUP, e0 = DPB * (b / (kvh * GROUP));
+    const int tk = pos + 1;  // at most T (the host's plan)
+    const int heads = a.heads;
+    const auto index = [g, heads, kvh](int i) {
+        if (i < GROUP * HD) return g * GROUP * HD + i;
+        if (i < (GROUP + 1) * HD) return (heads + g) * HD + (i - GROUP * HD);
+        return (heads + kvh + g) * HD + (i - (GROUP + 1) * HD);
+    };
+    const _Float16* K = L.kcache + (size_t)g * a.max_pos * HD;
+    const _Float16* V = L.vcache + (size_t)g * a.max_pos * HD;
+    const int w = t / WAVE, lane = t % WAVE;
+    // Key t (all 128 dims) and, in wave w < DPB, dim e0 + w of keys
+    // PK lane .. PK lane + PK - 1, load while the qkv rows arrive.
+    uint4 kk[HD / 8];
+#pragma unroll
+    for (int i = 0; i < HD / 8; ++i) kk[i] = make_uint4(0, 0, 0, 0);
+    if (t < tk && t != pos) {
+        const uint4* src = (const uint4*)(K + (size_t)t * HD);
+#pragma unroll
+        for (int i = 0; i < HD / 8; ++i) kk[i] = src[i];
+    }
+    float vv[PK];
+#pragma unroll
+    for (int i = 0; i < PK; ++i) {
+        const int j = PK * lane + i;
+        vv[i] = (w < DPB && j < tk && j != pos) ? (float)V[(size_t)j * HD + e0 + w] : 0.0f;
+    }
+    const int hh = w, i = lane;
+    float nw0 = 1.0f, nw1 = 1.0f, sn = 0.0f, cs = 1.0f;
+    if (hh <= GROUP) {
+        if (a.qk_norm) {
+            const float* nw = hh < GROUP ? L.q_norm : L.k_norm;
+            nw0 = nw[i];
+            nw1 = nw[i + HD / 2];
+        }
+        sn = a.rope_sin[(size_t)pos * (HD / 2) + i];
+        cs = a.rope_cos[(size_t)pos * (HD / 2) + i];
+    }
+    if (!gather<8>(t, a.QKV, (GROUP + 2) * HD, index, tag_in, sm.qkv, sm, deadline, a.st, NW - a.rq / 4 - 1))
+        return false;
+
+    // Qwen3's per-head RMSNorm (the serial sum of the squares, lane L
+    // holding dims 2L, 2L + 1) and the rotary halves, wave hh head hh, lane
+    // i dims i and i + 64 (src/models/parts/causal_lm.rs:428-446,
+    // src/layers.rs:136-144,303-334); the first block of the head appends
+    // the new key and value (agent scope: later steps read them elsewhere).
+    if (hh < GROUP + 2) {
+        float x0 = sm.qkv[hh * HD + i], x1 = sm.qkv[hh * HD + i + HD / 2];
+        if (hh <= GROUP) {
+            if (a.qk_norm) {
+                const float2 pr = *(const float2*)(sm.qkv + hh * HD + 2 * i);
+                const float sq[2] = {pr.x * pr.x, pr.y * pr.y};
+                const float sum = lane_chain<2>(sq, 0.0f, WAVE);
+                const float inv = 1.0f / __builtin_sqrtf(sum / (float)HD + a.eps);
+                x0 = x0 * (inv * nw0);
+                x1 = x1 * (inv * nw1);
+            }
+            const float ac = x0 * cs, bs = x1 * sn, bc = x1 * cs, as = x0 * sn;
+            x0 = ac - bs;
+            x1 = bc + as;
+        }
+        if (hh < GROUP) {
+            const float scale = 1.0f / __builtin_sqrtf((float)HD);
+            x0 = x0 * scale;
+            x1 = x1 * scale;
+        } else {
+            const int which = hh - GROUP;
+            const _Float16 c0 = (_Float16)x0, c1 = (_Float16)x1;
+            if (b < kvh) {
+                uint16_t* cache =
+                    (uint16_t*)(which == 0 ? L.kcache : L.vcache) + ((size_t)g * a.max_pos + pos) * HD;
+                __hip_atomic_store(cache + i, __builtin_bit_cast(uint16_t, c0), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(cache + i + HD / 2, __builtin_bit_cast(uint16_t, c1), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
+            sm.kvn[which][i] = (float)c0;
+            sm.kvn[which][i + HD / 2] = (float)c1;
+        }
+        // The norm's chain read the raw values of this head: rewrite them
+        // only after every lane of the wave has read its pair.
+        __builtin_amdgcn_wave_barrier();
+        if (hh < GROUP) {
+            sm.qkv[hh * HD + i] = x0;
+            sm.qkv[hh * HD + i + HD / 2] = x1;
+        }
+    }
+    __syncthreads();
+
+    // Scores: thread t key t, the fused chain over the dims in order.
+    float* probs = &sm.gpart[0][0];  // T values
+    float* wmax = &sm.gpart[4][0];   // NW values
+    float score = -INFINITY;
+    if (t < tk) {
+        const float* q = sm.qkv + hq * HD;
+        float acc = 0.0f;
+        if (t == pos) {
+#pragma unroll 16
+            for (int e = 0; e < HD; ++e) acc = __builtin_fmaf(q[e], sm.kvn[0][e], acc);
+        } else {
+#pragma unroll
+            for (int c = 0; c < HD / 8; ++c) {
+                float k8[8];
+                unpack8(kk[c], k8);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(q[8 * c + u], k8[u], acc);
+            }
+        }
+        score = acc;
+    }
+    const float m_w = wave_max(score);
+    if (lane == 0) wmax[w] = m_w;
+    __syncthreads();
+    float mx = wmax[0];
+#pragma unroll
+    for (int q = 1; q < NW; ++q) mx = __builtin_fmaxf(mx, wmax[q]);
+    probs[t] = t < tk ? exp_trit(score - mx) : 0.0f;
+    __syncthreads();
+    // The sum in key order from 0 (the zeros past the keys add nothing),
+    // then p_j = e_j * (1/sum) and the p.V chains, wave w dim e0 + w.
+    if (w < DPB) {
+        const int rounds = (tk + PK - 1) / PK;
+        float e[PK];
+#pragma unroll
+        for (int q = 0; q < PK; q += 4) {
+            const float4 v4 = *(const float4*)(probs + PK * lane + q);
+            e[q] = v4.x;
+            e[q + 1] = v4.y;
+            e[q + 2] = v4.z;
+            e[q + 3] = v4.w;
+        }
+        const float sum = lane_chain<PK>(e, 0.0f, rounds);
+        const float inv = 1.0f / sum;
+        float carry = 0.0f;
+        for (int Ln = 0; Ln < rounds; ++Ln) {
+            float acc = carry;
+#pragma unroll
+            for (int q = 0; q < PK; ++q) {
+                const int j = PK * lane + q;
+                const float v = j == pos ? sm.kvn[1][e0 + w] : vv[q];
+                acc = __builtin_fmaf(e[q] * inv, v, acc);
+            }
+            carry = lane_f(acc, Ln);
+        }
+        if (lane == 0) put(a.ATT + (size_t)(g * GROUP + hq) * HD + e0 + w, carry, tag_out);
+    }
+    return true;
+}
+
 __device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
     if (v > bv || (v == bv && i < bi)) {
         bv = v;
@@ -862,7 +1063,7 @@ __device__ __forceinline__ void best_of_wave(float& bv, int& bi) {
     for (int r = 1; r < 4; ++r) better(bv, bi, v[r], i[r]);
 }
 
-template <int JD, int JO, int JF, int GROUP, int DPB>
+template <int JD, int JO, int JF, int GROUP, int DPB, bool EXACT>
 __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int pos0, uint32_t seq0, int nsteps) {
     __shared__ Smem sm;
     State* st = a.st;
@@ -979,7 +1180,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         if (layer > 0 && !gather<6>(t, a.X, a.d, lin, tag_of(tag0, layer - 1, 5), sm.xres, sm, deadline, st))
             return;
         if (w == 0) {
-            const float inv = norm_inv_wave<JD>(t, sm.xres, a.eps);
+            const float inv = EXACT ? norm_inv_serial<JD>(t, sm.xres, a.eps) : norm_inv_wave<JD>(t, sm.xres, a.eps);
             if (lane == 0) sm.inv = inv;
         }
         __syncthreads();
@@ -992,9 +1193,11 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         __syncthreads();
         if constexpr (DPB > 0) {
             // attention in one pass: its outputs are the o product's input.
-            if (!attention_all<GROUP, DPB>(t, a, L, pos, tag_of(tag0, layer, 0), tag_of(tag0, layer, 2), sm,
-                                           deadline))
-                return;
+            const bool ok = EXACT ? attention_exact<GROUP, DPB>(t, a, L, pos, tag_of(tag0, layer, 0),
+                                                                tag_of(tag0, layer, 2), sm, deadline)
+                                  : attention_all<GROUP, DPB>(t, a, L, pos, tag_of(tag0, layer, 0),
+                                                              tag_of(tag0, layer, 2), sm, deadline);
+            if (!ok) return;
             // o + residual; the o and gate_up rows stream in meanwhile, and
             // the qkv waves (nothing in flight) poll.
             if (ao)
@@ -1038,7 +1241,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         __syncthreads();
         if (!gather<MAXK / T>(t, a.X, a.d, lin, tag_of(tag0, layer, 3), sm.xres, sm, deadline, st)) return;
         if (w == 0) {
-            const float inv = norm_inv_wave<JD>(t, sm.xres, a.eps);
+            const float inv = EXACT ? norm_inv_serial<JD>(t, sm.xres, a.eps) : norm_inv_wave<JD>(t, sm.xres, a.eps);
             if (lane == 0) sm.inv = inv;
         }
         __syncthreads();
@@ -1096,7 +1299,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     for (int q = 0; q < (MAXD + T - 1) / T; ++q) fn[q] = t + T * q < a.d ? a.final_norm[t + T * q] : 0.0f;
     if (!gather<MAXD / T>(t, a.X, a.d, lin, tag_of(tag0, a.n_layers - 1, 5), sm.xres, sm, deadline, st)) return;
     if (w == 0) {
-        const float inv = norm_inv_wave<JD>(t, sm.xres, a.eps);
+        const float inv = EXACT ? norm_inv_serial<JD>(t, sm.xres, a.eps) : norm_inv_wave<JD>(t, sm.xres, a.eps);
         if (lane == 0) sm.inv = inv;
     }
     __syncthreads();
@@ -1210,14 +1413,16 @@ using StepFn = void (*)(StepArgs, int, int, uint32_t, int);
 // The instantiated shapes: (d/256, heads*hd/256, ffn/256, q heads per kv head).
 // dpb: output dims of one query head a block takes in the one-pass
 // attention, 0 for the split attention and its combine.
-StepFn step_fn(int jd, int jo, int jf, int group, int dpb) {
+StepFn step_fn(int jd, int jo, int jf, int group, int dpb, bool exact) {
     if (jd == 4 && jo == 8 && jf == 12 && group == 2) {  // Qwen3-0.6B
-        if (dpb == 0) return step_kernel<4, 8, 12, 2, 0>;
-        if (dpb == 8) return step_kernel<4, 8, 12, 2, 8>;
+        if (exact) return dpb == 8 ? step_kernel<4, 8, 12, 2, 8, true> : nullptr;
+        if (dpb == 0) return step_kernel<4, 8, 12, 2, 0, false>;
+        if (dpb == 8) return step_kernel<4, 8, 12, 2, 8, false>;
     }
     if (jd == 4 && jo == 4 && jf == 8 && group == 2) {
-        if (dpb == 0) return step_kernel<4, 4, 8, 2, 0>;
-        if (dpb == 4) return step_kernel<4, 4, 8, 2, 4>;
+        if (exact) return dpb == 4 ? step_kernel<4, 4, 8, 2, 4, true> : nullptr;
+        if (dpb == 0) return step_kernel<4, 4, 8, 2, 0, false>;
+        if (dpb == 4) return step_kernel<4, 4, 8, 2, 4, false>;
     }
     return nullptr;
 }
@@ -1245,7 +1450,7 @@ bool split_forced() {
 bool plan(const SessionImpl& S, Plan& p) {
     const DecoderImpl& D = *S.dec;
     const auto& c = D.c;
-    if (S.exact || S.kv32) return false;
+    if (S.kv32) return false;
     if (c.head_dim != HD || c.kv_heads <= 0 || c.heads % c.kv_heads != 0) return false;
     const int group = c.heads / c.kv_heads, qd = c.heads * HD;
     if (c.d % 256 || qd % 256 || c.ffn % 256 || c.d > MAXD || qd > MAXK || c.ffn > MAXK) return false;
@@ -1277,17 +1482,28 @@ bool plan(const SessionImpl& S, Plan& p) {
     // The one-pass attention: every key of the session in registers, each
     // block dpb dims of one query head.
     p.dpb = (qd % p.blocks) ? 0 : qd / p.blocks;
+    if (S.exact) {
+        // Trit's sum orders: the one-pass attention with a thread per key
+        // (up to T positions), wave w output dim w of the block's DPB.
+        if (S.max_pos > T || (p.dpb != 4 && p.dpb != 8) || p.blocks % (c.kv_heads * group) ||
+            !fits(qd, NW - nqw, 8))
+            return false;
+        p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group, p.dpb, true);
+        if (!p.fn) return false;
+        p.rh = (c.vocab + p.blocks - 1) / p.blocks;
+        return true;
+    }
     const bool one_pass = !split_forced() && S.max_pos <= 32 * MAXF && (p.dpb == 4 || p.dpb == 8) &&
                           p.blocks % (c.kv_heads * group) == 0 && fits(qd, NW - nqw, 8);
     if (one_pass) {
-        p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group, p.dpb);
+        p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group, p.dpb, false);
     } else {
         p.dpb = 0;
         if (S.max_pos > p.splits * 32 * MAXC) return false;
         if ((qd % p.blocks) || HD % p.comb) return false;
         if (p.splits > WAVE || p.comb > NW || p.splits * (2 + p.comb) > MAXK) return false;
         if (!fits(p.splits * (2 + p.comb), NW - nqw, 2) || !fits(qd, nu, 8)) return false;
-        p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group, 0);
+        p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group, 0, false);
     }
     if (!p.fn) return false;
     p.rh = (c.vocab + p.blocks - 1) / p.blocks;

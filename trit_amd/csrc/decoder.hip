@@ -1027,6 +1027,13 @@ void ensure_rows(SessionImpl& S, int rows) {
     }
 }
 
+// TRIT_HIP_QK_WAVE=0 runs the prompt's q/k norm and rotary one block a
+// head (qk_rope_kernel) at head_dim 128 too.
+bool use_qk_wave() {
+    const char* v = getenv("TRIT_HIP_QK_WAVE");
+    return !(v && v[0] == '0');
+}
+
 // TRIT_HIP_FLASH=0 keeps prompt attention on the split kernel.
 bool use_flash() {
     const char* v = getenv("TRIT_HIP_FLASH");
@@ -1134,14 +1141,22 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
         // q/k norm, rotary, cache append, attention.
         const bool fused = !S.exact && rows == 1;
         if (!fused) {
-            if (S.kv32) {
+            if (S.exact && !S.kv32) {
+                // Trit's serial q/k norm sums, f16 caches.
+                hipLaunchKernelGGL(qk_rope_kernel<_Float16>, dim3(rows * (c.heads + 2 * c.kv_heads)),
+                                   dim3(hd < 64 ? 64 : hd), 0, s, S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
+                                   c.qk_norm, D.q_norm(l), D.k_norm(l), c.eps, S.rope_sin.as<float>(),
+                                   S.rope_cos.as<float>(),
+                                   S.kcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd,
+                                   S.vcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, st);
+            } else if (S.kv32) {
                 hipLaunchKernelGGL(qk_rope_kernel<float>, dim3(rows * (c.heads + 2 * c.kv_heads)),
                                    dim3(hd < 64 ? 64 : hd), 0, s, S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
                                    c.qk_norm, D.q_norm(l), D.k_norm(l), c.eps, S.rope_sin.as<float>(),
                                    S.rope_cos.as<float>(),
                                    S.kcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd,
                                    S.vcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, st);
-            } else if (hd == 128) {
+            } else if (hd == 128 && use_qk_wave()) {
                 const int items = rows * (c.heads + 2 * c.kv_heads);
                 hipLaunchKernelGGL(qk_rope_wave_kernel<_Float16>, dim3((items + 3) / 4), dim3(256), 0, s,
                                    S.qkv.as<float>(), stride, rows, c.heads, c.kv_heads, c.qk_norm, D.q_norm(l),
@@ -1161,11 +1176,18 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
         if (S.exact) {
             // The host sizes shared memory for the largest key count this forward can see.
             const size_t lds = (size_t)(MAX_HD + S.max_pos + ATT_THREADS) * 4;
-            hipLaunchKernelGGL(attention_kernel<float>, dim3(c.heads, rows), dim3(ATT_THREADS), lds, s,
-                               S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
-                               S.kcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd,
-                               S.vcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, rows,
-                               S.att.as<float>(), 1, st);
+            if (S.kv32)
+                hipLaunchKernelGGL(attention_kernel<float>, dim3(c.heads, rows), dim3(ATT_THREADS), lds, s,
+                                   S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
+                                   S.kcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd,
+                                   S.vcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, rows,
+                                   S.att.as<float>(), 1, st, 1);
+            else
+                hipLaunchKernelGGL(attention_kernel<_Float16>, dim3(c.heads, rows), dim3(ATT_THREADS), lds, s,
+                                   S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
+                                   S.kcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd,
+                                   S.vcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos,
+                                   rows, S.att.as<float>(), 1, st, 1);
         } else if (fused && (S.kv32 ? launch_decode<float>(S, l, s) : launch_decode<_Float16>(S, l, s))) {
             // One block per key/value head.
         } else if (!fused && rows > 1 && flash_prefill_supported(S) && use_flash()) {
@@ -1390,8 +1412,12 @@ int trit_hip_session_new(const TritHipDecoder* decoder, int max_positions, int f
             const auto& c = s.dec->c;
             s.max_pos = max_positions;
             s.flags = flags;
-            s.exact = (flags & TRIT_HIP_EXACT) != 0;
-            s.kv32 = s.exact || (flags & TRIT_HIP_KV_F32) != 0;
+            // Trit's sum orders unless tree sums are asked for; f32 caches
+            // with EXACT (Trit's own arithmetic) or KV_F32.
+            s.exact = (flags & TRIT_HIP_EXACT) != 0 || (flags & TRIT_HIP_TREE_SUMS) == 0;
+            s.kv32 = (flags & (TRIT_HIP_EXACT | TRIT_HIP_KV_F32)) != 0;
+            if ((flags & TRIT_HIP_EXACT) && (flags & TRIT_HIP_TREE_SUMS))
+                fail("session: EXACT and TREE_SUMS exclude each other");
             const size_t lds = (size_t)(MAX_HD + max_positions + ATT_THREADS) * 4;
             if (lds > 64 * 1024) fail("session: max_positions above the attention kernel's limit (16000)");
             const size_t kvb = (size_t)c.layers * c.kv_heads * max_positions * c.head_dim * (s.kv32 ? 4 : 2);

@@ -18,7 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libtrit_hip.so")
 
 Q8_0, INT8, TERNARY, Q4_K, F16 = 1, 2, 3, 4, 5
-EXACT, KV_F32 = 1, 2
+EXACT, KV_F32, TREE_SUMS = 1, 2, 4
 
 _lib = None
 
