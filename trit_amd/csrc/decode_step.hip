@@ -44,6 +44,7 @@ constexpr int MAXF = 12;       // 32-key chunks of the one-pass attention (384 p
 constexpr int MAXD = 2048;     // largest d
 constexpr int MAXK = 3072;     // largest product input
 constexpr int PH = 6;          // exchange phases per layer
+constexpr int MAXL = 41;       // layers: the exchange tags of a step fit in 8 bits
 
 constexpr int cmax(int x, int y) { return x > y ? x : y; }
 
@@ -84,18 +85,31 @@ struct StepArgs {
 };
 
 struct Smem {
+    // The per-layer pointers, copied from the table at the launch's start:
+    // reading them from LDS waits for nothing else, where a vector load of
+    // the table would wait for every weight load in flight.
+    LayerPtrs layers[MAXL];
     alignas(16) float xres[MAXD];  // the residual stream, this phase's copy
     alignas(16) float xin[MAXK];   // a product's input / gathered partials
     alignas(16) int8_t xq[MAXK];
     alignas(16) float xs[MAXK / 32];
     alignas(16) float qkv[6 * HD];  // a key/value head's q heads, k, v
     alignas(16) float kvn[2][HD];   // the new key and value, as cached
-    alignas(16) float gpart[32][2 * HD];  // attention: per 16-lane group p.V of two heads
+    union {
+        alignas(16) float gpart[32][2 * HD];  // attention: per 16-lane group p.V of two heads
+        // The exact attention: the keys' values of the block's 64 dims,
+        // dim-major, rows padded by 16 bytes (a wave's 16-byte reads of 64
+        // rows then fall on distinct banks in each group of 16 lanes).
+        alignas(16) _Float16 vs[HD / 2][T + 8];
+    };
+    alignas(16) float probs[T];               // the exact attention's probabilities
+    float wmax[NW];
     float gmax[32][2];
     float gl[32][2];
     float bv[T];
     int bi[T];
     float inv;
+    float chain;  // a plain serial chain's result, passed between waves
     int abort;
     int token;
 };
@@ -236,7 +250,7 @@ __device__ __forceinline__ void load_rows(int t, const uint8_t* codes, const uin
         const uint8_t* src = codes + (size_t)(p * part_rows + row) * K;
 #pragma unroll
         for (int j = 0; j < J; ++j) r.w[p * J + j] = load_stream(src + (size_t)(l + 16 * j) * 16);
-        const uint16_t* sc = scales + (size_t)(p * part_rows + row) * G + (l >> 1);
+        const TRIT_GLOBAL uint16_t* sc = gmem(scales) + (size_t)(p * part_rows + row) * G + (l >> 1);
 #pragma unroll
         for (int j = 0; j < J; j += 2)
             r.ws[p * ((J + 1) / 2) + j / 2] =
@@ -303,23 +317,28 @@ __device__ __forceinline__ float lane_chain(const float (&v)[N], float c0, int l
 }
 
 // RMSNorm factor of x (K = 256 J values in LDS) in Trit's order: the
-// squares added one after another from 0 (src/layers.rs:138-139), by one
-// wave (lane L holds values [4J L, 4J L + 4J)).
+// squares added one after another from 0 (src/layers.rs:138-139) by the
+// first wave, lane L holding values [K/32 L, K/32 (L + 1)) of the chain
+// (a dependent add per value, a lane move per K/32 values). Every thread
+// calls it and gets the factor.
 template <int J>
-__device__ __forceinline__ float norm_inv_serial(int t, const float* x, float eps) {
-    constexpr int K = J * 256, N = K / WAVE;
-    const int lane = t % WAVE;
-    float sq[N];
+__device__ float norm_inv_exact(int t, const float* x, float eps, Smem& sm) {
+    constexpr int K = J * 256, N = K / 32;
+    if (t < WAVE) {
+        float sq[N];
 #pragma unroll
-    for (int i = 0; i < N; i += 4) {
-        const float4 v = *(const float4*)(x + (size_t)lane * N + i);
-        sq[i] = v.x * v.x;
-        sq[i + 1] = v.y * v.y;
-        sq[i + 2] = v.z * v.z;
-        sq[i + 3] = v.w * v.w;
+        for (int i = 0; i < N; i += 4) {
+            const float4 v = t < 32 ? *(const float4*)(x + (size_t)t * N + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            sq[i] = v.x * v.x;
+            sq[i + 1] = v.y * v.y;
+            sq[i + 2] = v.z * v.z;
+            sq[i + 3] = v.w * v.w;
+        }
+        const float sum = lane_chain<N>(sq, 0.0f, 32);
+        if (t == 0) sm.chain = 1.0f / __builtin_sqrtf(sum / (float)K + eps);
     }
-    const float sum = lane_chain<N>(sq, 0.0f, WAVE);
-    return 1.0f / __builtin_sqrtf(sum / (float)K + eps);
+    __syncthreads();
+    return sm.chain;
 }
 
 // The RMSNorm weights of the quantizer items a thread takes (item t + T i),
@@ -335,7 +354,7 @@ __device__ __forceinline__ void load_norm(int t, const float* norm_w, NormRegs<J
 #pragma unroll
     for (int i = 0; i < NormRegs<J>::N; ++i) {
         const int item = t + T * i;
-        r.w[i] = item < J * 64 ? *(const float4*)(norm_w + (size_t)item * 4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        r.w[i] = item < J * 64 ? gload_f4(norm_w + (size_t)item * 4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
 }
 
@@ -423,8 +442,8 @@ __device__ __forceinline__ void kv_prefetch(int t, const _Float16* K, const _Flo
         if (j0 + 32 * i >= j1) continue;  // past the split's keys (uniform)
         const int j = j0 + G + 32 * i;
         if (j < j1 && j != pos) {  // the new key comes from the qkv product
-            kv.k[i] = *(const uint4*)(K + (size_t)j * HD + l16 * 8);
-            kv.v[i] = *(const uint4*)(V + (size_t)j * HD + l16 * 8);
+            kv.k[i] = gload_u4(K + (size_t)j * HD + l16 * 8);
+            kv.v[i] = gload_u4(V + (size_t)j * HD + l16 * 8);
         }
     }
 }
@@ -462,12 +481,12 @@ __device__ bool attention(int t, const StepArgs& a, const LayerPtrs& L, int pos,
     float nw0 = 1.0f, nw1 = 1.0f, sn = 0.0f, cs = 1.0f;
     if (hh <= GROUP) {
         if (a.qk_norm) {
-            const float* nw = hh < GROUP ? L.q_norm : L.k_norm;
+            const TRIT_GLOBAL float* nw = gmem(hh < GROUP ? L.q_norm : L.k_norm);
             nw0 = nw[i];
             nw1 = nw[i + HD / 2];
         }
-        sn = a.rope_sin[(size_t)pos * (HD / 2) + i];
-        cs = a.rope_cos[(size_t)pos * (HD / 2) + i];
+        sn = gmem(a.rope_sin)[(size_t)pos * (HD / 2) + i];
+        cs = gmem(a.rope_cos)[(size_t)pos * (HD / 2) + i];
     }
     // One wave polls: the first whose 16-lane groups load no key and that
     // stored no qkv value (the qkv rows sit in the last a.rq / 4 waves).
@@ -504,8 +523,8 @@ __device__ bool attention(int t, const StepArgs& a, const LayerPtrs& L, int pos,
                 // Later steps of this launch read them from other CUs: the
                 // stores are agent-scope (written through to where every CU
                 // reads).
-                uint16_t* cache =
-                    (uint16_t*)(which == 0 ? L.kcache : L.vcache) + ((size_t)g * a.max_pos + pos) * HD;
+                TRIT_GLOBAL uint16_t* cache =
+                    gmem((uint16_t*)(which == 0 ? L.kcache : L.vcache)) + ((size_t)g * a.max_pos + pos) * HD;
                 __hip_atomic_store(cache + i, __builtin_bit_cast(uint16_t, c0), __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_store(cache + i + HD / 2, __builtin_bit_cast(uint16_t, c1), __ATOMIC_RELAXED,
@@ -708,25 +727,30 @@ __device__ bool attention_all(int t, const StepArgs& a, const LayerPtrs& L, int 
         if (i >= rounds) continue;  // uniform
         const int j = G + 64 * i;
         if (j < tk && j != pos) {
-            const uint4* src = (const uint4*)(K + (size_t)j * HD + l8 * 16);
-            kr[i][0] = src[0];
-            kr[i][1] = src[1];
+            const _Float16* src = K + (size_t)j * HD + l8 * 16;
+            kr[i][0] = gload_u4(src);
+            kr[i][1] = gload_u4(src + 8);
         }
     }
     using VT = typename std::conditional<DPB == 8, uint4, uint2>::type;
     VT vr{};
     const int jv = G + 64 * l8;  // the key of this lane's probability
-    if (l8 < rounds && jv < tk && jv != pos) vr = *(const VT*)(V + (size_t)jv * HD + e0);
+    if (l8 < rounds && jv < tk && jv != pos) {
+        if constexpr (DPB == 8)
+            vr = gload_u4(V + (size_t)jv * HD + e0);
+        else
+            vr = gload_u2(V + (size_t)jv * HD + e0);
+    }
     const int hh = t / WAVE, i = t % WAVE;
     float nw0 = 1.0f, nw1 = 1.0f, sn = 0.0f, cs = 1.0f;
     if (hh <= GROUP) {
         if (a.qk_norm) {
-            const float* nw = hh < GROUP ? L.q_norm : L.k_norm;
+            const TRIT_GLOBAL float* nw = gmem(hh < GROUP ? L.q_norm : L.k_norm);
             nw0 = nw[i];
             nw1 = nw[i + HD / 2];
         }
-        sn = a.rope_sin[(size_t)pos * (HD / 2) + i];
-        cs = a.rope_cos[(size_t)pos * (HD / 2) + i];
+        sn = gmem(a.rope_sin)[(size_t)pos * (HD / 2) + i];
+        cs = gmem(a.rope_cos)[(size_t)pos * (HD / 2) + i];
     }
     if (!gather<8>(t, a.QKV, (GROUP + 2) * HD, index, tag_in, sm.qkv, sm, deadline, a.st, NW - a.rq / 4 - 1))
         return false;
@@ -756,8 +780,8 @@ __device__ bool attention_all(int t, const StepArgs& a, const LayerPtrs& L, int 
             const int which = hh - GROUP;
             const _Float16 c0 = (_Float16)x0, c1 = (_Float16)x1;
             if (b < kvh) {
-                uint16_t* cache =
-                    (uint16_t*)(which == 0 ? L.kcache : L.vcache) + ((size_t)g * a.max_pos + pos) * HD;
+                TRIT_GLOBAL uint16_t* cache =
+                    gmem((uint16_t*)(which == 0 ? L.kcache : L.vcache)) + ((size_t)g * a.max_pos + pos) * HD;
                 __hip_atomic_store(cache + i, __builtin_bit_cast(uint16_t, c0), __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_store(cache + i + HD / 2, __builtin_bit_cast(uint16_t, c1), __ATOMIC_RELAXED,
@@ -866,73 +890,123 @@ __device__ bool attention_all(int t, const StepArgs& a, const LayerPtrs& L, int 
     return true;
 }
 
-// One pass over every key in Trit's order (src/layers.rs:442-504,571-587;
-// the orders of src/cpu/fgemm.rs:665-793 and src/cpu/activation.rs
-// exp_sums): the block's query head and output dims as in attention_all,
-// but thread j scores key j (up to T keys) as one fused chain over the 128
-// dims of q * (1/sqrt(hd)); the maximum (order-free); e_j = exp(s_j - max);
-// their sum added in key order from 0; p_j = e_j * (1/sum); and each output
-// dim a fused chain of p_j * v_j over the keys in order -- wave w the dim
-// e0 + w. The q/k norm sums are serial too. The values are Trit's with the
-// f16 caches, bit for bit.
+// The chain sum ((0 + v_0) + v_1) + ... of n <= 32 N values in LDS, in
+// order, by one wave: lane L takes values [N L, N L + N) (zeros past n,
+// which add nothing) and lane_chain passes the carry through the lanes.
+// Every lane of the wave returns the sum.
+template <int N>
+__device__ __forceinline__ float wave_chain_sum(const float* v, int n, int lane) {
+    float x[N];
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+        const float4 f = N * lane + i < n ? *(const float4*)(v + N * lane + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        x[i] = f.x, x[i + 1] = f.y, x[i + 2] = f.z, x[i + 3] = f.w;
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if (N * lane + i >= n) x[i] = 0.0f;
+    return lane_chain<N>(x, 0.0f, (n + N - 1) / N);
+}
+
+// Attention in Trit's order (src/layers.rs:442-504,571-587; the orders of
+// src/cpu/fgemm.rs:665-793 and src/cpu/activation.rs exp_sums), on
+// 2 * heads blocks: block b < 2 heads takes key/value head g = b % kvh (so
+// a head's blocks share an XCD and its L2), query head g GROUP + (b / kvh)
+// % GROUP, and output dims [64 h2, 64 h2 + 64), h2 = b / (kvh GROUP). The
+// other blocks go on to the o product. Thread j scores key j (up to T
+// keys) as one fused chain over the 128 dims of q * (1/sqrt(hd)), the f16
+// key bits widened inside each multiply-add; the maximum (order-free);
+// e_j = exp(s_j - max); their sum in key order from 0; p_j = e_j *
+// (1/sum); and lane d of wave 0 chains p_j * v_j over the keys in order for
+// dim 64 h2 + d, the values loaded straight into LDS while the qkv rows
+// arrive. The q/k norm sums are serial chains too. The values are Trit's
+// with the f16 caches, bit for bit.
 template <int GROUP, int DPB>
 __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, int pos, uint32_t tag_in,
                                 uint32_t tag_out, Smem& sm, unsigned long long deadline) {
-    static_assert(DPB == 4 || DPB == 8, "4 or 8 dims a block");
-    constexpr int PK = T / WAVE;  // keys a lane holds in the sum and p.V chains
-    const int b = blockIdx.x, kvh = a.kvh, g = b % kvh, hq = (b / kvh) % GROUP, e0 = DPB * (b / (kvh * GROUP));
+    const int b = blockIdx.x, kvh = a.kvh;
+    if (b >= 2 * a.heads) return true;  // uniform over the block
+    const int g = b % kvh, hq = g * GROUP + (b / kvh) % GROUP, h2 = b / (kvh * GROUP);
     const int tk = pos + 1;  // at most T (the host's plan)
     const int heads = a.heads;
-    const auto index = [g, heads, kvh](int i) {
-        if (i < GROUP * HD) return g * GROUP * HD + i;
-        if (i < (GROUP + 1) * HD) return (heads + g) * HD + (i - GROUP * HD);
-        return (heads + kvh + g) * HD + (i - (GROUP + 1) * HD);
+    // Exchange word i: q head hq, then k head g, then v head g.
+    const auto index = [hq, g, heads, kvh](int i) {
+        if (i < HD) return hq * HD + i;
+        if (i < 2 * HD) return (heads + g) * HD + (i - HD);
+        return (heads + kvh + g) * HD + (i - 2 * HD);
     };
     const _Float16* K = L.kcache + (size_t)g * a.max_pos * HD;
     const _Float16* V = L.vcache + (size_t)g * a.max_pos * HD;
     const int w = t / WAVE, lane = t % WAVE;
-    // Key t (all 128 dims) and, in wave w < DPB, dim e0 + w of keys
-    // PK lane .. PK lane + PK - 1, load while the qkv rows arrive.
+    // The first half of key t (dims 0 .. 63) and the cached values'
+    // 16-byte chunks (the block's 64 dims: chunk c is key c / 8, dims
+    // 64 h2 + 8 (c % 8) ..) t, t + VT, ... of the first VT threads load
+    // while the qkv rows arrive; the values go to LDS once the rows are
+    // there, and the keys' second halves load then.
+    constexpr int VT = T - WAVE, VC = (8 * T + VT - 1) / VT;
     uint4 kk[HD / 8];
 #pragma unroll
     for (int i = 0; i < HD / 8; ++i) kk[i] = make_uint4(0, 0, 0, 0);
-    if (t < tk && t != pos) {
-        const uint4* src = (const uint4*)(K + (size_t)t * HD);
+    if (t < pos) {
 #pragma unroll
-        for (int i = 0; i < HD / 8; ++i) kk[i] = src[i];
+        for (int i = 0; i < HD / 16; ++i) kk[i] = gload_u4(K + (size_t)t * HD + 8 * i);
     }
-    float vv[PK];
+    uint4 vr[VC];
 #pragma unroll
-    for (int i = 0; i < PK; ++i) {
-        const int j = PK * lane + i;
-        vv[i] = (w < DPB && j < tk && j != pos) ? (float)V[(size_t)j * HD + e0 + w] : 0.0f;
+    for (int i = 0; i < VC; ++i) {
+        vr[i] = make_uint4(0, 0, 0, 0);
+        const int c = t + VT * i;
+        if (t < VT && c < 8 * pos) vr[i] = gload_u4(V + (size_t)(c / 8) * HD + 64 * h2 + 8 * (c % 8));
     }
-    const int hh = w, i = lane;
+    // Wave 0 the q head, 1 the k head, 2 the v head; lane i dims i, i + 64.
     float nw0 = 1.0f, nw1 = 1.0f, sn = 0.0f, cs = 1.0f;
-    if (hh <= GROUP) {
+    if (w <= 1) {
         if (a.qk_norm) {
-            const float* nw = hh < GROUP ? L.q_norm : L.k_norm;
-            nw0 = nw[i];
-            nw1 = nw[i + HD / 2];
+            const TRIT_GLOBAL float* nw = gmem(w == 0 ? L.q_norm : L.k_norm);
+            nw0 = nw[lane];
+            nw1 = nw[lane + HD / 2];
         }
-        sn = a.rope_sin[(size_t)pos * (HD / 2) + i];
-        cs = a.rope_cos[(size_t)pos * (HD / 2) + i];
+        sn = gmem(a.rope_sin)[(size_t)pos * (HD / 2) + lane];
+        cs = gmem(a.rope_cos)[(size_t)pos * (HD / 2) + lane];
     }
-    if (!gather<8>(t, a.QKV, (GROUP + 2) * HD, index, tag_in, sm.qkv, sm, deadline, a.st, NW - a.rq / 4 - 1))
-        return false;
+    // The last wave polls: it loads no value, and no key while the session
+    // has at most (NW - 1) * 64 positions.
+    const int p0 = pos <= VT ? NW - 1 : NW - a.rq / 4 - 1;
+    if (!gather<8>(t, a.QKV, 3 * HD, index, tag_in, sm.qkv, sm, deadline, a.st, p0)) return false;
+    // The cached values into LDS, dim-major [64 dims][key].
+#pragma unroll
+    for (int i = 0; i < VC; ++i) {
+        const int c = t + VT * i;
+        if (t < VT && c < 8 * pos) {
+            const uint32_t wd[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                sm.vs[8 * (c % 8) + u][c / 8] = __builtin_bit_cast(_Float16, (uint16_t)(wd[u >> 1] >> (16 * (u & 1))));
+        }
+    }
+    if (t < pos) {
+#pragma unroll
+        for (int i = HD / 16; i < HD / 8; ++i) kk[i] = gload_u4(K + (size_t)t * HD + 8 * i);
+    }
 
-    // Qwen3's per-head RMSNorm (the serial sum of the squares, lane L
-    // holding dims 2L, 2L + 1) and the rotary halves, wave hh head hh, lane
-    // i dims i and i + 64 (src/models/parts/causal_lm.rs:428-446,
-    // src/layers.rs:136-144,303-334); the first block of the head appends
-    // the new key and value (agent scope: later steps read them elsewhere).
-    if (hh < GROUP + 2) {
-        float x0 = sm.qkv[hh * HD + i], x1 = sm.qkv[hh * HD + i + HD / 2];
-        if (hh <= GROUP) {
+    // Qwen3's per-head RMSNorm (Trit's serial sum of the squares) and the
+    // rotary halves, wave 0 the q head and wave 1 the k head, lane i dims i
+    // and i + 64 (src/models/parts/causal_lm.rs:428-446, src/layers.rs:
+    // 136-144,303-334); v as cached. The blocks with h2 = 0 and the first
+    // query head of a group append the new key and value (agent scope:
+    // later steps read them elsewhere).
+    if (w < 3) {
+        float x0 = sm.qkv[w * HD + lane], x1 = sm.qkv[w * HD + lane + HD / 2];
+        if (w <= 1) {
             if (a.qk_norm) {
-                const float2 pr = *(const float2*)(sm.qkv + hh * HD + 2 * i);
-                const float sq[2] = {pr.x * pr.x, pr.y * pr.y};
-                const float sum = lane_chain<2>(sq, 0.0f, WAVE);
+                float sq[16];
+#pragma unroll
+                for (int i = 0; i < 16; i += 4) {
+                    const float4 f = lane < 8 ? *(const float4*)(sm.qkv + w * HD + 16 * lane + i)
+                                              : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    sq[i] = f.x * f.x, sq[i + 1] = f.y * f.y, sq[i + 2] = f.z * f.z, sq[i + 3] = f.w * f.w;
+                }
+                const float sum = lane_chain<16>(sq, 0.0f, HD / 16);
                 const float inv = 1.0f / __builtin_sqrtf(sum / (float)HD + a.eps);
                 x0 = x0 * (inv * nw0);
                 x1 = x1 * (inv * nw1);
@@ -941,90 +1015,141 @@ __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, in
             x0 = ac - bs;
             x1 = bc + as;
         }
-        if (hh < GROUP) {
+        if (w == 0) {
             const float scale = 1.0f / __builtin_sqrtf((float)HD);
             x0 = x0 * scale;
             x1 = x1 * scale;
         } else {
-            const int which = hh - GROUP;
+            const int which = w - 1;
             const _Float16 c0 = (_Float16)x0, c1 = (_Float16)x1;
             if (b < kvh) {
-                uint16_t* cache =
-                    (uint16_t*)(which == 0 ? L.kcache : L.vcache) + ((size_t)g * a.max_pos + pos) * HD;
-                __hip_atomic_store(cache + i, __builtin_bit_cast(uint16_t, c0), __ATOMIC_RELAXED,
+                TRIT_GLOBAL uint16_t* cache =
+                    gmem((uint16_t*)(which == 0 ? L.kcache : L.vcache)) + ((size_t)g * a.max_pos + pos) * HD;
+                __hip_atomic_store(cache + lane, __builtin_bit_cast(uint16_t, c0), __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(cache + i + HD / 2, __builtin_bit_cast(uint16_t, c1), __ATOMIC_RELAXED,
+                __hip_atomic_store(cache + lane + HD / 2, __builtin_bit_cast(uint16_t, c1), __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
             }
-            sm.kvn[which][i] = (float)c0;
-            sm.kvn[which][i + HD / 2] = (float)c1;
+            sm.kvn[which][lane] = (float)c0;
+            sm.kvn[which][lane + HD / 2] = (float)c1;
         }
         // The norm's chain read the raw values of this head: rewrite them
-        // only after every lane of the wave has read its pair.
+        // only after every lane of the wave has read its values.
         __builtin_amdgcn_wave_barrier();
-        if (hh < GROUP) {
-            sm.qkv[hh * HD + i] = x0;
-            sm.qkv[hh * HD + i + HD / 2] = x1;
+        if (w == 0) {
+            sm.qkv[lane] = x0;
+            sm.qkv[lane + HD / 2] = x1;
         }
     }
     __syncthreads();
 
-    // Scores: thread t key t, the fused chain over the dims in order.
-    float* probs = &sm.gpart[0][0];  // T values
-    float* wmax = &sm.gpart[4][0];   // NW values
+    // Scores: thread t key t, the fused chain over the dims in order (the
+    // new key as cached: its f16 bits). q is read from LDS 16 values at a
+    // time, the next 16 values' loads in flight during the current ones'
+    // multiply-adds.
+    if (t == pos) {
+#pragma unroll
+        for (int c = 0; c < HD / 8; ++c) {
+            uint32_t nb[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                nb[u] = (uint32_t)f32_to_f16(sm.kvn[0][8 * c + 2 * u]) |
+                        ((uint32_t)f32_to_f16(sm.kvn[0][8 * c + 2 * u + 1]) << 16);
+            kk[c] = make_uint4(nb[0], nb[1], nb[2], nb[3]);
+        }
+    }
     float score = -INFINITY;
     if (t < tk) {
-        const float* q = sm.qkv + hq * HD;
         float acc = 0.0f;
-        if (t == pos) {
-#pragma unroll 16
-            for (int e = 0; e < HD; ++e) acc = __builtin_fmaf(q[e], sm.kvn[0][e], acc);
-        } else {
+        float4 qc[4], qn[4];
 #pragma unroll
-            for (int c = 0; c < HD / 8; ++c) {
-                float k8[8];
-                unpack8(kk[c], k8);
+        for (int i = 0; i < 4; ++i) qc[i] = *(const float4*)(sm.qkv + 4 * i);
 #pragma unroll
-                for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(q[8 * c + u], k8[u], acc);
+        for (int part = 0; part < HD / 16; ++part) {
+            if (part + 1 < HD / 16) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) qn[i] = *(const float4*)(sm.qkv + 16 * (part + 1) + 4 * i);
             }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const uint4 kw = kk[2 * part + c];
+                const uint32_t wd[4] = {kw.x, kw.y, kw.z, kw.w};
+                const float q8[8] = {qc[2 * c].x, qc[2 * c].y, qc[2 * c].z, qc[2 * c].w,
+                                     qc[2 * c + 1].x, qc[2 * c + 1].y, qc[2 * c + 1].z, qc[2 * c + 1].w};
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    acc = __builtin_fmaf(q8[u], f16_to_f32((uint16_t)(wd[u >> 1] >> (16 * (u & 1)))), acc);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) qc[i] = qn[i];
         }
         score = acc;
     }
     const float m_w = wave_max(score);
-    if (lane == 0) wmax[w] = m_w;
+    if (lane == 0) sm.wmax[w] = m_w;
     __syncthreads();
-    float mx = wmax[0];
+    float mx = sm.wmax[0];
 #pragma unroll
-    for (int q = 1; q < NW; ++q) mx = __builtin_fmaxf(mx, wmax[q]);
-    probs[t] = t < tk ? exp_trit(score - mx) : 0.0f;
+    for (int q = 1; q < NW; ++q) mx = __builtin_fmaxf(mx, sm.wmax[q]);
+    const float e = t < tk ? exp_trit(score - mx) : 0.0f;
+    sm.probs[t] = e;
     __syncthreads();
-    // The sum in key order from 0 (the zeros past the keys add nothing),
-    // then p_j = e_j * (1/sum) and the p.V chains, wave w dim e0 + w.
-    if (w < DPB) {
-        const int rounds = (tk + PK - 1) / PK;
-        float e[PK];
+    // Their sum in key order from 0, then p_j = e_j * (1/sum).
+    if (w == 0) {
+        const float sum = wave_chain_sum<16>(sm.probs, tk, lane);
+        if (lane == 0) sm.chain = 1.0f / sum;
+    }
+    __syncthreads();
+    sm.probs[t] = e * sm.chain;
+    __syncthreads();
+    // p.V: lane d of wave 0 chains dim 64 h2 + d over the keys in order, 16
+    // keys a step (two 16-byte reads of its row), two buffers in turn so
+    // that one's reads are in flight during the other's multiply-adds; the
+    // new key's value (position pos = tk - 1) comes last, from the qkv
+    // product.
+    if (w == 0) {
+        float acc = 0.0f;
+        const _Float16* vrow = sm.vs[lane];
+        struct Keys16 {
+            float4 p[4];
+            uint4 v[2];
+        };
+        auto load = [&](int j, Keys16& k) {
 #pragma unroll
-        for (int q = 0; q < PK; q += 4) {
-            const float4 v4 = *(const float4*)(probs + PK * lane + q);
-            e[q] = v4.x;
-            e[q + 1] = v4.y;
-            e[q + 2] = v4.z;
-            e[q + 3] = v4.w;
-        }
-        const float sum = lane_chain<PK>(e, 0.0f, rounds);
-        const float inv = 1.0f / sum;
-        float carry = 0.0f;
-        for (int Ln = 0; Ln < rounds; ++Ln) {
-            float acc = carry;
+            for (int i = 0; i < 4; ++i) k.p[i] = *(const float4*)(sm.probs + j + 4 * i);
+            k.v[0] = *(const uint4*)(vrow + j);
+            k.v[1] = *(const uint4*)(vrow + j + 8);
+        };
+        auto fma16 = [&](const Keys16& k) {
 #pragma unroll
-            for (int q = 0; q < PK; ++q) {
-                const int j = PK * lane + q;
-                const float v = j == pos ? sm.kvn[1][e0 + w] : vv[q];
-                acc = __builtin_fmaf(e[q] * inv, v, acc);
+            for (int u = 0; u < 16; ++u) {
+                const float4 pq = k.p[u / 4];
+                const float pu = (u & 3) == 0 ? pq.x : (u & 3) == 1 ? pq.y : (u & 3) == 2 ? pq.z : pq.w;
+                const uint4 vq = k.v[u / 8];
+                const uint32_t wd = (u & 7) < 2 ? vq.x : (u & 7) < 4 ? vq.y : (u & 7) < 6 ? vq.z : vq.w;
+                acc = __builtin_fmaf(pu, f16_to_f32((uint16_t)(wd >> (16 * (u & 1)))), acc);
             }
-            carry = lane_f(acc, Ln);
+        };
+        const int steps = pos / 16;
+        Keys16 ka, kb;
+        if (steps > 0) load(0, ka);
+        int q = 0;
+        for (; q + 2 <= steps; q += 2) {
+            load(16 * (q + 1), kb);
+            __builtin_amdgcn_sched_barrier(0);
+            fma16(ka);
+            __builtin_amdgcn_sched_barrier(0);
+            if (q + 2 < steps) load(16 * (q + 2), ka);
+            __builtin_amdgcn_sched_barrier(0);
+            fma16(kb);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        if (lane == 0) put(a.ATT + (size_t)(g * GROUP + hq) * HD + e0 + w, carry, tag_out);
+        if (q < steps) fma16(ka);
+        for (int j = 16 * steps; j < pos; ++j) acc = __builtin_fmaf(sm.probs[j], (float)vrow[j], acc);
+        acc = __builtin_fmaf(sm.probs[pos], sm.kvn[1][64 * h2 + lane], acc);
+        put(a.ATT + (size_t)hq * HD + 64 * h2 + lane, acc, tag_out);
     }
     return true;
 }
@@ -1070,6 +1195,9 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     if (st->done) return;
     const int b = blockIdx.x;
     if (threadIdx.x == 0) sm.abort = 0;
+    for (int i = threadIdx.x; i < a.n_layers * (int)(sizeof(LayerPtrs) / 8); i += T)
+        ((uint64_t*)sm.layers)[i] = gmem((const uint64_t*)a.layers)[i];
+    __syncthreads();
 
     // Waves by product, four rows a wave: gate_up [0, nu), o [nu, nu + no),
     // down [nu, nu + nd), qkv [NW - nqw, NW). Each product's rows load one
@@ -1117,7 +1245,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     // The first layer's qkv rows stream in during the choice. (Declared per
     // step so that nothing of it stays live through the head.)
     Rows<RN, RS> rr{};
-    if (aq) load_rows<JD, 1>(t, a.layers[0].codes[0], a.layers[0].scales[0], 0, rowq, rr);
+    if (aq) load_rows<JD, 1>(t, sm.layers[0].codes[0], sm.layers[0].scales[0], 0, rowq, rr);
 
     // ---- the greedy choice over the blocks' candidates -------------------
     {
@@ -1131,7 +1259,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
                 index = __float_as_int(sm.xin[2 * t + 1]);
             }
         } else if (t < (int)gridDim.x) {
-            const float2 c = a.cand[t];
+            const float2 c = gload_f2(a.cand + t);
             best = c.x;
             index = __float_as_int(c.y);
         }
@@ -1162,7 +1290,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         const int s_count = a.d / 16;
         for (int kk = t; kk < a.d; kk += T) {
             const int s = kk / 16, i = kk % 16;
-            sm.xres[kk] = f16_to_f32(a.embed[((size_t)token * 16 + i) * s_count + s]);
+            sm.xres[kk] = f16_to_f32(gmem(a.embed)[((size_t)token * 16 + i) * s_count + s]);
         }
         __syncthreads();
     }
@@ -1172,15 +1300,18 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     // that no register stays live across the layer loop.)
     for (int layer = 0; layer < a.n_layers; ++layer) {
         fresh();
-        const LayerPtrs& L = a.layers[layer];
+        const LayerPtrs& L = sm.layers[layer];
         // qkv: x (gathered, or the embedding) -> RMSNorm -> quantize -> rows.
         NormRegs<JD> nq;
         load_norm<JD>(t, L.norm_attn, nq);
         // Polled by the first waves (the down rows' wave stored x).
         if (layer > 0 && !gather<6>(t, a.X, a.d, lin, tag_of(tag0, layer - 1, 5), sm.xres, sm, deadline, st))
             return;
-        if (w == 0) {
-            const float inv = EXACT ? norm_inv_serial<JD>(t, sm.xres, a.eps) : norm_inv_wave<JD>(t, sm.xres, a.eps);
+        if constexpr (EXACT) {
+            const float inv = norm_inv_exact<JD>(t, sm.xres, a.eps, sm);
+            if (t == 0) sm.inv = inv;
+        } else if (w == 0) {
+            const float inv = norm_inv_wave<JD>(t, sm.xres, a.eps);
             if (lane == 0) sm.inv = inv;
         }
         __syncthreads();
@@ -1240,8 +1371,11 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         load_norm<JD>(t, L.norm_mlp, ngu);
         __syncthreads();
         if (!gather<MAXK / T>(t, a.X, a.d, lin, tag_of(tag0, layer, 3), sm.xres, sm, deadline, st)) return;
-        if (w == 0) {
-            const float inv = EXACT ? norm_inv_serial<JD>(t, sm.xres, a.eps) : norm_inv_wave<JD>(t, sm.xres, a.eps);
+        if constexpr (EXACT) {
+            const float inv = norm_inv_exact<JD>(t, sm.xres, a.eps, sm);
+            if (t == 0) sm.inv = inv;
+        } else if (w == 0) {
+            const float inv = norm_inv_wave<JD>(t, sm.xres, a.eps);
             if (lane == 0) sm.inv = inv;
         }
         __syncthreads();
@@ -1257,7 +1391,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         else
             zero_rows(rr);
         if (aq && layer + 1 < a.n_layers)
-            load_rows<JD, 1>(t, a.layers[layer + 1].codes[0], a.layers[layer + 1].scales[0], 0, rowq, rr);
+            load_rows<JD, 1>(t, sm.layers[layer + 1].codes[0], sm.layers[layer + 1].scales[0], 0, rowq, rr);
         __syncthreads();
         if (!gather<MAXK / T>(t, a.H, a.ffn, lin, tag_of(tag0, layer, 4), sm.xin, sm, deadline, st)) return;
         quantize_block<JF>(t, sm.xin, (const NormRegs<JF>*)nullptr, sm);
@@ -1296,10 +1430,13 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         if (q < passes) load_pass(q, ring[q]);
     float fn[(MAXD + T - 1) / T];
 #pragma unroll
-    for (int q = 0; q < (MAXD + T - 1) / T; ++q) fn[q] = t + T * q < a.d ? a.final_norm[t + T * q] : 0.0f;
+    for (int q = 0; q < (MAXD + T - 1) / T; ++q) fn[q] = t + T * q < a.d ? gmem(a.final_norm)[t + T * q] : 0.0f;
     if (!gather<MAXD / T>(t, a.X, a.d, lin, tag_of(tag0, a.n_layers - 1, 5), sm.xres, sm, deadline, st)) return;
-    if (w == 0) {
-        const float inv = EXACT ? norm_inv_serial<JD>(t, sm.xres, a.eps) : norm_inv_wave<JD>(t, sm.xres, a.eps);
+    if constexpr (EXACT) {
+        const float inv = norm_inv_exact<JD>(t, sm.xres, a.eps, sm);
+        if (t == 0) sm.inv = inv;
+    } else if (w == 0) {
+        const float inv = norm_inv_wave<JD>(t, sm.xres, a.eps);
         if (lane == 0) sm.inv = inv;
     }
     __syncthreads();
@@ -1454,7 +1591,7 @@ bool plan(const SessionImpl& S, Plan& p) {
     if (c.head_dim != HD || c.kv_heads <= 0 || c.heads % c.kv_heads != 0) return false;
     const int group = c.heads / c.kv_heads, qd = c.heads * HD;
     if (c.d % 256 || qd % 256 || c.ffn % 256 || c.d > MAXD || qd > MAXK || c.ffn > MAXK) return false;
-    if (c.layers <= 0 || c.layers * PH + PH >= 256) return false;
+    if (c.layers <= 0 || c.layers > MAXL || c.layers * PH + PH >= 256) return false;
     auto q8 = [](const LayerRef& L) { return (L->kind == Q8_0 || L->kind == Q4_K) && !L->bias.ptr; };
     for (int l = 0; l < c.layers; ++l)
         if (!q8(D.qkv[l]) || !q8(D.o[l]) || !q8(D.gate_up[l]) || !q8(D.down[l])) return false;

@@ -68,10 +68,48 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
+// Global-memory views of device pointers. A pointer the compiler cannot
+// trace to a kernel argument (one read from a table in memory) is generic
+// to it, and its accesses become flat instructions; a flat load also holds
+// the LDS wait counter, so every later LDS read would wait for it too (a
+// weight stream in flight would stall each LDS access). Accesses through
+// these views are global instructions.
+#define TRIT_GLOBAL __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ const TRIT_GLOBAL T* gmem(const T* p) {
+    return (const TRIT_GLOBAL T*)p;
+}
+template <class T>
+__device__ __forceinline__ TRIT_GLOBAL T* gmem(T* p) {
+    return (TRIT_GLOBAL T*)p;
+}
+
+// 16-, 8- and 4-float loads through the global view (HIP's vector structs
+// do not copy from another address space; the native vectors do).
+__device__ __forceinline__ uint4 gload_u4(const void* p) {
+    const u32x4 v = *(const TRIT_GLOBAL u32x4*)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 gload_u2(const void* p) {
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = *(const TRIT_GLOBAL u32x2*)p;
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ float4 gload_f4(const void* p) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const f32x4 v = *(const TRIT_GLOBAL f32x4*)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float2 gload_f2(const void* p) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const f32x2 v = *(const TRIT_GLOBAL f32x2*)p;
+    return make_float2(v.x, v.y);
+}
+
 // A 16-byte load of streamed weights (read once per token): nontemporal,
 // so it does not displace the activations in the caches.
 __device__ __forceinline__ uint4 load_stream(const void* p) {
-    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+    const u32x4 v = __builtin_nontemporal_load((const TRIT_GLOBAL u32x4*)p);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
