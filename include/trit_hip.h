@@ -102,6 +102,22 @@ int trit_hip_layer_forward(const TritHipLayer *layer, const float *x, int m, int
 int trit_hip_layer_forward_device(const TritHipLayer *layer, const float *x, int m, int relu, float *y,
                                   void *stream);
 
+/* trit_hip_layer_forward_device that allocates nothing. It has no
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid it). The activations of 2 or more rows are
+ * quantized into one 4 MiB array per device that is part of the library
+ * (its address found by trit_hip_init on that device, else by the first
+ * call there), not into a per-thread buffer the library grows. A product
+ * whose quantized rows need more than that fails with an error naming the
+ * bytes it needs. All calls on one device share the array and it keeps the
+ * last call's contents: calls on one device must not overlap (queue them
+ * on one stream). Results are trit_hip_layer_forward_device's, bit for
+ * bit. Call trit_hip_init on the calling thread first (it creates the
+ * library's stream), or pass a stream. */
+int trit_hip_layer_forward_device_noalloc(const TritHipLayer *layer, const float *x, int m, int relu, float *y,
+                                          void *stream);
+
 /* The measurement hook (the counterpart of Trit's kernel bench timing,
  * src/cpu/v2/bench.rs:42-54): trit_hip_layer_forward_device with the
  * product kernel's launch stamped with start_event and stop_event

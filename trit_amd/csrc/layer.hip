@@ -162,6 +162,35 @@ Staging& staging() {
 // Rows above this many run on the matrix cores when the layer allows it.
 constexpr int GEMM_MIN_ROWS = 9;
 
+// The scratch of trit_hip_layer_forward_device_noalloc: one array per
+// device in the library's own code object, so that call allocates nothing.
+// Every such call on a device shares that device's array (calls that
+// overlap on one device race), and it keeps the last call's contents: the
+// products write all of it they read before reading it.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)4 << 20;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+// The device address of `scratch` per device, found once per device with
+// that device current (in host code the array's name is no device address).
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES] = {};
+
+void resolve_noalloc_scratch(int dev) {
+    if (dev < 0 || dev >= MAX_DEVICES) fail("device " + std::to_string(dev) + " is beyond the library's table");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev]) return;
+    void* ptr = nullptr;
+    TRIT_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (!ptr) fail("no device address for the no-allocation scratch");
+    g_scratch_ptr[dev] = ptr;
+}
+
+void* noalloc_scratch(int dev) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    return g_scratch_ptr[dev];
+}
+
 // Grows the calling thread's scratch to `need` bytes.
 void* staging_scratch(size_t need) {
     Staging& g = staging();
@@ -175,13 +204,16 @@ void* staging_scratch(size_t need) {
 
 // One product of m rows: the matrix-core product for many rows, else the
 // small-batch kernels in calls of up to 8 rows (2..8 rows of an integer
-// layer with their activations quantized once, in the scratch).
-void forward_rows(const Layer& L, GemvArgs a, int m, hipStream_t s) {
+// layer with their activations quantized once, in the scratch). `get`
+// gives the scratch of `need` bytes (staging_scratch, or the no-allocation
+// array).
+template <class Scratch>
+void forward_rows(const Layer& L, GemvArgs a, int m, hipStream_t s, Scratch get) {
     a.m = m;
-    if (m >= GEMM_MIN_ROWS && gemm_supported(L, a)) return gemm_int(L, a, staging_scratch(gemm_scratch_bytes(m, L.k)), s);
+    if (m >= GEMM_MIN_ROWS && gemm_supported(L, a)) return gemm_int(L, a, get(gemm_scratch_bytes(m, L.k)), s);
     if (m >= 2 && L.kind != F16) {
         a.scratch_bytes = gemv_scratch_bytes(m < 8 ? m : 8, L.k);
-        a.scratch = staging_scratch(a.scratch_bytes);
+        a.scratch = get(a.scratch_bytes);
     }
     if (a.ev_start || a.ev_stop) {
         if (m > 8) fail("timed forward: more than 8 rows of this layer take several launches");
@@ -242,6 +274,7 @@ int trit_hip_init(int device) {
         TRIT_HIP(hipSetDevice(device));
         g_device = device;
         stream();
+        resolve_noalloc_scratch(device);
         return 0;
     });
 }
@@ -390,7 +423,38 @@ int trit_hip_layer_forward_device(const TritHipLayer* layer, const float* x, int
         a.y = y;
         a.relu = relu;
         if (m <= 0) fail("m must be positive");
-        forward_rows(*layer->layer, a, m, s ? (hipStream_t)s : stream());
+        forward_rows(*layer->layer, a, m, s ? (hipStream_t)s : stream(), staging_scratch);
+        return 0;
+    });
+}
+
+int trit_hip_layer_forward_device_noalloc(const TritHipLayer* layer, const float* x, int m, int relu, float* y,
+                                          void* s) {
+    return guard(-1, [&] {
+        if (!layer || !x || !y) fail("layer, x or y is NULL");
+        if (m <= 0) fail("m must be positive");
+        const int dev = device_id();
+        if (dev < 0 || dev >= MAX_DEVICES) fail("device " + std::to_string(dev) + " is beyond the library's table");
+        void* base = noalloc_scratch(dev);
+        if (!base) {
+            // trit_hip_init found it for the devices it set up; otherwise the
+            // first call on this device does.
+            resolve_noalloc_scratch(dev);
+            base = noalloc_scratch(dev);
+        }
+        GemvArgs a;
+        a.x = x;
+        a.m = m;
+        a.y = y;
+        a.relu = relu;
+        const Layer& L = *layer->layer;
+        forward_rows(L, a, m, s ? (hipStream_t)s : stream(), [&](size_t need) -> void* {
+            if (need > NOALLOC_SCRATCH_BYTES)
+                fail("no-allocation forward: " + std::to_string(m) + " rows of a " + std::to_string(L.n) + "x" +
+                     std::to_string(L.k) + " layer need " + std::to_string(need) + " bytes of scratch, more than the " +
+                     std::to_string(NOALLOC_SCRATCH_BYTES) + " it holds");
+            return base;
+        });
         return 0;
     });
 }
@@ -406,7 +470,7 @@ int trit_hip_layer_forward_timed(const TritHipLayer* layer, const float* x, int 
         a.relu = relu;
         a.ev_start = (hipEvent_t)start_event;
         a.ev_stop = (hipEvent_t)stop_event;
-        forward_rows(*layer->layer, a, m, s ? (hipStream_t)s : stream());
+        forward_rows(*layer->layer, a, m, s ? (hipStream_t)s : stream(), staging_scratch);
         return 0;
     });
 }

@@ -52,6 +52,7 @@ def lib():
             "trit_hip_layer_f16": (i, [i, i, p, p, pp]),
             "trit_hip_layer_forward": (i, [p, p, i, i, p]),
             "trit_hip_layer_forward_device": (i, [p, p, i, i, p, p]),
+            "trit_hip_layer_forward_device_noalloc": (i, [p, p, i, i, p, p]),
             "trit_hip_layer_forward_timed": (i, [p, p, i, i, p, p, p, p]),
             "trit_hip_layer_info": (i, [p, C.POINTER(i), C.POINTER(i), C.POINTER(i), C.POINTER(C.c_int64)]),
             "trit_hip_layer_row": (i, [p, i, p]),
