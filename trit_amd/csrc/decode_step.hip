@@ -95,12 +95,12 @@ struct Smem {
     alignas(16) float xs[MAXK / 32];
     alignas(16) float qkv[6 * HD];  // a key/value head's q heads, k, v
     alignas(16) float kvn[2][HD];   // the new key and value, as cached
+    alignas(16) uint16_t knew[HD];  // the new key's f16 bits
     union {
         alignas(16) float gpart[32][2 * HD];  // attention: per 16-lane group p.V of two heads
         // The exact attention: the keys' values of the block's 64 dims,
-        // dim-major, rows padded by 16 bytes (a wave's 16-byte reads of 64
-        // rows then fall on distinct banks in each group of 16 lanes).
-        alignas(16) _Float16 vs[HD / 2][T + 8];
+        // row-major (key j's 64 values: 128 contiguous bytes).
+        alignas(16) _Float16 vs[T][HD / 2];
     };
     alignas(16) float probs[T];               // the exact attention's probabilities
     float wmax[NW];
@@ -221,6 +221,7 @@ __device__ bool gather(int t, const uint64_t* src, int n, Index index, uint32_t 
     return !aborted(sm);
 }
 
+
 struct Linear {
     __device__ int operator()(int i) const { return i; }
 };
@@ -232,17 +233,21 @@ struct Linear {
 // of their blocks, as the one-row kernel loads them. A wave holds one
 // product's rows at a time, so every product shares one register set:
 // N chunks and NS scale words, product (J, P) using w[p J + j] and
-// ws[p ((J + 1) / 2) + j / 2].
+// ws[p J + j].
 template <int N, int NS>
 struct Rows {
     uint4 w[N];
-    uint32_t ws[NS];  // f16 scale bits, two a register
+    // f16 scale bits, one a register, each the destination of its own load:
+    // no arithmetic touches a loaded value before the product needs it
+    // (packing two loaded halves into one register would wait for the
+    // loads, and with them for every load issued before).
+    uint32_t ws[NS];
 };
 
 template <int J, int P, int N, int NS>
 __device__ __forceinline__ void load_rows(int t, const uint8_t* codes, const uint16_t* scales, int part_rows, int row,
                                           Rows<N, NS>& r) {
-    static_assert(P * J <= N && P * ((J + 1) / 2) <= NS, "the row registers hold the product");
+    static_assert(P * J <= N && P * J <= NS, "the row registers hold the product");
     constexpr int K = J * 256, G = K / 32;
     const int l = t & 15;
 #pragma unroll
@@ -252,15 +257,13 @@ __device__ __forceinline__ void load_rows(int t, const uint8_t* codes, const uin
         for (int j = 0; j < J; ++j) r.w[p * J + j] = load_stream(src + (size_t)(l + 16 * j) * 16);
         const TRIT_GLOBAL uint16_t* sc = gmem(scales) + (size_t)(p * part_rows + row) * G + (l >> 1);
 #pragma unroll
-        for (int j = 0; j < J; j += 2)
-            r.ws[p * ((J + 1) / 2) + j / 2] =
-                (uint32_t)sc[8 * j] | (j + 1 < J ? (uint32_t)sc[8 * (j + 1)] << 16 : 0u);
+        for (int j = 0; j < J; ++j) r.ws[p * J + j] = sc[8 * j];
     }
     // The rest of the set is zeroed: after any load no earlier rows stay live.
 #pragma unroll
     for (int i = P * J; i < N; ++i) r.w[i] = make_uint4(0, 0, 0, 0);
 #pragma unroll
-    for (int i = P * ((J + 1) / 2); i < NS; ++i) r.ws[i] = 0;
+    for (int i = P * J; i < NS; ++i) r.ws[i] = 0;
 }
 
 // The row set zeroed, in the waves that load no rows in a phase: every path
@@ -413,7 +416,7 @@ __device__ __forceinline__ void row_chain(int t, const Rows<N, NS>& r, const Sme
             d = sdot4(wc.w, xc.w, d);
             d += dpp<DPP_XOR1>(d);
             df[p] = (float)d;
-            prod[p] = f16_to_f32((uint16_t)(r.ws[p * ((J + 1) / 2) + j / 2] >> (16 * (j & 1)))) * sc;
+            prod[p] = f16_to_f32((uint16_t)r.ws[p * J + j]) * sc;
         }
 #pragma unroll
         for (int q = 0; q < 8; ++q)
@@ -947,9 +950,13 @@ __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, in
     uint4 kk[HD / 8];
 #pragma unroll
     for (int i = 0; i < HD / 8; ++i) kk[i] = make_uint4(0, 0, 0, 0);
+    uint32_t touch = 0;
     if (t < pos) {
 #pragma unroll
         for (int i = 0; i < HD / 16; ++i) kk[i] = gload_u4(K + (size_t)t * HD + 8 * i);
+        // One word of the key's second 128-byte line: the line comes to the
+        // caches now, and the loads of that half after the hand-over hit them.
+        touch = *gmem((const uint32_t*)(K + (size_t)t * HD + HD / 2));
     }
     uint4 vr[VC];
 #pragma unroll
@@ -973,16 +980,12 @@ __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, in
     // has at most (NW - 1) * 64 positions.
     const int p0 = pos <= VT ? NW - 1 : NW - a.rq / 4 - 1;
     if (!gather<8>(t, a.QKV, 3 * HD, index, tag_in, sm.qkv, sm, deadline, a.st, p0)) return false;
-    // The cached values into LDS, dim-major [64 dims][key].
+    asm volatile("" ::"v"(touch));
+    // The cached values into LDS, row-major [key][64 dims].
 #pragma unroll
     for (int i = 0; i < VC; ++i) {
         const int c = t + VT * i;
-        if (t < VT && c < 8 * pos) {
-            const uint32_t wd[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                sm.vs[8 * (c % 8) + u][c / 8] = __builtin_bit_cast(_Float16, (uint16_t)(wd[u >> 1] >> (16 * (u & 1))));
-        }
+        if (t < VT && c < 8 * pos) *(uint4*)&sm.vs[c / 8][8 * (c % 8)] = vr[i];
     }
     if (t < pos) {
 #pragma unroll
@@ -1032,6 +1035,10 @@ __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, in
             }
             sm.kvn[which][lane] = (float)c0;
             sm.kvn[which][lane + HD / 2] = (float)c1;
+            if (which == 0) {
+                sm.knew[lane] = __builtin_bit_cast(uint16_t, c0);
+                sm.knew[lane + HD / 2] = __builtin_bit_cast(uint16_t, c1);
+            }
         }
         // The norm's chain read the raw values of this head: rewrite them
         // only after every lane of the wave has read its values.
@@ -1049,14 +1056,7 @@ __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, in
     // multiply-adds.
     if (t == pos) {
 #pragma unroll
-        for (int c = 0; c < HD / 8; ++c) {
-            uint32_t nb[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                nb[u] = (uint32_t)f32_to_f16(sm.kvn[0][8 * c + 2 * u]) |
-                        ((uint32_t)f32_to_f16(sm.kvn[0][8 * c + 2 * u + 1]) << 16);
-            kk[c] = make_uint4(nb[0], nb[1], nb[2], nb[3]);
-        }
+        for (int c = 0; c < HD / 8; ++c) kk[c] = *(const uint4*)&sm.knew[8 * c];
     }
     float score = -INFINITY;
     if (t < tk) {
@@ -1104,32 +1104,29 @@ __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, in
     __syncthreads();
     sm.probs[t] = e * sm.chain;
     __syncthreads();
-    // p.V: lane d of wave 0 chains dim 64 h2 + d over the keys in order, 16
-    // keys a step (two 16-byte reads of its row), two buffers in turn so
-    // that one's reads are in flight during the other's multiply-adds; the
-    // new key's value (position pos = tk - 1) comes last, from the qkv
-    // product.
+    // p.V: lane d of wave 0 chains dim 64 h2 + d over the keys in order (key
+    // j's value: one 2-byte read of row j, the 64 lanes reading its 128
+    // bytes), 16 keys a step, two buffers in turn so that one's reads are in
+    // flight during the other's multiply-adds; the new key's value (position
+    // pos = tk - 1) comes last, from the qkv product.
     if (w == 0) {
         float acc = 0.0f;
-        const _Float16* vrow = sm.vs[lane];
         struct Keys16 {
             float4 p[4];
-            uint4 v[2];
+            uint32_t v[16];
         };
         auto load = [&](int j, Keys16& k) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) k.p[i] = *(const float4*)(sm.probs + j + 4 * i);
-            k.v[0] = *(const uint4*)(vrow + j);
-            k.v[1] = *(const uint4*)(vrow + j + 8);
+#pragma unroll
+            for (int u = 0; u < 16; ++u) k.v[u] = __builtin_bit_cast(uint16_t, sm.vs[j + u][lane]);
         };
         auto fma16 = [&](const Keys16& k) {
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
                 const float4 pq = k.p[u / 4];
                 const float pu = (u & 3) == 0 ? pq.x : (u & 3) == 1 ? pq.y : (u & 3) == 2 ? pq.z : pq.w;
-                const uint4 vq = k.v[u / 8];
-                const uint32_t wd = (u & 7) < 2 ? vq.x : (u & 7) < 4 ? vq.y : (u & 7) < 6 ? vq.z : vq.w;
-                acc = __builtin_fmaf(pu, f16_to_f32((uint16_t)(wd >> (16 * (u & 1)))), acc);
+                acc = __builtin_fmaf(pu, f16_to_f32((uint16_t)k.v[u]), acc);
             }
         };
         const int steps = pos / 16;
@@ -1147,7 +1144,7 @@ __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, in
             __builtin_amdgcn_sched_barrier(0);
         }
         if (q < steps) fma16(ka);
-        for (int j = 16 * steps; j < pos; ++j) acc = __builtin_fmaf(sm.probs[j], (float)vrow[j], acc);
+        for (int j = 16 * steps; j < pos; ++j) acc = __builtin_fmaf(sm.probs[j], (float)sm.vs[j][lane], acc);
         acc = __builtin_fmaf(sm.probs[pos], sm.kvn[1][64 * h2 + lane], acc);
         put(a.ATT + (size_t)hq * HD + 64 * h2 + lane, acc, tag_out);
     }
@@ -1208,7 +1205,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     // The one row register set (see Rows); the first layer's qkv rows
     // stream in during the choice.
     constexpr int RN = cmax(cmax(2 * JD, JO), JF);
-    constexpr int RS = cmax(cmax(2 * ((JD + 1) / 2), (JO + 1) / 2), (JF + 1) / 2);
+    constexpr int RS = RN;
     const Linear lin;
 
     // Token steps: step it forwards the token chosen from step it - 1's
