@@ -82,6 +82,7 @@ struct StepArgs {
     int rq, ro, rgu, rd;      // rows per block (gate_up: pairs), multiples of 4
     int rh;                   // head rows per block
     unsigned long long ticks; // wall-clock ticks a block may wait in a step
+    int norm_window;          // RMSNorm: candidate starts on either side of the estimate
 };
 
 struct Smem {
@@ -98,11 +99,18 @@ struct Smem {
     alignas(16) uint16_t knew[HD];  // the new key's f16 bits
     union {
         alignas(16) float gpart[32][2 * HD];  // attention: per 16-lane group p.V of two heads
-        // The exact attention: the keys' values of the block's 64 dims,
+        struct {
+            alignas(16) float sq[MAXD];  // RMSNorm: the squares
+            float part[NW];              // each segment's sum as a tree
+            float res[NW][WAVE];         // each segment's chain, lane L from candidate L
+        } ns;
+        // The exact attention: the cached values of the block's 64 dims,
         // row-major (key j's 64 values: 128 contiguous bytes).
         alignas(16) _Float16 vs[T][HD / 2];
     };
-    alignas(16) float probs[T];               // the exact attention's probabilities
+    alignas(16) float probs[T];           // the exact attention's probabilities
+    float carry[WAVE];                    // its p.V sums, passed from wave to wave
+    float ppos;                           // the new key's probability
     float wmax[NW];
     float gmax[32][2];
     float gl[32][2];
@@ -148,6 +156,10 @@ __device__ __forceinline__ float row16_max(float v) {
     v = __builtin_fmaxf(v, dpp<DPP_MIRROR>(v));
     return v;
 }
+// s_waitcnt vmcnt(0), the other counters left alone (gfx9 encoding:
+// vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+constexpr int VMCNT0 = 0x0f70;
+
 __device__ __forceinline__ float lane_f(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
@@ -160,8 +172,19 @@ __device__ __forceinline__ float wave_max(float v) {
     return __builtin_fmaxf(__builtin_fmaxf(lane_f(v, 0), lane_f(v, 16)), __builtin_fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
+// A block that missed a deadline leaves the launch where it finds out
+// (every wave of the block reads the same flag after a barrier). Ending
+// the program there, rather than returning through the layer loop, keeps
+// the abort paths out of the loop's control flow: joined to it, their
+// loads in flight would make the compiler wait for everything a wave has
+// in flight (its exchange stores too) on the paths that go on.
+[[noreturn]] __device__ __forceinline__ void leave() { __builtin_amdgcn_endpgm(); }
+
+// Whether the block has given up (one LDS word; read into a scalar
+// register, so that the branch on it is uniform to the compiler too).
 __device__ __forceinline__ bool aborted(Smem& sm) {
-    return __hip_atomic_load(&sm.abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0;
+    return __builtin_amdgcn_readfirstlane(__hip_atomic_load(&sm.abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) !=
+           0;
 }
 
 // Waits for n exchange words tagged `tag` (word i at src[index(i)]) and
@@ -319,29 +342,77 @@ __device__ __forceinline__ float lane_chain(const float (&v)[N], float c0, int l
     return carry;
 }
 
-// RMSNorm factor of x (K = 256 J values in LDS) in Trit's order: the
-// squares added one after another from 0 (src/layers.rs:138-139) by the
-// first wave, lane L holding values [K/32 L, K/32 (L + 1)) of the chain
-// (a dependent add per value, a lane move per K/32 values). Every thread
-// calls it and gets the factor.
+// RMSNorm factor of x (K = 256 J values in LDS) with Trit's sum -- the
+// squares added one after another from 0 (src/layers.rs:138-139) -- bit
+// for bit, by all the waves at once. Wave w chains segment w (values
+// [S w, S w + S), S = K / NW) in order: wave 0 from 0, and each other wave,
+// whose true start (the chain's value after the segments before) is not
+// known yet, from 64 candidate starts at once, lane L from the float L - 32
+// steps from an estimate of that start (the earlier segments' sums as
+// trees, within a few steps of the chain: each add of the chain rounds by
+// at most half a step of its value). The segments are then joined in
+// order: the lane of segment w whose start equals the chain's value after
+// segment w - 1 holds the chain's value after segment w; when no lane of
+// the `window` lanes on either side does (the estimate that far off), the
+// segment is chained again from that value. Every wave joins the segments
+// itself and returns the factor.
 template <int J>
-__device__ float norm_inv_exact(int t, const float* x, float eps, Smem& sm) {
-    constexpr int K = J * 256, N = K / 32;
-    if (t < WAVE) {
-        float sq[N];
+__device__ float norm_inv_spec(int t, const float* x, float eps, int window, Smem& sm) {
+    constexpr int K = J * 256, S = K / NW, PER = S / WAVE;
+    static_assert(S % WAVE == 0 && PER <= 4, "a wave's segment: PER values a lane");
+    const int w = __builtin_amdgcn_readfirstlane(t / WAVE), lane = t % WAVE;
+    float* sq = sm.ns.sq;
+    float part = 0.0f;
 #pragma unroll
-        for (int i = 0; i < N; i += 4) {
-            const float4 v = t < 32 ? *(const float4*)(x + (size_t)t * N + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            sq[i] = v.x * v.x;
-            sq[i + 1] = v.y * v.y;
-            sq[i + 2] = v.z * v.z;
-            sq[i + 3] = v.w * v.w;
-        }
-        const float sum = lane_chain<N>(sq, 0.0f, 32);
-        if (t == 0) sm.chain = 1.0f / __builtin_sqrtf(sum / (float)K + eps);
+    for (int i = 0; i < PER; ++i) {
+        const float v = x[S * w + PER * lane + i];
+        const float q = v * v;
+        sq[S * w + PER * lane + i] = q;
+        part += q;
     }
+    const float seg = wave_sum(part);
+    if (lane == 0) sm.ns.part[w] = seg;
     __syncthreads();
-    return sm.chain;
+    float est[NW];
+    est[0] = 0.0f;
+#pragma unroll
+    for (int q = 1; q < NW; ++q) est[q] = est[q - 1] + sm.ns.part[q - 1];
+    const auto cand = [&](int q) {
+        const int off = lane - WAVE / 2;
+        if (q == 0) return 0.0f;
+        if (off < -window || off > window) return __builtin_nanf("");
+        const int bits = (int)__float_as_uint(est[q]) + off;
+        return __uint_as_float((uint32_t)(bits < 0 ? 0 : bits));
+    };
+    float c = cand(0);
+#pragma unroll
+    for (int q = 1; q < NW; ++q)
+        if (w == q) c = cand(q);
+    const float* seg_p = sq + S * w;
+#pragma unroll
+    for (int i = 0; i < S; i += 4) {
+        const float4 v = *(const float4*)(seg_p + i);
+        c = c + v.x;
+        c = c + v.y;
+        c = c + v.z;
+        c = c + v.w;
+    }
+    sm.ns.res[w][lane] = c;
+    __syncthreads();
+    float r[NW];
+#pragma unroll
+    for (int q = 0; q < NW; ++q) r[q] = sm.ns.res[q][lane];
+    float sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, r[0])));
+#pragma unroll
+    for (int q = 1; q < NW; ++q) {
+        const unsigned long long m = __ballot(cand(q) == sum);
+        if (m) {
+            sum = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r[q]), __builtin_ctzll(m)));
+        } else {
+            for (int i = 0; i < S; ++i) sum = sum + sq[S * q + i];
+        }
+    }
+    return 1.0f / __builtin_sqrtf(sum / (float)K + eps);
 }
 
 // The RMSNorm weights of the quantizer items a thread takes (item t + T i),
@@ -911,6 +982,27 @@ __device__ __forceinline__ float wave_chain_sum(const float* v, int n, int lane)
     return lane_chain<N>(x, 0.0f, (n + N - 1) / N);
 }
 
+// The cached keys and values that the next attention of a key/value head
+// reads come into the L2 of the XCD its blocks share while the rest of the
+// layer runs (from memory they arrive too slowly for one block to wait on):
+// block r of the head's nb blocks loads one word of every nb-th 128-byte
+// line of the head's n_keys keys and values, from `threads` threads, NT
+// words a thread. The words stay in registers until the caller consumes
+// them (a load whose value is dropped is not made).
+template <int NT>
+__device__ __forceinline__ void touch_kv(int t, int threads, const LayerPtrs& L, int g, int r, int nb, int n_keys,
+                                         int max_pos, uint32_t (&v)[NT]) {
+    const uint8_t* kb = (const uint8_t*)(L.kcache + (size_t)g * max_pos * HD);
+    const uint8_t* vb = (const uint8_t*)(L.vcache + (size_t)g * max_pos * HD);
+    constexpr int LINE = 128, PER_KEY = HD * 2 / LINE;
+    const int lines = PER_KEY * n_keys;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const int i = r + nb * (t + threads * j);
+        if (i < 2 * lines) v[j] = *gmem((const uint32_t*)(i < lines ? kb + (size_t)LINE * i : vb + (size_t)LINE * (i - lines)));
+    }
+}
+
 // Attention in Trit's order (src/layers.rs:442-504,571-587; the orders of
 // src/cpu/fgemm.rs:665-793 and src/cpu/activation.rs exp_sums), on
 // 2 * heads blocks: block b < 2 heads takes key/value head g = b % kvh (so
@@ -928,7 +1020,13 @@ template <int GROUP, int DPB>
 __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, int pos, uint32_t tag_in,
                                 uint32_t tag_out, Smem& sm, unsigned long long deadline) {
     const int b = blockIdx.x, kvh = a.kvh;
-    if (b >= 2 * a.heads) return true;  // uniform over the block
+    if (b >= 2 * a.heads) {  // uniform over the block
+        // These blocks wait for the attention's outputs: waiting for their
+        // own stores now is free, and leaves the code after the attention
+        // nothing in flight to wait for (see the end of this function).
+        __builtin_amdgcn_s_waitcnt(VMCNT0);
+        return true;
+    }
     const int g = b % kvh, hq = g * GROUP + (b / kvh) % GROUP, h2 = b / (kvh * GROUP);
     const int tk = pos + 1;  // at most T (the host's plan)
     const int heads = a.heads;
@@ -979,7 +1077,7 @@ __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, in
     // The last wave polls: it loads no value, and no key while the session
     // has at most (NW - 1) * 64 positions.
     const int p0 = pos <= VT ? NW - 1 : NW - a.rq / 4 - 1;
-    if (!gather<8>(t, a.QKV, 3 * HD, index, tag_in, sm.qkv, sm, deadline, a.st, p0)) return false;
+    if (!gather<8>(t, a.QKV, 3 * HD, index, tag_in, sm.qkv, sm, deadline, a.st, p0)) leave();
     asm volatile("" ::"v"(touch));
     // The cached values into LDS, row-major [key][64 dims].
 #pragma unroll
@@ -1087,6 +1185,27 @@ __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, in
         }
         score = acc;
     }
+    // The cached values for p.V: wave w holds keys [64 w, 64 w + 64) before
+    // pos, lane d the block's dim 64 h2 + d, read from the LDS rows by
+    // transposing reads (ds_read_b64_tr_b16: in each 16-lane group, lane r
+    // gives the address of 4 halves, and lane i receives half i % 4 of the
+    // rows of lanes i / 4, 4 + i / 4, 8 + i / 4, 12 + i / 4): lane r of group
+    // G points at key 4 j + r / 4, dims 16 G + 4 (r % 4) .., so lane i gets
+    // dim i of keys 4 j .. 4 j + 3. The values past the last cached key are
+    // zeroed before use.
+    const int nkw = (pos + WAVE - 1) / WAVE;  // the waves that hold cached keys
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+    f16x4 vv[WAVE / 4];
+    if (__builtin_amdgcn_readfirstlane(w) < nkw) {
+        const int r = lane % 16, grp = lane / 16;
+        typedef __attribute__((address_space(3))) s16x4 LdsS16x4;
+#pragma unroll
+        for (int j = 0; j < WAVE / 4; ++j) {
+            const _Float16* row = &sm.vs[WAVE * w + 4 * j + r / 4][16 * grp + 4 * (r % 4)];
+            vv[j] = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsS16x4*)row));
+        }
+    }
     const float m_w = wave_max(score);
     if (lane == 0) sm.wmax[w] = m_w;
     __syncthreads();
@@ -1096,58 +1215,68 @@ __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, in
     const float e = t < tk ? exp_trit(score - mx) : 0.0f;
     sm.probs[t] = e;
     __syncthreads();
-    // Their sum in key order from 0, then p_j = e_j * (1/sum).
-    if (w == 0) {
+    // Their sum in key order from 0 (by the last wave, which holds no
+    // values for p.V while the session is short), then p_j = e_j * (1/sum).
+    if (w == NW - 1) {
         const float sum = wave_chain_sum<16>(sm.probs, tk, lane);
         if (lane == 0) sm.chain = 1.0f / sum;
     }
     __syncthreads();
-    sm.probs[t] = e * sm.chain;
-    __syncthreads();
-    // p.V: lane d of wave 0 chains dim 64 h2 + d over the keys in order (key
-    // j's value: one 2-byte read of row j, the 64 lanes reading its 128
-    // bytes), 16 keys a step, two buffers in turn so that one's reads are in
-    // flight during the other's multiply-adds; the new key's value (position
-    // pos = tk - 1) comes last, from the qkv product.
-    if (w == 0) {
-        float acc = 0.0f;
-        struct Keys16 {
-            float4 p[4];
-            uint32_t v[16];
-        };
-        auto load = [&](int j, Keys16& k) {
+    // p_j = e_j * (1/sum); the chain below reads -0 (adding nothing) past
+    // the cached keys, and the new key's probability on its own.
+    const float p = e * sm.chain;
+    sm.probs[t] = t < pos ? p : -0.0f;
+    if (t == pos) sm.ppos = p;
+    // p.V in key order: lane d chains dim 64 h2 + d, wave w over keys
+    // [64 w, 64 w + 64) from the sums wave w - 1 left in LDS (a block
+    // barrier between turns), its values in registers and its 64
+    // probabilities read (one broadcast read per four) before its turn; the
+    // new key's value (position pos = tk - 1) comes last, from the qkv
+    // product.
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    f32x4 pr[WAVE / 4];
+    // The wave index as the compiler can see it: uniform over the wave.
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    if (wu < nkw) {
+        const int nv = min(pos - WAVE * wu, WAVE);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) k.p[i] = *(const float4*)(sm.probs + j + 4 * i);
+        for (int i = 0; i < WAVE / 4; ++i) pr[i] = *(const f32x4*)(sm.probs + WAVE * w + 4 * i);
+        if (nv < WAVE) {  // the last wave: the slots past the last key
+            typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
-            for (int u = 0; u < 16; ++u) k.v[u] = __builtin_bit_cast(uint16_t, sm.vs[j + u][lane]);
-        };
-        auto fma16 = [&](const Keys16& k) {
+            for (int j = 0; j < WAVE / 4; ++j) {
+                u32x2 bits = __builtin_bit_cast(u32x2, vv[j]);
 #pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                const float4 pq = k.p[u / 4];
-                const float pu = (u & 3) == 0 ? pq.x : (u & 3) == 1 ? pq.y : (u & 3) == 2 ? pq.z : pq.w;
-                acc = __builtin_fmaf(pu, f16_to_f32((uint16_t)k.v[u]), acc);
+                for (int h = 0; h < 2; ++h) {
+                    const int k = 4 * j + 2 * h;
+                    bits[h] &= (k < nv ? 0xffffu : 0u) | (k + 1 < nv ? 0xffff0000u : 0u);
+                }
+                vv[j] = __builtin_bit_cast(f16x4, bits);
             }
-        };
-        const int steps = pos / 16;
-        Keys16 ka, kb;
-        if (steps > 0) load(0, ka);
-        int q = 0;
-        for (; q + 2 <= steps; q += 2) {
-            load(16 * (q + 1), kb);
-            __builtin_amdgcn_sched_barrier(0);
-            fma16(ka);
-            __builtin_amdgcn_sched_barrier(0);
-            if (q + 2 < steps) load(16 * (q + 2), ka);
-            __builtin_amdgcn_sched_barrier(0);
-            fma16(kb);
-            __builtin_amdgcn_sched_barrier(0);
         }
-        if (q < steps) fma16(ka);
-        for (int j = 16 * steps; j < pos; ++j) acc = __builtin_fmaf(sm.probs[j], (float)sm.vs[j][lane], acc);
-        acc = __builtin_fmaf(sm.probs[pos], sm.kvn[1][64 * h2 + lane], acc);
-        put(a.ATT + (size_t)hq * HD + 64 * h2 + lane, acc, tag_out);
+#pragma unroll
+        for (int j = 0; j < WAVE / 4; ++j) asm volatile("" : "+v"(vv[j]));
+#pragma unroll
+        for (int i = 0; i < WAVE / 4; ++i) asm volatile("" : "+v"(pr[i]));
     }
+    // Every wave passes nkw barriers: the turns before its own, then its
+    // turn's end and the rest.
+    float acc = 0.0f;
+    for (int cw = 0; cw < min(wu, nkw); ++cw) __syncthreads();
+    if (wu < nkw) {
+        if (wu > 0) acc = sm.carry[lane];
+#pragma unroll
+        for (int i = 0; i < WAVE; ++i) acc = __builtin_fmaf(pr[i / 4][i & 3], (float)vv[i / 4][i & 3], acc);
+        if (wu + 1 < nkw) sm.carry[lane] = acc;
+    }
+    for (int cw = wu; cw < nkw; ++cw) __syncthreads();
+    // Every load of the attention has arrived: the explicit wait costs
+    // nothing here, and the compiler's later waits (for registers that its
+    // analysis may see as loading) no longer wait for the put's store.
+    __builtin_amdgcn_s_waitcnt(VMCNT0);
+    // After a barrier (or in the wave that wrote it): the new key's term.
+    if (wu == (nkw > 0 ? nkw - 1 : 0))
+        put(a.ATT + (size_t)hq * HD + 64 * h2 + lane, __builtin_fmaf(sm.ppos, sm.kvn[1][64 * h2 + lane], acc), tag_out);
     return true;
 }
 
@@ -1250,7 +1379,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         int index = INT_MAX;
         if (it > 0) {
             const uint32_t tag_c = ((seq0 + (uint32_t)it - 1) << 8) + (uint32_t)(a.n_layers * PH + 1);
-            if (!gather<MAXD / T>(t, a.CAND, 2 * (int)gridDim.x, lin, tag_c, sm.xin, sm, deadline, st)) return;
+            if (!gather<MAXD / T>(t, a.CAND, 2 * (int)gridDim.x, lin, tag_c, sm.xin, sm, deadline, st)) leave();
             if (t < (int)gridDim.x) {
                 best = sm.xin[2 * t];
                 index = __float_as_int(sm.xin[2 * t + 1]);
@@ -1301,11 +1430,15 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         // qkv: x (gathered, or the embedding) -> RMSNorm -> quantize -> rows.
         NormRegs<JD> nq;
         load_norm<JD>(t, L.norm_attn, nq);
+        // The touched words (see touch_kv); left unset where nothing is
+        // touched: zeroing them would wait for whatever the registers last
+        // loaded, and for the stores issued since.
+        uint32_t kvt[4];
         // Polled by the first waves (the down rows' wave stored x).
         if (layer > 0 && !gather<6>(t, a.X, a.d, lin, tag_of(tag0, layer - 1, 5), sm.xres, sm, deadline, st))
-            return;
+            leave();
         if constexpr (EXACT) {
-            const float inv = norm_inv_exact<JD>(t, sm.xres, a.eps, sm);
+            const float inv = norm_inv_spec<JD>(t, sm.xres, a.eps, a.norm_window, sm);
             if (t == 0) sm.inv = inv;
         } else if (w == 0) {
             const float inv = norm_inv_wave<JD>(t, sm.xres, a.eps);
@@ -1325,7 +1458,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
                                                                 tag_of(tag0, layer, 2), sm, deadline)
                                   : attention_all<GROUP, DPB>(t, a, L, pos, tag_of(tag0, layer, 0),
                                                               tag_of(tag0, layer, 2), sm, deadline);
-            if (!ok) return;
+            if (!ok) leave();
             // o + residual; the o and gate_up rows stream in meanwhile, and
             // the qkv waves (nothing in flight) poll.
             if (ao)
@@ -1333,20 +1466,28 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             else
                 zero_rows(rr);
             if (agu) load_rows<JD, 2>(t, L.codes[2], L.scales[2], a.ffn, rowgu, rr);
+            // Then the attention blocks' waves before the qkv waves load the
+            // next attention's keys and values into L2.
+            if (EXACT && b < 2 * a.heads && w < NW - nqw) {
+                const bool last = layer + 1 == a.n_layers;
+                const int kvh = a.kvh;
+                touch_kv(t, (NW - nqw) * WAVE, sm.layers[last ? 0 : layer + 1], b % kvh, b / kvh, 2 * a.heads / kvh,
+                         last ? pos + 1 : pos, a.max_pos, kvt);
+            }
             __syncthreads();
             if (!gather<8>(t, a.ATT, a.qd, lin, tag_of(tag0, layer, 2), sm.xin, sm, deadline, st, NW - nqw))
-                return;
+                leave();
         } else {
             // attention partials.
             if (!attention<GROUP>(t, a, L, pos, tag_of(tag0, layer, 0), tag_of(tag0, layer, 1), sm, deadline))
-                return;
+                leave();
             // combine; the o rows stream in meanwhile.
             if (ao)
                 load_rows<JO, 1>(t, L.codes[1], L.scales[1], 0, rowo, rr);
             else
                 zero_rows(rr);
             __syncthreads();
-            if (!combine(t, a, tag_of(tag0, layer, 1), tag_of(tag0, layer, 2), sm, deadline, nu + no)) return;
+            if (!combine(t, a, tag_of(tag0, layer, 1), tag_of(tag0, layer, 2), sm, deadline, nu + no)) leave();
             // o + residual; the gate_up rows stream in meanwhile.
             if (agu)
                 load_rows<JD, 2>(t, L.codes[2], L.scales[2], a.ffn, rowgu, rr);
@@ -1355,7 +1496,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             __syncthreads();
             // Polled from the first o wave on: the gate_up waves' loads are
             // in flight.
-            if (!gather<8>(t, a.ATT, a.qd, lin, tag_of(tag0, layer, 2), sm.xin, sm, deadline, st, nu)) return;
+            if (!gather<8>(t, a.ATT, a.qd, lin, tag_of(tag0, layer, 2), sm.xin, sm, deadline, st, nu)) leave();
         }
         quantize_block<JO>(t, sm.xin, (const NormRegs<JO>*)nullptr, sm);
         if (ao) {
@@ -1363,13 +1504,16 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             row_chain<JO, 1>(t, rr, sm, acc);
             if ((lane & 15) == 14) put(a.X + rowo, sm.xres[rowo] + acc[0], tag_of(tag0, layer, 3));
         }
+        // The touched words are consumed here, where they have long arrived
+        // (before the polls of the gather below).
+        asm volatile("" ::"v"(kvt[0]), "v"(kvt[1]), "v"(kvt[2]), "v"(kvt[3]));
         // gate_up + SwiGLU.
         NormRegs<JD> ngu;
         load_norm<JD>(t, L.norm_mlp, ngu);
         __syncthreads();
-        if (!gather<MAXK / T>(t, a.X, a.d, lin, tag_of(tag0, layer, 3), sm.xres, sm, deadline, st)) return;
+        if (!gather<MAXK / T>(t, a.X, a.d, lin, tag_of(tag0, layer, 3), sm.xres, sm, deadline, st)) leave();
         if constexpr (EXACT) {
-            const float inv = norm_inv_exact<JD>(t, sm.xres, a.eps, sm);
+            const float inv = norm_inv_spec<JD>(t, sm.xres, a.eps, a.norm_window, sm);
             if (t == 0) sm.inv = inv;
         } else if (w == 0) {
             const float inv = norm_inv_wave<JD>(t, sm.xres, a.eps);
@@ -1390,7 +1534,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         if (aq && layer + 1 < a.n_layers)
             load_rows<JD, 1>(t, sm.layers[layer + 1].codes[0], sm.layers[layer + 1].scales[0], 0, rowq, rr);
         __syncthreads();
-        if (!gather<MAXK / T>(t, a.H, a.ffn, lin, tag_of(tag0, layer, 4), sm.xin, sm, deadline, st)) return;
+        if (!gather<MAXK / T>(t, a.H, a.ffn, lin, tag_of(tag0, layer, 4), sm.xin, sm, deadline, st)) leave();
         quantize_block<JF>(t, sm.xin, (const NormRegs<JF>*)nullptr, sm);
         if (ad) {
             float acc[1];
@@ -1430,7 +1574,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     for (int q = 0; q < (MAXD + T - 1) / T; ++q) fn[q] = t + T * q < a.d ? gmem(a.final_norm)[t + T * q] : 0.0f;
     if (!gather<MAXD / T>(t, a.X, a.d, lin, tag_of(tag0, a.n_layers - 1, 5), sm.xres, sm, deadline, st)) return;
     if constexpr (EXACT) {
-        const float inv = norm_inv_exact<JD>(t, sm.xres, a.eps, sm);
+        const float inv = norm_inv_spec<JD>(t, sm.xres, a.eps, a.norm_window, sm);
         if (t == 0) sm.inv = inv;
     } else if (w == 0) {
         const float inv = norm_inv_wave<JD>(t, sm.xres, a.eps);
@@ -1756,6 +1900,10 @@ void decode_step_launch(SessionImpl& S, int step, int pos, int nsteps, hipStream
     // path: 0 makes every block's first wait give up, and the launch drains).
     if (const char* v = getenv("TRIT_HIP_STEP_DEADLINE_US"))
         a.ticks = (unsigned long long)(rate_khz > 0 ? rate_khz : 100000) * strtoull(v, nullptr, 10) / 1000ull;
+    // TRIT_HIP_NORM_WINDOW narrows the RMSNorm's candidate starts (tests of
+    // the path that chains a segment again: 0 leaves only the estimate).
+    a.norm_window = 31;
+    if (const char* v = getenv("TRIT_HIP_NORM_WINDOW")) a.norm_window = (int)strtol(v, nullptr, 10);
     void* args[] = {&a, &step, &pos, (void*)&seq0, &nsteps};
     TRIT_HIP(hipLaunchCooperativeKernel((const void*)p.fn, dim3(p.blocks), dim3(T), args, 0, s));
 }
