@@ -147,6 +147,12 @@ typedef struct {
     float eps;        /* rms_norm_eps, 1e-6 when the config has none       */
     float rope_base;  /* rope_theta, 1e6 when the config has none          */
     int qk_norm;      /* Qwen3's per-head q and k norms                     */
+    /* Granite's multipliers (Config, reference causal_lm.rs:17-27,62-65):
+     * on the input embeddings, on q in place of 1/sqrt(head_dim) (0: none),
+     * on each residual branch, and (as a divisor) on the logits. 0 in
+     * embedding_multiplier, residual_multiplier or logits_scaling means 1,
+     * so a zeroed tail describes a Qwen3 / Llama decoder. */
+    float embedding_multiplier, attention_multiplier, residual_multiplier, logits_scaling;
 } TritHipLmConfig;
 
 /* A decoder from its layers (CausalLm::from_tensors, reference
@@ -159,6 +165,12 @@ int trit_hip_decoder_new(const TritHipLmConfig *config, const TritHipLayer *cons
                          const float *norms, const TritHipLayer *embed, const TritHipLayer *head,
                          TritHipDecoder **out);
 void trit_hip_decoder_free(TritHipDecoder *decoder);
+
+/* CausalLm::set_ffn_scales (reference causal_lm.rs:304-307,458-464):
+ * layers x d f32 scales on each layer's normed MLP input (Voxtral
+ * Realtime's 1 + ada(t)); NULL removes them. Sessions see the change from
+ * their next call; not while a session of the decoder runs a call. */
+int trit_hip_decoder_set_ffn_scales(TritHipDecoder *decoder, const float *scales);
 
 /* Session flags. Every sum runs in Trit's order unless TRIT_HIP_TREE_SUMS
  * is given: the default (0) is Trit's arithmetic with f16 keys and values
@@ -206,6 +218,31 @@ int trit_hip_session_generate_timed(TritHipSession *session, int max_new, const 
 
 /* Clears the caches (a new call). */
 int trit_hip_session_reset(TritHipSession *session);
+
+/* CausalLm::generate_additive (reference causal_lm.rs:313-345): greedy
+ * tokens with audio rows added to every input -- the prompt's embeddings
+ * plus audio rows 0..n, then each new token's embedding plus the row of
+ * its position -- until a stop token or the rows end. audio: rows x d
+ * host f32. Starts from a fresh (or reset) session, whose positions must
+ * hold `rows`; out holds rows - n + 1 tokens. Returns the count (0 when
+ * n is 0 or rows < n, as Trit does), or -1. */
+int trit_hip_session_generate_additive(TritHipSession *session, const int32_t *prompt, int n, const float *audio,
+                                       int rows, const int32_t *stop, int n_stop, int32_t *out);
+
+/* A prompt start that many calls share (CausalLm::prefix and Prefix,
+ * reference causal_lm.rs:118-122,200-215): its keys and values, computed
+ * once in a session of the given flags. */
+typedef struct TritHipPrefix TritHipPrefix;
+int trit_hip_prefix_new(const TritHipDecoder *decoder, const int32_t *tokens, int n, int flags, TritHipPrefix **out);
+void trit_hip_prefix_free(TritHipPrefix *prefix);
+/* The prompt `tokens` of a fresh (or reset) session that may begin with
+ * `prefix` (CausalLm::generate with Some(prefix), causal_lm.rs:217-249):
+ * when it is longer than the prefix and starts with its tokens, the
+ * session takes the prefix's keys and values and runs only the rest;
+ * otherwise the whole prompt. The prefix must come from the session's
+ * decoder and flags. Logits as trit_hip_session_prefill. */
+int trit_hip_session_prefill_prefixed(TritHipSession *session, const TritHipPrefix *prefix, const int32_t *tokens,
+                                      int n, float *logits);
 
 /* Position count the caches hold. */
 int trit_hip_session_position(const TritHipSession *session);

@@ -1729,6 +1729,9 @@ bool plan(const SessionImpl& S, Plan& p) {
     const DecoderImpl& D = *S.dec;
     const auto& c = D.c;
     if (S.kv32) return false;
+    // Granite's multipliers, per-layer MLP scales and added input rows run
+    // on the per-kernel loop.
+    if (D.granite() || D.has_ffn_scales || S.additive_rows) return false;
     if (c.head_dim != HD || c.kv_heads <= 0 || c.heads % c.kv_heads != 0) return false;
     const int group = c.heads / c.kv_heads, qd = c.heads * HD;
     if (c.d % 256 || qd % 256 || c.ffn % 256 || c.d > MAXD || qd > MAXK || c.ffn > MAXK) return false;

@@ -65,9 +65,11 @@ __global__ void norm_inv_kernel(const float* __restrict__ x, int d, float eps, f
     }
 }
 
-// out = x * (inv * w), inv from `inv` (exact) or a fixed tree (fast).
+// out = x * (inv * w), inv from `inv` (exact) or a fixed tree (fast); then,
+// with `scale`, out *= scale (the MLP scales, causal_lm.rs:458-464).
 __global__ void rmsnorm_kernel(const float* __restrict__ x, int d, const float* __restrict__ w, float eps,
-                               const float* __restrict__ inv_in, float* __restrict__ out, const State* st) {
+                               const float* __restrict__ inv_in, float* __restrict__ out, const State* st,
+                               const float* __restrict__ scale = nullptr) {
     if (st && st->done) return;
     __shared__ float red[256];
     __shared__ float inv_s;
@@ -90,7 +92,45 @@ __global__ void rmsnorm_kernel(const float* __restrict__ x, int d, const float* 
     }
     __syncthreads();
     const float inv = inv_s;
-    for (int i = threadIdx.x; i < d; i += 256) out[(size_t)blockIdx.x * d + i] = row[i] * (inv * w[i]);
+    for (int i = threadIdx.x; i < d; i += 256) {
+        float v = row[i] * (inv * w[i]);
+        if (scale) v = v * scale[i];
+        out[(size_t)blockIdx.x * d + i] = v;
+    }
+}
+
+// x *= w (scale_all, src/layers.rs:219-223; the caller skips w == 1).
+__global__ void scale_kernel(float* __restrict__ x, int n, float w, const State* st) {
+    if (st && st->done) return;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) x[i] = x[i] * w;
+}
+
+// The first qd values (q) of each row of the qkv product times w, after
+// the rotary (causal_lm.rs:438-442).
+__global__ void scale_q_kernel(float* __restrict__ qkv, int stride, int rows, int qd, float w, const State* st) {
+    if (st && st->done) return;
+    const int n = rows * qd;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        float* v = qkv + (size_t)(i / qd) * stride + i % qd;
+        *v = *v * w;
+    }
+}
+
+// x += w * y, two roundings (add_scaled_into, src/layers.rs:226-236, for
+// w != 1).
+__global__ void add_scaled_kernel(float* __restrict__ x, const float* __restrict__ y, int n, float w,
+                                  const State* st) {
+    if (st && st->done) return;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) x[i] = x[i] + w * y[i];
+}
+
+// x += rows of `add` (add_into, src/layers.rs:245-252): the n x d rows at `add`, or
+// with `by_pos` the one row at position st->pos (a decode step's input).
+__global__ void add_rows_kernel(float* __restrict__ x, const float* __restrict__ add, int n, int d, int by_pos,
+                                const State* st) {
+    if (st->done) return;
+    const float* a = by_pos ? add + (size_t)st->pos * d : add;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) x[i] = x[i] + a[i];
 }
 
 // Embedding rows of `tokens` (or of st->token when tokens is null) from the
@@ -1003,6 +1043,11 @@ void rope_table(int dims, float base, int positions, std::vector<float>& sn, std
         }
 }
 
+void drop_graph(SessionImpl& S) {
+    if (S.graph) (void)hipGraphExecDestroy(S.graph);
+    S.graph = nullptr;
+}
+
 void ensure_rows(SessionImpl& S, int rows) {
     if (rows <= S.rows_cap) return;
     const auto& c = S.dec->c;
@@ -1012,6 +1057,7 @@ void ensure_rows(SessionImpl& S, int rows) {
     S.att.alloc((size_t)rows * qd * 4);
     S.hid.alloc((size_t)rows * c.ffn * 4);
     S.inv.alloc((size_t)rows * 4);
+    S.xn.alloc((size_t)rows * c.d * 4);
     S.normed.alloc((size_t)c.d * 4);
     S.tokens_in.alloc((size_t)rows * 4);
     S.max_splits = (S.max_pos + Split<float>::CH - 1) / Split<float>::CH;
@@ -1021,10 +1067,7 @@ void ensure_rows(SessionImpl& S, int rows) {
     S.gemm_scratch.alloc(std::max(gemm_scratch_bytes(rows, kmax), gemv_scratch_bytes(8, kmax)));
     TRIT_HIP(hipMemset(S.att_arrived.ptr, 0, (size_t)rows * c.kv_heads * 4));
     S.rows_cap = rows;
-    if (S.graph) {
-        (void)hipGraphExecDestroy(S.graph);
-        S.graph = nullptr;
-    }
+    drop_graph(S);
 }
 
 // TRIT_HIP_QK_WAVE=0 runs the prompt's q/k norm and rotary one block a
@@ -1124,6 +1167,16 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
     const int hd = c.head_dim, qd = c.heads * hd, kv = c.kv_heads * hd, stride = qd + 2 * kv;
     State* st = S.st();
     float* x = S.x.as<float>();
+    const int ew = 256, eblocks = std::min((rows * c.d + 255) / 256, 1024);
+    // Granite: the input rows times embedding_multiplier (causal_lm.rs:420).
+    if (c.embedding_multiplier != 1.0f)
+        hipLaunchKernelGGL(scale_kernel, dim3(eblocks), dim3(ew), 0, s, x, rows * c.d, c.embedding_multiplier, st);
+    // q times attention_multiplier * sqrt(head_dim) after the rotary
+    // (causal_lm.rs:422-424,438-442); off without the multiplier.
+    const float q_scale = c.attention_multiplier != 0.0f ? c.attention_multiplier * sqrtf((float)hd) : 1.0f;
+    const float rm = c.residual_multiplier;
+    const float* ffn_scales = D.has_ffn_scales ? D.ffn_scales.as<float>() : nullptr;
+    float* xn = S.xn.as<float>();
     for (int l = 0; l < c.layers; ++l) {
         GemvArgs a;
         a.eps = c.eps;
@@ -1139,7 +1192,7 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
         a.y = S.qkv.as<float>();
         product(S, *D.qkv[l], a, rows, s, stride);
         // q/k norm, rotary, cache append, attention.
-        const bool fused = !S.exact && rows == 1;
+        const bool fused = !S.exact && rows == 1 && q_scale == 1.0f;
         if (!fused) {
             if (S.exact && !S.kv32) {
                 // Trit's serial q/k norm sums, f16 caches.
@@ -1172,6 +1225,9 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
                                    S.vcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, st);
             }
             TRIT_HIP(hipGetLastError());
+            if (q_scale != 1.0f)
+                hipLaunchKernelGGL(scale_q_kernel, dim3(std::min((rows * qd + 255) / 256, 1024)), dim3(256), 0, s,
+                                   S.qkv.as<float>(), stride, rows, qd, q_scale, st);
         }
         if (S.exact) {
             // The host sizes shared memory for the largest key count this forward can see.
@@ -1199,15 +1255,27 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
             launch_split<_Float16>(S, l, rows, fused, s);
         }
         TRIT_HIP(hipGetLastError());
-        // o with the residual add.
-        GemvArgs o;
-        o.skip = &st->done;
-        o.x = S.att.as<float>();
-        o.y = x;
-        o.residual = x;
-        o.epilogue = EPI_RESIDUAL;
-        product(S, *D.o[l], o, rows, s, c.d);
-        // gate_up with the MLP norm in the prologue and SwiGLU after.
+        // o with the residual add; with Granite's residual_multiplier the
+        // product is stored and added times it (causal_lm.rs:456).
+        auto residual = [&](const LayerRef& L, const float* in) {
+            GemvArgs r;
+            r.skip = &st->done;
+            r.x = in;
+            if (rm == 1.0f) {
+                r.y = x;
+                r.residual = x;
+                r.epilogue = EPI_RESIDUAL;
+                product(S, *L, r, rows, s, c.d);
+            } else {
+                r.y = xn;
+                product(S, *L, r, rows, s, c.d);
+                hipLaunchKernelGGL(add_scaled_kernel, dim3(eblocks), dim3(ew), 0, s, x, xn, rows * c.d, rm, st);
+            }
+        };
+        residual(D.o[l], S.att.as<float>());
+        // gate_up with the MLP norm in the prologue and SwiGLU after; with
+        // MLP scales the normed rows are made first and scaled
+        // (causal_lm.rs:457-464).
         GemvArgs gu;
         gu.skip = &st->done;
         gu.eps = c.eps;
@@ -1216,19 +1284,20 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
                                S.inv.as<float>(), st);
             gu.norm_inv = S.inv.as<float>();
         }
-        gu.x = x;
-        gu.norm_w = D.norm_mlp(l);
+        if (ffn_scales) {
+            hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, s, x, c.d, D.norm_mlp(l), c.eps,
+                               S.exact ? S.inv.as<float>() : nullptr, xn, st, ffn_scales + (size_t)l * c.d);
+            gu.x = xn;
+            gu.norm_inv = nullptr;
+        } else {
+            gu.x = x;
+            gu.norm_w = D.norm_mlp(l);
+        }
         gu.y = S.hid.as<float>();
         gu.epilogue = EPI_SILU_PAIR;
         product(S, *D.gate_up[l], gu, rows, s, c.ffn);
         // down with the residual add.
-        GemvArgs dn;
-        dn.skip = &st->done;
-        dn.x = S.hid.as<float>();
-        dn.y = x;
-        dn.residual = x;
-        dn.epilogue = EPI_RESIDUAL;
-        product(S, *D.down[l], dn, rows, s, c.d);
+        residual(D.down[l], S.hid.as<float>());
     }
     // Final norm of the last row, then the head.
     const float* last = x + (size_t)(rows - 1) * c.d;
@@ -1243,6 +1312,11 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
     h.x = S.normed.as<float>();
     h.y = S.logits.as<float>();
     layer_forward(D.head ? *D.head : *D.embed, h, s);
+    // Granite: logits times 1 / logits_scaling (causal_lm.rs:387).
+    const float lw = 1.0f / c.logits_scaling;
+    if (lw != 1.0f)
+        hipLaunchKernelGGL(scale_kernel, dim3((c.vocab + 255) / 256), dim3(256), 0, s, S.logits.as<float>(), c.vocab,
+                           lw, st);
     hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, st, rows);
     TRIT_HIP(hipGetLastError());
 }
@@ -1286,6 +1360,9 @@ void step(SessionImpl& S, hipStream_t s) {
     hipLaunchKernelGGL(choose_kernel, dim3(blocks), dim3(CHOOSE_THREADS), 0, s, S.logits.as<float>(), c.vocab,
                        S.st(), S.tokens_out.as<int>(), S.partials.as<float2>(), S.dec->embed->codes.as<uint16_t>(),
                        c.d, S.x.as<float>());
+    if (S.additive_rows)
+        hipLaunchKernelGGL(add_rows_kernel, dim3((c.d + 255) / 256), dim3(256), 0, s, S.x.as<float>(),
+                           S.additive.as<float>(), c.d, c.d, 1, S.st());
     forward(S, 1, s);
 }
 
@@ -1305,7 +1382,11 @@ bool use_step(const SessionImpl& S) {
 }
 
 void build_graph(SessionImpl& S) {
-    if (S.graph) return;
+    // The captured step holds the MLP scales' buffer and whether rows are
+    // added to its input.
+    const bool additive = S.additive_rows != 0;
+    if (S.graph && S.graph_ffn_version == S.dec->ffn_version && S.graph_additive == additive) return;
+    drop_graph(S);
     hipStream_t s = stream();
     hipGraph_t g = nullptr;
     TRIT_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
@@ -1322,6 +1403,8 @@ void build_graph(SessionImpl& S) {
     (void)hipGraphDestroy(g);
     TRIT_HIP(e);
     S.graph = exec;
+    S.graph_ffn_version = S.dec->ffn_version;
+    S.graph_additive = additive;
 }
 
 }  // namespace
@@ -1333,6 +1416,52 @@ struct TritHipDecoder {
 struct TritHipSession {
     trit::SessionImpl impl;
 };
+// Prefix (causal_lm.rs:118-122): the tokens and, per layer and key/value
+// head, their n keys and values in the cache type of the flags it was made
+// with.
+struct TritHipPrefix {
+    std::shared_ptr<trit::DecoderImpl> dec;
+    std::vector<int32_t> tokens;
+    bool exact = false, kv32 = false;
+    trit::DeviceMemory keys, values;  // [layer][kv head][n][head_dim]
+};
+
+namespace trit {
+namespace {
+
+// A session's caches and buffers for `max_positions` positions.
+void init_session(SessionImpl& s, std::shared_ptr<DecoderImpl> dec, int max_positions, int flags) {
+    if (max_positions <= 0) fail("session: max_positions must be positive");
+    s.dec = std::move(dec);
+    const auto& c = s.dec->c;
+    s.max_pos = max_positions;
+    s.flags = flags;
+    // Trit's sum orders unless tree sums are asked for; f32 caches
+    // with EXACT (Trit's own arithmetic) or KV_F32.
+    s.exact = (flags & TRIT_HIP_EXACT) != 0 || (flags & TRIT_HIP_TREE_SUMS) == 0;
+    s.kv32 = (flags & (TRIT_HIP_EXACT | TRIT_HIP_KV_F32)) != 0;
+    if ((flags & TRIT_HIP_EXACT) && (flags & TRIT_HIP_TREE_SUMS))
+        fail("session: EXACT and TREE_SUMS exclude each other");
+    const size_t lds = (size_t)(MAX_HD + max_positions + ATT_THREADS) * 4;
+    if (lds > 64 * 1024) fail("session: max_positions above the attention kernel's limit (16000)");
+    const size_t kvb = (size_t)c.layers * c.kv_heads * max_positions * c.head_dim * (s.kv32 ? 4 : 2);
+    s.kcache.alloc(kvb);
+    s.vcache.alloc(kvb);
+    std::vector<float> sn, cs;
+    rope_table(c.head_dim, c.rope_base, max_positions, sn, cs);
+    s.rope_sin.alloc(sn.size() * 4);
+    s.rope_sin.upload(sn.data(), sn.size() * 4);
+    s.rope_cos.alloc(cs.size() * 4);
+    s.rope_cos.upload(cs.data(), cs.size() * 4);
+    s.logits.alloc((size_t)c.vocab * 4);
+    s.partials.alloc((size_t)((c.vocab + CHOOSE_SPAN - 1) / CHOOSE_SPAN) * 8);
+    s.state.alloc(sizeof(State));
+    ensure_rows(s, 8);
+    reset_state(s);
+}
+
+}  // namespace
+}  // namespace trit
 
 using namespace trit;
 
@@ -1350,6 +1479,10 @@ int trit_hip_decoder_new(const TritHipLmConfig* config, const TritHipLayer* cons
         if (c.heads / c.kv_heads > 4) fail("decoder: at most 4 query heads per key/value head");
         auto D = std::make_shared<DecoderImpl>();
         D->c = c;
+        // Zeros in the Granite fields mean none.
+        if (D->c.embedding_multiplier == 0.0f) D->c.embedding_multiplier = 1.0f;
+        if (D->c.residual_multiplier == 0.0f) D->c.residual_multiplier = 1.0f;
+        if (D->c.logits_scaling == 0.0f) D->c.logits_scaling = 1.0f;
         const int hd = c.head_dim, qkv_rows = (c.heads + 2 * c.kv_heads) * hd;
         auto want = [&](const TritHipLayer* h, int n, int k, const char* what, int l) {
             LayerRef L = layer_ref(h);
@@ -1401,39 +1534,29 @@ int trit_hip_decoder_new(const TritHipLmConfig* config, const TritHipLayer* cons
 
 void trit_hip_decoder_free(TritHipDecoder* decoder) { delete decoder; }
 
+int trit_hip_decoder_set_ffn_scales(TritHipDecoder* decoder, const float* scales) {
+    return guard(-1, [&] {
+        if (!decoder) fail("decoder is NULL");
+        DecoderImpl& D = *decoder->impl;
+        if (scales) {
+            const size_t bytes = (size_t)D.c.layers * D.c.d * 4;
+            if (D.ffn_scales.bytes != bytes) D.ffn_scales.alloc(bytes);
+            D.ffn_scales.upload(scales, bytes);
+            D.has_ffn_scales = true;
+        } else {
+            D.has_ffn_scales = false;
+        }
+        D.ffn_version += 1;
+        return 0;
+    });
+}
+
 int trit_hip_session_new(const TritHipDecoder* decoder, int max_positions, int flags, TritHipSession** out) {
     return guard(-1, [&] {
         if (!decoder || !out) fail("session: decoder or out is NULL");
-        if (max_positions <= 0) fail("session: max_positions must be positive");
         auto* S = new TritHipSession();
         try {
-            SessionImpl& s = S->impl;
-            s.dec = decoder->impl;
-            const auto& c = s.dec->c;
-            s.max_pos = max_positions;
-            s.flags = flags;
-            // Trit's sum orders unless tree sums are asked for; f32 caches
-            // with EXACT (Trit's own arithmetic) or KV_F32.
-            s.exact = (flags & TRIT_HIP_EXACT) != 0 || (flags & TRIT_HIP_TREE_SUMS) == 0;
-            s.kv32 = (flags & (TRIT_HIP_EXACT | TRIT_HIP_KV_F32)) != 0;
-            if ((flags & TRIT_HIP_EXACT) && (flags & TRIT_HIP_TREE_SUMS))
-                fail("session: EXACT and TREE_SUMS exclude each other");
-            const size_t lds = (size_t)(MAX_HD + max_positions + ATT_THREADS) * 4;
-            if (lds > 64 * 1024) fail("session: max_positions above the attention kernel's limit (16000)");
-            const size_t kvb = (size_t)c.layers * c.kv_heads * max_positions * c.head_dim * (s.kv32 ? 4 : 2);
-            s.kcache.alloc(kvb);
-            s.vcache.alloc(kvb);
-            std::vector<float> sn, cs;
-            rope_table(c.head_dim, c.rope_base, max_positions, sn, cs);
-            s.rope_sin.alloc(sn.size() * 4);
-            s.rope_sin.upload(sn.data(), sn.size() * 4);
-            s.rope_cos.alloc(cs.size() * 4);
-            s.rope_cos.upload(cs.data(), cs.size() * 4);
-            s.logits.alloc((size_t)c.vocab * 4);
-            s.partials.alloc((size_t)((c.vocab + CHOOSE_SPAN - 1) / CHOOSE_SPAN) * 8);
-            s.state.alloc(sizeof(State));
-            ensure_rows(s, 8);
-            reset_state(s);
+            init_session(S->impl, decoder->impl, max_positions, flags);
         } catch (...) {
             delete S;
             throw;
@@ -1443,7 +1566,10 @@ int trit_hip_session_new(const TritHipDecoder* decoder, int max_positions, int f
     });
 }
 
-static int prefill_common(TritHipSession* session, int n, float* logits, const int32_t* tokens, const float* rows) {
+// The prompt's rows (embeddings of `tokens`, or host `rows`) plus, with
+// `add`, n x d device rows, at the next positions.
+static int prefill_common(TritHipSession* session, int n, float* logits, const int32_t* tokens, const float* rows,
+                          const float* add = nullptr) {
     if (!session) fail("session is NULL");
     if (n <= 0) fail("prefill: no rows");
     SessionImpl& S = session->impl;
@@ -1468,6 +1594,11 @@ static int prefill_common(TritHipSession* session, int n, float* logits, const i
         TRIT_HIP(hipGetLastError());
     } else {
         TRIT_HIP(hipMemcpyAsync(S.x.ptr, rows, (size_t)n * c.d * 4, hipMemcpyHostToDevice, s));
+    }
+    if (add) {
+        hipLaunchKernelGGL(add_rows_kernel, dim3(std::min((n * c.d + 255) / 256, 1024)), dim3(256), 0, s,
+                           S.x.as<float>(), add, n * c.d, c.d, 0, S.st());
+        TRIT_HIP(hipGetLastError());
     }
     forward(S, n, s);
     S.host_pos += n;
@@ -1506,10 +1637,7 @@ static int generate_common(TritHipSession* session, int max_new, const int32_t* 
     if (S.graph_out_cap < max_new) {
         S.tokens_out.alloc((size_t)max_new * 4);
         S.graph_out_cap = max_new;
-        if (S.graph) {
-            (void)hipGraphExecDestroy(S.graph);
-            S.graph = nullptr;
-        }
+        drop_graph(S);
     }
     arm_state(S, max_new, stop, n_stop);
     hipStream_t s = stream();
@@ -1551,6 +1679,109 @@ int trit_hip_session_generate_timed(TritHipSession* session, int max_new, const 
     return guard(-1, [&] {
         if (persistent) *persistent = session && use_step(session->impl) ? 1 : 0;
         return generate_common(session, max_new, stop, n_stop, out, (hipEvent_t)start_event, (hipEvent_t)stop_event);
+    });
+}
+
+int trit_hip_session_generate_additive(TritHipSession* session, const int32_t* prompt, int n, const float* audio,
+                                       int rows, const int32_t* stop, int n_stop, int32_t* out) {
+    return guard(-1, [&] {
+        if (!session) fail("session is NULL");
+        SessionImpl& S = session->impl;
+        check_usable(S);
+        if (n < 0 || rows < 0) fail("generate_additive: negative sizes");
+        // Trit returns no tokens for an empty prompt or too few rows.
+        if (n == 0 || rows < n) return 0;
+        if (!prompt || !audio || !out) fail("generate_additive: prompt, audio or out is NULL");
+        if (S.host_pos != 0) fail("generate_additive: the session holds positions; reset it first");
+        if (rows > S.max_pos)
+            fail("generate_additive: " + std::to_string(rows) + " rows exceed the session's " +
+                 std::to_string(S.max_pos) + " positions");
+        const auto& c = S.dec->c;
+        const size_t bytes = (size_t)rows * c.d * 4;
+        if (S.additive.bytes < bytes) {
+            // The captured step holds the old buffer.
+            drop_graph(S);
+            S.additive.alloc(bytes);
+        }
+        S.additive.upload(audio, bytes);
+        struct Off {
+            SessionImpl& S;
+            ~Off() { S.additive_rows = 0; }
+        } off{S};
+        S.additive_rows = rows;
+        prefill_common(session, n, nullptr, prompt, nullptr, S.additive.as<float>());
+        // The choice after the prompt, then one per row n..rows-1.
+        return generate_common(session, rows - n + 1, stop, n_stop, out, nullptr, nullptr);
+    });
+}
+
+int trit_hip_prefix_new(const TritHipDecoder* decoder, const int32_t* tokens, int n, int flags, TritHipPrefix** out) {
+    return guard(-1, [&] {
+        if (!decoder || !out) fail("prefix: decoder or out is NULL");
+        if (n < 0) fail("prefix: negative token count");
+        if (n && !tokens) fail("prefix: tokens is NULL");
+        auto P = std::make_unique<TritHipPrefix>();
+        P->dec = decoder->impl;
+        P->tokens.assign(tokens, tokens + n);
+        const auto& c = decoder->impl->c;
+        if (n) {
+            auto* T = new TritHipSession();
+            std::unique_ptr<TritHipSession> own(T);
+            init_session(T->impl, decoder->impl, n, flags);
+            prefill_common(T, n, nullptr, tokens, nullptr);
+            SessionImpl& S = T->impl;
+            const size_t es = S.kv32 ? 4 : 2, run = (size_t)n * c.head_dim * es;
+            const size_t bytes = run * c.layers * c.kv_heads;
+            P->keys.alloc(bytes);
+            P->values.alloc(bytes);
+            // The session holds exactly n positions: its caches are the prefix's.
+            TRIT_HIP(hipMemcpy(P->keys.ptr, S.kcache.ptr, bytes, hipMemcpyDeviceToDevice));
+            TRIT_HIP(hipMemcpy(P->values.ptr, S.vcache.ptr, bytes, hipMemcpyDeviceToDevice));
+            P->exact = S.exact;
+            P->kv32 = S.kv32;
+        } else {
+            // The session flags' modes, as init_session reads them.
+            P->exact = (flags & TRIT_HIP_EXACT) != 0 || (flags & TRIT_HIP_TREE_SUMS) == 0;
+            P->kv32 = (flags & (TRIT_HIP_EXACT | TRIT_HIP_KV_F32)) != 0;
+        }
+        *out = P.release();
+        return 0;
+    });
+}
+
+void trit_hip_prefix_free(TritHipPrefix* prefix) { delete prefix; }
+
+int trit_hip_session_prefill_prefixed(TritHipSession* session, const TritHipPrefix* prefix, const int32_t* tokens,
+                                      int n, float* logits) {
+    return guard(-1, [&] {
+        if (!session || !prefix || !tokens) fail("prefill_prefixed: session, prefix or tokens is NULL");
+        SessionImpl& S = session->impl;
+        check_usable(S);
+        if (prefix->dec != S.dec) fail("prefill_prefixed: the prefix belongs to another decoder");
+        if (prefix->exact != S.exact || prefix->kv32 != S.kv32)
+            fail("prefill_prefixed: the prefix was made with other session flags");
+        if (S.host_pos != 0) fail("prefill_prefixed: the session holds positions; reset it first");
+        const int p = (int)prefix->tokens.size();
+        // Trit takes the prefix only for a longer prompt that starts with it.
+        const bool take = n > p && std::equal(prefix->tokens.begin(), prefix->tokens.end(), tokens);
+        if (!take || p == 0) return prefill_common(session, n, logits, tokens, nullptr);
+        if (n > S.max_pos)
+            fail("prefill: " + std::to_string(n) + " positions exceed the session's " + std::to_string(S.max_pos));
+        const auto& c = S.dec->c;
+        const size_t es = S.kv32 ? 4 : 2, run = (size_t)p * c.head_dim * es;
+        const size_t pitch = (size_t)S.max_pos * c.head_dim * es;
+        hipStream_t s = stream();
+        TRIT_HIP(hipMemcpy2DAsync(S.kcache.ptr, pitch, prefix->keys.ptr, run, run, (size_t)c.layers * c.kv_heads,
+                                  hipMemcpyDeviceToDevice, s));
+        TRIT_HIP(hipMemcpy2DAsync(S.vcache.ptr, pitch, prefix->values.ptr, run, run, (size_t)c.layers * c.kv_heads,
+                                  hipMemcpyDeviceToDevice, s));
+        TRIT_HIP(hipStreamSynchronize(s));
+        State h{};
+        TRIT_HIP(hipMemcpy(&h, S.state.ptr, sizeof(State), hipMemcpyDeviceToHost));
+        h.pos = p;
+        TRIT_HIP(hipMemcpy(S.state.ptr, &h, sizeof(State), hipMemcpyHostToDevice));
+        S.host_pos = p;
+        return prefill_common(session, n - p, logits, tokens + p, nullptr);
     });
 }
 

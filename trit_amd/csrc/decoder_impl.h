@@ -40,6 +40,16 @@ struct DecoderImpl {
     // The head in the persistent step's tiled f16 layout, made on first use.
     mutable DeviceMemory step_head;
     mutable std::once_flag step_head_once;
+    // Per layer, d scales on the normed MLP input (set_ffn_scales); a
+    // counter of their changes (sessions rebuild what depends on them).
+    DeviceMemory ffn_scales;
+    bool has_ffn_scales = false;
+    int ffn_version = 0;
+    // Granite's multipliers (1, and 0 for the attention's, elsewhere).
+    bool granite() const {
+        return c.embedding_multiplier != 1.0f || c.attention_multiplier != 0.0f || c.residual_multiplier != 1.0f ||
+               c.logits_scaling != 1.0f;
+    }
 };
 
 struct SessionImpl {
@@ -51,6 +61,13 @@ struct SessionImpl {
     DeviceMemory x, qkv, att, hid, inv, normed, logits, state, tokens_in, tokens_out, partials;
     DeviceMemory att_part, att_arrived;  // split attention: chunk partials, per (row, kv head) counters
     DeviceMemory gemm_scratch;           // quantized rows of the matrix-core products
+    DeviceMemory xn;                     // rows x d: the normed MLP input, a residual branch
+    // generate_additive: rows x d f32 added to each input, by position.
+    DeviceMemory additive;
+    int additive_rows = 0;
+    // What the captured step was built with.
+    int graph_ffn_version = -1;
+    bool graph_additive = false;
     int max_splits = 0;
     int host_pos = 0;
     hipGraphExec_t graph = nullptr;

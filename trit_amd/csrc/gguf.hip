@@ -426,6 +426,11 @@ int trit_hip_decoder_from_gguf(const char* path, const char* prefix, TritHipLmCo
         c.vocab = num("vocab_size");
         c.eps = (float)real("rms_norm_eps", 1e-6);
         c.rope_base = (float)real("rope_theta", 1e6);
+        // Granite's multipliers where the file has them (granite_speech.rs:33-36).
+        c.embedding_multiplier = (float)real("embedding_multiplier", 1.0);
+        c.attention_multiplier = (float)real("attention_multiplier", 0.0);
+        c.residual_multiplier = (float)real("residual_multiplier", 1.0);
+        c.logits_scaling = (float)real("logits_scaling", 1.0);
         const GgufValue* tie_v = g.get(std::string(pre) + ".tie_word_embeddings");
         const bool tie = !(tie_v && tie_v->kind == GgufValue::B && !tie_v->b);
         c.qk_norm = g.tensor("dec.blocks.0.attn.q_norm.weight") || g.tensor("dec.layers.0.attn.q_norm.weight");

@@ -29,7 +29,18 @@ class TritError(RuntimeError):
 
 class LmConfig(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("d", "ffn", "layers", "heads", "kv_heads", "head_dim", "vocab")] + [
-        ("eps", C.c_float), ("rope_base", C.c_float), ("qk_norm", C.c_int)]
+        ("eps", C.c_float), ("rope_base", C.c_float), ("qk_norm", C.c_int),
+        ("embedding_multiplier", C.c_float), ("attention_multiplier", C.c_float),
+        ("residual_multiplier", C.c_float), ("logits_scaling", C.c_float)]
+
+    @classmethod
+    def of(cls, cfg: dict) -> "LmConfig":
+        """From a config dict; Granite's keys as in causal_lm.rs:58-61
+        (missing: 1, and no attention multiplier)."""
+        return cls(cfg["d"], cfg["ffn"], cfg["layers"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"],
+                   cfg["vocab"], cfg["eps"], cfg["rope_base"], int(cfg.get("qk_norm", 1)),
+                   cfg.get("embedding_multiplier", 1.0), cfg.get("attention_multiplier") or 0.0,
+                   cfg.get("residual_multiplier", 1.0), cfg.get("logits_scaling", 1.0))
 
 
 def lib():
@@ -59,6 +70,11 @@ def lib():
             "trit_hip_layer_free": (None, [p]),
             "trit_hip_decoder_new": (i, [C.POINTER(LmConfig), p, p, p, p, pp]),
             "trit_hip_decoder_free": (None, [p]),
+            "trit_hip_decoder_set_ffn_scales": (i, [p, p]),
+            "trit_hip_session_generate_additive": (i, [p, p, i, p, i, p, i, p]),
+            "trit_hip_prefix_new": (i, [p, p, i, i, pp]),
+            "trit_hip_prefix_free": (None, [p]),
+            "trit_hip_session_prefill_prefixed": (i, [p, p, p, i, p]),
             "trit_hip_session_new": (i, [p, i, i, pp]),
             "trit_hip_session_prefill": (i, [p, p, i, p]),
             "trit_hip_session_prefill_rows": (i, [p, p, i, p]),
@@ -203,8 +219,7 @@ class CausalLm:
     """The decoder on the device (src/models/parts/causal_lm.rs:93-481)."""
 
     def __init__(self, cfg: dict, linears, norms, embed: Dense, head: Dense | None = None):
-        c = LmConfig(cfg["d"], cfg["ffn"], cfg["layers"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"],
-                     cfg["vocab"], cfg["eps"], cfg["rope_base"], int(cfg.get("qk_norm", 1)))
+        c = LmConfig.of(cfg)
         self.cfg = cfg
         arr = (C.c_void_p * len(linears))(*[l.h for l in linears])
         norms = np.ascontiguousarray(norms, np.float32)
@@ -223,18 +238,50 @@ class CausalLm:
                                                C.byref(c), C.byref(out)))
         self.h = out
         self.cfg = dict(d=c.d, ffn=c.ffn, layers=c.layers, heads=c.heads, kv_heads=c.kv_heads,
-                        head_dim=c.head_dim, vocab=c.vocab, eps=c.eps, rope_base=c.rope_base, qk_norm=c.qk_norm)
+                        head_dim=c.head_dim, vocab=c.vocab, eps=c.eps, rope_base=c.rope_base, qk_norm=c.qk_norm,
+                        embedding_multiplier=c.embedding_multiplier,
+                        attention_multiplier=c.attention_multiplier or None,
+                        residual_multiplier=c.residual_multiplier, logits_scaling=c.logits_scaling)
         return self
 
     def session(self, max_positions, flags=0):
         return Session(self, max_positions, flags)
 
-    def generate(self, prompt, max_new, stop=(), flags=0):
-        """CausalLm::generate without a prefix (causal_lm.rs:217-249)."""
+    def generate(self, prompt, max_new, stop=(), flags=0, prefix=None):
+        """CausalLm::generate (causal_lm.rs:217-249); `prefix` a Prefix of
+        this decoder made with the same flags, or None."""
         s = self.session(len(prompt) + max_new + 1, flags)
         try:
-            s.prefill(prompt)
+            if prefix is None:
+                s.prefill(prompt, want_logits=False)
+            else:
+                s.prefill_prefixed(prefix, prompt, want_logits=False)
             return s.generate(max_new, stop)
+        finally:
+            s.free()
+
+    def prefix(self, tokens, flags=0):
+        """CausalLm::prefix (causal_lm.rs:200-215): the keys and values of a
+        prompt start that many calls share."""
+        return Prefix(self, tokens, flags)
+
+    def set_ffn_scales(self, scales):
+        """CausalLm::set_ffn_scales (causal_lm.rs:304-307): layers x d
+        scales on each layer's normed MLP input, or None."""
+        if scales is None:
+            check(lib().trit_hip_decoder_set_ffn_scales(self.h, None))
+            return
+        s = np.ascontiguousarray(scales, np.float32)
+        assert s.size == self.cfg["layers"] * self.cfg["d"]
+        check(lib().trit_hip_decoder_set_ffn_scales(self.h, ptr(s)))
+
+    def generate_additive(self, prompt, audio, stop=(), flags=0):
+        """CausalLm::generate_additive (causal_lm.rs:313-345): greedy tokens
+        with audio rows (rows x d) added to every input."""
+        audio = np.ascontiguousarray(audio, np.float32).reshape(-1, self.cfg["d"])
+        s = self.session(max(audio.shape[0], 1), flags)
+        try:
+            return s.generate_additive(prompt, audio, stop)
         finally:
             s.free()
 
@@ -299,6 +346,28 @@ class Gguf:
             pass
 
 
+class Prefix:
+    """Prefix (causal_lm.rs:118-122,200-215) on the device."""
+
+    def __init__(self, lm: CausalLm, tokens, flags=0):
+        self.lm = lm
+        self.tokens = np.ascontiguousarray(tokens, np.int32)
+        out = C.c_void_p()
+        check(lib().trit_hip_prefix_new(lm.h, ptr(self.tokens), self.tokens.size, flags, C.byref(out)))
+        self.h = out
+
+    def free(self):
+        if self.h:
+            lib().trit_hip_prefix_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class Session:
     def __init__(self, lm: CausalLm, max_positions, flags=0):
         self.lm = lm
@@ -317,6 +386,25 @@ class Session:
         logits = np.empty(self.lm.cfg["vocab"], np.float32) if want_logits else None
         check(lib().trit_hip_session_prefill_rows(self.h, ptr(r), r.shape[0], ptr(logits)))
         return logits
+
+    def prefill_prefixed(self, prefix: Prefix, tokens, want_logits=True):
+        """The prompt of a fresh session from `prefix`'s caches when it
+        starts with the prefix's tokens (trit_hip_session_prefill_prefixed)."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        logits = np.empty(self.lm.cfg["vocab"], np.float32) if want_logits else None
+        check(lib().trit_hip_session_prefill_prefixed(self.h, prefix.h, ptr(t), t.size, ptr(logits)))
+        return logits
+
+    def generate_additive(self, prompt, audio, stop=()):
+        """trit_hip_session_generate_additive on a fresh session."""
+        t = np.ascontiguousarray(prompt, np.int32)
+        audio = np.ascontiguousarray(audio, np.float32).reshape(-1, self.lm.cfg["d"])
+        stop = np.ascontiguousarray(np.array(stop, np.int32).reshape(-1))
+        rows = audio.shape[0]
+        out = np.empty(max(rows - t.size + 1, 1), np.int32)
+        n = check(lib().trit_hip_session_generate_additive(self.h, ptr(t), t.size, ptr(audio), rows,
+                                                           ptr(stop) if stop.size else None, stop.size, ptr(out)))
+        return out[:n].copy()
 
     def generate(self, max_new, stop=()):
         """Greedy tokens (trit_hip_session_generate); `self.persistent` then
