@@ -255,6 +255,43 @@ def config_lines(H, sweeps=10):
         note="gemm_us: the MFMA kernels (event-stamped); call_us adds the activation quantization pass; "
              "valu_frac: the exact f32 group chain's vector operations against the vector ALU peak")
 
+    # Beam decode: one Whisper large-v3 decoder layer's step for 5 beams --
+    # the f16 products of 5 rows (self q/k/v/o and cross q/o 1280 x 1280,
+    # fc1 5120 x 1280, fc2 1280 x 5120, biases) over 8 copies of the layer
+    # (367 MB), and the self-attention of the 5 beams over 448 keys each.
+    shapes = [(1280, 1280)] * 6 + [(5120, 1280), (1280, 5120)]
+    host = [(synth.f16_bits((synth.activations(synth.seed_for(0, 60 + i), nn, kk) * 0.02).astype(np.float32)),
+             synth.activations(synth.seed_for(0, 70 + i), 1, nn)[0]) for i, (nn, kk) in enumerate(shapes)]
+    f16s = [hip.Dense.f16(wb, bias) for _ in range(8) for wb, bias in host]
+    del host
+    ms = timed_sweeps(H, stream, f16s, xbuf, ybuf, 5, sweeps)
+    per_layer_ms = ms * len(shapes)
+    wbytes = sum(nn * kk * 2 + nn * 4 for nn, kk in shapes) + sum(5 * (nn + kk) * 4 for nn, kk in shapes)
+    del f16s
+    beams, tk, d, heads = 5, 448, 1280, 20
+    kvb = tk * d * 4
+    kv = H.malloc(2 * beams * kvb)
+    H.upload(kv, synth.activations(synth.seed_for(0, 80), 2 * beams * tk, d))
+    steps_dev = hip.lib().trit_hip_attention_steps_device
+    keys = (C.c_void_p * beams)(*[kv.value + b * kvb for b in range(beams)])
+    values = (C.c_void_p * beams)(*[kv.value + (beams + b) * kvb for b in range(beams)])
+    tks = (C.c_int * beams)(*([tk] * beams))
+    a, b = H.event(), H.event()
+    hip.check(steps_dev(xbuf, d, keys, values, tks, beams, d, heads, heads, ybuf, stream))
+    H.record(a, stream)
+    for _ in range(sweeps):
+        hip.check(steps_dev(xbuf, d, keys, values, tks, beams, d, heads, heads, ybuf, stream))
+    H.record(b, stream)
+    att_ms = H.elapsed_ms(a, b) / sweeps
+    H.L.hipFree(kv)
+    att_bytes = 2 * beams * kvb
+    out["beam_step_whisper_large_v3_5beams"] = dict(
+        products_us=round(per_layer_ms * 1e3, 2), products_bytes=wbytes, products_gb_s=gbs(wbytes, per_layer_ms),
+        products_frac=round(gbs(wbytes, per_layer_ms) / HBM_PEAK_GBS, 4),
+        attention_us=round(att_ms * 1e3, 2), attention_bytes=att_bytes, attention_gb_s=gbs(att_bytes, att_ms),
+        note="per decoder layer: eight f16 products of 5 rows (kernel time, event-stamped), and "
+             "trit_hip_attention_steps_device over 448 f32 keys a beam (back-to-back calls, host launch included)")
+
     # C5 end to end: one decoder layer of the prefill's shape (hidden 2048,
     # 16/8 heads x 128, SwiGLU 3072) over the 1564-row prompt: the MFMA
     # products, q/k norm + rotary + cache append, causal GQA attention on

@@ -264,6 +264,25 @@ void trit_hip_session_free(TritHipSession *session);
 int trit_hip_attention(const float *q, int qs, const float *k, const float *v, int kvs, int tq, int tk, int heads,
                        int kv_heads, int hd, int causal, int flags, float *out);
 
+/* The self-attention of one decoder step for several sequences (beams):
+ * layers::attention_steps (src/layers.rs:505-562). Sequence b asks its one
+ * query (row b of q, stride qs floats, heads * hd values, hd = d / heads)
+ * over its own tk[b] keys and values (keys[b], values[b]: tk[b] rows of
+ * kv_heads * hd f32 each, the rows of Trit's per-sequence caches); out is
+ * sequences x d. Trit's orders and sums, bit for bit (the values of
+ * trit_hip_attention with EXACT on each sequence alone). 1 to 32
+ * sequences; head_dim a multiple of 8 up to 256; up to 16000 keys. Host
+ * memory. */
+int trit_hip_attention_steps(const float *q, int qs, const float *const *keys, const float *const *values,
+                             const int *tk, int sequences, int d, int heads, int kv_heads, float *out);
+/* The same on device memory (q, out and each keys[b] / values[b], 16-byte
+ * aligned; the pointer arrays and tk in host memory), queued on `stream`
+ * (a hipStream_t; NULL: the calling thread's stream) without waiting.
+ * Allocates nothing. */
+int trit_hip_attention_steps_device(const float *q, int qs, const float *const *keys, const float *const *values,
+                                    const int *tk, int sequences, int d, int heads, int kv_heads, float *out,
+                                    void *stream);
+
 /* ---- GGUF files (reference src/models/gguf/mod.rs:130-300) ------------- */
 
 typedef struct TritHipGguf TritHipGguf;

@@ -231,6 +231,23 @@ def attention(q, k, v, heads, kv_heads, hd, causal=True):
     return out
 
 
+def attention_steps(q, caches, heads, kv_heads):
+    """layers::attention_steps (src/layers.rs:505-562). For sequence b it
+    makes the calls attention_with (src/layers.rs:442-504) makes for one
+    query row that sees every key: qh = q * (1/sqrt(hd)), matmul_nn_into for
+    the scores, softmax_rows over all tk keys, matmul_nn_into for p.V. So
+    each output row is the oracle's attention of that row alone over the
+    sequence's keys (tq = 1; causal or not, the row sees all tk keys)."""
+    q = np.ascontiguousarray(q, np.float32)
+    kvs = np.asarray(caches[0][0]).shape[1]
+    hd = kvs // kv_heads
+    d = heads * hd
+    out = np.empty((q.shape[0], d), np.float32)
+    for b, (k, v) in enumerate(caches):
+        out[b] = attention(q[b:b + 1, :d], k, v, heads, kv_heads, hd, causal=False)[0]
+    return out
+
+
 def exp(x: float) -> float:
     return lib().or_exp(x)
 

@@ -1001,6 +1001,79 @@ __global__ void advance_kernel(State* st, int rows) {
     st->pos += rows;
 }
 
+// The sequences of one decoder step with several sequences (beams): each
+// its own keys and values, tk rows of kv_heads * hd f32 (the row layout of
+// the reference's per-sequence caches).
+constexpr int STEPS_MAX = 32;
+struct StepsSeq {
+    const float* k;
+    const float* v;
+    int tk;
+};
+struct StepsTable {
+    StepsSeq s[STEPS_MAX];
+};
+
+// layers::attention_steps (src/layers.rs:505-562): block (h, b) is query
+// head h of sequence b, its one query over all of the sequence's keys, in
+// attention_kernel's orders (qh = q * (1/sqrt(hd)); score_j a fused chain
+// over e; max; e_j = exp(s_j - max); a serial sum over j; p_j = e_j *
+// (1/sum); out_e a fused chain of p_j * v_je over j). out row b holds
+// heads * hd values at stride d.
+__global__ __launch_bounds__(ATT_THREADS) void attention_steps_kernel(const float* __restrict__ q, int qs,
+                                                                      StepsTable table, int heads, int kvh, int hd,
+                                                                      int d, float* __restrict__ out) {
+    extern __shared__ float sm[];  // qh[MAX_HD] | probs[tk] | red[ATT_THREADS]
+    const int h = blockIdx.x, b = blockIdx.y;
+    const StepsSeq seq = table.s[b];
+    const int tk = seq.tk, stride = kvh * hd;
+    const int g = h / (heads / kvh);
+    float* qh = sm;
+    float* probs = sm + MAX_HD;
+    float* red = probs + tk;
+    const float scale = 1.0f / __builtin_sqrtf((float)hd);
+    for (int e = threadIdx.x; e < hd; e += ATT_THREADS) qh[e] = q[(size_t)b * qs + (size_t)h * hd + e] * scale;
+    __syncthreads();
+    float best = -INFINITY;
+    for (int j = threadIdx.x; j < tk; j += ATT_THREADS) {
+        const float* kr = seq.k + (size_t)j * stride + (size_t)g * hd;
+        float acc = 0.0f;
+        for (int e = 0; e < hd; e += 8) {
+            float kv[8];
+            kv_load8(kr + e, kv);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(qh[e + u], kv[u], acc);
+        }
+        probs[j] = acc;
+        best = __builtin_fmaxf(best, acc);
+    }
+    red[threadIdx.x] = best;
+    __syncthreads();
+    for (int s = ATT_THREADS / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) red[threadIdx.x] = __builtin_fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
+        __syncthreads();
+    }
+    const float mx = red[0];
+    __syncthreads();
+    for (int j = threadIdx.x; j < tk; j += ATT_THREADS) probs[j] = exp_trit(probs[j] - mx);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float sum = 0.0f;
+        for (int j = 0; j < tk; ++j) sum = sum + probs[j];
+        red[0] = sum;
+    }
+    __syncthreads();
+    const float inv = 1.0f / red[0];
+    for (int j = threadIdx.x; j < tk; j += ATT_THREADS) probs[j] = probs[j] * inv;
+    __syncthreads();
+    const float* V = seq.v + (size_t)g * hd;
+    for (int e = threadIdx.x; e < hd; e += ATT_THREADS) {
+        float acc = 0.0f;
+        for (int j = 0; j < tk; ++j) acc = __builtin_fmaf(probs[j], V[(size_t)j * stride + e], acc);
+        out[(size_t)b * d + (size_t)h * hd + e] = acc;
+    }
+}
+
 // Rows of keys and values (tk x kvs floats each, head g at g * hd) into the
 // cache layout [g][position][hd] of type KV.
 template <typename KV>
@@ -1801,6 +1874,81 @@ int trit_hip_session_position(const TritHipSession* session) {
 }
 
 void trit_hip_session_free(TritHipSession* session) { delete session; }
+
+// Checks of attention_steps' arguments; returns head_dim and the shared
+// memory of the largest sequence.
+static int steps_check(const float* q, int qs, const float* const* keys, const float* const* values, const int* tk,
+                       int sequences, int d, int heads, int kv_heads, const float* out, size_t* lds) {
+    if (!q || !keys || !values || !tk || !out) fail("attention_steps: q, keys, values, tk or out is NULL");
+    if (sequences <= 0 || sequences > STEPS_MAX) fail("attention_steps: 1 to 32 sequences");
+    if (heads <= 0 || kv_heads <= 0 || heads % kv_heads)
+        fail("attention_steps: the query heads do not share the key heads evenly");
+    if (d <= 0 || d % heads) fail("attention_steps: d is not a multiple of the heads");
+    const int hd = d / heads;
+    if (hd > MAX_HD || hd % 8) fail("attention_steps: head_dim must be a multiple of 8 and at most 256");
+    if (qs < d) fail("attention_steps: the query stride is shorter than d");
+    int most = 0;
+    for (int b = 0; b < sequences; ++b) {
+        if (tk[b] <= 0) fail("attention_steps: sequence " + std::to_string(b) + " has no keys");
+        if (!keys[b] || !values[b]) fail("attention_steps: sequence " + std::to_string(b) + " has NULL keys or values");
+        most = std::max(most, tk[b]);
+    }
+    *lds = (size_t)(MAX_HD + most + ATT_THREADS) * 4;
+    if (*lds > 64 * 1024) fail("attention_steps: more keys than one block's shared memory holds (16000)");
+    return hd;
+}
+
+int trit_hip_attention_steps(const float* q, int qs, const float* const* keys, const float* const* values,
+                             const int* tk, int sequences, int d, int heads, int kv_heads, float* out) {
+    return guard(-1, [&] {
+        size_t lds = 0;
+        const int hd = steps_check(q, qs, keys, values, tk, sequences, d, heads, kv_heads, out, &lds);
+        const size_t kvs = (size_t)kv_heads * hd;
+        size_t rows = 0;
+        for (int b = 0; b < sequences; ++b) rows += (size_t)tk[b];
+        hipStream_t s = stream();
+        const size_t qb = ((size_t)(sequences - 1) * qs + d) * 4, ob = (size_t)sequences * d * 4;
+        DeviceMemory dq(qb), dk(rows * kvs * 4), dv(rows * kvs * 4), dout(ob);
+        TRIT_HIP(hipMemcpyAsync(dq.ptr, q, qb, hipMemcpyHostToDevice, s));
+        StepsTable table{};
+        size_t at = 0;
+        for (int b = 0; b < sequences; ++b) {
+            const size_t bytes = (size_t)tk[b] * kvs * 4;
+            TRIT_HIP(hipMemcpyAsync(dk.as<float>() + at, keys[b], bytes, hipMemcpyHostToDevice, s));
+            TRIT_HIP(hipMemcpyAsync(dv.as<float>() + at, values[b], bytes, hipMemcpyHostToDevice, s));
+            table.s[b] = StepsSeq{dk.as<float>() + at, dv.as<float>() + at, tk[b]};
+            at += (size_t)tk[b] * kvs;
+        }
+        hipLaunchKernelGGL(attention_steps_kernel, dim3(heads, sequences), dim3(ATT_THREADS), lds, s, dq.as<float>(),
+                           qs, table, heads, kv_heads, hd, d, dout.as<float>());
+        TRIT_HIP(hipGetLastError());
+        TRIT_HIP(hipMemcpyAsync(out, dout.ptr, ob, hipMemcpyDeviceToHost, s));
+        TRIT_HIP(hipStreamSynchronize(s));
+        return 0;
+    });
+}
+
+int trit_hip_attention_steps_device(const float* q, int qs, const float* const* keys, const float* const* values,
+                                    const int* tk, int sequences, int d, int heads, int kv_heads, float* out,
+                                    void* stream_) {
+    return guard(-1, [&] {
+        size_t lds = 0;
+        const int hd = steps_check(q, qs, keys, values, tk, sequences, d, heads, kv_heads, out, &lds);
+        const size_t kvs = (size_t)kv_heads * hd;
+        StepsTable table{};
+        for (int b = 0; b < sequences; ++b) {
+            // float4 loads of each key row.
+            if (((uintptr_t)keys[b] | (uintptr_t)values[b]) % 16 || kvs % 4)
+                fail("attention_steps: keys and values must be 16-byte aligned");
+            table.s[b] = StepsSeq{keys[b], values[b], tk[b]};
+        }
+        hipStream_t s = stream_ ? (hipStream_t)stream_ : stream();
+        hipLaunchKernelGGL(attention_steps_kernel, dim3(heads, sequences), dim3(ATT_THREADS), lds, s, q, qs, table,
+                           heads, kv_heads, hd, d, out);
+        TRIT_HIP(hipGetLastError());
+        return 0;
+    });
+}
 
 int trit_hip_attention(const float* q, int qs, const float* k, const float* v, int kvs, int tq, int tk, int heads,
                        int kv_heads, int hd, int causal, int flags, float* out) {

@@ -19,14 +19,21 @@ constexpr int THREADS = 256;
 constexpr int MAXF = 8;
 constexpr int ROWS = THREADS / 16;  // rows per block step
 
-template <int S8>  // S8 = 16-byte loads per chain (k / 128); 0: any k (2-byte loads)
+// S8 = 16-byte loads per chain (k / 128); 0: any k (2-byte loads). LDS:
+// the rows are staged in shared memory; else (m x k above 64 KB) every
+// block reads them from global memory, where they stay in the caches.
+template <int S8, bool LDS>
 __global__ __launch_bounds__(THREADS) void f16_kernel(const uint16_t* __restrict__ w, const float* __restrict__ bias,
                                                       int n, int k, GemvArgs a) {
-    extern __shared__ __align__(16) float xs[];  // m x k
+    extern __shared__ __align__(16) float xs_lds[];  // m x k
     if (a.skip && *a.skip) return;
     const int m = a.m;
-    for (int i = threadIdx.x; i < m * k; i += THREADS) xs[i] = a.x[i];
-    __syncthreads();
+    const float* xs = a.x;
+    if constexpr (LDS) {
+        for (int i = threadIdx.x; i < m * k; i += THREADS) xs_lds[i] = a.x[i];
+        __syncthreads();
+        xs = xs_lds;
+    }
     const int lane = threadIdx.x & 15;
     const int s_count = k / 16;
     const int steps = (n + ROWS - 1) / ROWS;
@@ -98,23 +105,21 @@ __global__ void row_kernel(const uint16_t* __restrict__ w, int k, int index, flo
 void gemv_f16(const Layer& L, const GemvArgs& a, hipStream_t s) {
     if (a.m < 1 || a.m > MAXF) fail("f16 gemv: 1 to 8 rows per call");
     if (a.epilogue == EPI_SILU_PAIR) fail("f16 gemv: no SwiGLU pair epilogue");
-    const size_t lds = (size_t)a.m * L.k * 4;
-    if (lds > 64 * 1024) fail("f16 gemv: m x k is too large for one block's shared memory");
+    const size_t bytes = (size_t)a.m * L.k * 4;
+    const bool in_lds = bytes <= 64 * 1024;
+    const size_t lds = in_lds ? bytes : 0;
     const int steps = (L.n + ROWS - 1) / ROWS;
     const int grid = steps < 4096 ? steps : 4096;
     const uint16_t* w = L.codes.as<uint16_t>();
     const float* b = L.bias.as<float>();
-    switch (L.k) {
-        case 1024:
-            launch_timed(a, f16_kernel<8>, dim3(grid), dim3(THREADS), lds, s, w, b, L.n, L.k, a);
-            break;
-        case 2048:
-            launch_timed(a, f16_kernel<16>, dim3(grid), dim3(THREADS), lds, s, w, b, L.n, L.k, a);
-            break;
-        default:
-            launch_timed(a, f16_kernel<0>, dim3(grid), dim3(THREADS), lds, s, w, b, L.n, L.k, a);
-            break;
-    }
+    if (!in_lds)
+        launch_timed(a, f16_kernel<0, false>, dim3(grid), dim3(THREADS), lds, s, w, b, L.n, L.k, a);
+    else if (L.k == 1024)
+        launch_timed(a, f16_kernel<8, true>, dim3(grid), dim3(THREADS), lds, s, w, b, L.n, L.k, a);
+    else if (L.k == 2048)
+        launch_timed(a, f16_kernel<16, true>, dim3(grid), dim3(THREADS), lds, s, w, b, L.n, L.k, a);
+    else
+        launch_timed(a, f16_kernel<0, true>, dim3(grid), dim3(THREADS), lds, s, w, b, L.n, L.k, a);
     TRIT_HIP(hipGetLastError());
 }
 

@@ -93,6 +93,8 @@ def lib():
             "trit_hip_gguf_meta_str": (i, [p, C.c_char_p, C.POINTER(C.c_char_p)]),
             "trit_hip_decoder_from_gguf": (i, [C.c_char_p, C.c_char_p, C.POINTER(LmConfig), pp]),
             "trit_hip_attention": (i, [p, i, p, p, i, i, i, i, i, i, i, i, p]),
+            "trit_hip_attention_steps": (i, [p, i, p, p, p, i, i, i, i, p]),
+            "trit_hip_attention_steps_device": (i, [p, i, p, p, p, i, i, i, i, p, p]),
         }
         for name, (res, args) in sig.items():
             if not hasattr(L, name):
@@ -130,6 +132,26 @@ def attention(q, k, v, heads, kv_heads, hd, causal=True, flags=0):
     out = np.empty((q.shape[0], heads * hd), np.float32)
     check(lib().trit_hip_attention(ptr(q), q.shape[1], ptr(k), ptr(v), k.shape[1], q.shape[0], k.shape[0], heads,
                                    kv_heads, hd, int(causal), flags, ptr(out)))
+    return out
+
+
+def attention_steps(q, caches, heads, kv_heads):
+    """layers::attention_steps (src/layers.rs:505-562) on the device: row b
+    of q (sequences x qs) asks sequence b's cache (keys, values), each
+    tk_b x (kv_heads * hd) f32; returns sequences x d, d = heads * hd."""
+    q = np.ascontiguousarray(q, np.float32)
+    sequences = q.shape[0]
+    assert len(caches) == sequences
+    ks = [np.ascontiguousarray(k, np.float32) for k, _ in caches]
+    vs = [np.ascontiguousarray(v, np.float32) for _, v in caches]
+    kvs = ks[0].shape[1]
+    d = kvs // kv_heads * heads
+    keys = (C.c_void_p * sequences)(*[k.ctypes.data for k in ks])
+    values = (C.c_void_p * sequences)(*[v.ctypes.data for v in vs])
+    tk = (C.c_int * sequences)(*[k.shape[0] for k in ks])
+    out = np.empty((sequences, d), np.float32)
+    check(lib().trit_hip_attention_steps(ptr(q), q.shape[1], keys, values, tk, sequences, d, heads, kv_heads,
+                                         ptr(out)))
     return out
 
 
