@@ -202,7 +202,8 @@ def test_q4_k(gpu, n, k, m):
     assert bits_equal(got, ref)
 
 
-@pytest.mark.parametrize("n,k,m", [(4096, 1024, 1), (1000, 1024, 3), (300, 2048, 2), (77, 160, 5)])
+@pytest.mark.parametrize("n,k,m", [(4096, 1024, 1), (1000, 1024, 3), (300, 2048, 2), (77, 160, 5), (300, 384, 8),
+                                   (65, 3072, 6), (100, 8192, 3)])
 def test_f16(gpu, n, k, m):
     print(f"case f16 n={n} k={k} m={m}", flush=True)
     w = synth.f16_bits(synth.activations(51 + n, n, k) * 0.02).reshape(n, k)
