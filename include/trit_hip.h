@@ -51,14 +51,18 @@ enum {
     TRIT_HIP_INT8 = 2,    /* Trit int8: one f32 scale per row and 128 inputs  */
     TRIT_HIP_TERNARY = 3, /* codes 0..2, w = scale * (code - 1), 128 groups   */
     TRIT_HIP_Q4_K = 4,    /* ggml Q4_K super-blocks, run as Trit's Q8_0 codes */
-    TRIT_HIP_F16 = 5      /* f16 weights, f32 math (token tables, the head)   */
+    TRIT_HIP_F16 = 5,     /* f16 weights, f32 math (token tables, the head)   */
+    TRIT_HIP_F32 = 6,     /* f32 weights, f32 math                            */
+    TRIT_HIP_Q8 = 7       /* int8 storage, f32 scale per 32, f32 math         */
 };
 
 /* ggml Q8_0 weights as stored in GGUF: n*k/32 blocks of 34 bytes (f16 d,
  * little endian, then 32 int8 codes), row-major n x k. bias: n floats or
  * NULL. Replaces Dense::q8_0 + Int8::from_q8_0
- * (reference src/cpu/gemm.rs:225-247, src/cpu/int8.rs:256-289,
- * src/cpu/tensors.rs:282-305). k % 32 == 0. */
+ * (reference src/cpu/gemm.rs:225-247, src/cpu/int8.rs:234-236,256-289,
+ * src/cpu/tensors.rs:282-305): int8 activations when n % 32 == 0, else
+ * (a shape Trit's int8 kernels refuse) the codes with f32 math, as
+ * trit_hip_layer_q8_0_f32. k % 32 == 0. */
 int trit_hip_layer_q8_0(int n, int k, const void *blocks, const float *bias, TritHipLayer **out);
 
 /* Trit int8 weights: codes row-major n x k, scales n x (k/128).
@@ -83,6 +87,24 @@ int trit_hip_layer_ternary_base3(int n, int k, const uint8_t *packed, const floa
  * src/cpu/tensors.rs:263-286); products then run on those codes.
  * k % 256 == 0. */
 int trit_hip_layer_q4_k(int n, int k, const void *blocks, TritHipLayer **out);
+
+/* f32 weights, row-major n x k, f32 math in Trit's 16-lane order.
+ * Replaces Dense::new / Weights::F32 and Dense::table under F32
+ * (reference src/cpu/gemm.rs:190-204,395). k % 16 == 0. */
+int trit_hip_layer_f32(int n, int k, const float *weights, const float *bias, TritHipLayer **out);
+
+/* Int8 storage with f32 math (Weights::Q8, reference src/cpu/gemm.rs:37-44,
+ * 117-187): codes row-major n x k, scales n x (k/32) f32; the product
+ * widens each weight to f32(code) * scale (one rounding) and runs the f32
+ * product. Replaces Q8::quantize's layer and Dense::table under Int8 or
+ * Auto (:396-399). k % 32 == 0. */
+int trit_hip_layer_q8(int n, int k, const int8_t *codes, const float *scales, const float *bias,
+                      TritHipLayer **out);
+
+/* ggml Q8_0 blocks (as trit_hip_layer_q8_0) held with f32 math: Dense::table
+ * under Q8_0 (reference src/cpu/gemm.rs:386-393) -- a token table or an
+ * untied head never takes int8 activations. k % 32 == 0. */
+int trit_hip_layer_q8_0_f32(int n, int k, const void *blocks, const float *bias, TritHipLayer **out);
 
 /* f16 weights (bits), row-major n x k. Replaces Dense::half / Dense::table
  * with F16 weights (reference src/cpu/gemm.rs:206-221,383-409). k % 16 == 0. */

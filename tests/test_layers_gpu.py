@@ -216,6 +216,52 @@ def test_f16(gpu, n, k, m):
     assert np.array_equal(row, w[n // 2].view(np.float16).astype(np.float32))
 
 
+def widened_q8(codes, scales):
+    """widen_q8 (src/cpu/gemm.rs:171-179): f32(code) * its 32-group's scale,
+    one f32 rounding."""
+    return codes.astype(np.float32) * np.repeat(np.asarray(scales, np.float32), 32, axis=1)
+
+
+@pytest.mark.parametrize("n,k,m", [(300, 1024, 1), (77, 160, 5), (1280, 1280, 5), (100, 4096, 8), (4096, 2048, 2),
+                                   (33, 48, 3)])
+def test_f32(gpu, n, k, m):
+    print(f"case f32 n={n} k={k} m={m}", flush=True)
+    w = synth.activations(61 + n, n, k) * np.float32(0.05)
+    bias = synth.activations(62 + n, 1, n)[0]
+    x = synth.activations(63 + m, m, k)
+    layer = gpu.Dense.f32(w, bias)
+    assert bits_equal(layer.forward(x), O.matmul_f32(x, w) + bias)
+    assert np.array_equal(layer.row(n - 1), w[n - 1])
+
+
+@pytest.mark.parametrize("n,k,m", [(300, 1024, 1), (77, 160, 5), (1280, 1280, 5), (96, 4096, 8), (5000, 1024, 1),
+                                   (40, 96, 2)])
+def test_q8_table(gpu, n, k, m):
+    """Weights::Q8 (int8 storage, f32 scale per 32, f32 math)."""
+    print(f"case q8 n={n} k={k} m={m}", flush=True)
+    codes = synth.ints(71 + n, (n, k), -127, 127).astype(np.int8)
+    scales = (np.abs(synth.activations(72 + n, n, k // 32)) * np.float32(0.01)).astype(np.float32)
+    x = synth.activations(73 + m, m, k)
+    layer = gpu.Dense.q8(codes, scales)
+    w = widened_q8(codes, scales)
+    assert bits_equal(layer.forward(x), O.matmul_f32(x, w))
+    assert bits_equal(layer.row(n // 3), w[n // 3])
+
+
+@pytest.mark.parametrize("n,k,m,table", [(100, 256, 3, False), (1000, 1024, 1, True), (64, 512, 4, True)])
+def test_q8_0_f32_math(gpu, n, k, m, table):
+    """Q8_0 blocks with f32 math: a layer whose n is no multiple of 32
+    (Dense::q8_0 outside Int8::fits_group) and a token table (Dense::table
+    under Q8_0): the codes times the widened f16 block scales."""
+    print(f"case q8_0 f32 math n={n} k={k} m={m} table={table}", flush=True)
+    codes, sbits, blocks = q8_layer(synth.seed_for(2, n + k), n, k)
+    x = synth.activations(74 + m, m, k)
+    layer = gpu.Dense.q8_0_f32(n, k, blocks) if table else gpu.Dense.q8_0(n, k, blocks)
+    assert layer.info()["kind"] == gpu.Q8
+    w = widened_q8(codes, sbits.view(np.float16).astype(np.float32).reshape(n, k // 32))
+    assert bits_equal(layer.forward(x), O.matmul_f32(x, w))
+
+
 def test_errors(gpu):
     from trit_amd.hip import TritError
 

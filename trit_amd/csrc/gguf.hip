@@ -300,20 +300,6 @@ const char* decoder_prefix(const GgufFile& g) {
     return nullptr;
 }
 
-// f32 (IEEE binary32) to f16 bits, round to nearest even (as Trit's
-// f32_to_f16, src/cpu/tensors.rs:542-573): the hardware conversion.
-uint16_t f16_bits(float v) {
-    const _Float16 h = (_Float16)v;
-    uint16_t b;
-    std::memcpy(&b, &h, 2);
-    return b;
-}
-
-float f16_value(uint16_t b) {
-    _Float16 h;
-    std::memcpy(&h, &b, 2);
-    return (float)h;
-}
 
 struct LayerOwner {
     std::vector<TritHipLayer*> all;
@@ -463,7 +449,7 @@ int trit_hip_decoder_from_gguf(const char* path, const char* prefix, TritHipLmCo
                 for (uint64_t k = 0; k < n; ++k) {
                     uint16_t h;
                     std::memcpy(&h, b.data() + 2 * k, 2);
-                    dst.push_back(f16_value(h));
+                    dst.push_back(f16_bits_to_f32(h));
                 }
             } else {
                 fail(std::string(path) + ": norm " + name + " is " + t.dtype + "; the loader reads F32 and F16");
@@ -528,7 +514,7 @@ int trit_hip_decoder_from_gguf(const char* path, const char* prefix, TritHipLmCo
                 for (size_t k = 0; k < bits.size(); ++k) {
                     float v;
                     std::memcpy(&v, b.data() + 4 * k, 4);
-                    bits[k] = f16_bits(v);
+                    bits[k] = f32_to_f16_bits(v);
                 }
             } else {
                 fail(std::string(path) + ": " + name + " is " + t.dtype + "; the token table is read as F16 or F32");

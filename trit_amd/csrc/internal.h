@@ -76,15 +76,32 @@ struct DeviceMemory {
     }
 };
 
+// Host f16 conversions, round to nearest even with subnormals, infinities
+// and NaN (Trit's f32_to_f16 / f16_to_f32, src/cpu/tensors.rs:542-595): the
+// compiler's _Float16 conversions.
+inline uint16_t f32_to_f16_bits(float v) {
+    const _Float16 h = (_Float16)v;
+    uint16_t b;
+    __builtin_memcpy(&b, &h, 2);
+    return b;
+}
+inline float f16_bits_to_f32(uint16_t b) {
+    _Float16 h;
+    __builtin_memcpy(&h, &b, 2);
+    return (float)h;
+}
+
 // A layer's weights in device memory. Layouts:
 //  Q8_0, Q4_K (after requantization), INT8: codes int8 row-major n x k;
 //    scales row-major n x (k/group): f16 bits for Q8_0/Q4_K, f32 for INT8.
 //  TERNARY: codes 2 bits each, row-major n x k/4 bytes; in each 16-code
 //    span (4 bytes) byte j holds codes j, 4+j, 8+j, 12+j at bits 0,2,4,6;
 //    scales f32 n x (k/128).
-//  F16: for each row, the 16 lane chains of the 16-lane sum order: element
-//    kk = 16*s + i at [row][i][s] (k/16 values per chain).
-enum Kind { Q8_0 = 1, INT8 = 2, TERNARY = 3, Q4_K = 4, F16 = 5 };
+//  F16, F32, Q8 (f32 math): for each row, the 16 lane chains of the 16-lane
+//    sum order: element kk = 16*s + i at [row][i][s] (k/16 values per
+//    chain; f16 bits, f32, or int8 codes); Q8 scales f32 n x (k/32).
+enum Kind { Q8_0 = 1, INT8 = 2, TERNARY = 3, Q4_K = 4, F16 = 5, F32 = 6, Q8_F32 = 7 };
+inline bool float_kind(int kind) { return kind == F16 || kind == F32 || kind == Q8_F32; }
 
 struct Layer {
     int kind = 0, n = 0, k = 0, group = 0;
@@ -160,8 +177,9 @@ bool gemv_stream(const Layer& L, const GemvArgs& a, hipStream_t s);
 // The one-row Q8_0 decode product (k 1024, 2048 or 3072); false when the
 // shape or kind is not one it takes.
 bool gemv_row(const Layer& L, const GemvArgs& a, hipStream_t s);
-// f16 products, m <= 8.
-void gemv_f16(const Layer& L, const GemvArgs& a, hipStream_t s);
+// Float-math products (F16, F32, Q8), m <= 8; no RMSNorm prologue, no
+// SwiGLU epilogue.
+void gemv_float(const Layer& L, const GemvArgs& a, hipStream_t s);
 // Integer products of any row count on the matrix cores (Q8_0, Q4_K, INT8
 // with n % 128 == 0 and k % 256 == 0). `scratch` holds gemm_scratch_bytes(m, k) bytes of
 // device memory the product may overwrite.
@@ -174,10 +192,11 @@ void layer_forward(const Layer& L, const GemvArgs& a, hipStream_t s);
 // Requantizes Q4_K super-blocks (device bytes) into Q8_0 codes and f16
 // scales in L.codes / L.scales.
 void q4_k_requantize(const uint8_t* blocks, int n, int k, Layer& L, hipStream_t s);
-// Repacks f16 row-major weights (device) into the lane-chain layout.
-void f16_repack(const uint16_t* src, int n, int k, uint16_t* dst, hipStream_t s);
-// Row `index` of an F16 layer as f32 (device out).
-void f16_row(const Layer& L, int index, float* out, hipStream_t s);
+// Repacks row-major weights of a float kind (device; f16 bits, f32 or int8
+// codes) into the lane-chain layout.
+void float_repack(const void* src, int kind, int n, int k, void* dst, hipStream_t s);
+// Row `index` of a float-kind layer as f32 (device out).
+void float_row(const Layer& L, int index, float* out, hipStream_t s);
 
 }  // namespace trit
 

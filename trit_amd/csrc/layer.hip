@@ -96,7 +96,7 @@ void q4_k_requantize(const uint8_t* blocks, int n, int k, Layer& L, hipStream_t 
 }
 
 void layer_forward(const Layer& L, const GemvArgs& a, hipStream_t s) {
-    if (L.kind == F16) return gemv_f16(L, a, s);
+    if (float_kind(L.kind)) return gemv_float(L, a, s);
     return gemv_int(L, a, s);
 }
 
@@ -211,7 +211,7 @@ template <class Scratch>
 void forward_rows(const Layer& L, GemvArgs a, int m, hipStream_t s, Scratch get) {
     a.m = m;
     if (m >= GEMM_MIN_ROWS && gemm_supported(L, a)) return gemm_int(L, a, get(gemm_scratch_bytes(m, L.k)), s);
-    if (m >= 2 && L.kind != F16) {
+    if (m >= 2 && !float_kind(L.kind)) {
         a.scratch_bytes = gemv_scratch_bytes(m < 8 ? m : 8, L.k);
         a.scratch = get(a.scratch_bytes);
     }
@@ -257,6 +257,45 @@ int finish(std::shared_ptr<Layer> L, TritHipLayer** out) {
     return 0;
 }
 
+// A float-math layer (F32, or Q8 with f32 scales n x k/32) from row-major
+// host weights, repacked into the lane-chain layout.
+int float_layer(int kind, int n, int k, const void* weights, const float* scales, const float* bias,
+                TritHipLayer** out, const char* what) {
+    check_shape(n, k, kind == Q8_F32 ? 32 : 16, what);
+    if (!weights) fail(std::string(what) + ": weights is NULL");
+    auto L = std::make_shared<Layer>();
+    L->kind = kind;
+    L->n = n;
+    L->k = k;
+    const size_t bytes = (size_t)n * k * (kind == F32 ? 4 : 1);
+    DeviceMemory raw(bytes);
+    raw.upload(weights, bytes);
+    L->codes.alloc(bytes);
+    float_repack(raw.ptr, kind, n, k, L->codes.ptr, stream());
+    if (kind == Q8_F32) {
+        L->scales.alloc((size_t)n * (k / 32) * 4);
+        L->scales.upload(scales, (size_t)n * (k / 32) * 4);
+    }
+    upload_bias(*L, bias);
+    TRIT_HIP(hipStreamSynchronize(stream()));
+    return finish(L, out);
+}
+
+// Q8_0 blocks as int8 storage with f32 math: the codes as stored and each
+// block's f16 scale widened to f32 (Q8 built from Blocks, src/cpu/gemm.rs:
+// 238-244,386-393).
+int q8_from_blocks(int n, int k, const void* blocks, const float* bias, TritHipLayer** out) {
+    const size_t nb = (size_t)n * k / 32;
+    std::vector<int8_t> codes((size_t)n * k);
+    std::vector<float> scales(nb);
+    const uint8_t* p = static_cast<const uint8_t*>(blocks);
+    for (size_t b = 0; b < nb; ++b) {
+        scales[b] = f16_bits_to_f32((uint16_t)(p[b * 34] | (p[b * 34 + 1] << 8)));
+        std::memcpy(&codes[b * 32], p + b * 34 + 2, 32);
+    }
+    return float_layer(Q8_F32, n, k, codes.data(), scales.data(), bias, out, "Q8_0 table");
+}
+
 }  // namespace
 
 extern "C" {
@@ -283,6 +322,10 @@ int trit_hip_layer_q8_0(int n, int k, const void* blocks, const float* bias, Tri
     return guard(-1, [&] {
         check_shape(n, k, 32, "Q8_0 layer");
         if (!blocks) fail("Q8_0 layer: blocks is NULL");
+        // Dense::q8_0: int8 activations where the int8 kernels take the
+        // shape (Int8::fits_group: n % 32 == 0), else int8 storage with f32
+        // math (src/cpu/gemm.rs:225-247, src/cpu/int8.rs:234-236).
+        if (n % 32) return q8_from_blocks(n, k, blocks, bias, out);
         auto L = std::make_shared<Layer>();
         L->kind = Q8_0;
         L->n = n;
@@ -394,6 +437,26 @@ int trit_hip_layer_q4_k(int n, int k, const void* blocks, TritHipLayer** out) {
     });
 }
 
+int trit_hip_layer_f32(int n, int k, const float* weights, const float* bias, TritHipLayer** out) {
+    return guard(-1, [&] { return float_layer(F32, n, k, weights, nullptr, bias, out, "f32 layer"); });
+}
+
+int trit_hip_layer_q8(int n, int k, const int8_t* codes, const float* scales, const float* bias,
+                      TritHipLayer** out) {
+    return guard(-1, [&] {
+        if (!scales) fail("q8 layer: scales is NULL");
+        return float_layer(Q8_F32, n, k, codes, scales, bias, out, "q8 layer");
+    });
+}
+
+int trit_hip_layer_q8_0_f32(int n, int k, const void* blocks, const float* bias, TritHipLayer** out) {
+    return guard(-1, [&] {
+        check_shape(n, k, 32, "Q8_0 table");
+        if (!blocks) fail("Q8_0 table: blocks is NULL");
+        return q8_from_blocks(n, k, blocks, bias, out);
+    });
+}
+
 int trit_hip_layer_f16(int n, int k, const uint16_t* weights, const float* bias, TritHipLayer** out) {
     return guard(-1, [&] {
         check_shape(n, k, 16, "f16 layer");
@@ -406,7 +469,7 @@ int trit_hip_layer_f16(int n, int k, const uint16_t* weights, const float* bias,
         DeviceMemory raw(bytes);
         raw.upload(weights, bytes);
         L->codes.alloc(bytes);
-        f16_repack(raw.as<uint16_t>(), n, k, L->codes.as<uint16_t>(), stream());
+        float_repack(raw.ptr, F16, n, k, L->codes.ptr, stream());
         upload_bias(*L, bias);
         TRIT_HIP(hipStreamSynchronize(stream()));
         return finish(L, out);
@@ -510,10 +573,10 @@ int trit_hip_layer_row(const TritHipLayer* layer, int index, float* out) {
     return guard(-1, [&] {
         if (!layer || !out) fail("layer or out is NULL");
         const Layer& L = *layer->layer;
-        if (L.kind != F16) fail("row: only F16 token tables");
+        if (!float_kind(L.kind)) fail("row: only F16, F32 and Q8 token tables");
         if (index < 0 || index >= L.n) fail("row: index out of range");
         DeviceMemory d((size_t)L.k * 4);
-        f16_row(L, index, d.as<float>(), stream());
+        float_row(L, index, d.as<float>(), stream());
         TRIT_HIP(hipMemcpyAsync(out, d.ptr, (size_t)L.k * 4, hipMemcpyDeviceToHost, stream()));
         TRIT_HIP(hipStreamSynchronize(stream()));
         return 0;

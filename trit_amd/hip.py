@@ -17,7 +17,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libtrit_hip.so")
 
-Q8_0, INT8, TERNARY, Q4_K, F16 = 1, 2, 3, 4, 5
+Q8_0, INT8, TERNARY, Q4_K, F16, F32, Q8 = 1, 2, 3, 4, 5, 6, 7
 EXACT, KV_F32, TREE_SUMS = 1, 2, 4
 
 _lib = None
@@ -61,6 +61,9 @@ def lib():
             "trit_hip_layer_ternary_base3": (i, [i, i, p, p, pp]),
             "trit_hip_layer_q4_k": (i, [i, i, p, pp]),
             "trit_hip_layer_f16": (i, [i, i, p, p, pp]),
+            "trit_hip_layer_f32": (i, [i, i, p, p, pp]),
+            "trit_hip_layer_q8": (i, [i, i, p, p, p, pp]),
+            "trit_hip_layer_q8_0_f32": (i, [i, i, p, p, pp]),
             "trit_hip_layer_forward": (i, [p, p, i, i, p]),
             "trit_hip_layer_forward_device": (i, [p, p, i, i, p, p]),
             "trit_hip_layer_forward_device_noalloc": (i, [p, p, i, i, p, p]),
@@ -207,6 +210,31 @@ class Dense:
         bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
         n, k = w.shape
         return cls._make(lib().trit_hip_layer_f16, n, k, ptr(w), ptr(bias))
+
+    @classmethod
+    def f32(cls, weights, bias=None):
+        """Dense::new (f32 weights, f32 math)."""
+        w = np.ascontiguousarray(weights, np.float32)
+        bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        n, k = w.shape
+        return cls._make(lib().trit_hip_layer_f32, n, k, ptr(w), ptr(bias))
+
+    @classmethod
+    def q8(cls, codes, scales, bias=None):
+        """Weights::Q8: int8 storage, an f32 scale per 32 values, f32 math."""
+        codes = np.ascontiguousarray(codes, np.int8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        n, k = codes.shape
+        return cls._make(lib().trit_hip_layer_q8, n, k, ptr(codes), ptr(scales), ptr(bias))
+
+    @classmethod
+    def q8_0_f32(cls, n, k, blocks, bias=None):
+        """Q8_0 blocks with f32 math (Dense::table under Q8_0)."""
+        blocks = np.ascontiguousarray(blocks, np.uint8)
+        assert blocks.size == n * k // 32 * 34
+        bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        return cls._make(lib().trit_hip_layer_q8_0_f32, n, k, ptr(blocks), ptr(bias))
 
     def forward(self, x, rows=None, relu=False):
         x = np.ascontiguousarray(x, np.float32).reshape(-1, self.k)
