@@ -289,3 +289,123 @@ def test_prefix_errors(qshape):
     small = lm.session(10, 0)
     with pytest.raises(hip.TritError, match="exceed"):
         small.prefill_prefixed(pre, p)
+
+
+def widened(L_blocks, n, k):
+    """f32 values of Q8_0 blocks (codes times widened f16 scales)."""
+    b = np.asarray(L_blocks, np.uint8).reshape(-1, 34)
+    d = b[:, :2].copy().view(np.float16).astype(np.float32)
+    codes = b[:, 2:].copy().view(np.int8).astype(np.float32)
+    return (codes * d).reshape(n, k)
+
+
+def build(w, kinds, embed=("f16",), head=None):
+    """A device decoder with linears of `kinds` (per layer, per linear:
+    "q8_0", "f16" or "f32") and the given tables; the matching oracle
+    (f32 caches and f16 caches)."""
+    cfg = w.cfg
+    d, ffn, hd = cfg["d"], cfg["ffn"], cfg["head_dim"]
+    qkv_rows = (cfg["heads"] + 2 * cfg["kv_heads"]) * hd
+    shapes = [(qkv_rows, d), (d, cfg["heads"] * hd), (2 * ffn, d), (d, ffn)]
+    refs = oracles(cfg, w)
+    linears = []
+    for li, L in enumerate(w.layers):
+        for which, (blocks, (n, k)) in enumerate(zip((L.qkv, L.o, L.gate_up, L.down), shapes)):
+            kind = kinds[li][which]
+            if kind == "q8_0":
+                linears.append(hip.Dense.q8_0(n, k, blocks))
+                continue
+            vals = widened(blocks, n, k)
+            if kind == "f16":
+                bits = synth.f16_bits(vals)
+                linears.append(hip.Dense.f16(bits))
+                for r in refs:
+                    r.set_linear_float(li, which, bits)
+            else:
+                linears.append(hip.Dense.f32(vals))
+                for r in refs:
+                    r.set_linear_float(li, which, vals)
+
+    def table(spec, which):
+        kind = spec[0]
+        if kind == "f16":
+            data = w.embed if which == 0 else synth.f16_bits(synth.activations(900, cfg["vocab"], d) * 0.1)
+            for r in refs:
+                r.set_table(which, O.TABLE_F16, data)
+            return hip.Dense.f16(data)
+        if kind == "f32":
+            data = synth.activations(901 + which, cfg["vocab"], d) * np.float32(0.1)
+            for r in refs:
+                r.set_table(which, O.TABLE_F32, data)
+            return hip.Dense.f32(data)
+        codes = synth.ints(902 + which, (cfg["vocab"], d), -127, 127).astype(np.int8)
+        scales = (np.abs(synth.activations(903 + which, cfg["vocab"], d // 32)) * np.float32(0.002)).astype(np.float32)
+        for r in refs:
+            r.set_table(which, O.TABLE_Q8, codes, scales)
+        return hip.Dense.q8(codes, scales)
+
+    emb = table(embed, 0)
+    hd_layer = table(head, 1) if head else None
+    lm = hip.CausalLm(cfg, linears, w.norms_packed(), emb, hd_layer)
+    return lm, refs
+
+
+@pytest.fixture(scope="module")
+def small_w(gpu):
+    return synth.lm_weights(SMALL, config=120, sigma=0.2, norm_jitter=0.2)
+
+
+@pytest.mark.parametrize("flags", [0, hip.EXACT, hip.TREE_SUMS])
+def test_float_linears(small_w, flags):
+    """f16 and f32 linears (Dense::half / Dense::new, f32 math in the 16-lane
+    order) mixed with Q8_0 ones: the normed rows go to the product, and a
+    float gate_up's SwiGLU runs after it."""
+    print(f"case float linears flags={flags}", flush=True)
+    kinds = [["f32", "q8_0", "f16", "q8_0"], ["q8_0", "f16", "f32", "f32"]]
+    lm, (ref, ref16) = build(small_w, kinds)
+    p = synth.prompt(120, 31, SMALL["vocab"])
+    check_run(lm, pick(flags, ref, ref16), flags, p, 12)
+
+
+@pytest.mark.parametrize("embed,head", [(("q8",), ("f32",)), (("f32",), None), (("q8",), None),
+                                        (("f16",), ("q8",))])
+@pytest.mark.parametrize("flags", [0, hip.EXACT])
+def test_tables(small_w, embed, head, flags):
+    """Token tables of f16, f32 and int8-storage (Q8) weights, tied or with
+    an untied head (Dense::table, src/cpu/gemm.rs:376-409): rows widened for
+    the embeddings (the chosen token's too), f32 math for the logits."""
+    print(f"case tables embed={embed[0]} head={head[0] if head else 'tied'} flags={flags}", flush=True)
+    kinds = [["q8_0"] * 4] * SMALL["layers"]
+    lm, (ref, ref16) = build(small_w, kinds, embed, head)
+    p = synth.prompt(121, 23, SMALL["vocab"])
+    check_run(lm, pick(flags, ref, ref16), flags, p, 12)
+
+
+def test_tables_refused(small_w, qshape):
+    """A head of int8 activations is refused (a table never takes them); a
+    Q8 table leaves the persistent step for the per-kernel loop."""
+    print("case table kinds refused / step fallback", flush=True)
+    w = small_w
+    cfg = w.cfg
+    d, hd = cfg["d"], cfg["head_dim"]
+    qkv_rows = (cfg["heads"] + 2 * cfg["kv_heads"]) * hd
+    linears = []
+    for L in w.layers:
+        linears += [hip.Dense.q8_0(qkv_rows, d, L.qkv), hip.Dense.q8_0(d, cfg["heads"] * hd, L.o),
+                    hip.Dense.q8_0(2 * cfg["ffn"], d, L.gate_up), hip.Dense.q8_0(d, cfg["ffn"], L.down)]
+    int8_head = hip.Dense.int8(synth.ints(5, (cfg["vocab"], d), -127, 127).astype(np.int8),
+                               np.full((cfg["vocab"], d // 128), 0.01, np.float32))
+    with pytest.raises(hip.TritError, match="head must be a table"):
+        hip.CausalLm(cfg, linears, w.norms_packed(), hip.Dense.f16(w.embed), int8_head)
+    # The Qwen3-shaped model with a Q8 head: tokens as the oracle's, on the
+    # per-kernel loop.
+    wq = qshape[0]
+    lm, (ref, ref16) = build(wq, [["q8_0"] * 4] * QS["layers"], ("f16",), ("q8",))
+    p = synth.prompt(122, 20, QS["vocab"])
+    ref16.reset()
+    want = greedy(ref16, ref16.forward(p), 10)
+    s = lm.session(64, 0)
+    s.prefill(p)
+    got = s.generate(10)
+    assert not s.persistent
+    assert got.tolist() == want

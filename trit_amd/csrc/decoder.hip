@@ -133,16 +133,43 @@ __global__ void add_rows_kernel(float* __restrict__ x, const float* __restrict__
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) x[i] = x[i] + a[i];
 }
 
-// Embedding rows of `tokens` (or of st->token when tokens is null) from the
-// lane-chain f16 table (Dense::row, src/cpu/gemm.rs:412-429).
-__global__ void embed_kernel(const uint16_t* __restrict__ table, int k, const int* __restrict__ tokens,
-                             float* __restrict__ x, const State* st) {
+// A token table in the lane-chain layout (f16 bits, f32, or int8 codes
+// with f32 scales n x k/32).
+struct TableRef {
+    int kind;
+    const void* codes;
+    const float* scales;
+};
+
+TableRef table_ref(const Layer& L) { return TableRef{L.kind, L.codes.ptr, L.scales.as<float>()}; }
+
+// Value kk of row `token` as f32 (Dense::row, src/cpu/gemm.rs:412-429; Q8:
+// f32(code) * scale, widen_q8 :171-179).
+__device__ __forceinline__ float table_value(const TableRef& t, int token, int kk, int k) {
+    const int s_count = k / 16;
+    const size_t at = ((size_t)token * 16 + (kk & 15)) * s_count + (kk >> 4);
+    if (t.kind == F16) return f16_to_f32(((const uint16_t*)t.codes)[at]);
+    if (t.kind == F32) return ((const float*)t.codes)[at];
+    return (float)((const int8_t*)t.codes)[at] * t.scales[(size_t)token * (k / 32) + kk / 32];
+}
+
+// Embedding rows of `tokens` (or of st->token when tokens is null).
+__global__ void embed_kernel(TableRef table, int k, const int* __restrict__ tokens, float* __restrict__ x,
+                             const State* st) {
     if (st->done) return;
     const int token = tokens ? tokens[blockIdx.x] : st->token;
-    const int s_count = k / 16;
-    for (int kk = threadIdx.x; kk < k; kk += blockDim.x) {
-        const int s = kk / 16, i = kk % 16;
-        x[(size_t)blockIdx.x * k + kk] = f16_to_f32(table[((size_t)token * 16 + i) * s_count + s]);
+    for (int kk = threadIdx.x; kk < k; kk += blockDim.x) x[(size_t)blockIdx.x * k + kk] = table_value(table, token, kk, k);
+}
+
+// SwiGLU of the stacked gate_up product's rows (2 * ffn wide): h = silu(gate)
+// * up (causal_lm.rs:464-473), for float-math gate_up layers.
+__global__ void silu_pair_kernel(const float* __restrict__ wide, int rows, int ffn, float* __restrict__ h,
+                                 const State* st) {
+    if (st && st->done) return;
+    const int n = rows * ffn;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const int r = i / ffn, j = i - r * ffn;
+        h[i] = silu_trit(wide[(size_t)r * 2 * ffn + j]) * wide[(size_t)r * 2 * ffn + ffn + j];
     }
 }
 
@@ -920,8 +947,7 @@ __device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
 
 __global__ __launch_bounds__(CHOOSE_THREADS) void choose_kernel(const float* __restrict__ logits, int n, State* st,
                                                                  int* __restrict__ out, float2* __restrict__ part,
-                                                                 const uint16_t* __restrict__ table, int d,
-                                                                 float* __restrict__ x) {
+                                                                 TableRef table, int d, float* __restrict__ x) {
     if (st->done) return;
     __shared__ float bv[CHOOSE_THREADS];
     __shared__ int bi[CHOOSE_THREADS];
@@ -989,11 +1015,7 @@ __global__ __launch_bounds__(CHOOSE_THREADS) void choose_kernel(const float* __r
     if (!commit) return;
     // Dense::row of the chosen token (src/cpu/gemm.rs:412-429).
     const int token = bi[0];
-    const int s_count = d / 16;
-    for (int kk = threadIdx.x; kk < d; kk += CHOOSE_THREADS) {
-        const int s = kk / 16, i = kk % 16;
-        x[kk] = f16_to_f32(table[((size_t)token * 16 + i) * s_count + s]);
-    }
+    for (int kk = threadIdx.x; kk < d; kk += CHOOSE_THREADS) x[kk] = table_value(table, token, kk, d);
 }
 
 __global__ void advance_kernel(State* st, int rows) {
@@ -1131,6 +1153,7 @@ void ensure_rows(SessionImpl& S, int rows) {
     S.hid.alloc((size_t)rows * c.ffn * 4);
     S.inv.alloc((size_t)rows * 4);
     S.xn.alloc((size_t)rows * c.d * 4);
+    if (S.dec->float_gate_up) S.wide.alloc((size_t)rows * 2 * c.ffn * 4);
     S.normed.alloc((size_t)c.d * 4);
     S.tokens_in.alloc((size_t)rows * 4);
     S.max_splits = (S.max_pos + Split<float>::CH - 1) / Split<float>::CH;
@@ -1254,14 +1277,22 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
         GemvArgs a;
         a.eps = c.eps;
         a.skip = &st->done;
-        // qkv with the attention norm in the prologue.
+        // qkv with the attention norm in the prologue (a float-math qkv
+        // takes the normed rows).
         if (S.exact) {
             hipLaunchKernelGGL(norm_inv_kernel, dim3(rows), dim3(256), c.d * 4, s, x, c.d, c.eps,
                                S.inv.as<float>(), st);
             a.norm_inv = S.inv.as<float>();
         }
-        a.x = x;
-        a.norm_w = D.norm_attn(l);
+        if (float_kind(D.qkv[l]->kind)) {
+            hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, s, x, c.d, D.norm_attn(l), c.eps,
+                               S.exact ? S.inv.as<float>() : nullptr, xn, st, nullptr);
+            a.x = xn;
+            a.norm_inv = nullptr;
+        } else {
+            a.x = x;
+            a.norm_w = D.norm_attn(l);
+        }
         a.y = S.qkv.as<float>();
         product(S, *D.qkv[l], a, rows, s, stride);
         // q/k norm, rotary, cache append, attention.
@@ -1357,18 +1388,28 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
                                S.inv.as<float>(), st);
             gu.norm_inv = S.inv.as<float>();
         }
-        if (ffn_scales) {
+        const bool float_gu = float_kind(D.gate_up[l]->kind);
+        if (ffn_scales || float_gu) {
             hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, s, x, c.d, D.norm_mlp(l), c.eps,
-                               S.exact ? S.inv.as<float>() : nullptr, xn, st, ffn_scales + (size_t)l * c.d);
+                               S.exact ? S.inv.as<float>() : nullptr, xn, st,
+                               ffn_scales ? ffn_scales + (size_t)l * c.d : nullptr);
             gu.x = xn;
             gu.norm_inv = nullptr;
         } else {
             gu.x = x;
             gu.norm_w = D.norm_mlp(l);
         }
-        gu.y = S.hid.as<float>();
-        gu.epilogue = EPI_SILU_PAIR;
-        product(S, *D.gate_up[l], gu, rows, s, c.ffn);
+        if (float_gu) {
+            // The stacked product, then SwiGLU.
+            gu.y = S.wide.as<float>();
+            product(S, *D.gate_up[l], gu, rows, s, 2 * c.ffn);
+            hipLaunchKernelGGL(silu_pair_kernel, dim3(std::min((rows * c.ffn + 255) / 256, 1024)), dim3(256), 0, s,
+                               S.wide.as<float>(), rows, c.ffn, S.hid.as<float>(), st);
+        } else {
+            gu.y = S.hid.as<float>();
+            gu.epilogue = EPI_SILU_PAIR;
+            product(S, *D.gate_up[l], gu, rows, s, c.ffn);
+        }
         // down with the residual add.
         residual(D.down[l], S.hid.as<float>());
     }
@@ -1431,8 +1472,8 @@ void step(SessionImpl& S, hipStream_t s) {
     const auto& c = S.dec->c;
     const int blocks = (c.vocab + CHOOSE_SPAN - 1) / CHOOSE_SPAN;
     hipLaunchKernelGGL(choose_kernel, dim3(blocks), dim3(CHOOSE_THREADS), 0, s, S.logits.as<float>(), c.vocab,
-                       S.st(), S.tokens_out.as<int>(), S.partials.as<float2>(), S.dec->embed->codes.as<uint16_t>(),
-                       c.d, S.x.as<float>());
+                       S.st(), S.tokens_out.as<int>(), S.partials.as<float2>(), table_ref(*S.dec->embed), c.d,
+                       S.x.as<float>());
     if (S.additive_rows)
         hipLaunchKernelGGL(add_rows_kernel, dim3((c.d + 255) / 256), dim3(256), 0, s, S.x.as<float>(),
                            S.additive.as<float>(), c.d, c.d, 1, S.st());
@@ -1563,9 +1604,9 @@ int trit_hip_decoder_new(const TritHipLmConfig* config, const TritHipLayer* cons
             if (L->n != n || L->k != k)
                 fail(std::string("decoder: layer ") + std::to_string(l) + " " + what + " is " + std::to_string(L->n) +
                      "x" + std::to_string(L->k) + ", expected " + std::to_string(n) + "x" + std::to_string(k));
-            if (L->kind == F16 || L->kind == TERNARY)
+            if (L->kind == TERNARY)
                 fail(std::string("decoder: layer ") + std::to_string(l) + " " + what +
-                     " must be Q8_0, Q4_K or int8");
+                     " must be Q8_0, Q4_K, int8, f16, f32 or Q8");
             return L;
         };
         for (int l = 0; l < c.layers; ++l) {
@@ -1574,12 +1615,18 @@ int trit_hip_decoder_new(const TritHipLmConfig* config, const TritHipLayer* cons
             D->gate_up.push_back(want(linears[4 * l + 2], 2 * c.ffn, c.d, "gate_up", l));
             D->down.push_back(want(linears[4 * l + 3], c.d, c.ffn, "down", l));
         }
+        for (int l = 0; l < c.layers; ++l) D->float_gate_up |= float_kind(D->gate_up[l]->kind);
+        // Token tables take f32 math, never int8 activations (Dense::table,
+        // src/cpu/gemm.rs:376-409).
         D->embed = layer_ref(embed);
-        if (D->embed->kind != F16 || D->embed->n != c.vocab || D->embed->k != c.d)
-            fail("decoder: embed must be an F16 vocab x d table");
+        if (!float_kind(D->embed->kind) || D->embed->n != c.vocab || D->embed->k != c.d)
+            fail("decoder: embed must be a vocab x d table of f16, f32 or Q8 weights");
         if (head) {
             D->head = layer_ref(head);
             if (D->head->n != c.vocab || D->head->k != c.d) fail("decoder: head must be vocab x d");
+            if (!float_kind(D->head->kind))
+                fail("decoder: head must be a table of f16, f32 or Q8 weights (f32 math; for Q8_0 blocks "
+                     "trit_hip_layer_q8_0_f32)");
         }
         D->layer_norm_stride = (size_t)2 * c.d + (c.qk_norm ? 2 * hd : 0);
         const size_t count = D->layer_norm_stride * c.layers + c.d;
@@ -1662,7 +1709,7 @@ static int prefill_common(TritHipSession* session, int n, float* logits, const i
         for (int i = 0; i < n; ++i)
             if (tokens[i] < 0 || tokens[i] >= c.vocab) fail("prefill: token " + std::to_string(tokens[i]) + " out of range");
         TRIT_HIP(hipMemcpyAsync(S.tokens_in.ptr, tokens, (size_t)n * 4, hipMemcpyHostToDevice, s));
-        hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, s, S.dec->embed->codes.as<uint16_t>(), c.d,
+        hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, s, table_ref(*S.dec->embed), c.d,
                            S.tokens_in.as<int>(), S.x.as<float>(), S.st());
         TRIT_HIP(hipGetLastError());
     } else {

@@ -40,6 +40,8 @@ struct DecoderImpl {
     // The head in the persistent step's tiled f16 layout, made on first use.
     mutable DeviceMemory step_head;
     mutable std::once_flag step_head_once;
+    // Some layer's gate_up takes f32 math (its SwiGLU is a kernel of its own).
+    bool float_gate_up = false;
     // Per layer, d scales on the normed MLP input (set_ffn_scales); a
     // counter of their changes (sessions rebuild what depends on them).
     DeviceMemory ffn_scales;
@@ -61,7 +63,8 @@ struct SessionImpl {
     DeviceMemory x, qkv, att, hid, inv, normed, logits, state, tokens_in, tokens_out, partials;
     DeviceMemory att_part, att_arrived;  // split attention: chunk partials, per (row, kv head) counters
     DeviceMemory gemm_scratch;           // quantized rows of the matrix-core products
-    DeviceMemory xn;                     // rows x d: the normed MLP input, a residual branch
+    DeviceMemory xn;                     // rows x d: normed rows, a residual branch
+    DeviceMemory wide;                   // rows x 2 ffn: a float-math gate_up's product
     // generate_additive: rows x d f32 added to each input, by position.
     DeviceMemory additive;
     int additive_rows = 0;
