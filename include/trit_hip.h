@@ -88,6 +88,18 @@ int trit_hip_layer_ternary_base3(int n, int k, const uint8_t *packed, const floa
  * k % 256 == 0. */
 int trit_hip_layer_q4_k(int n, int k, const void *blocks, TritHipLayer **out);
 
+/* A GGUF tensor of ggml type `ggml_type` as Trit loads it under Auto
+ * precision (Tensors::precision_of / q8_0, reference src/cpu/tensors.rs:
+ * 262-305; Dense::load / Dense::table, src/cpu/gemm.rs:225-247,287-409):
+ * Q8_0 (8) as stored; Q4_0 (2), Q4_1 (3), Q5_0 (6), Q5_1 (7), Q4_K (12),
+ * Q5_K (13) and Q6_K (14) expanded as ggml's dequantize_row_* and
+ * requantized to Q8_0 codes (src/cpu/ggml_quants.rs:103-245, gemm.rs:58-76),
+ * on the device. Then int8 activations, unless f32_math (a token table) or
+ * n % 32 != 0 ask for the codes with f32 math. k a multiple of the type's
+ * block (32, or 256 for the K types). bias: n floats or NULL. */
+int trit_hip_layer_ggml(int n, int k, int ggml_type, const void *blocks, const float *bias, int f32_math,
+                        TritHipLayer **out);
+
 /* f32 weights, row-major n x k, f32 math in Trit's 16-lane order.
  * Replaces Dense::new / Weights::F32 and Dense::table under F32
  * (reference src/cpu/gemm.rs:190-204,395). k % 16 == 0. */

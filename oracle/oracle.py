@@ -58,6 +58,7 @@ def _bind(L):
         "or_q8_0_quantize": (None, [p, i64, p, p]),
         "or_q8_0_parse": (None, [p, i64, p, p]),
         "or_q4_k_expand": (None, [p, i64, p]),
+        "or_ggml_expand": (i, [i, p, i64, p]),
         "or_int8_new": (p, [i, i, i, i, i, p, p]),
         "or_int8_forward": (None, [p, p, i, p]),
         "or_int8_free": (None, [p]),
@@ -137,6 +138,20 @@ def q8_0_quantize(values: np.ndarray):
     scales = np.empty(v.size // 32, np.float32)
     lib().or_q8_0_quantize(ptr(v), v.size, ptr(codes), ptr(scales))
     return codes, scales
+
+
+GGML_BLOCKS = {2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
+
+
+def ggml_expand(ggml_type: int, blocks: np.ndarray) -> np.ndarray:
+    """ggml's block types (Q4_0 2, Q4_1 3, Q5_0 6, Q5_1 7, Q4_K 12, Q5_K 13,
+    Q6_K 14) as f32 (src/cpu/ggml_quants.rs:103-245)."""
+    values, size = GGML_BLOCKS[ggml_type]
+    b = np.ascontiguousarray(blocks, np.uint8).reshape(-1)
+    nb = b.size // size
+    out = np.empty(nb * values, np.float32)
+    assert lib().or_ggml_expand(ggml_type, ptr(b), nb, ptr(out)) == 0
+    return out
 
 
 def q4_k_expand(blocks: np.ndarray) -> np.ndarray:

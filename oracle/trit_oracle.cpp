@@ -1406,6 +1406,132 @@ void or_q4_k_expand(const uint8_t* blocks, int64_t nblocks, float* out) {
     }
 }
 
+// ggml's other block types expanded to f32 (src/cpu/ggml_quants.rs:103-245,
+// ggml's dequantize_row_* in the same float order): Q4_0 (2), Q4_1 (3),
+// Q5_0 (6), Q5_1 (7), Q4_K (12), Q5_K (13), Q6_K (14). Returns 0, or -1
+// for another type.
+int or_ggml_expand(int type, const uint8_t* blocks, int64_t nblocks, float* out) {
+    auto half = [](const uint8_t* b, int at) { return f16_to_f32((uint16_t)(b[at] | (b[at + 1] << 8))); };
+    auto scale_min = [](int j, const uint8_t* q, int* sc, int* m) {
+        if (j < 4) {
+            *sc = q[j] & 63;
+            *m = q[j + 4] & 63;
+        } else {
+            *sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+            *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+        }
+    };
+    switch (type) {
+        case 2:  // Q4_0: f16 d, 16 bytes; (q - 8) * d (:125-132)
+            for (int64_t b = 0; b < nblocks; ++b) {
+                const uint8_t* p = blocks + b * 18;
+                float* y = out + b * 32;
+                const float d = half(p, 0);
+                for (int j = 0; j < 16; ++j) {
+                    y[j] = (float)((p[2 + j] & 0x0F) - 8) * d;
+                    y[j + 16] = (float)((p[2 + j] >> 4) - 8) * d;
+                }
+            }
+            return 0;
+        case 3:  // Q4_1: f16 d, f16 m, 16 bytes; q * d + m (:134-141)
+            for (int64_t b = 0; b < nblocks; ++b) {
+                const uint8_t* p = blocks + b * 20;
+                float* y = out + b * 32;
+                const float d = half(p, 0), m = half(p, 2);
+                for (int j = 0; j < 16; ++j) {
+                    const float a = (float)(p[4 + j] & 0x0F) * d, c = (float)(p[4 + j] >> 4) * d;
+                    y[j] = a + m;
+                    y[j + 16] = c + m;
+                }
+            }
+            return 0;
+        case 6:  // Q5_0: f16 d, u32 high bits, 16 bytes; (q - 16) * d (:143-153)
+        case 7:  // Q5_1: f16 d, f16 m, u32 high bits, 16 bytes; q * d + m (:155-166)
+            for (int64_t b = 0; b < nblocks; ++b) {
+                const bool one = type == 7;
+                const uint8_t* p = blocks + b * (one ? 24 : 22);
+                float* y = out + b * 32;
+                const float d = half(p, 0), m = one ? half(p, 2) : 0.0f;
+                const uint8_t* h = p + (one ? 4 : 2);
+                const uint32_t qh = (uint32_t)h[0] | ((uint32_t)h[1] << 8) | ((uint32_t)h[2] << 16) | ((uint32_t)h[3] << 24);
+                const uint8_t* qs = h + 4;
+                for (int j = 0; j < 16; ++j) {
+                    const int xh0 = (int)(((qh >> j) << 4) & 0x10), xh1 = (int)((qh >> (j + 12)) & 0x10);
+                    const int q0 = (qs[j] & 0x0F) | xh0, q1 = (qs[j] >> 4) | xh1;
+                    if (one) {
+                        const float a = (float)q0 * d, c = (float)q1 * d;
+                        y[j] = a + m;
+                        y[j + 16] = c + m;
+                    } else {
+                        y[j] = (float)(q0 - 16) * d;
+                        y[j + 16] = (float)(q1 - 16) * d;
+                    }
+                }
+            }
+            return 0;
+        case 12:
+            or_q4_k_expand(blocks, nblocks, out);
+            return 0;
+        case 13:  // Q5_K: f16 d, f16 dmin, 12 scale bytes, 32 high-bit bytes, 128 bytes (:198-221)
+            for (int64_t b = 0; b < nblocks; ++b) {
+                const uint8_t* p = blocks + b * 176;
+                float* y = out + b * 256;
+                const float d = half(p, 0), dmin = half(p, 2);
+                const uint8_t* scales = p + 4;
+                const uint8_t* qh = p + 16;
+                const uint8_t* ql = p + 48;
+                int u1 = 1, u2 = 2;
+                for (int is = 0; is < 8; is += 2) {
+                    int sc, m;
+                    scale_min(is, scales, &sc, &m);
+                    const float d1 = d * (float)sc, m1 = dmin * (float)m;
+                    scale_min(is + 1, scales, &sc, &m);
+                    const float d2 = d * (float)sc, m2 = dmin * (float)m;
+                    for (int l = 0; l < 32; ++l) {
+                        const int h1 = (qh[l] & u1) ? 16 : 0, h2 = (qh[l] & u2) ? 16 : 0;
+                        const float a = d1 * (float)((ql[l] & 0xF) + h1), c = d2 * (float)((ql[l] >> 4) + h2);
+                        y[l] = a - m1;
+                        y[32 + l] = c - m2;
+                    }
+                    y += 64;
+                    ql += 32;
+                    u1 <<= 2;
+                    u2 <<= 2;
+                }
+            }
+            return 0;
+        case 14:  // Q6_K: 128 low bytes, 64 high-bit bytes, 16 int8 scales, f16 d (:223-245)
+            for (int64_t b = 0; b < nblocks; ++b) {
+                const uint8_t* p = blocks + b * 210;
+                float* y = out + b * 256;
+                const float d = half(p, 208);
+                const uint8_t* ql = p;
+                const uint8_t* qh = p + 128;
+                const int8_t* sc = (const int8_t*)(p + 192);
+                for (int n = 0; n < 2; ++n) {
+                    for (int l = 0; l < 32; ++l) {
+                        const int is = l / 16;
+                        const int q1 = (int8_t)((ql[l] & 0xF) | ((qh[l] & 3) << 4)) - 32;
+                        const int q2 = (int8_t)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                        const int q3 = (int8_t)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                        const int q4 = (int8_t)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                        y[l] = d * (float)sc[is] * (float)q1;
+                        y[l + 32] = d * (float)sc[is + 2] * (float)q2;
+                        y[l + 64] = d * (float)sc[is + 4] * (float)q3;
+                        y[l + 96] = d * (float)sc[is + 6] * (float)q4;
+                    }
+                    y += 128;
+                    ql += 64;
+                    qh += 32;
+                    sc += 8;
+                }
+            }
+            return 0;
+        default:
+            return -1;
+    }
+}
+
 void* or_int8_new(int isa, int n, int k, int group, int half_scales, const int8_t* codes, const float* scales) {
     if (k % group != 0 || group % 4 != 0) return nullptr;
     if (isa != OR_SCALAR && n % 32 != 0) isa = OR_SCALAR;

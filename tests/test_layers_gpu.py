@@ -262,6 +262,29 @@ def test_q8_0_f32_math(gpu, n, k, m, table):
     assert bits_equal(layer.forward(x), O.matmul_f32(x, w))
 
 
+@pytest.mark.parametrize("ggml_type", [2, 3, 6, 7, 12, 13, 14])
+@pytest.mark.parametrize("n,k,m,f32_math", [(512, 512, 1, False), (256, 1024, 5, False), (96, 256, 3, True),
+                                            (100, 512, 2, False)])
+def test_ggml_types(gpu, ggml_type, n, k, m, f32_math):
+    """ggml's other block types as Trit loads them: expanded as ggml does and
+    requantized to Q8_0 (the oracle's expansion, then Blocks::quantize),
+    then int8 activations, or f32 math for a table or an n that is no
+    multiple of 32."""
+    print(f"case ggml type {ggml_type} n={n} k={k} m={m} f32_math={f32_math}", flush=True)
+    blocks = synth.ggml_blocks(synth.seed_for(3, ggml_type * 7 + n), ggml_type, n, k)
+    codes, scales = O.q8_0_quantize(O.ggml_expand(ggml_type, blocks))
+    codes = codes.reshape(n, k)
+    scales = scales.reshape(n, k // 32)
+    x = synth.activations(81 + m, m, k)
+    layer = gpu.Dense.ggml(n, k, ggml_type, blocks, f32_math=f32_math)
+    if f32_math or n % 32:
+        assert layer.info()["kind"] == gpu.Q8
+        want = O.matmul_f32(x, widened_q8(codes, scales))
+    else:
+        want = O.Int8(codes, scales, 32, True)(x)
+    assert bits_equal(layer.forward(x), want)
+
+
 def test_errors(gpu):
     from trit_amd.hip import TritError
 

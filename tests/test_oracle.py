@@ -337,3 +337,88 @@ def test_lm_paths_agree():
         assert a.tolist() == b.tolist()
         assert np.array_equal(bits(la), bits(lb))
     assert len(a) == 8
+
+
+def _f16(v):
+    return np.array([np.float16(v)]).view(np.uint8)
+
+
+def _k_scales(sc, mn):
+    """The 12 bytes of 6-bit scales and mins of a Q4_K / Q5_K block (ggml's
+    get_scale_min_k4 layout)."""
+    b = np.zeros(12, np.uint8)
+    for j in range(4):
+        b[j] = sc[j]
+        b[4 + j] = mn[j]
+    for j in range(4, 8):
+        b[8 + j - 4] = (sc[j] & 0xF) | ((mn[j] & 0xF) << 4)
+        b[j - 4] |= (sc[j] >> 4) << 6
+        b[j] |= (mn[j] >> 4) << 6
+    return b
+
+
+def test_ggml_expand_known_answers():
+    """Each of ggml's other block types from a block packed by hand in its
+    published layout (ggml-quants block_q4_0 .. block_q6_K): every value
+    lands where the layout puts it, with the block's scale arithmetic."""
+    f = np.float32
+    rng = np.random.default_rng(5)
+    d, m = f(0.25), f(-1.5)
+    # Q4_0 / Q4_1: 32 nibbles, value j in the low half of byte j, j + 16 in the high half.
+    q = rng.integers(0, 16, 32)
+    qs = (q[:16] | (q[16:] << 4)).astype(np.uint8)
+    assert np.array_equal(O.ggml_expand(2, np.concatenate([_f16(d), qs])), (q - 8).astype(f) * d)
+    want = (q.astype(f) * d + m).astype(f)
+    assert np.array_equal(O.ggml_expand(3, np.concatenate([_f16(d), _f16(m), qs])), want)
+    # Q5_0 / Q5_1: the fifth bit of value j in bit j of a little-endian u32.
+    q = rng.integers(0, 32, 32)
+    qs = ((q[:16] & 15) | ((q[16:] & 15) << 4)).astype(np.uint8)
+    qh = np.array([int(sum(((int(q[j]) >> 4) & 1) << j for j in range(32)))], np.uint32).view(np.uint8)
+    assert np.array_equal(O.ggml_expand(6, np.concatenate([_f16(d), qh, qs])), (q - 16).astype(f) * d)
+    want = (q.astype(f) * d + m).astype(f)
+    assert np.array_equal(O.ggml_expand(7, np.concatenate([_f16(d), _f16(m), qh, qs])), want)
+    # Q5_K: sub-block j's low nibbles in byte 32*(j//2) + l (low half for
+    # even j), its fifth bit in bit j of high byte l; scales/mins 6-bit.
+    sc, mn = list(range(3, 11)), list(range(7, -1, -1))
+    q = rng.integers(0, 32, (8, 32))
+    ql = np.zeros(128, np.uint8)
+    qh = np.zeros(32, np.uint8)
+    for j in range(8):
+        pair, odd = divmod(j, 2)
+        ql[pair * 32:(pair + 1) * 32] |= ((q[j] & 15) << (4 * odd)).astype(np.uint8)
+        qh |= (((q[j] >> 4) & 1) << j).astype(np.uint8)
+    dk, dmin = f(0.5), f(0.125)
+    blk = np.concatenate([_f16(dk), _f16(dmin), _k_scales(sc, mn), qh, ql])
+    assert blk.size == 176
+    y = O.ggml_expand(13, blk)
+    for j in range(8):
+        want = (f(dk * f(sc[j])) * q[j].astype(f) - f(dmin * f(mn[j]))).astype(f)
+        assert np.array_equal(y[32 * j:32 * (j + 1)], want), j
+    # Q6_K: half h, quarter t, element l: low nibble of ql[64h + l + 32*(t%2)]
+    # (high half for t >= 2), two high bits at bits 2t of qh[32h + l];
+    # scale sc[8h + l//16 + 2t] (int8); value (q - 32) * (d * sc).
+    q = rng.integers(0, 64, (2, 4, 32))
+    ql = np.zeros(128, np.uint8)
+    qh = np.zeros(64, np.uint8)
+    for h in range(2):
+        for t in range(4):
+            at = 64 * h + 32 * (t % 2)
+            ql[at:at + 32] |= ((q[h, t] & 15) << (4 * (t // 2))).astype(np.uint8)
+            qh[32 * h:32 * (h + 1)] |= (((q[h, t] >> 4) & 3) << (2 * t)).astype(np.uint8)
+    scales = rng.integers(-128, 128, 16).astype(np.int8)
+    d6 = f(0.0625)
+    blk = np.concatenate([ql, qh, scales.view(np.uint8), _f16(d6)])
+    assert blk.size == 210
+    y = O.ggml_expand(14, blk)
+    for h in range(2):
+        for t in range(4):
+            l = np.arange(32)
+            s = scales[8 * h + l // 16 + 2 * t].astype(f)
+            want = ((d6 * s).astype(f) * (q[h, t] - 32).astype(f)).astype(f)
+            got = y[128 * h + 32 * t:128 * h + 32 * (t + 1)]
+            assert np.array_equal(got, want), (h, t)
+    # Q4_K through the same entry point as its own.
+    blk = rng.integers(0, 256, 144).astype(np.uint8)
+    blk[0:2] = _f16(0.5)
+    blk[2:4] = _f16(0.25)
+    assert np.array_equal(O.ggml_expand(12, blk), O.q4_k_expand(blk))

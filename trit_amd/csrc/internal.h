@@ -192,6 +192,14 @@ void layer_forward(const Layer& L, const GemvArgs& a, hipStream_t s);
 // Requantizes Q4_K super-blocks (device bytes) into Q8_0 codes and f16
 // scales in L.codes / L.scales.
 void q4_k_requantize(const uint8_t* blocks, int n, int k, Layer& L, hipStream_t s);
+// ggml's other block types: values and bytes per block (false for a type
+// that is not one of Q4_0 2, Q4_1 3, Q5_0 6, Q5_1 7, Q4_K 12, Q5_K 13, Q6_K 14).
+bool ggml_block_type(int type, int* values, int* bytes);
+// Blocks of such a type (device bytes, n x k values) expanded and
+// requantized into Q8_0 codes (n x k) and f16 scales (n x k/32).
+void ggml_requantize(const uint8_t* blocks, int type, int n, int k, int8_t* codes, uint16_t* scales, hipStream_t s);
+// f16 scales widened to f32 (device).
+void widen_scales(const uint16_t* in, int64_t n, float* out, hipStream_t s);
 // Repacks row-major weights of a float kind (device; f16 bits, f32 or int8
 // codes) into the lane-chain layout.
 void float_repack(const void* src, int kind, int n, int k, void* dst, hipStream_t s);

@@ -38,41 +38,115 @@ hipStream_t stream() {
 
 namespace {
 
-// Q4_K super-block (144 bytes): f16 d, f16 dmin, 12 scale bytes, 128 bytes
-// of 4-bit codes. Expanded as ggml's dequantize_row_q4_K
-// (src/cpu/ggml_quants.rs:168-196): y = d*sc*q - dmin*m with two roundings;
-// then each 32-value block requantized as Blocks::quantize
-// (src/cpu/gemm.rs:58-76): d8 = max|y|/127, code = round(y * (1/d8)) half
-// away from zero, d8 stored as f16. One thread per 32-value block.
-__global__ void q4_k_requant_kernel(const uint8_t* __restrict__ blocks, int64_t nsub, int8_t* __restrict__ codes,
-                                    uint16_t* __restrict__ scales) {
-    for (int64_t sb = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; sb < nsub;
-         sb += (int64_t)gridDim.x * blockDim.x) {
+__device__ __forceinline__ float half_at(const uint8_t* p, int at) {
+    return f16_to_f32((uint16_t)(p[at] | (p[at + 1] << 8)));
+}
+
+// The 6-bit scale and min j of a K-quant block's 12 scale bytes.
+__device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, int& sc, int& m) {
+    if (j < 4) {
+        sc = q[j] & 63;
+        m = q[j + 4] & 63;
+    } else {
+        sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+// The 32 values of output block `sb` (32 consecutive weights) of ggml type
+// T, expanded as ggml's dequantize_row_* in the same float order
+// (src/cpu/ggml_quants.rs:125-245): Q4_0 2, Q4_1 3, Q5_0 6, Q5_1 7 (one
+// 32-value block each); Q4_K 12, Q5_K 13, Q6_K 14 (eight per 256-value
+// super-block).
+template <int T>
+__device__ void expand32(const uint8_t* __restrict__ blocks, int64_t sb, float (&y)[32]) {
+    if constexpr (T == 2 || T == 3 || T == 6 || T == 7) {
+        constexpr int size = T == 2 ? 18 : T == 3 ? 20 : T == 6 ? 22 : 24;
+        const uint8_t* p = blocks + sb * size;
+        const float d = half_at(p, 0);
+        const float m = (T == 3 || T == 7) ? half_at(p, 2) : 0.0f;
+        if constexpr (T == 2 || T == 3) {
+            const uint8_t* qs = p + (T == 2 ? 2 : 4);
+            for (int j = 0; j < 16; ++j) {
+                if constexpr (T == 2) {
+                    y[j] = (float)((qs[j] & 0x0F) - 8) * d;
+                    y[j + 16] = (float)((qs[j] >> 4) - 8) * d;
+                } else {
+                    const float a = (float)(qs[j] & 0x0F) * d, c = (float)(qs[j] >> 4) * d;
+                    y[j] = a + m;
+                    y[j + 16] = c + m;
+                }
+            }
+        } else {
+            const uint8_t* h = p + (T == 6 ? 2 : 4);
+            const uint32_t qh = (uint32_t)h[0] | ((uint32_t)h[1] << 8) | ((uint32_t)h[2] << 16) | ((uint32_t)h[3] << 24);
+            const uint8_t* qs = h + 4;
+            for (int j = 0; j < 16; ++j) {
+                const int q0 = (qs[j] & 0x0F) | (int)(((qh >> j) << 4) & 0x10);
+                const int q1 = (qs[j] >> 4) | (int)((qh >> (j + 12)) & 0x10);
+                if constexpr (T == 6) {
+                    y[j] = (float)(q0 - 16) * d;
+                    y[j + 16] = (float)(q1 - 16) * d;
+                } else {
+                    const float a = (float)q0 * d, c = (float)q1 * d;
+                    y[j] = a + m;
+                    y[j + 16] = c + m;
+                }
+            }
+        }
+    } else if constexpr (T == 12 || T == 13) {
         const int64_t super = sb / 8;
         const int j = (int)(sb % 8);
-        const uint8_t* p = blocks + super * 144;
-        const float d = f16_to_f32((uint16_t)(p[0] | (p[1] << 8)));
-        const float dmin = f16_to_f32((uint16_t)(p[2] | (p[3] << 8)));
-        const uint8_t* sc = p + 4;
-        int s, mn;
-        if (j < 4) {
-            s = sc[j] & 63;
-            mn = sc[j + 4] & 63;
-        } else {
-            s = (sc[j + 4] & 0xF) | ((sc[j - 4] >> 6) << 4);
-            mn = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
-        }
-        const float d1 = d * (float)s;
-        const float m1 = dmin * (float)mn;
-        const uint8_t* q = p + 16 + (j / 2) * 32;
+        const uint8_t* p = blocks + super * (T == 12 ? 144 : 176);
+        const float d = half_at(p, 0), dmin = half_at(p, 2);
+        int sc, mn;
+        scale_min_k4(j, p + 4, sc, mn);
+        const float d1 = d * (float)sc, m1 = dmin * (float)mn;
         const int shift = (j & 1) * 4;
-        float y[32];
-        float mx = 0.0f;
-        for (int l = 0; l < 32; ++l) {
-            const float t = d1 * (float)((q[l] >> shift) & 0xF);
-            y[l] = t - m1;
-            mx = __builtin_fmaxf(mx, __builtin_fabsf(y[l]));
+        if constexpr (T == 12) {
+            const uint8_t* q = p + 16 + (j / 2) * 32;
+            for (int l = 0; l < 32; ++l) {
+                const float t = d1 * (float)((q[l] >> shift) & 0xF);
+                y[l] = t - m1;
+            }
+        } else {
+            const uint8_t* qh = p + 16;
+            const uint8_t* ql = p + 48 + (j / 2) * 32;
+            for (int l = 0; l < 32; ++l) {
+                const int high = (qh[l] >> j) & 1 ? 16 : 0;
+                const float t = d1 * (float)(((ql[l] >> shift) & 0xF) + high);
+                y[l] = t - m1;
+            }
         }
+    } else {
+        static_assert(T == 14, "ggml type");
+        const int64_t super = sb / 8;
+        const int j = (int)(sb % 8), half = j / 4, quarter = j % 4;
+        const uint8_t* p = blocks + super * 210;
+        const float d = half_at(p, 208);
+        const uint8_t* ql = p + half * 64 + (quarter & 1) * 32;
+        const uint8_t* qh = p + 128 + half * 32;
+        const int8_t* scales = (const int8_t*)(p + 192 + half * 8);
+        const int lshift = (quarter >> 1) * 4, hshift = quarter * 2;
+        for (int l = 0; l < 32; ++l) {
+            const int q = (int)(int8_t)(((ql[l] >> lshift) & 0xF) | (((qh[l] >> hshift) & 3) << 4)) - 32;
+            y[l] = d * (float)scales[l / 16 + 2 * quarter] * (float)q;
+        }
+    }
+}
+
+// Output blocks of ggml type T, each requantized as Blocks::quantize
+// (src/cpu/gemm.rs:58-76): d8 = max|y| / 127, code = round(y * (1/d8))
+// half away from zero, d8 stored as f16. One thread per 32-value block.
+template <int T>
+__global__ void requant_kernel(const uint8_t* __restrict__ blocks, int64_t nsub, int8_t* __restrict__ codes,
+                               uint16_t* __restrict__ scales) {
+    for (int64_t sb = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; sb < nsub;
+         sb += (int64_t)gridDim.x * blockDim.x) {
+        float y[32];
+        expand32<T>(blocks, sb, y);
+        float mx = 0.0f;
+        for (int l = 0; l < 32; ++l) mx = __builtin_fmaxf(mx, __builtin_fabsf(y[l]));
         const float d8 = mx / 127.0f;
         const float inverse = d8 != 0.0f ? 1.0f / d8 : 0.0f;
         for (int l = 0; l < 32; ++l) {
@@ -84,14 +158,51 @@ __global__ void q4_k_requant_kernel(const uint8_t* __restrict__ blocks, int64_t 
     }
 }
 
+__global__ void widen_scales_kernel(const uint16_t* __restrict__ in, int64_t n, float* __restrict__ out) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = f16_to_f32(in[i]);
+}
+
 }  // namespace
+
+bool ggml_block_type(int type, int* values, int* bytes) {
+    switch (type) {
+        case 2: *values = 32, *bytes = 18; return true;
+        case 3: *values = 32, *bytes = 20; return true;
+        case 6: *values = 32, *bytes = 22; return true;
+        case 7: *values = 32, *bytes = 24; return true;
+        case 12: *values = 256, *bytes = 144; return true;
+        case 13: *values = 256, *bytes = 176; return true;
+        case 14: *values = 256, *bytes = 210; return true;
+        default: return false;
+    }
+}
+
+void ggml_requantize(const uint8_t* blocks, int type, int n, int k, int8_t* codes, uint16_t* scales, hipStream_t s) {
+    const int64_t nsub = (int64_t)n * k / 32;
+    const dim3 grid(2048), block(256);
+    switch (type) {
+        case 2: hipLaunchKernelGGL(requant_kernel<2>, grid, block, 0, s, blocks, nsub, codes, scales); break;
+        case 3: hipLaunchKernelGGL(requant_kernel<3>, grid, block, 0, s, blocks, nsub, codes, scales); break;
+        case 6: hipLaunchKernelGGL(requant_kernel<6>, grid, block, 0, s, blocks, nsub, codes, scales); break;
+        case 7: hipLaunchKernelGGL(requant_kernel<7>, grid, block, 0, s, blocks, nsub, codes, scales); break;
+        case 12: hipLaunchKernelGGL(requant_kernel<12>, grid, block, 0, s, blocks, nsub, codes, scales); break;
+        case 13: hipLaunchKernelGGL(requant_kernel<13>, grid, block, 0, s, blocks, nsub, codes, scales); break;
+        case 14: hipLaunchKernelGGL(requant_kernel<14>, grid, block, 0, s, blocks, nsub, codes, scales); break;
+        default: fail("ggml type " + std::to_string(type) + " is not a block type the loader expands");
+    }
+    TRIT_HIP(hipGetLastError());
+}
 
 void q4_k_requantize(const uint8_t* blocks, int n, int k, Layer& L, hipStream_t s) {
     const int64_t nsub = (int64_t)n * k / 32;
     L.codes.alloc((size_t)n * k);
     L.scales.alloc((size_t)nsub * 2);
-    hipLaunchKernelGGL(q4_k_requant_kernel, dim3(2048), dim3(256), 0, s, blocks, nsub, L.codes.as<int8_t>(),
-                       L.scales.as<uint16_t>());
+    ggml_requantize(blocks, 12, n, k, L.codes.as<int8_t>(), L.scales.as<uint16_t>(), s);
+}
+
+void widen_scales(const uint16_t* in, int64_t n, float* out, hipStream_t s) {
+    hipLaunchKernelGGL(widen_scales_kernel, dim3(1024), dim3(256), 0, s, in, n, out);
     TRIT_HIP(hipGetLastError());
 }
 
@@ -281,6 +392,44 @@ int float_layer(int kind, int n, int k, const void* weights, const float* scales
     return finish(L, out);
 }
 
+// A layer from ggml blocks of another type (not Q8_0): expanded and
+// requantized to Q8_0 codes on the device (Tensors::q8_0 of such a tensor,
+// src/cpu/tensors.rs:262-305), then held as Dense::q8_0 holds them -- int8
+// activations when n % 32 == 0 and f32_math is false, else the codes with
+// f32 math (a table, or a shape the int8 kernels refuse).
+int ggml_layer(int n, int k, int type, const void* blocks, const float* bias, bool f32_math, TritHipLayer** out) {
+    int values = 0, size = 0;
+    if (!ggml_block_type(type, &values, &size))
+        fail("ggml layer: type " + std::to_string(type) + " is not Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K or Q6_K");
+    check_shape(n, k, values, "ggml layer");
+    const size_t bytes = (size_t)n * k / values * size;
+    DeviceMemory raw(bytes);
+    raw.upload(blocks, bytes);
+    const int64_t nsub = (int64_t)n * k / 32;
+    auto L = std::make_shared<Layer>();
+    L->n = n;
+    L->k = k;
+    if (!f32_math && n % 32 == 0) {
+        L->kind = type == 12 ? Q4_K : Q8_0;
+        L->group = 32;
+        L->codes.alloc((size_t)n * k);
+        L->scales.alloc((size_t)nsub * 2);
+        ggml_requantize(raw.as<uint8_t>(), type, n, k, L->codes.as<int8_t>(), L->scales.as<uint16_t>(), stream());
+    } else {
+        L->kind = Q8_F32;
+        DeviceMemory codes((size_t)n * k), half((size_t)nsub * 2);
+        ggml_requantize(raw.as<uint8_t>(), type, n, k, codes.as<int8_t>(), half.as<uint16_t>(), stream());
+        L->codes.alloc((size_t)n * k);
+        float_repack(codes.ptr, Q8_F32, n, k, L->codes.ptr, stream());
+        L->scales.alloc((size_t)nsub * 4);
+        widen_scales(half.as<uint16_t>(), nsub, L->scales.as<float>(), stream());
+        TRIT_HIP(hipStreamSynchronize(stream()));  // before the temporaries go
+    }
+    upload_bias(*L, bias);
+    TRIT_HIP(hipStreamSynchronize(stream()));
+    return finish(L, out);
+}
+
 // Q8_0 blocks as int8 storage with f32 math: the codes as stored and each
 // block's f16 scale widened to f32 (Q8 built from Blocks, src/cpu/gemm.rs:
 // 238-244,386-393).
@@ -421,22 +570,24 @@ int trit_hip_layer_ternary_base3(int n, int k, const uint8_t* packed, const floa
 
 int trit_hip_layer_q4_k(int n, int k, const void* blocks, TritHipLayer** out) {
     return guard(-1, [&] {
-        check_shape(n, k, 256, "Q4_K layer");
         if (!blocks) fail("Q4_K layer: blocks is NULL");
-        auto L = std::make_shared<Layer>();
-        L->kind = Q4_K;
-        L->n = n;
-        L->k = k;
-        L->group = 32;
-        const size_t bytes = (size_t)n * k / 256 * 144;
-        DeviceMemory raw(bytes);
-        raw.upload(blocks, bytes);
-        q4_k_requantize(raw.as<uint8_t>(), n, k, *L, stream());
-        TRIT_HIP(hipStreamSynchronize(stream()));
-        return finish(L, out);
+        return ggml_layer(n, k, 12, blocks, nullptr, false, out);
     });
 }
 
+int trit_hip_layer_ggml(int n, int k, int ggml_type, const void* blocks, const float* bias, int f32_math,
+                        TritHipLayer** out) {
+    return guard(-1, [&] {
+        if (!blocks) fail("ggml layer: blocks is NULL");
+        if (ggml_type == 8) {
+            check_shape(n, k, 32, "Q8_0 layer");
+            if (f32_math || n % 32) return q8_from_blocks(n, k, blocks, bias, out);
+            if (trit_hip_layer_q8_0(n, k, blocks, bias, out) != 0) fail(error_text());
+            return 0;
+        }
+        return ggml_layer(n, k, ggml_type, blocks, bias, f32_math != 0, out);
+    });
+}
 int trit_hip_layer_f32(int n, int k, const float* weights, const float* bias, TritHipLayer** out) {
     return guard(-1, [&] { return float_layer(F32, n, k, weights, nullptr, bias, out, "f32 layer"); });
 }

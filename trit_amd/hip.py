@@ -64,6 +64,7 @@ def lib():
             "trit_hip_layer_f32": (i, [i, i, p, p, pp]),
             "trit_hip_layer_q8": (i, [i, i, p, p, p, pp]),
             "trit_hip_layer_q8_0_f32": (i, [i, i, p, p, pp]),
+            "trit_hip_layer_ggml": (i, [i, i, i, p, p, i, pp]),
             "trit_hip_layer_forward": (i, [p, p, i, i, p]),
             "trit_hip_layer_forward_device": (i, [p, p, i, i, p, p]),
             "trit_hip_layer_forward_device_noalloc": (i, [p, p, i, i, p, p]),
@@ -235,6 +236,14 @@ class Dense:
         assert blocks.size == n * k // 32 * 34
         bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
         return cls._make(lib().trit_hip_layer_q8_0_f32, n, k, ptr(blocks), ptr(bias))
+
+    @classmethod
+    def ggml(cls, n, k, ggml_type, blocks, bias=None, f32_math=False):
+        """A GGUF tensor of ggml type `ggml_type` as Trit loads it under Auto
+        precision (trit_hip_layer_ggml)."""
+        blocks = np.ascontiguousarray(blocks, np.uint8)
+        bias = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        return cls._make(lib().trit_hip_layer_ggml, n, k, ggml_type, ptr(blocks), ptr(bias), int(f32_math))
 
     def forward(self, x, rows=None, relu=False):
         x = np.ascontiguousarray(x, np.float32).reshape(-1, self.k)

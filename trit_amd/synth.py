@@ -135,6 +135,25 @@ def q4_k_blocks(seed: int, n: int, k: int) -> np.ndarray:
     return out.reshape(-1)
 
 
+GGML_SCALE_FIELDS = {2: (0,), 3: (0, 2), 6: (0,), 7: (0, 2), 12: (0, 2), 13: (0, 2), 14: (208,)}
+GGML_BLOCK_BYTES = {2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 12: (256, 144), 13: (256, 176),
+                    14: (256, 210)}
+
+
+def ggml_blocks(seed: int, ggml_type: int, n: int, k: int) -> np.ndarray:
+    """Random blocks of a ggml block type: random code bytes, and each f16
+    scale field (d, and the min where the type has one) set to a finite
+    value in +-[0.0005, 0.004]."""
+    values, size = GGML_BLOCK_BYTES[ggml_type]
+    nb = n * k // values
+    b = ints(seed, (nb, size), 0, 255).astype(np.uint8)
+    for i, at in enumerate(GGML_SCALE_FIELDS[ggml_type]):
+        mag = 0.0005 + 0.0035 * uniform(seed ^ (0x77 + i), nb)
+        sign = np.where(ints(seed ^ (0x99 + i), nb, 0, 1) == 0, -1.0, 1.0) if i else 1.0
+        b[:, at:at + 2] = f16_bits((mag * sign).astype(np.float32)).view(np.uint8).reshape(nb, 2)
+    return b.reshape(-1)
+
+
 def ternary_matrix(seed: int, n: int, k: int):
     """Ternary codes 0/1/2 (w = -1/0/1) with probabilities .25/.5/.25 and one
     f32 scale per row uniform in [0.01, 0.05], held per (row, 128-group)."""
