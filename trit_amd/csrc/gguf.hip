@@ -471,15 +471,21 @@ int trit_hip_decoder_from_gguf(const char* path, const char* prefix, TritHipLmCo
                 all.insert(all.end(), b.begin(), b.end());
                 n += rows[i];
             }
+            // Dense::load under Auto (src/cpu/gemm.rs:287-333, tensors.rs:
+            // 262-279): Q8_0 and ggml's other block types as Q8_0 codes; F16
+            // as f16 weights and F32 as f32 weights, f32 math.
             TritHipLayer* L = nullptr;
             int rc = -1;
-            if (first.type == 8)
-                rc = trit_hip_layer_q8_0((int)n, (int)k, all.data(), nullptr, &L);
-            else if (first.type == 12)
-                rc = trit_hip_layer_q4_k((int)n, (int)k, all.data(), &L);
+            int values = 0, size = 0;
+            if (first.type == 8 || ggml_block_type((int)first.type, &values, &size))
+                rc = trit_hip_layer_ggml((int)n, (int)k, (int)first.type, all.data(), nullptr, 0, &L);
+            else if (first.type == 1)
+                rc = trit_hip_layer_f16((int)n, (int)k, (const uint16_t*)all.data(), nullptr, &L);
+            else if (first.type == 0)
+                rc = trit_hip_layer_f32((int)n, (int)k, (const float*)all.data(), nullptr, &L);
             else
                 fail(std::string(path) + ": " + parts[0] + " is " + first.dtype +
-                     "; the device loader reads Q8_0 and Q4_K linears");
+                     "; the device loader reads F32, F16, Q8_0 and ggml's Q4/Q5/Q6 block types");
             if (rc != 0) fail(error_text());
             return own.keep(L);
         };
@@ -503,35 +509,31 @@ int trit_hip_decoder_from_gguf(const char* path, const char* prefix, TritHipLmCo
             }
         }
         vec("dec.output_norm.weight", c.d, norms);
+        // Dense::table under Auto (src/cpu/gemm.rs:376-409): F16 and F32 as
+        // stored; Q8_0 and ggml's other block types as Q8_0 codes with f32
+        // math -- never int8 activations.
         auto table = [&](const std::string& name) {
             const GgufTensor& t = need(name);
             shape(t, c.vocab, c.d);
             const std::vector<uint8_t> b = g.bytes(t);
-            std::vector<uint16_t> bits((size_t)c.vocab * c.d);
-            if (t.type == 1) {
-                std::memcpy(bits.data(), b.data(), bits.size() * 2);
-            } else if (t.type == 0) {
-                for (size_t k = 0; k < bits.size(); ++k) {
-                    float v;
-                    std::memcpy(&v, b.data() + 4 * k, 4);
-                    bits[k] = f32_to_f16_bits(v);
-                }
-            } else {
-                fail(std::string(path) + ": " + name + " is " + t.dtype + "; the token table is read as F16 or F32");
-            }
             TritHipLayer* L = nullptr;
-            if (trit_hip_layer_f16(c.vocab, c.d, bits.data(), nullptr, &L) != 0) fail(error_text());
+            int rc = -1;
+            int values = 0, size = 0;
+            if (t.type == 1)
+                rc = trit_hip_layer_f16(c.vocab, c.d, (const uint16_t*)b.data(), nullptr, &L);
+            else if (t.type == 0)
+                rc = trit_hip_layer_f32(c.vocab, c.d, (const float*)b.data(), nullptr, &L);
+            else if (t.type == 8 || ggml_block_type((int)t.type, &values, &size))
+                rc = trit_hip_layer_ggml(c.vocab, c.d, (int)t.type, b.data(), nullptr, 1, &L);
+            else
+                fail(std::string(path) + ": " + name + " is " + t.dtype +
+                     "; a token table is read as F16, F32, Q8_0 or ggml's Q4/Q5/Q6 block types");
+            if (rc != 0) fail(error_text());
             return own.keep(L);
         };
         TritHipLayer* embed = table("dec.token_embd.weight");
         TritHipLayer* head = nullptr;
-        if (!tie || g.tensor("dec.output.weight")) {
-            const GgufTensor& h = need("dec.output.weight");
-            if (h.type == 1 || h.type == 0)
-                head = table("dec.output.weight");
-            else
-                head = linear({"dec.output.weight"}, {(uint64_t)c.vocab}, c.d);
-        }
+        if (!tie || g.tensor("dec.output.weight")) head = table("dec.output.weight");
         TritHipDecoder* dec = nullptr;
         if (trit_hip_decoder_new(&c, linears.data(), norms.data(), embed, head, &dec) != 0) fail(error_text());
         if (config) *config = c;

@@ -143,12 +143,13 @@ GGML_BLOCK_BYTES = {2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 12: (256
 def ggml_blocks(seed: int, ggml_type: int, n: int, k: int) -> np.ndarray:
     """Random blocks of a ggml block type: random code bytes, and each f16
     scale field (d, and the min where the type has one) set to a finite
-    value in +-[0.0005, 0.004]."""
+    value in +-[0.0005, 0.004] (a 32nd of that for the K types, whose
+    6-bit sub-block scales multiply it)."""
     values, size = GGML_BLOCK_BYTES[ggml_type]
     nb = n * k // values
     b = ints(seed, (nb, size), 0, 255).astype(np.uint8)
     for i, at in enumerate(GGML_SCALE_FIELDS[ggml_type]):
-        mag = 0.0005 + 0.0035 * uniform(seed ^ (0x77 + i), nb)
+        mag = (0.0005 + 0.0035 * uniform(seed ^ (0x77 + i), nb)) / (32.0 if values == 256 else 1.0)
         sign = np.where(ints(seed ^ (0x99 + i), nb, 0, 1) == 0, -1.0, 1.0) if i else 1.0
         b[:, at:at + 2] = f16_bits((mag * sign).astype(np.float32)).view(np.uint8).reshape(nb, 2)
     return b.reshape(-1)
