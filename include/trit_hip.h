@@ -174,6 +174,16 @@ int trit_hip_layer_row(const TritHipLayer *layer, int index, float *out);
 
 void trit_hip_layer_free(TritHipLayer *layer);
 
+/* ---- f16 conversions (reference src/cpu/tensors.rs:542-595) ------------ */
+
+/* f32_to_f16 / f16_to_f32 of n values (host arrays) by the device's
+ * conversion -- the one the kernels use for Q8_0 scales, f16 weights and
+ * the f16 key/value caches: round to nearest even with subnormals and
+ * infinities, bit for bit Trit's for every value but NaN (a NaN stays a
+ * NaN; its payload bits are the hardware's). */
+int trit_hip_f32_to_f16(const float *in, int64_t n, uint16_t *out);
+int trit_hip_f16_to_f32(const uint16_t *in, int64_t n, float *out);
+
 /* ---- Decoder: CausalLm (reference src/models/parts/causal_lm.rs) ------- */
 
 typedef struct {

@@ -59,6 +59,8 @@ def _bind(L):
         "or_q8_0_parse": (None, [p, i64, p, p]),
         "or_q4_k_expand": (None, [p, i64, p]),
         "or_ggml_expand": (i, [i, p, i64, p]),
+        "or_f32_to_f16_n": (None, [p, i64, p]),
+        "or_f16_to_f32_n": (None, [p, i64, p]),
         "or_int8_new": (p, [i, i, i, i, i, p, p]),
         "or_int8_forward": (None, [p, p, i, p]),
         "or_int8_free": (None, [p]),
@@ -138,6 +140,41 @@ def q8_0_quantize(values: np.ndarray):
     scales = np.empty(v.size // 32, np.float32)
     lib().or_q8_0_quantize(ptr(v), v.size, ptr(codes), ptr(scales))
     return codes, scales
+
+
+def f32_to_f16(values) -> np.ndarray:
+    """f32_to_f16 (src/cpu/tensors.rs:542-573) of every value: f16 bits."""
+    v = np.ascontiguousarray(values, np.float32).reshape(-1)
+    out = np.empty(v.size, np.uint16)
+    lib().or_f32_to_f16_n(ptr(v), v.size, ptr(out))
+    return out
+
+
+def f16_to_f32(bits) -> np.ndarray:
+    """f16_to_f32 (src/cpu/tensors.rs:575-595) of every f16 bit pattern."""
+    b = np.ascontiguousarray(bits, np.uint16).reshape(-1)
+    out = np.empty(b.size, np.float32)
+    lib().or_f16_to_f32_n(ptr(b), b.size, ptr(out))
+    return out
+
+
+def f16_boundaries() -> np.ndarray:
+    """Every f32 value where f32 -> f16 rounding can turn: each finite f16
+    value, and the midpoint to the next one in magnitude with its f32
+    neighbours (ties to even, the subnormal steps, the overflow edge at
+    65520); then +-0, +-inf and NaNs."""
+    h = np.arange(0x7C00, dtype=np.uint32)  # non-negative finite f16 values
+    lo = h.astype(np.uint16).view(np.float16).astype(np.float64)
+    hi = (h + 1).astype(np.uint16).view(np.float16).astype(np.float64)  # 0x7C00 is +inf
+    hi[-1] = 65520.0 * 2 - 65504.0  # the step above 65504 (its midpoint is 65520)
+    mid = ((lo + hi) / 2).astype(np.float32)  # exact in f32
+    mb = mid.view(np.uint32)
+    vals = np.concatenate([lo.astype(np.float32).view(np.uint32), mb - 1, mb, mb + 1])
+    vals = np.unique(vals)
+    vals = np.concatenate([vals, vals | np.uint32(0x80000000)])
+    special = np.array([0x7F800000, 0xFF800000, 0x7FC00000, 0xFFC00001, 0x7F800001, 0x477FF000, 0x477FEFFF,
+                        0x00000001, 0x80000001, 0x33000000, 0x33000001, 0x387FE000], np.uint32)
+    return np.concatenate([vals, special]).view(np.float32)
 
 
 GGML_BLOCKS = {2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 12: (256, 144), 13: (256, 176), 14: (256, 210)}

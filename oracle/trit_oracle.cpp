@@ -1406,6 +1406,14 @@ void or_q4_k_expand(const uint8_t* blocks, int64_t nblocks, float* out) {
     }
 }
 
+// f32_to_f16 / f16_to_f32 (src/cpu/tensors.rs:542-595) over arrays.
+void or_f32_to_f16_n(const float* in, int64_t n, uint16_t* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = f32_to_f16(in[i]);
+}
+void or_f16_to_f32_n(const uint16_t* in, int64_t n, float* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = f16_to_f32(in[i]);
+}
+
 // ggml's other block types expanded to f32 (src/cpu/ggml_quants.rs:103-245,
 // ggml's dequantize_row_* in the same float order): Q4_0 (2), Q4_1 (3),
 // Q5_0 (6), Q5_1 (7), Q4_K (12), Q5_K (13), Q6_K (14). Returns 0, or -1

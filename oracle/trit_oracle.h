@@ -63,6 +63,9 @@ void or_q8_0_parse(const uint8_t* blocks, int64_t nblocks, int8_t* codes, float*
 /* GGUF Q4_K super-blocks (144 bytes per 256 values) to f32
  * (src/cpu/ggml_quants.rs:168-196). */
 void or_q4_k_expand(const uint8_t* blocks, int64_t nblocks, float* out);
+/* f32_to_f16 / f16_to_f32 over arrays (src/cpu/tensors.rs:542-595). */
+void or_f32_to_f16_n(const float* in, int64_t n, uint16_t* out);
+void or_f16_to_f32_n(const uint16_t* in, int64_t n, float* out);
 /* ggml's block types expanded to f32 (src/cpu/ggml_quants.rs:103-245):
  * Q4_0 2, Q4_1 3, Q5_0 6, Q5_1 7, Q4_K 12, Q5_K 13, Q6_K 14; -1 for others. */
 int or_ggml_expand(int type, const uint8_t* blocks, int64_t nblocks, float* out);

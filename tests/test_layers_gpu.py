@@ -285,6 +285,26 @@ def test_ggml_types(gpu, ggml_type, n, k, m, f32_math):
     assert bits_equal(layer.forward(x), want)
 
 
+def test_f16_conversions(gpu):
+    """The device's f16 conversions against the oracle's (Trit's f32_to_f16 /
+    f16_to_f32): all 65536 f16 patterns; every f32 value where rounding to
+    f16 can turn (each f16 value, each midpoint and its neighbours, both
+    signs, the subnormal steps and the overflow edge); and every 4093rd of
+    the 2^32 f32 patterns. Bit for bit but NaN, which stays NaN."""
+    print("case f16 conversions", flush=True)
+    h = np.arange(65536, dtype=np.uint16)
+    got, want = gpu.f16_to_f32(h), O.f16_to_f32(h)
+    nan = np.isnan(want)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    assert np.all(np.isnan(got[nan]))
+    sweep = (np.arange(0, 1 << 32, 4093, dtype=np.uint64)).astype(np.uint32).view(np.float32)
+    for v in (O.f16_boundaries(), sweep):
+        got, want = gpu.f32_to_f16(v), O.f32_to_f16(v)
+        nan = np.isnan(v)
+        assert np.array_equal(got[~nan], want[~nan])
+        assert np.all((got[nan] & 0x7C00) == 0x7C00) and np.all((got[nan] & 0x03FF) != 0)
+
+
 def test_errors(gpu):
     from trit_amd.hip import TritError
 

@@ -48,6 +48,24 @@ def test_f32_to_f16_rounding():
     assert np.array_equal(got, want)
 
 
+def test_f32_to_f16_boundaries():
+    """The oracle's f32 -> f16 at every rounding boundary (each f16 value,
+    each midpoint and its f32 neighbours, both signs) against numpy's IEEE
+    conversion, and f16 -> f32 of all 65536 patterns through the array entry."""
+    v = O.f16_boundaries()
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = v.astype(np.float16).view(np.uint16)
+    got = O.f32_to_f16(v)
+    nan = np.isnan(v)
+    assert np.array_equal(got[~nan], want[~nan])
+    assert np.all((got[nan] & 0x7C00) == 0x7C00) and np.all((got[nan] & 0x03FF) != 0)
+    h = np.arange(65536, dtype=np.uint16)
+    f = O.f16_to_f32(h)
+    ref = h.view(np.float16).astype(np.float32)
+    ok = ~np.isnan(ref)
+    assert np.array_equal(bits(f[ok]), bits(ref[ok])) and np.all(np.isnan(f[~ok]))
+
+
 def test_quantizer_known_answers():
     # Peak 127 gives scale 1, so each code is the value rounded half to even.
     x = np.zeros((1, 32), np.float32)

@@ -158,6 +158,17 @@ __global__ void requant_kernel(const uint8_t* __restrict__ blocks, int64_t nsub,
     }
 }
 
+// The library's f16 conversions (the hardware's, round to nearest even)
+// over arrays.
+__global__ void f32_to_f16_kernel(const float* __restrict__ in, int64_t n, uint16_t* __restrict__ out) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = f32_to_f16(in[i]);
+}
+__global__ void f16_to_f32_kernel(const uint16_t* __restrict__ in, int64_t n, float* __restrict__ out) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = f16_to_f32(in[i]);
+}
+
 __global__ void widen_scales_kernel(const uint16_t* __restrict__ in, int64_t n, float* __restrict__ out) {
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
         out[i] = f16_to_f32(in[i]);
@@ -447,6 +458,30 @@ int q8_from_blocks(int n, int k, const void* blocks, const float* bias, TritHipL
 
 }  // namespace
 
+namespace {
+
+// Host arrays through the device in chunks of 16 Mi values.
+template <typename In, typename Out, typename K>
+int convert(const In* in, int64_t n, Out* out, K kernel, const char* what) {
+    if (n < 0) fail(std::string(what) + ": negative count");
+    if (n && (!in || !out)) fail(std::string(what) + ": in or out is NULL");
+    const int64_t chunk = (int64_t)1 << 24;
+    const int64_t first = n < chunk ? n : chunk;
+    DeviceMemory din((size_t)first * sizeof(In)), dout((size_t)first * sizeof(Out));
+    hipStream_t s = stream();
+    for (int64_t at = 0; at < n; at += chunk) {
+        const int64_t c = n - at < chunk ? n - at : chunk;
+        TRIT_HIP(hipMemcpyAsync(din.ptr, in + at, (size_t)c * sizeof(In), hipMemcpyHostToDevice, s));
+        hipLaunchKernelGGL(kernel, dim3(1024), dim3(256), 0, s, din.as<In>(), c, dout.as<Out>());
+        TRIT_HIP(hipGetLastError());
+        TRIT_HIP(hipMemcpyAsync(out + at, dout.ptr, (size_t)c * sizeof(Out), hipMemcpyDeviceToHost, s));
+    }
+    TRIT_HIP(hipStreamSynchronize(s));
+    return 0;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* trit_hip_version(void) { return "trit_hip 0.1.0 (gfx950)"; }
@@ -566,6 +601,14 @@ int trit_hip_layer_ternary_base3(int n, int k, const uint8_t* packed, const floa
         }
         return ternary_from_codes(n, k, codes.data(), scales, out);
     });
+}
+
+int trit_hip_f32_to_f16(const float* in, int64_t n, uint16_t* out) {
+    return guard(-1, [&] { return convert(in, n, out, f32_to_f16_kernel, "f32_to_f16"); });
+}
+
+int trit_hip_f16_to_f32(const uint16_t* in, int64_t n, float* out) {
+    return guard(-1, [&] { return convert(in, n, out, f16_to_f32_kernel, "f16_to_f32"); });
 }
 
 int trit_hip_layer_q4_k(int n, int k, const void* blocks, TritHipLayer** out) {

@@ -97,6 +97,8 @@ def lib():
             "trit_hip_gguf_meta_str": (i, [p, C.c_char_p, C.POINTER(C.c_char_p)]),
             "trit_hip_decoder_from_gguf": (i, [C.c_char_p, C.c_char_p, C.POINTER(LmConfig), pp]),
             "trit_hip_attention": (i, [p, i, p, p, i, i, i, i, i, i, i, i, p]),
+            "trit_hip_f32_to_f16": (i, [p, C.c_int64, p]),
+            "trit_hip_f16_to_f32": (i, [p, C.c_int64, p]),
             "trit_hip_attention_steps": (i, [p, i, p, p, p, i, i, i, i, p]),
             "trit_hip_attention_steps_device": (i, [p, i, p, p, p, i, i, i, i, p, p]),
         }
@@ -136,6 +138,22 @@ def attention(q, k, v, heads, kv_heads, hd, causal=True, flags=0):
     out = np.empty((q.shape[0], heads * hd), np.float32)
     check(lib().trit_hip_attention(ptr(q), q.shape[1], ptr(k), ptr(v), k.shape[1], q.shape[0], k.shape[0], heads,
                                    kv_heads, hd, int(causal), flags, ptr(out)))
+    return out
+
+
+def f32_to_f16(values):
+    """f32 -> f16 bits on the device (trit_hip_f32_to_f16)."""
+    v = np.ascontiguousarray(values, np.float32).reshape(-1)
+    out = np.empty(v.size, np.uint16)
+    check(lib().trit_hip_f32_to_f16(ptr(v), v.size, ptr(out)))
+    return out
+
+
+def f16_to_f32(bits):
+    """f16 bits -> f32 on the device (trit_hip_f16_to_f32)."""
+    b = np.ascontiguousarray(bits, np.uint16).reshape(-1)
+    out = np.empty(b.size, np.float32)
+    check(lib().trit_hip_f16_to_f32(ptr(b), b.size, ptr(out)))
     return out
 
 
