@@ -1592,7 +1592,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     float best = -INFINITY;
     int index = INT_MAX;
     auto head_pass = [&](int p, uint4 (&wv)[S8]) {
-        // Trit's 16-lane f16 order (gemv_f16.hip): lane chain, then the tree.
+        // Trit's 16-lane f16 order (gemv_float.hip): lane chain, then the tree.
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < S8; ++j) {
@@ -1604,7 +1604,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             }
         }
         // Lane i adds lane i - 8, - 4, - 2, - 1 of its row (rotations): in
-        // lane 0 that is the xor tree of gemv_f16.hip, bit for bit (the
+        // lane 0 that is the xor tree of gemv_float.hip, bit for bit (the
         // pairs it adds are the same sums with their operands swapped).
         float v = acc;
         v = v + dpp<0x128>(v);
