@@ -21,6 +21,7 @@
 #ifndef TRIT_HIP_H
 #define TRIT_HIP_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -326,6 +327,49 @@ int trit_hip_attention_steps(const float *q, int qs, const float *const *keys, c
 int trit_hip_attention_steps_device(const float *q, int qs, const float *const *keys, const float *const *values,
                                     const int *tk, int sequences, int d, int heads, int kv_heads, float *out,
                                     void *stream);
+
+/* ---- Tokenizer (reference src/text/bpe.rs, src/text/mod.rs) ----------- */
+
+/* Byte-level BPE from a Hugging Face tokenizer.json (Bpe::open / Bpe::parse,
+ * reference src/text/bpe.rs:76-174): the vocabulary, the merges in rank
+ * order, the added (special) tokens, and Trit's Qwen or GPT-2 word split
+ * (chosen as Trit chooses it, by the Qwen regex in pre_tokenizer). Host
+ * code. */
+typedef struct TritHipBpe TritHipBpe;
+int trit_hip_bpe_open(const char *path, TritHipBpe **out);
+int trit_hip_bpe_parse(const char *json, size_t len, TritHipBpe **out);
+void trit_hip_bpe_free(TritHipBpe *bpe);
+/* Bpe::id (:176-183): the id of a token as the vocabulary writes it, or -1. */
+int trit_hip_bpe_id(const TritHipBpe *bpe, const char *token);
+/* Bpe::encode (:197-227; plain != 0: encode_plain, :229-237): the ids of
+ * `len` bytes of UTF-8 text, special tokens written in it becoming their
+ * ids unless plain. Writes up to cap ids and returns the count (which may
+ * exceed cap: call again with room), or -1. */
+int trit_hip_bpe_encode(const TritHipBpe *bpe, const char *text, size_t len, int plain, int32_t *out, int cap);
+/* Bpe::decode (:185-195): the text of ids without special tokens, a last
+ * character cut short dropped and other invalid bytes as U+FFFD. Writes up
+ * to cap - 1 bytes and a NUL; returns the text's length, or -1. */
+int64_t trit_hip_bpe_decode(const TritHipBpe *bpe, const int32_t *ids, int n, char *out, size_t cap);
+
+/* The prompt of Trit's transcript cleanup with S1-mini (Cleaner,
+ * reference src/cleanup.rs:19-21,156-158,199-215,280-301). _system: the
+ * ids of the fixed system turn that every call shares (the Prefix the
+ * cleaner makes once). _prompt: the ids of one call -- the system turn and
+ * the control line ("[Styling: ...] [Structure: ...] [Context: ...]";
+ * styling 0 casual, 1 semi-casual, 2 semi-formal, 3 formal; structure 0
+ * prose, 1 lists; context 0 general, 1 email), the transcript as plain text
+ * (a spoken "<|im_end|>" cannot end the turn), then the assistant turn with
+ * thinking off. Counts and capacity as trit_hip_bpe_encode. */
+int trit_hip_cleanup_system(const TritHipBpe *bpe, int32_t *out, int cap);
+int trit_hip_cleanup_prompt(const TritHipBpe *bpe, const char *transcript, size_t len, int styling, int structure,
+                            int context, int32_t *out, int cap);
+/* Cleaner::parts (reference src/cleanup.rs:240-278) of the trimmed
+ * transcript: whole sentences, or words of a sentence longer alone, joined
+ * with one space into parts of at most `limit` tokens (Trit's PART_TOKENS
+ * is 800). Writes up to cap bytes of the parts, each followed by a NUL, and
+ * returns their total bytes, or -1. */
+int64_t trit_hip_cleanup_parts(const TritHipBpe *bpe, const char *transcript, size_t len, int limit, char *out,
+                               size_t cap);
 
 /* ---- GGUF files (reference src/models/gguf/mod.rs:130-300) ------------- */
 

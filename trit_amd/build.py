@@ -13,7 +13,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "lib", "libtrit_hip.so")
-SOURCES = ["layer.hip", "gemv.hip", "gemv_decode.hip", "gemv_stream.hip", "gemv_float.hip", "gemm.hip", "decoder.hip", "decode_step.hip", "attention_mfma.hip", "gguf.hip"]
+SOURCES = ["layer.hip", "gemv.hip", "gemv_decode.hip", "gemv_stream.hip", "gemv_float.hip", "gemm.hip", "decoder.hip", "decode_step.hip", "attention_mfma.hip", "gguf.hip", "tokenizer.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -39,7 +39,7 @@ def build(verbose: bool = False, jobs: int = 0) -> str:
         path = os.path.join(CSRC, src)
         if not os.path.exists(path):
             raise RuntimeError(f"build: source {path} is missing")
-        obj = os.path.join(HERE, "lib", src.replace(".hip", ".o"))
+        obj = os.path.join(HERE, "lib", os.path.splitext(src)[0] + ".o")
         cmds.append([HIPCC, *FLAGS, "-c", path, "-o", obj])
         objs.append(obj)
     if verbose:

@@ -99,6 +99,15 @@ def lib():
             "trit_hip_attention": (i, [p, i, p, p, i, i, i, i, i, i, i, i, p]),
             "trit_hip_f32_to_f16": (i, [p, C.c_int64, p]),
             "trit_hip_f16_to_f32": (i, [p, C.c_int64, p]),
+            "trit_hip_bpe_open": (i, [C.c_char_p, pp]),
+            "trit_hip_bpe_parse": (i, [C.c_char_p, C.c_size_t, pp]),
+            "trit_hip_bpe_free": (None, [p]),
+            "trit_hip_bpe_id": (i, [p, C.c_char_p]),
+            "trit_hip_bpe_encode": (i, [p, C.c_char_p, C.c_size_t, i, p, i]),
+            "trit_hip_bpe_decode": (C.c_int64, [p, p, i, p, C.c_size_t]),
+            "trit_hip_cleanup_system": (i, [p, p, i]),
+            "trit_hip_cleanup_prompt": (i, [p, C.c_char_p, C.c_size_t, i, i, i, p, i]),
+            "trit_hip_cleanup_parts": (C.c_int64, [p, C.c_char_p, C.c_size_t, i, p, C.c_size_t]),
             "trit_hip_attention_steps": (i, [p, i, p, p, p, i, i, i, i, p]),
             "trit_hip_attention_steps_device": (i, [p, i, p, p, p, i, i, i, i, p, p]),
         }
@@ -365,6 +374,74 @@ class CausalLm:
     def free(self):
         if self.h:
             lib().trit_hip_decoder_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Bpe:
+    """Byte-level BPE from a tokenizer.json (src/text/bpe.rs): `encode`,
+    `encode_plain`, `decode`, `id`, as Trit's Bpe."""
+
+    def __init__(self, path=None, text=None):
+        out = C.c_void_p()
+        if text is not None:
+            b = text.encode() if isinstance(text, str) else bytes(text)
+            check(lib().trit_hip_bpe_parse(b, len(b), C.byref(out)))
+        else:
+            check(lib().trit_hip_bpe_open(str(path).encode(), C.byref(out)))
+        self.h = out
+
+    @staticmethod
+    def _ids(call):
+        n = check(call(None, 0))
+        out = np.empty(max(n, 1), np.int32)
+        check(call(ptr(out), n))
+        return out[:n].tolist()
+
+    def encode(self, text, plain=False):
+        b = text.encode()
+        return self._ids(lambda out, cap: lib().trit_hip_bpe_encode(self.h, b, len(b), int(plain), out, cap))
+
+    def encode_plain(self, text):
+        return self.encode(text, plain=True)
+
+    def decode(self, ids):
+        a = np.ascontiguousarray(ids, np.int32)
+        n = check(lib().trit_hip_bpe_decode(self.h, ptr(a), a.size, None, 0))
+        buf = C.create_string_buffer(n + 1)
+        check(lib().trit_hip_bpe_decode(self.h, ptr(a), a.size, buf, n + 1))
+        return buf.raw[:n].decode()
+
+    def id(self, token):
+        v = lib().trit_hip_bpe_id(self.h, token.encode())
+        return None if v < 0 else v
+
+    def cleanup_system(self):
+        """The ids of the cleanup's shared system turn (src/cleanup.rs:156-158)."""
+        return self._ids(lambda out, cap: lib().trit_hip_cleanup_system(self.h, out, cap))
+
+    def cleanup_prompt(self, transcript, styling=2, structure=0, context=0):
+        """The ids of one cleanup call (Cleaner::clean_part, src/cleanup.rs:280-301)."""
+        b = transcript.encode()
+        return self._ids(lambda out, cap: lib().trit_hip_cleanup_prompt(self.h, b, len(b), styling, structure,
+                                                                        context, out, cap))
+
+    def cleanup_parts(self, transcript, limit=800):
+        """Cleaner::parts of the trimmed transcript (src/cleanup.rs:240-278)."""
+        b = transcript.encode()
+        n = check(lib().trit_hip_cleanup_parts(self.h, b, len(b), limit, None, 0))
+        buf = C.create_string_buffer(max(n, 1))
+        check(lib().trit_hip_cleanup_parts(self.h, b, len(b), limit, buf, n))
+        return [p.decode() for p in buf.raw[:n].split(b"\0")[:-1]]
+
+    def free(self):
+        if self.h:
+            lib().trit_hip_bpe_free(self.h)
             self.h = None
 
     def __del__(self):
