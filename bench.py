@@ -468,6 +468,62 @@ def _timed(fn):
     return time.perf_counter() - t0
 
 
+def load_times(w, prompt):
+    """Seconds to a ready decoder of the workload's shape: from host layers
+    (Q8_0 blocks and the f16 table as Trit holds them), from a GGUF file
+    (read, split and uploaded), and from the device weight-cache file
+    (uploaded without converting); with the file sizes and the time to read
+    each file alone (its pages were just written, so reads come from the
+    page cache). The decoders' logits for the prompt agree bit for bit."""
+    import tempfile
+
+    from trit_amd import gguf_writer as G
+
+    def best(fn, n=3):
+        return min(_timed(fn) for _ in range(n))
+
+    def read_file(path):
+        with open(path, "rb") as f:
+            while f.read(64 << 20):
+                pass
+
+    out = {}
+    with tempfile.TemporaryDirectory() as tmp:
+        gguf = os.path.join(tmp, "lm.gguf")
+        cache = os.path.join(tmp, "weights.bin")
+        G.write_decoder(gguf, w)
+        held = []
+
+        def from_layers():
+            lm, linears, embed = build_layers(w)
+            for L in linears:
+                L.free()
+            embed.free()
+            held.append(lm)
+
+        out["from_layers_s"] = round(best(from_layers), 3)
+        out["from_gguf_s"] = round(best(lambda: held.append(hip.CausalLm.from_gguf(gguf))), 3)
+        held[-1].save(cache)
+        out["from_cache_s"] = round(best(lambda: held.append(hip.CausalLm.load(cache))), 3)
+        out["gguf_bytes"] = os.path.getsize(gguf)
+        out["cache_bytes"] = os.path.getsize(cache)
+        out["read_gguf_s"] = round(best(lambda: read_file(gguf)), 3)
+        out["read_cache_s"] = round(best(lambda: read_file(cache)), 3)
+        logits = []
+        for lm in (held[0], held[3], held[-1]):
+            s = lm.session(len(prompt) + 1, hip.EXACT)
+            logits.append(s.prefill(prompt))
+            s.free()
+        out["same_logits"] = bool(all(np.array_equal(logits[0].view(np.uint32), x.view(np.uint32))
+                                      for x in logits[1:]))
+        for lm in held:
+            lm.free()
+    out["note"] = ("seconds to a ready decoder (best of 3): host layers through trit_hip_layer_q8_0/f16 + "
+                   "trit_hip_decoder_new; trit_hip_decoder_from_gguf; trit_hip_decoder_load of the file "
+                   "trit_hip_decoder_save wrote; read_*: the file read alone")
+    return out
+
+
 def cpu_baseline(w, prompt, steps, rounds):
     """Trit's loop on the oracle (Trit's f32 caches): the prompt once, then
     `rounds` runs of the greedy steps from the same prompt caches (the
@@ -514,6 +570,9 @@ def main():
     ap.add_argument("--cpu-rounds", type=int, default=5, help="timed runs of the CPU baseline's greedy steps")
     ap.add_argument("--configs-pass", action="store_true",
                     help="only the per-product configuration lines (for profiler runs)")
+    ap.add_argument("--load-pass", action="store_true",
+                    help="only the load times of the workload's decoder: from host layers, from a GGUF file, "
+                         "from the device weight-cache file")
     ap.add_argument("--profile-pass", action="store_true",
                     help="only the roofline sweeps and a 256 MiB device copy (the counter scale for "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs)")
@@ -532,6 +591,9 @@ def main():
     hip.init(0)
     if args.configs_pass:
         print(json.dumps({"configs_pass": True, "configs": config_lines(Hip(), sweeps=args.sweeps)}), flush=True)
+        return
+    if args.load_pass:
+        print(json.dumps({"load_pass": True, **load_times(w, prompt)}), flush=True)
         return
     lm, linears, embed = build_layers(w)
     if args.profile_pass:

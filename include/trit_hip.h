@@ -211,6 +211,17 @@ int trit_hip_decoder_new(const TritHipLmConfig *config, const TritHipLayer *cons
                          TritHipDecoder **out);
 void trit_hip_decoder_free(TritHipDecoder *decoder);
 
+/* The device weight-cache file (the role of Trit's Store cache file,
+ * reference src/cpu/store.rs:1-16,369-428,508-524): _save writes a
+ * decoder's device layouts (repacked and requantized as they sit in HBM)
+ * to `path`, keyed by this library's version and target; _load uploads
+ * them into a new decoder without converting anything, and fails on a file
+ * of another key or format, or one whose checksum does not hold (a stale
+ * or damaged cache never changes a product). config (optional) receives
+ * the decoder's config. MLP scales are not part of the file. */
+int trit_hip_decoder_save(const TritHipDecoder *decoder, const char *path);
+int trit_hip_decoder_load(const char *path, TritHipLmConfig *config, TritHipDecoder **out);
+
 /* CausalLm::set_ffn_scales (reference causal_lm.rs:304-307,458-464):
  * layers x d f32 scales on each layer's normed MLP input (Voxtral
  * Realtime's 1 + ada(t)); NULL removes them. Sessions see the change from

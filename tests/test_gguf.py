@@ -8,7 +8,7 @@ import struct
 import numpy as np
 import pytest
 
-from tests import gguf_writer as G
+from trit_amd import gguf_writer as G
 from trit_amd import hip
 
 TYPES = "F32, F16, BF16, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K, and Q6_K"

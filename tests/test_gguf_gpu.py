@@ -7,7 +7,7 @@ mixed ggml types against the oracle."""
 import numpy as np
 import pytest
 
-from tests import gguf_writer as G
+from trit_amd import gguf_writer as G
 from trit_amd import hip, model, synth
 
 pytestmark = pytest.mark.gpu
@@ -173,3 +173,43 @@ def test_gguf_types_against_oracle(weights, tmp_path):
     G.write_decoder(path, weights, untied_head=weights.embed, replace=repl)
     with pytest.raises(hip.TritError, match="stacked rows take one type"):
         hip.CausalLm.from_gguf(path)
+
+
+def test_weight_cache(weights, tmp_path):
+    """The device weight-cache file: a decoder saved and loaded again (Q8_0,
+    Q4_K and float-math layers, an untied head) gives the same logits bit
+    for bit and the same tokens; a file of another key, a damaged one and a
+    cut one fail the load."""
+    print("case weight cache file", flush=True)
+    c = QS
+    d, ffn = c["d"], c["ffn"]
+    gate = synth.q4_k_blocks(synth.seed_for(93, 911), ffn, d)
+    up = synth.q4_k_blocks(synth.seed_for(93, 912), ffn, d)
+    head = synth.activations(synth.seed_for(93, 913), c["vocab"], d) * np.float32(0.1)
+    path = tmp_path / "lm.gguf"
+    G.write_decoder(path, weights, untied_head=weights.embed,
+                    replace={"dec.blocks.1.ffn.gate.weight": (G.GGML["Q4_K"], [d, ffn], gate.tobytes()),
+                             "dec.blocks.1.ffn.up.weight": (G.GGML["Q4_K"], [d, ffn], up.tobytes()),
+                             "dec.output.weight": (G.GGML["F32"], [d, c["vocab"]], head.tobytes())})
+    lm = hip.CausalLm.from_gguf(path)
+    cache = tmp_path / "weights.bin"
+    lm.save(cache)
+    again = hip.CausalLm.load(cache)
+    assert again.cfg["d"] == d and again.cfg["layers"] == c["layers"]
+    p = synth.prompt(96, 30, c["vocab"])
+    a, ta = exact_logits(lm, p)
+    b, tb = exact_logits(again, p)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert ta.tolist() == tb.tolist()
+    s1, s2 = lm.session(64, 0), again.session(64, 0)
+    s1.prefill(p, want_logits=False)
+    s2.prefill(p, want_logits=False)
+    assert s1.generate(12).tolist() == s2.generate(12).tolist()
+    raw = bytearray(cache.read_bytes())
+    bad = tmp_path / "bad.bin"
+    for what, data in (("damaged", raw[:len(raw) // 2] + bytes([raw[len(raw) // 2] ^ 1]) + raw[len(raw) // 2 + 1:]),
+                       ("cut short", raw[:len(raw) - 100]),
+                       ("made by", raw[:16] + b"X" + raw[17:])):
+        bad.write_bytes(bytes(data))
+        with pytest.raises(hip.TritError, match=what):
+            hip.CausalLm.load(bad)

@@ -17,6 +17,7 @@
 // computes it with a fixed tree.
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 
@@ -1653,6 +1654,245 @@ int trit_hip_decoder_new(const TritHipLmConfig* config, const TritHipLayer* cons
 }
 
 void trit_hip_decoder_free(TritHipDecoder* decoder) { delete decoder; }
+
+// ---- The device weight-cache file --------------------------------------
+//
+// A decoder's device layouts as they sit in HBM (codes repacked, Q4_K and
+// the other block types already requantized, f16 tables in lane chains),
+// so a later load uploads them without converting. Layout: "TRITHIPW", a
+// format version, the library's key (its version and target), the config,
+// the norms as trit_hip_decoder_new takes them, the 4 linears of each layer,
+// the embedding and the head (when untied), each as kind, n, k, group and
+// the byte runs of its codes, scales and bias; then a 64-bit checksum of
+// everything before it. Stale or damaged files fail the load.
+
+}  // extern "C"
+
+namespace trit {
+namespace {
+
+constexpr char CACHE_MAGIC[8] = {'T', 'R', 'I', 'T', 'H', 'I', 'P', 'W'};
+constexpr uint32_t CACHE_FORMAT = 1;
+
+struct Hash {
+    uint64_t h = 0x9E3779B97F4A7C15ull;
+    uint64_t tail = 0;
+    int tail_bytes = 0;
+    void add(const void* data, size_t n) {
+        const uint8_t* p = (const uint8_t*)data;
+        while (n && tail_bytes) {
+            tail |= (uint64_t)*p++ << (8 * tail_bytes);
+            --n;
+            if (++tail_bytes == 8) {
+                word(tail);
+                tail = 0;
+                tail_bytes = 0;
+            }
+        }
+        for (; n >= 8; n -= 8, p += 8) {
+            uint64_t w;
+            std::memcpy(&w, p, 8);
+            word(w);
+        }
+        while (n--) tail |= (uint64_t)*p++ << (8 * tail_bytes++);
+    }
+    void word(uint64_t w) {
+        h ^= w;
+        h *= 0x100000001B3ull;
+        h ^= h >> 29;
+    }
+    uint64_t value() const {
+        uint64_t v = h;
+        if (tail_bytes) {
+            v ^= tail;
+            v *= 0x100000001B3ull;
+        }
+        return v ^ (v >> 32);
+    }
+};
+
+struct CacheWriter {
+    FILE* f;
+    Hash hash;
+    void put(const void* p, size_t n) {
+        if (n && std::fwrite(p, 1, n, f) != n) fail("cache: write failed");
+        hash.add(p, n);
+    }
+    template <class T>
+    void val(T v) {
+        put(&v, sizeof v);
+    }
+    void device(const DeviceMemory& m) {
+        val<uint64_t>(m.bytes);
+        std::vector<uint8_t> host(std::min<size_t>(m.bytes, (size_t)64 << 20));
+        for (size_t at = 0; at < m.bytes; at += host.size()) {
+            const size_t c = std::min(host.size(), m.bytes - at);
+            TRIT_HIP(hipMemcpy(host.data(), (const uint8_t*)m.ptr + at, c, hipMemcpyDeviceToHost));
+            put(host.data(), c);
+        }
+    }
+    void layer(const Layer& L) {
+        val<int32_t>(L.kind);
+        val<int32_t>(L.n);
+        val<int32_t>(L.k);
+        val<int32_t>(L.group);
+        device(L.codes);
+        device(L.scales);
+        device(L.bias);
+    }
+};
+
+struct CacheReader {
+    FILE* f;
+    Hash hash;
+    const char* path;
+    void get(void* p, size_t n) {
+        if (n && std::fread(p, 1, n, f) != n) fail(std::string(path) + ": the cache file is cut short");
+        hash.add(p, n);
+    }
+    template <class T>
+    T val() {
+        T v;
+        get(&v, sizeof v);
+        return v;
+    }
+    void device(DeviceMemory& m, size_t limit) {
+        const uint64_t bytes = val<uint64_t>();
+        if (bytes > limit) fail(std::string(path) + ": a buffer of the cache file is larger than its layer");
+        m.alloc(bytes);
+        std::vector<uint8_t> host(std::min<size_t>(bytes, (size_t)64 << 20));
+        for (size_t at = 0; at < bytes; at += host.size()) {
+            const size_t c = std::min<size_t>(host.size(), bytes - at);
+            get(host.data(), c);
+            TRIT_HIP(hipMemcpy((uint8_t*)m.ptr + at, host.data(), c, hipMemcpyHostToDevice));
+        }
+    }
+    LayerRef layer() {
+        auto L = std::make_shared<Layer>();
+        L->kind = val<int32_t>();
+        L->n = val<int32_t>();
+        L->k = val<int32_t>();
+        L->group = val<int32_t>();
+        if (L->kind < Q8_0 || L->kind > Q8_F32 || L->n <= 0 || L->k <= 0)
+            fail(std::string(path) + ": a layer of the cache file is not valid");
+        const size_t limit = (size_t)L->n * L->k * 4 + (size_t)L->n * 4 + 64;
+        device(L->codes, limit);
+        device(L->scales, limit);
+        device(L->bias, (size_t)L->n * 4);
+        return L;
+    }
+};
+
+std::string cache_key() { return trit_hip_version(); }
+
+}  // namespace
+}  // namespace trit
+
+extern "C" {
+
+int trit_hip_decoder_save(const TritHipDecoder* decoder, const char* path) {
+    return guard(-1, [&] {
+        if (!decoder || !path) fail("cache: decoder or path is NULL");
+        const DecoderImpl& D = *decoder->impl;
+        const auto& c = D.c;
+        const std::string tmp = std::string(path) + ".tmp";
+        FILE* f = std::fopen(tmp.c_str(), "wb");
+        if (!f) fail(std::string("cache: cannot write ") + tmp);
+        try {
+            CacheWriter w{f};
+            w.put(CACHE_MAGIC, 8);
+            w.val<uint32_t>(CACHE_FORMAT);
+            const std::string key = cache_key();
+            w.val<uint32_t>((uint32_t)key.size());
+            w.put(key.data(), key.size());
+            w.val<uint32_t>((uint32_t)sizeof(TritHipLmConfig));
+            w.put(&c, sizeof c);
+            // The norms as the caller gave them: attn, mlp, [q, k] a layer; final.
+            std::vector<float> all(D.norms.bytes / 4), norms;
+            TRIT_HIP(hipMemcpy(all.data(), D.norms.ptr, D.norms.bytes, hipMemcpyDeviceToHost));
+            for (int l = 0; l < c.layers; ++l) {
+                const float* at = all.data() + l * D.layer_norm_stride;
+                norms.insert(norms.end(), at, at + 2 * c.d + (c.qk_norm ? 2 * c.head_dim : 0));
+            }
+            const float* fin = all.data() + c.layers * D.layer_norm_stride;
+            norms.insert(norms.end(), fin, fin + c.d);
+            w.val<uint64_t>(norms.size());
+            w.put(norms.data(), norms.size() * 4);
+            for (int l = 0; l < c.layers; ++l) {
+                w.layer(*D.qkv[l]);
+                w.layer(*D.o[l]);
+                w.layer(*D.gate_up[l]);
+                w.layer(*D.down[l]);
+            }
+            w.layer(*D.embed);
+            w.val<uint8_t>(D.head ? 1 : 0);
+            if (D.head) w.layer(*D.head);
+            const uint64_t sum = w.hash.value();
+            if (std::fwrite(&sum, 8, 1, f) != 1) fail("cache: write failed");
+        } catch (...) {
+            std::fclose(f);
+            std::remove(tmp.c_str());
+            throw;
+        }
+        if (std::fclose(f) != 0 || std::rename(tmp.c_str(), path) != 0) {
+            std::remove(tmp.c_str());
+            fail(std::string("cache: cannot write ") + path);
+        }
+        return 0;
+    });
+}
+
+int trit_hip_decoder_load(const char* path, TritHipLmConfig* config, TritHipDecoder** out) {
+    return guard(-1, [&] {
+        if (!path || !out) fail("cache: path or out is NULL");
+        FILE* f = std::fopen(path, "rb");
+        if (!f) fail(std::string("cache: cannot read ") + path);
+        std::vector<TritHipLayer*> handles;
+        auto cleanup = [&] {
+            for (TritHipLayer* h : handles) trit_hip_layer_free(h);
+            std::fclose(f);
+        };
+        try {
+            CacheReader r{f, {}, path};
+            char magic[8];
+            r.get(magic, 8);
+            if (std::memcmp(magic, CACHE_MAGIC, 8) != 0) fail(std::string(path) + ": not a trit_hip weight cache");
+            if (r.val<uint32_t>() != CACHE_FORMAT) fail(std::string(path) + ": another cache format");
+            const uint32_t klen = r.val<uint32_t>();
+            if (klen > 256) fail(std::string(path) + ": not a trit_hip weight cache");
+            std::string key(klen, '\0');
+            r.get(key.data(), klen);
+            if (key != cache_key())
+                fail(std::string(path) + ": made by " + key + ", not by " + cache_key() + " (build it again)");
+            if (r.val<uint32_t>() != sizeof(TritHipLmConfig)) fail(std::string(path) + ": another config layout");
+            TritHipLmConfig c;
+            r.get(&c, sizeof c);
+            if (c.layers <= 0 || c.layers > 4096 || c.d <= 0) fail(std::string(path) + ": a bad config");
+            const uint64_t nn = r.val<uint64_t>();
+            if (nn > (uint64_t)(c.layers + 1) * (2 * (uint64_t)c.d + 2 * (uint64_t)c.head_dim))
+                fail(std::string(path) + ": a bad norm count");
+            std::vector<float> norms(nn);
+            r.get(norms.data(), nn * 4);
+            for (int i = 0; i < 4 * c.layers + 1; ++i) handles.push_back(layer_handle(r.layer()));
+            if (r.val<uint8_t>()) handles.push_back(layer_handle(r.layer()));
+            const uint64_t want = r.hash.value();
+            uint64_t sum = 0;
+            if (std::fread(&sum, 8, 1, f) != 1 || sum != want)
+                fail(std::string(path) + ": the cache file is damaged (checksum)");
+            TritHipDecoder* dec = nullptr;
+            const TritHipLayer* head = handles.size() > (size_t)(4 * c.layers + 1) ? handles.back() : nullptr;
+            if (trit_hip_decoder_new(&c, handles.data(), norms.data(), handles[4 * c.layers], head, &dec) != 0)
+                fail(error_text());
+            if (config) *config = c;
+            *out = dec;
+        } catch (...) {
+            cleanup();
+            throw;
+        }
+        cleanup();  // the decoder holds its layers
+        return 0;
+    });
+}
 
 int trit_hip_decoder_set_ffn_scales(TritHipDecoder* decoder, const float* scales) {
     return guard(-1, [&] {

@@ -211,4 +211,5 @@ void float_row(const Layer& L, int index, float* out, hipStream_t s);
 struct TritHipLayer;
 namespace trit {
 LayerRef layer_ref(const TritHipLayer* handle);
+TritHipLayer* layer_handle(LayerRef layer);
 }  // namespace trit

@@ -783,4 +783,5 @@ void trit_hip_layer_free(TritHipLayer* layer) { delete layer; }
 
 namespace trit {
 LayerRef layer_ref(const TritHipLayer* h) { return h ? h->layer : nullptr; }
+TritHipLayer* layer_handle(LayerRef L) { return new TritHipLayer{std::move(L)}; }
 }  // namespace trit

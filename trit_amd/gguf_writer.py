@@ -1,4 +1,4 @@
-"""A GGUF v3 writer for tests: metadata of every GGUF type, tensors at
+"""A GGUF v3 writer (tests and the load-time measurement): metadata of every GGUF type, tensors at
 aligned offsets (the format the reference reads, src/models/gguf/mod.rs:
 130-226), and a decoder laid out as transcribe.cpp writes a Qwen3-ASR
 language model (`stt.qwen3_asr.decoder.*` keys, `dec.*` tensors,

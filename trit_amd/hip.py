@@ -74,6 +74,8 @@ def lib():
             "trit_hip_layer_free": (None, [p]),
             "trit_hip_decoder_new": (i, [C.POINTER(LmConfig), p, p, p, p, pp]),
             "trit_hip_decoder_free": (None, [p]),
+            "trit_hip_decoder_save": (i, [p, C.c_char_p]),
+            "trit_hip_decoder_load": (i, [C.c_char_p, C.POINTER(LmConfig), pp]),
             "trit_hip_decoder_set_ffn_scales": (i, [p, p]),
             "trit_hip_session_generate_additive": (i, [p, p, i, p, i, p, i, p]),
             "trit_hip_prefix_new": (i, [p, p, i, i, pp]),
@@ -323,12 +325,30 @@ class CausalLm:
         check(lib().trit_hip_decoder_from_gguf(str(path).encode(), prefix.encode() if prefix else None,
                                                C.byref(c), C.byref(out)))
         self.h = out
-        self.cfg = dict(d=c.d, ffn=c.ffn, layers=c.layers, heads=c.heads, kv_heads=c.kv_heads,
-                        head_dim=c.head_dim, vocab=c.vocab, eps=c.eps, rope_base=c.rope_base, qk_norm=c.qk_norm,
-                        embedding_multiplier=c.embedding_multiplier,
-                        attention_multiplier=c.attention_multiplier or None,
-                        residual_multiplier=c.residual_multiplier, logits_scaling=c.logits_scaling)
+        self.cfg = cls._cfg_of(c)
         return self
+
+    def save(self, path):
+        """The device layouts to a weight-cache file (trit_hip_decoder_save)."""
+        check(lib().trit_hip_decoder_save(self.h, str(path).encode()))
+
+    @classmethod
+    def load(cls, path):
+        """A decoder from a weight-cache file (trit_hip_decoder_load)."""
+        self = cls.__new__(cls)
+        c = LmConfig()
+        out = C.c_void_p()
+        check(lib().trit_hip_decoder_load(str(path).encode(), C.byref(c), C.byref(out)))
+        self.h = out
+        self.cfg = cls._cfg_of(c)
+        return self
+
+    @staticmethod
+    def _cfg_of(c):
+        return dict(d=c.d, ffn=c.ffn, layers=c.layers, heads=c.heads, kv_heads=c.kv_heads, head_dim=c.head_dim,
+                    vocab=c.vocab, eps=c.eps, rope_base=c.rope_base, qk_norm=c.qk_norm,
+                    embedding_multiplier=c.embedding_multiplier, attention_multiplier=c.attention_multiplier or None,
+                    residual_multiplier=c.residual_multiplier, logits_scaling=c.logits_scaling)
 
     def session(self, max_positions, flags=0):
         return Session(self, max_positions, flags)
