@@ -60,6 +60,9 @@ def _bind(L):
         "or_q4_k_expand": (None, [p, i64, p]),
         "or_ggml_expand": (i, [i, p, i64, p]),
         "or_f32_to_f16_n": (None, [p, i64, p]),
+        "or_gelu": (None, [p, i64]),
+        "or_layer_norm": (None, [p, i, i, p, p, f, p]),
+        "or_conv_columns": (None, [p, i, i, i, i, i, i, p]),
         "or_f16_to_f32_n": (None, [p, i64, p]),
         "or_int8_new": (p, [i, i, i, i, i, p, p]),
         "or_int8_forward": (None, [p, p, i, p]),
@@ -140,6 +143,66 @@ def q8_0_quantize(values: np.ndarray):
     scales = np.empty(v.size // 32, np.float32)
     lib().or_q8_0_quantize(ptr(v), v.size, ptr(codes), ptr(scales))
     return codes, scales
+
+
+def gelu(x):
+    """The exact GELU as every Trit path computes it (src/cpu/v2/activation.rs:33-39)."""
+    x = np.array(x, np.float32, copy=True, order="C")
+    lib().or_gelu(ptr(x), x.size)
+    return x
+
+
+def layer_norm(x, w, b, eps=1e-5):
+    """Norm::apply (src/layers.rs:50-121): rows of len(w)."""
+    w = np.ascontiguousarray(w, np.float32)
+    d = w.size
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, d)
+    b = np.ascontiguousarray(b, np.float32)
+    out = np.empty_like(x)
+    lib().or_layer_norm(ptr(x), x.shape[0], d, ptr(w), ptr(b), eps, ptr(out))
+    return out
+
+
+def conv_columns(x, kernel, stride, pad, out_frames):
+    """conv_columns (src/layers.rs:613-634) of x (frames x channels)."""
+    x = np.ascontiguousarray(x, np.float32)
+    frames, channels = x.shape
+    out = np.empty((out_frames, channels * kernel), np.float32)
+    lib().or_conv_columns(ptr(x), frames, channels, kernel, stride, pad, out_frames, ptr(out))
+    return out
+
+
+class Encoder:
+    """Encoder::encode (src/models/parts/audio_encoder.rs:111-138), the
+    Whisper encoder Voxtral and MOSS run, composed of the oracle's pieces:
+    im2col (kernel 3, stride 1, pad 1) -> conv1 -> GELU -> im2col (stride 2)
+    -> conv2 -> GELU -> + learned positions; per layer a pre-norm attention
+    block (stacked q/k/v, every position sees every other) and a pre-norm
+    GELU MLP, each added to the rows; then the final norm. `products` are
+    callables x -> x W^T + bias (the layer's own kind and order): conv1,
+    conv2, then qkv, out, fc1, fc2 of each layer; `norms` per layer
+    (attn w, b, ffn w, b), then the final (w, b)."""
+
+    def __init__(self, cfg, products, positions, norms):
+        self.cfg, self.products, self.positions, self.norms = cfg, products, positions, norms
+
+    def encode(self, mel):
+        c = self.cfg
+        d, P, heads = c["d"], c["positions"], c["heads"]
+        frames = 2 * P
+        mel = np.ascontiguousarray(mel, np.float32).reshape(frames, c["mels"])
+        h = gelu(self.products[0](conv_columns(mel, 3, 1, 1, frames)))
+        x = gelu(self.products[1](conv_columns(h, 3, 2, 1, P)))
+        x = (x + np.asarray(self.positions, np.float32).reshape(P, d)).astype(np.float32)
+        hd = d // heads
+        for l in range(c["layers"]):
+            qkv_p, out_p, fc1_p, fc2_p = self.products[2 + 4 * l:6 + 4 * l]
+            aw, ab, fw, fb = self.norms[4 * l:4 * l + 4]
+            qkv = qkv_p(layer_norm(x, aw, ab))
+            att = attention(qkv[:, :d], qkv[:, d:2 * d], qkv[:, 2 * d:], heads, heads, hd, causal=False)
+            x = (x + out_p(att)).astype(np.float32)
+            x = (x + fc2_p(gelu(fc1_p(layer_norm(x, fw, fb))))).astype(np.float32)
+        return layer_norm(x, self.norms[-2], self.norms[-1])
 
 
 def f32_to_f16(values) -> np.ndarray:

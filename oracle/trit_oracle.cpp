@@ -125,6 +125,22 @@ float exp_contract(float x) {
 
 float silu_one(float v) { return v / (1.0f + exp_contract(0.0f - v)); }
 
+// Numerical Recipes' erfcc coefficients, Horner order (src/cpu/activation.rs:15-28).
+constexpr float ERFC[10] = {0.17087277f, -0.82215223f, 1.4885159f, -1.135204f, 0.27886807f,
+                            -0.18628806f, 0.09678418f, 0.37409196f, 1.0000237f, -1.2655122f};
+constexpr float FRAC_1_SQRT_2 = 0.70710678118654752440f;
+
+// The exact GELU in the fused form every path gives (src/cpu/v2/activation.rs:
+// 33-39): v * erfc(-v / sqrt 2) / 2, erfc(z) = t * exp(-z^2 + P(t)).
+float gelu_one(float v) {
+    const float z = std::fabs(v) * FRAC_1_SQRT_2;
+    const float t = 1.0f / std::fmaf(z, 0.5f, 1.0f);
+    float p = 0.0f;
+    for (float c : ERFC) p = std::fmaf(p, t, c);
+    const float tail = t * exp_contract(std::fmaf(-z, z, p));
+    return (0.5f * v) * (v >= 0.0f ? 2.0f - tail : tail);
+}
+
 AVX512 __m512 exp512(__m512 x) {
     x = _mm512_min_ps(_mm512_max_ps(x, _mm512_set1_ps(EXP_LOW)), _mm512_set1_ps(EXP_HIGH));
     __m512i n_int = _mm512_cvtps_epi32(_mm512_mul_ps(x, _mm512_set1_ps(LOG2E)));
@@ -1404,6 +1420,50 @@ void or_q4_k_expand(const uint8_t* blocks, int64_t nblocks, float* out) {
             q += 32;
         }
     }
+}
+
+// ------------------------------------------------------------- encoder ---
+void or_gelu(float* values, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) values[i] = gelu_one(values[i]);
+}
+
+// Norm::apply (src/layers.rs:50-64,84-121): mean and variance each summed
+// in 32 lanes (lane j takes values j, j+32, ... in order), the lanes added
+// in order, then the tail; out = (v - mean) * inv * w + b.
+void or_layer_norm(const float* x, int rows, int d, const float* w, const float* b, float eps, float* out) {
+    auto lane_sum = [&](const float* row, auto term) {
+        float lanes[32] = {0};
+        const int whole = d / 32 * 32;
+        for (int i = 0; i < whole; i += 32)
+            for (int j = 0; j < 32; ++j) lanes[j] += term(row[i + j]);
+        float s = 0.0f;
+        for (int j = 0; j < 32; ++j) s += lanes[j];
+        float t = 0.0f;
+        for (int i = whole; i < d; ++i) t += term(row[i]);
+        return s + t;
+    };
+    for (int r = 0; r < rows; ++r) {
+        const float* row = x + (size_t)r * d;
+        const float n = (float)d;
+        const float mean = lane_sum(row, [](float v) { return v; }) / n;
+        const float var = lane_sum(row, [&](float v) { return (v - mean) * (v - mean); }) / n;
+        const float inv = 1.0f / std::sqrt(var + eps);
+        float* o = out + (size_t)r * d;
+        for (int i = 0; i < d; ++i) o[i] = (row[i] - mean) * inv * w[i] + b[i];
+    }
+}
+
+// conv_columns (src/layers.rs:613-634): output row t holds x[t*stride + tap
+// - pad][c] at c*kernel + tap; outside the frames, zero.
+void or_conv_columns(const float* x, int frames, int channels, int kernel, int stride, int pad, int out_frames,
+                     float* out) {
+    for (int t = 0; t < out_frames; ++t)
+        for (int tap = 0; tap < kernel; ++tap) {
+            const long src = (long)t * stride + tap - pad;
+            for (int c = 0; c < channels; ++c)
+                out[((size_t)t * channels + c) * kernel + tap] =
+                    src >= 0 && src < frames ? x[(size_t)src * channels + c] : 0.0f;
+        }
 }
 
 // f32_to_f16 / f16_to_f32 (src/cpu/tensors.rs:542-595) over arrays.

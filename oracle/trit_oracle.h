@@ -63,6 +63,13 @@ void or_q8_0_parse(const uint8_t* blocks, int64_t nblocks, int8_t* codes, float*
 /* GGUF Q4_K super-blocks (144 bytes per 256 values) to f32
  * (src/cpu/ggml_quants.rs:168-196). */
 void or_q4_k_expand(const uint8_t* blocks, int64_t nblocks, float* out);
+/* The audio encoder's pieces (src/models/parts/audio_encoder.rs): the exact
+ * GELU (src/cpu/v2/activation.rs:33-39), layer norm (src/layers.rs:50-121),
+ * im2col (src/layers.rs:613-634). */
+void or_gelu(float* values, int64_t n);
+void or_layer_norm(const float* x, int rows, int d, const float* w, const float* b, float eps, float* out);
+void or_conv_columns(const float* x, int frames, int channels, int kernel, int stride, int pad, int out_frames,
+                     float* out);
 /* f32_to_f16 / f16_to_f32 over arrays (src/cpu/tensors.rs:542-595). */
 void or_f32_to_f16_n(const float* in, int64_t n, uint16_t* out);
 void or_f16_to_f32_n(const uint16_t* in, int64_t n, float* out);
