@@ -292,6 +292,36 @@ def config_lines(H, sweeps=10):
         note="per decoder layer: eight f16 products of 5 rows (kernel time, event-stamped), and "
              "trit_hip_attention_steps_device over 448 f32 keys a beam (back-to-back calls, host launch included)")
 
+    # The audio encoder before the decoder (Whisper large-v3's, as Voxtral
+    # runs it): its stem and 4 of its 32 layers (d 1280, 20 heads, MLP 5120,
+    # 128 mel bins, 1500 positions) with Q8_0 products; wall clock of
+    # trit_hip_encoder_encode (host copies of the 3000 x 128 window and the
+    # 1500 x 1280 output included), best of 3.
+    ecfg = dict(d=1280, layers=4, heads=20, ffn=5120, mels=128, positions=1500)
+    ed, eff = ecfg["d"], ecfg["ffn"]
+
+    def eq8(n, k, i):
+        codes, sbits = synth.q8_0_matrix(synth.seed_for(0, 90 + i), n, k, scale="normal", sigma=0.2)
+        return hip.Dense.q8_0(n, k, synth.q8_0_blocks(codes, sbits), np.zeros(n, np.float32))
+
+    shared = [eq8(3 * ed, ed, 0), eq8(ed, ed, 1), eq8(eff, ed, 2), eq8(ed, eff, 3)]
+    norms = [np.ones(ed, np.float32), np.zeros(ed, np.float32)] * (2 * ecfg["layers"] + 1)
+    enc = hip.Encoder(ecfg, eq8(ed, 3 * ecfg["mels"], 4), eq8(ed, 3 * ed, 5),
+                      np.zeros((ecfg["positions"], ed), np.float32), shared * ecfg["layers"], norms)
+    mel = synth.activations(synth.seed_for(0, 96), 2 * ecfg["positions"], ecfg["mels"])
+    enc.encode(mel)  # warm-up
+    t_enc = min(_timed(lambda: enc.encode(mel)) for _ in range(3))
+    enc0 = hip.Encoder(dict(ecfg, layers=1), eq8(ed, 3 * ecfg["mels"], 4), eq8(ed, 3 * ed, 5),
+                       np.zeros((ecfg["positions"], ed), np.float32), shared, norms[:6])
+    enc0.encode(mel)
+    t_one = min(_timed(lambda: enc0.encode(mel)) for _ in range(3))
+    per_layer = (t_enc - t_one) / (ecfg["layers"] - 1)
+    out["audio_encoder_whisper_large_v3"] = dict(
+        encode_4_layers_ms=round(t_enc * 1e3, 2), per_layer_ms=round(per_layer * 1e3, 3),
+        stem_and_one_layer_ms=round(t_one * 1e3, 2), full_32_layers_ms_estimate=round((t_one + 31 * per_layer) * 1e3, 1),
+        note="Q8_0 products (int8 MFMA for the 1500-row products), Trit's exact attention over 1500 positions")
+    del enc, enc0, shared
+
     # C5 end to end: one decoder layer of the prefill's shape (hidden 2048,
     # 16/8 heads x 128, SwiGLU 3072) over the 1564-row prompt: the MFMA
     # products, q/k norm + rotary + cache append, causal GQA attention on

@@ -305,6 +305,32 @@ int trit_hip_session_position(const TritHipSession *session);
 
 void trit_hip_session_free(TritHipSession *session);
 
+/* ---- Audio encoder (reference src/models/parts/audio_encoder.rs) ------- */
+
+/* Whisper's audio encoder, which Voxtral and MOSS run (Encoder,
+ * reference src/models/parts/audio_encoder.rs:18-139). */
+typedef struct {
+    int d, layers, heads, ffn, mels, positions; /* EncoderShape (:40-60) */
+} TritHipEncoderConfig;
+typedef struct TritHipEncoder TritHipEncoder;
+/* Encoder::load (:62-108) from device layers with their biases: conv1
+ * (d x 3*mels) and conv2 (d x 3*d), their weights [out][in][kernel] as
+ * rows; per layer qkv (3d x d, q/k/v stacked, k's bias zero), out (d x d),
+ * fc1 (ffn x d), fc2 (d x ffn), 4 a layer in that order; positions
+ * (positions x d); norms per layer attn weight, attn bias, ffn weight, ffn
+ * bias (d each), then the final weight and bias. Layer kinds as the
+ * decoder takes them (int8 activations, or f32 math). */
+int trit_hip_encoder_new(const TritHipEncoderConfig *config, const TritHipLayer *conv1, const TritHipLayer *conv2,
+                         const float *positions, const TritHipLayer *const *linears, const float *norms,
+                         TritHipEncoder **out);
+void trit_hip_encoder_free(TritHipEncoder *encoder);
+/* Encoder::encode (:111-138): the positions x d output of one window of
+ * 2 * positions x mels features (host memory), with Trit's arithmetic:
+ * im2col, the products in their kinds' orders (biases after the chains),
+ * the exact GELU, layer norm in 32-lane order, Trit's attention over every
+ * position. */
+int trit_hip_encoder_encode(const TritHipEncoder *encoder, const float *mel, float *out);
+
 /* ---- Attention (reference src/layers.rs:343-504) ---------------------- */
 
 /* Grouped-query attention of tq query rows over tk keys, host memory:

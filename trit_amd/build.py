@@ -13,7 +13,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "lib", "libtrit_hip.so")
-SOURCES = ["layer.hip", "gemv.hip", "gemv_decode.hip", "gemv_stream.hip", "gemv_float.hip", "gemm.hip", "decoder.hip", "decode_step.hip", "attention_mfma.hip", "gguf.hip", "tokenizer.cpp"]
+SOURCES = ["layer.hip", "gemv.hip", "gemv_decode.hip", "gemv_stream.hip", "gemv_float.hip", "gemm.hip", "decoder.hip", "decode_step.hip", "attention_mfma.hip", "gguf.hip", "encoder.hip", "tokenizer.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -1115,6 +1115,22 @@ __global__ void rows_to_cache_kernel(const float* __restrict__ k, const float* _
 
 }  // namespace
 
+// Trit's attention over device rows (q rows of stride qs; k, v rows of
+// stride kvs): the rows go into head-major caches kc, vc (kv_heads x tk x
+// hd floats each) and the exact kernel runs per (head, query row). `st`
+// holds pos = tk - tq and done = 0.
+void exact_attention(const float* q, int qs, const float* k, const float* v, int kvs, int tq, int tk, int heads,
+                     int kv_heads, int hd, int causal, float* out, float* kc, float* vc, State* st, hipStream_t s) {
+    if ((size_t)(MAX_HD + tk + ATT_THREADS) * 4 > 64 * 1024)
+        fail("attention: more keys than the exact kernel's shared memory holds (16000)");
+    const int grid = (int)std::min<size_t>(4096, ((size_t)tk * kv_heads * hd + 255) / 256);
+    hipLaunchKernelGGL(rows_to_cache_kernel<float>, dim3(grid), dim3(256), 0, s, k, v, kvs, tk, kv_heads, hd, kc, vc);
+    const size_t lds = (size_t)(MAX_HD + tk + ATT_THREADS) * 4;
+    hipLaunchKernelGGL(attention_kernel<float>, dim3(heads, tq), dim3(ATT_THREADS), lds, s, q, qs, heads, kv_heads, hd,
+                       kc, vc, tk, tq, out, 1, st, causal);
+    TRIT_HIP(hipGetLastError());
+}
+
 // ---- host side ------------------------------------------------------------
 
 
@@ -2265,12 +2281,8 @@ int trit_hip_attention(const float* q, int qs, const float* k, const float* v, i
             State st{};
             st.pos = tk - tq;
             TRIT_HIP(hipMemcpyAsync(dst.ptr, &st, sizeof(State), hipMemcpyHostToDevice, s));
-            hipLaunchKernelGGL(rows_to_cache_kernel<float>, dim3(grid), dim3(256), 0, s, dk.as<float>(),
-                               dv.as<float>(), kvs, tk, kv_heads, hd, dkc.as<float>(), dvc.as<float>());
-            const size_t lds = (size_t)(MAX_HD + tk + ATT_THREADS) * 4;
-            hipLaunchKernelGGL(attention_kernel<float>, dim3(heads, tq), dim3(ATT_THREADS), lds, s, dq.as<float>(),
-                               qs, heads, kv_heads, hd, dkc.as<float>(), dvc.as<float>(), tk, tq, dout.as<float>(), 1,
-                               dst.as<State>(), causal);
+            exact_attention(dq.as<float>(), qs, dk.as<float>(), dv.as<float>(), kvs, tq, tk, heads, kv_heads, hd,
+                            causal, dout.as<float>(), dkc.as<float>(), dvc.as<float>(), dst.as<State>(), s);
         } else {
             hipLaunchKernelGGL(rows_to_cache_kernel<_Float16>, dim3(grid), dim3(256), 0, s, dk.as<float>(),
                                dv.as<float>(), kvs, tk, kv_heads, hd, dkc.as<_Float16>(), dvc.as<_Float16>());

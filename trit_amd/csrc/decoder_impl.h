@@ -101,6 +101,12 @@ void flash_prefill(SessionImpl& S, int layer, int rows, int pos0, hipStream_t s)
 void flash_attention(const float* q, int qs, const _Float16* kc, const _Float16* vc, int max_pos, int heads,
                      int kv_heads, int rows, int pos0, int tk, int causal, float* out, hipStream_t s);
 
+// Trit's attention (exact kernel) over device rows: q rows of stride qs,
+// k and v rows of stride kvs; kc / vc scratch of kv_heads x tk x hd floats;
+// st a device State with pos = tk - tq, done = 0 (decoder.hip).
+void exact_attention(const float* q, int qs, const float* k, const float* v, int kvs, int tq, int tk, int heads,
+                     int kv_heads, int hd, int causal, float* out, float* kc, float* vc, State* st, hipStream_t s);
+
 // The persistent decode step (decode_step.hip).
 // Whether the session's model and mode run on it.
 bool decode_step_supported(const SessionImpl& S);

@@ -53,6 +53,27 @@ __device__ __forceinline__ float exp_trit(float x) {
 // v / (1 + exp(0 - v)) (src/cpu/activation.rs:54-56,330).
 __device__ __forceinline__ float silu_trit(float v) { return v / (1.0f + exp_trit(0.0f - v)); }
 
+// The exact GELU in the fused form of every Trit path (src/cpu/v2/
+// activation.rs:33-39): v * erfc(-v / sqrt 2) / 2 with Numerical Recipes'
+// erfcc, erfc(z) = t * exp(-z^2 + P(t)), t = 1 / (1 + z / 2)
+// (src/cpu/activation.rs:15-28).
+__device__ __forceinline__ float gelu_trit(float v) {
+    const float z = __builtin_fabsf(v) * 0.70710678118654752440f;
+    const float t = 1.0f / __builtin_fmaf(z, 0.5f, 1.0f);
+    float p = 0.17087277f;
+    p = __builtin_fmaf(p, t, -0.82215223f);
+    p = __builtin_fmaf(p, t, 1.4885159f);
+    p = __builtin_fmaf(p, t, -1.135204f);
+    p = __builtin_fmaf(p, t, 0.27886807f);
+    p = __builtin_fmaf(p, t, -0.18628806f);
+    p = __builtin_fmaf(p, t, 0.09678418f);
+    p = __builtin_fmaf(p, t, 0.37409196f);
+    p = __builtin_fmaf(p, t, 1.0000237f);
+    p = __builtin_fmaf(p, t, -1.2655122f);
+    const float tail = t * exp_trit(__builtin_fmaf(-z, z, p));
+    return (0.5f * v) * (v >= 0.0f ? 2.0f - tail : tail);
+}
+
 // Activation code: round to nearest even, then the +-127 limits; a NaN
 // becomes -127 as cvtps2dq + clamp gives it (src/cpu/v2/quantize.rs:140-149).
 __device__ __forceinline__ int act_code(float scaled) {

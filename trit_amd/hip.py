@@ -43,6 +43,10 @@ class LmConfig(C.Structure):
                    cfg.get("residual_multiplier", 1.0), cfg.get("logits_scaling", 1.0))
 
 
+class EncoderConfig(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("d", "layers", "heads", "ffn", "mels", "positions")]
+
+
 def lib():
     global _lib
     if _lib is None:
@@ -101,6 +105,9 @@ def lib():
             "trit_hip_attention": (i, [p, i, p, p, i, i, i, i, i, i, i, i, p]),
             "trit_hip_f32_to_f16": (i, [p, C.c_int64, p]),
             "trit_hip_f16_to_f32": (i, [p, C.c_int64, p]),
+            "trit_hip_encoder_new": (i, [C.POINTER(EncoderConfig), p, p, p, p, p, pp]),
+            "trit_hip_encoder_free": (None, [p]),
+            "trit_hip_encoder_encode": (i, [p, p, p]),
             "trit_hip_bpe_open": (i, [C.c_char_p, pp]),
             "trit_hip_bpe_parse": (i, [C.c_char_p, C.c_size_t, pp]),
             "trit_hip_bpe_free": (None, [p]),
@@ -394,6 +401,42 @@ class CausalLm:
     def free(self):
         if self.h:
             lib().trit_hip_decoder_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Encoder:
+    """Whisper's audio encoder on the device (src/models/parts/audio_encoder.rs):
+    conv1 (d x 3 mels), conv2 (d x 3 d), then qkv, out, fc1, fc2 of each
+    layer, as Dense layers with their biases; positions (positions x d);
+    norms per layer attn w, b, ffn w, b, then the final w, b."""
+
+    def __init__(self, cfg: dict, conv1: Dense, conv2: Dense, positions, linears, norms):
+        c = EncoderConfig(*(cfg[k] for k in ("d", "layers", "heads", "ffn", "mels", "positions")))
+        self.cfg = cfg
+        pos = np.ascontiguousarray(positions, np.float32)
+        arr = (C.c_void_p * len(linears))(*[l.h for l in linears])
+        nrm = np.ascontiguousarray(np.concatenate([np.asarray(v, np.float32).reshape(-1) for v in norms]))
+        out = C.c_void_p()
+        check(lib().trit_hip_encoder_new(C.byref(c), conv1.h, conv2.h, ptr(pos), arr, ptr(nrm), C.byref(out)))
+        self.h = out
+
+    def encode(self, mel):
+        """Encoder::encode: positions x d of one 2 * positions x mels window."""
+        c = self.cfg
+        mel = np.ascontiguousarray(mel, np.float32).reshape(2 * c["positions"], c["mels"])
+        out = np.empty((c["positions"], c["d"]), np.float32)
+        check(lib().trit_hip_encoder_encode(self.h, ptr(mel), ptr(out)))
+        return out
+
+    def free(self):
+        if self.h:
+            lib().trit_hip_encoder_free(self.h)
             self.h = None
 
     def __del__(self):
