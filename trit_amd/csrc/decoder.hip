@@ -1097,6 +1097,184 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_steps_kernel(const floa
     }
 }
 
+// attention_kernel's arithmetic for R query rows of one head per block:
+// every row's scores, maximum, exponentials, serial sum and p.V chains in
+// the same orders (same bits), with each key and value read once for the R
+// rows. Scores: thread j chains its key against the R rows; p.V: thread
+// (e, group) chains dim e of rows group, group + G, ... (G = 256 / hd) from
+// values it loads once for its rows. probs rows have a pitch of tk rounded
+// up to 4 floats.
+template <typename KV, int R>
+__global__ __launch_bounds__(ATT_THREADS) void attention_rows_kernel(
+    const float* __restrict__ qkv, int stride, int heads, int kvh, int hd, const KV* __restrict__ kcache,
+    const KV* __restrict__ vcache, int max_pos, int rows, float* __restrict__ out, const State* st, int causal) {
+    if (st->done) return;
+    extern __shared__ float sm[];  // qh[R][MAX_HD] | probs[R][pitch] | red[R][ATT_THREADS / 64] | inv[R]
+    const int h = blockIdx.x, row0 = blockIdx.y * R;
+    const int nr = min(R, rows - row0);
+    const int g = h / (heads / kvh);
+    const int tk = st->pos + rows;
+    const int pitch = (tk + 3) & ~3;
+    float* qh = sm;
+    float* probs = sm + R * MAX_HD;
+    float* red = probs + R * pitch;
+    float* inv = red + R * (ATT_THREADS / 64);
+    const float scale = 1.0f / __builtin_sqrtf((float)hd);
+    for (int i = threadIdx.x; i < R * hd; i += ATT_THREADS) {
+        const int r = i / hd, e = i - r * hd;
+        qh[r * MAX_HD + e] = r < nr ? qkv[(size_t)(row0 + r) * stride + (size_t)h * hd + e] * scale : 0.0f;
+    }
+    __syncthreads();
+    const KV* K = kcache + (size_t)g * max_pos * hd;
+    const KV* V = vcache + (size_t)g * max_pos * hd;
+    float best[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) best[r] = -INFINITY;
+    for (int j = threadIdx.x; j < tk; j += ATT_THREADS) {
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+        const KV* kr = K + (size_t)j * hd;
+        for (int e = 0; e < hd; e += 8) {
+            float kv[8];
+            kv_load8(kr + e, kv);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float4 qa = *(const float4*)(qh + r * MAX_HD + e), qb = *(const float4*)(qh + r * MAX_HD + e + 4);
+                const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+                for (int u = 0; u < 8; ++u) acc[r] = __builtin_fmaf(qv[u], kv[u], acc[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int visible = causal ? st->pos + row0 + r + 1 : tk;
+            const float v = j < visible ? acc[r] : -INFINITY;
+            probs[r * pitch + j] = v;
+            best[r] = __builtin_fmaxf(best[r], v);
+        }
+    }
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float m = best[r];
+        for (int o = 32; o > 0; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o));
+        if (lane == 0) red[r * (ATT_THREADS / 64) + wave] = m;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < nr * tk; i += ATT_THREADS) {
+        const int r = i / tk, j = i - r * tk;
+        float mx = red[r * (ATT_THREADS / 64)];
+        for (int w = 1; w < ATT_THREADS / 64; ++w) mx = __builtin_fmaxf(mx, red[r * (ATT_THREADS / 64) + w]);
+        probs[r * pitch + j] = exp_trit(probs[r * pitch + j] - mx);
+    }
+    __syncthreads();
+    // The serial sum of each row (thread r), in key order from 0: 16
+    // values a step, the next 16 read while the current ones are added.
+    if ((int)threadIdx.x < nr) {
+        const float* pr = probs + threadIdx.x * pitch;
+        float sum = 0.0f;
+        int j = 0;
+        float4 cur[4], nxt[4];
+        if (tk >= 16) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) cur[q] = *(const float4*)(pr + 4 * q);
+        }
+        for (; j + 16 <= tk; j += 16) {
+            if (j + 32 <= tk) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) nxt[q] = *(const float4*)(pr + j + 16 + 4 * q);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                sum = sum + cur[q].x;
+                sum = sum + cur[q].y;
+                sum = sum + cur[q].z;
+                sum = sum + cur[q].w;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) cur[q] = nxt[q];
+        }
+        for (; j < tk; ++j) sum = sum + pr[j];
+        inv[threadIdx.x] = 1.0f / sum;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < nr * tk; i += ATT_THREADS) {
+        const int r = i / tk, j = i - r * tk;
+        probs[r * pitch + j] = probs[r * pitch + j] * inv[r];
+    }
+    __syncthreads();
+    // p.V: dim e of the rows group, group + G, ...; each value loaded once.
+    const int G = ATT_THREADS / hd;  // hd divides ATT_THREADS (8, 16, ..., 256)
+    const int e = threadIdx.x % hd, group = threadIdx.x / hd;
+    if (group < G) {
+        constexpr int MR = R;  // at most R rows a thread
+        float acc[MR];
+#pragma unroll
+        for (int k = 0; k < MR; ++k) acc[k] = 0.0f;
+        int j = 0;
+        for (; j + 16 <= tk; j += 16) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v[u] = kv_load(V + (size_t)(j + u) * hd + e);
+#pragma unroll
+            for (int k = 0; k < MR; ++k) {
+                const int r = group + k * G;
+                if (r >= nr) break;
+                const float4* p4 = (const float4*)(probs + r * pitch + j);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 pq = p4[q];
+                    acc[k] = __builtin_fmaf(pq.x, v[4 * q], acc[k]);
+                    acc[k] = __builtin_fmaf(pq.y, v[4 * q + 1], acc[k]);
+                    acc[k] = __builtin_fmaf(pq.z, v[4 * q + 2], acc[k]);
+                    acc[k] = __builtin_fmaf(pq.w, v[4 * q + 3], acc[k]);
+                }
+            }
+        }
+        for (; j < tk; ++j) {
+            const float v = kv_load(V + (size_t)j * hd + e);
+#pragma unroll
+            for (int k = 0; k < MR; ++k) {
+                const int r = group + k * G;
+                if (r >= nr) break;
+                acc[k] = __builtin_fmaf(probs[r * pitch + j], v, acc[k]);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < MR; ++k) {
+            const int r = group + k * G;
+            if (r >= nr) break;
+            out[(size_t)(row0 + r) * heads * hd + (size_t)h * hd + e] = acc[k];
+        }
+    }
+}
+
+// Shared memory of attention_rows_kernel for R rows over tk keys.
+size_t rows_lds(int R, int tk) {
+    return (size_t)(R * MAX_HD + R * ((tk + 3) & ~3) + R * (ATT_THREADS / 64) + R) * 4;
+}
+
+// Trit's attention of `rows` query rows (exact kernel's arithmetic) over
+// caches of max_tk positions: 4 rows a block (measured best: 8 rows share
+// more key reads but halve the resident blocks), 2 when 4 rows' scores do
+// not fit 64 KB of shared memory; false when not even two rows do.
+template <typename KV>
+bool launch_attention_rows(const float* qkv, int stride, int heads, int kvh, int hd, const KV* kc, const KV* vc,
+                           int max_pos, int rows, int max_tk, float* out, const State* st, int causal,
+                           hipStream_t s) {
+    constexpr size_t LIMIT = 64 * 1024;
+    auto go = [&](auto R_) {
+        constexpr int R = decltype(R_)::value;
+        hipLaunchKernelGGL((attention_rows_kernel<KV, R>), dim3(heads, (rows + R - 1) / R), dim3(ATT_THREADS),
+                           rows_lds(R, max_tk), s, qkv, stride, heads, kvh, hd, kc, vc, max_pos, rows, out, st, causal);
+        return true;
+    };
+    if (rows >= 4 && rows_lds(4, max_tk) <= LIMIT) return go(std::integral_constant<int, 4>{});
+    if (rows >= 2 && rows_lds(2, max_tk) <= LIMIT) return go(std::integral_constant<int, 2>{});
+    return false;
+}
+
 // Rows of keys and values (tk x kvs floats each, head g at g * hd) into the
 // cache layout [g][position][hd] of type KV.
 template <typename KV>
@@ -1125,9 +1303,11 @@ void exact_attention(const float* q, int qs, const float* k, const float* v, int
         fail("attention: more keys than the exact kernel's shared memory holds (16000)");
     const int grid = (int)std::min<size_t>(4096, ((size_t)tk * kv_heads * hd + 255) / 256);
     hipLaunchKernelGGL(rows_to_cache_kernel<float>, dim3(grid), dim3(256), 0, s, k, v, kvs, tk, kv_heads, hd, kc, vc);
-    const size_t lds = (size_t)(MAX_HD + tk + ATT_THREADS) * 4;
-    hipLaunchKernelGGL(attention_kernel<float>, dim3(heads, tq), dim3(ATT_THREADS), lds, s, q, qs, heads, kv_heads, hd,
-                       kc, vc, tk, tq, out, 1, st, causal);
+    if (!launch_attention_rows<float>(q, qs, heads, kv_heads, hd, kc, vc, tk, tq, tk, out, st, causal, s)) {
+        const size_t lds = (size_t)(MAX_HD + tk + ATT_THREADS) * 4;
+        hipLaunchKernelGGL(attention_kernel<float>, dim3(heads, tq), dim3(ATT_THREADS), lds, s, q, qs, heads, kv_heads,
+                           hd, kc, vc, tk, tq, out, 1, st, causal);
+    }
     TRIT_HIP(hipGetLastError());
 }
 
@@ -1353,18 +1533,26 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
         if (S.exact) {
             // The host sizes shared memory for the largest key count this forward can see.
             const size_t lds = (size_t)(MAX_HD + S.max_pos + ATT_THREADS) * 4;
-            if (S.kv32)
+            const size_t lo = (size_t)l * c.kv_heads * S.max_pos * hd;
+            const bool multi =
+                rows > 1 && (S.kv32 ? launch_attention_rows<float>(S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
+                                                                  S.kcache.as<float>() + lo, S.vcache.as<float>() + lo,
+                                                                  S.max_pos, rows, S.max_pos, S.att.as<float>(), st,
+                                                                  1, s)
+                                    : launch_attention_rows<_Float16>(
+                                          S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
+                                          S.kcache.as<_Float16>() + lo, S.vcache.as<_Float16>() + lo, S.max_pos,
+                                          rows, S.max_pos, S.att.as<float>(), st, 1, s));
+            if (multi) {
+                // R query rows a block.
+            } else if (S.kv32)
                 hipLaunchKernelGGL(attention_kernel<float>, dim3(c.heads, rows), dim3(ATT_THREADS), lds, s,
-                                   S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
-                                   S.kcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd,
-                                   S.vcache.as<float>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos, rows,
-                                   S.att.as<float>(), 1, st, 1);
+                                   S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd, S.kcache.as<float>() + lo,
+                                   S.vcache.as<float>() + lo, S.max_pos, rows, S.att.as<float>(), 1, st, 1);
             else
                 hipLaunchKernelGGL(attention_kernel<_Float16>, dim3(c.heads, rows), dim3(ATT_THREADS), lds, s,
-                                   S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd,
-                                   S.kcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd,
-                                   S.vcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * hd, S.max_pos,
-                                   rows, S.att.as<float>(), 1, st, 1);
+                                   S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd, S.kcache.as<_Float16>() + lo,
+                                   S.vcache.as<_Float16>() + lo, S.max_pos, rows, S.att.as<float>(), 1, st, 1);
         } else if (fused && (S.kv32 ? launch_decode<float>(S, l, s) : launch_decode<_Float16>(S, l, s))) {
             // One block per key/value head.
         } else if (!fused && rows > 1 && flash_prefill_supported(S) && use_flash()) {
