@@ -72,7 +72,8 @@ def test_q8_0_bias_relu(gpu):
 
 # More than 8 rows: the matrix-core product (int8 MFMA), same bits.
 @pytest.mark.parametrize("n,k,m", [(256, 512, 9), (384, 1024, 64), (128, 256, 100), (2048, 2048, 257),
-                                   (1024, 3072, 40)])
+                                   (1024, 3072, 40), (128, 384, 70), (256, 4320, 33), (128, 32, 12),
+                                   (384, 1248, 129)])
 def test_q8_0_many_rows(gpu, n, k, m):
     print(f"case q8_0 matrix cores n={n} k={k} m={m}", flush=True)
     codes, sbits, blocks = q8_layer(synth.seed_for(2, n + k), n, k)
@@ -110,7 +111,8 @@ def test_prefill_gemm_1564_rows(gpu, n):
     assert np.all(np.isfinite(got))
 
 
-@pytest.mark.parametrize("n,k,m", [(512, 1024, 1), (384, 2048, 4), (256, 512, 33), (512, 1024, 70)])
+@pytest.mark.parametrize("n,k,m", [(512, 1024, 1), (384, 2048, 4), (256, 512, 33), (512, 1024, 70), (256, 384, 40),
+                                   (128, 128, 20)])
 def test_int8(gpu, n, k, m):
     print(f"case int8 n={n} k={k} m={m}", flush=True)
     codes = synth.ints(21, (n, k), -127, 127).astype(np.int8)
@@ -203,7 +205,7 @@ def test_q4_k(gpu, n, k, m):
 
 
 @pytest.mark.parametrize("n,k,m", [(4096, 1024, 1), (1000, 1024, 3), (300, 2048, 2), (77, 160, 5), (300, 384, 8),
-                                   (65, 3072, 6), (100, 8192, 3)])
+                                   (65, 3072, 6), (100, 8192, 3), (480, 9, 8), (33, 71, 4), (480, 9, 130), (40, 64, 70)])
 def test_f16(gpu, n, k, m):
     print(f"case f16 n={n} k={k} m={m}", flush=True)
     w = synth.f16_bits(synth.activations(51 + n, n, k) * 0.02).reshape(n, k)
@@ -223,7 +225,8 @@ def widened_q8(codes, scales):
 
 
 @pytest.mark.parametrize("n,k,m", [(300, 1024, 1), (77, 160, 5), (1280, 1280, 5), (100, 4096, 8), (4096, 2048, 2),
-                                   (33, 48, 3)])
+                                   (33, 48, 3), (480, 9, 8), (70, 1, 3), (50, 37, 5), (100, 300, 2), (480, 9, 300),
+                                   (70, 100, 65), (300, 128, 9), (33, 17, 12)])
 def test_f32(gpu, n, k, m):
     print(f"case f32 n={n} k={k} m={m}", flush=True)
     w = synth.activations(61 + n, n, k) * np.float32(0.05)
@@ -235,7 +238,7 @@ def test_f32(gpu, n, k, m):
 
 
 @pytest.mark.parametrize("n,k,m", [(300, 1024, 1), (77, 160, 5), (1280, 1280, 5), (96, 4096, 8), (5000, 1024, 1),
-                                   (40, 96, 2)])
+                                   (40, 96, 2), (40, 96, 20)])
 def test_q8_table(gpu, n, k, m):
     """Weights::Q8 (int8 storage, f32 scale per 32, f32 math)."""
     print(f"case q8 n={n} k={k} m={m}", flush=True)

@@ -20,7 +20,8 @@
 //     (m x k) and group scales stored group-major (g x mpad), so that a
 //     lane's four consecutive output rows read one 16-byte load;
 //  3. gemm_kernel: 256 threads = 2 x 2 waves over 64 rows of x and 128
-//     weight rows. K runs in 256-byte chunks staged through LDS: 16 threads
+//     weight rows. K runs in 256-byte chunks staged through LDS (the last
+//     one zero past k when k % 256 != 0): 16 threads
 //     read a row's 256 contiguous bytes, and the next chunk's loads are in
 //     flight while this one computes. A wave owns 32 rows of x by two
 //     32-row MFMA tiles of weights (or, for the SwiGLU pair, the gate tile
@@ -153,7 +154,7 @@ __device__ __forceinline__ void read_scales(const float* xs, const float* ws, in
     s.w1 = ws[c1];
 }
 
-template <int G, bool HALF, int P>
+template <int G, bool HALF, int P, bool TAIL>
 __global__ __launch_bounds__(GEMM_THREADS, 2) void gemm_kernel(const int8_t* __restrict__ xq,
                                                                const float* __restrict__ xs, int m, int mpad,
                                                                const int8_t* __restrict__ codes,
@@ -164,7 +165,9 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void gemm_kernel(const int8_t* __r
     constexpr int CH = G / 32;   // MFMA steps per group
     __shared__ __align__(16) Stage<G> st;
     if (a.skip && *a.skip) return;
-    const int groups = k / G, chunks = k / KC;
+    // TAIL: k is not a multiple of KC; the last chunk holds k % KC bytes,
+    // zero past them, and chains only its real groups.
+    const int groups = k / G, chunks = (k + KC - 1) / KC;
     // Tiles in XCD order: block b runs on XCD b % 8; the blocks of one XCD
     // share weight tiles, which then stay in that XCD's L2.
     const int blk = blockIdx.x;
@@ -213,12 +216,34 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void gemm_kernel(const int8_t* __r
     uint4 rw = make_uint4(0, 0, 0, 0);  // HALF: 8 f16 scales; else 2 f32 in .x .y
     auto fetch = [&](int c) {
         const size_t off = (size_t)c * KC;
+        // Every piece of the thread sits at byte 16 (t % 16) of its row's chunk.
+        const bool in_k = !TAIL || 16 * (t % 16) < k - c * KC;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ra[i] = *(const v4i*)(xq + ag[i] + off);
+        for (int i = 0; i < 4; ++i) ra[i] = in_k ? *(const v4i*)(xq + ag[i] + off) : v4i{0, 0, 0, 0};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) rb[i] = *(const v4i*)(codes + bg[i] + off);
-        if (xs_thread) rx = *(const float4*)(xs + (size_t)(c * GPC + t / 16) * mpad + mbase + 4 * (t % 16));
-        if (ws_thread) {
+        for (int i = 0; i < 8; ++i) rb[i] = in_k ? *(const v4i*)(codes + bg[i] + off) : v4i{0, 0, 0, 0};
+        if (xs_thread) {
+            if (!TAIL || c * GPC + t / 16 < groups)
+                rx = *(const float4*)(xs + (size_t)(c * GPC + t / 16) * mpad + mbase + 4 * (t % 16));
+            else
+                rx = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        if (ws_thread && TAIL) {
+            // A row's scales start anywhere: one load a scale, none past the row.
+            uint32_t v[4] = {0, 0, 0, 0};
+            if (HALF) {
+#pragma unroll
+                for (int j = 0; j < GPC; ++j)
+                    if (c * GPC + j < groups)
+                        v[j / 2] |= (uint32_t)((const uint16_t*)scales)[ws_base + c * GPC + j] << (16 * (j % 2));
+            } else {
+#pragma unroll
+                for (int j = 0; j < GPC; ++j)
+                    if (c * GPC + j < groups)
+                        v[j] = __builtin_bit_cast(uint32_t, ((const float*)scales)[ws_base + c * GPC + j]);
+            }
+            rw = make_uint4(v[0], v[1], v[2], v[3]);
+        } else if (ws_thread) {
             if (HALF) {
                 rw = *(const uint4*)((const uint16_t*)scales + ws_base + c * GPC);
             } else {
@@ -296,6 +321,7 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void gemm_kernel(const int8_t* __r
             // Output (row 8*(r/4) + 4h + r%4, column lr) of a tile is register r.
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
+                if (TAIL && c * GPC + gi >= groups) break;  // past k: no chain step
                 const float xv[4] = {sc.x[q].x, sc.x[q].y, sc.x[q].z, sc.x[q].w};
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -370,9 +396,14 @@ template <int G, bool HALF, int P>
 void launch_gemm(const Layer& L, const GemvArgs& a, const Scratch& sc, hipStream_t s) {
     const int nb = P == 1 ? L.n / 128 : (L.n / 2) / 64;
     const int mb = sc.mpad / BM;
-    launch_timed(a, gemm_kernel<G, HALF, P>, dim3(nb * mb), dim3(GEMM_THREADS), 0, s, (const int8_t*)sc.xq,
-                 (const float*)sc.xs, a.m, sc.mpad, L.codes.as<int8_t>(), (const void*)L.scales.ptr,
-                 L.bias.as<float>(), L.n, L.k, nb, mb, a);
+    if (L.k % KC == 0)
+        launch_timed(a, gemm_kernel<G, HALF, P, false>, dim3(nb * mb), dim3(GEMM_THREADS), 0, s,
+                     (const int8_t*)sc.xq, (const float*)sc.xs, a.m, sc.mpad, L.codes.as<int8_t>(),
+                     (const void*)L.scales.ptr, L.bias.as<float>(), L.n, L.k, nb, mb, a);
+    else
+        launch_timed(a, gemm_kernel<G, HALF, P, true>, dim3(nb * mb), dim3(GEMM_THREADS), 0, s,
+                     (const int8_t*)sc.xq, (const float*)sc.xs, a.m, sc.mpad, L.codes.as<int8_t>(),
+                     (const void*)L.scales.ptr, L.bias.as<float>(), L.n, L.k, nb, mb, a);
     TRIT_HIP(hipGetLastError());
 }
 
@@ -380,7 +411,10 @@ void launch_gemm(const Layer& L, const GemvArgs& a, const Scratch& sc, hipStream
 
 bool gemm_supported(const Layer& L, const GemvArgs& a) {
     if (L.kind != Q8_0 && L.kind != Q4_K && L.kind != INT8) return false;
-    if (L.n % 128 != 0 || L.k % KC != 0) return false;
+    // k a multiple of the group (a partial last chunk of K is zero past k);
+    // RMSNorm computed here takes whole 256-value chunks.
+    if (L.n % 128 != 0 || L.k % group_of(L) != 0) return false;
+    if (a.norm_w && !a.norm_inv && L.k % KC != 0) return false;
     // 32-bit byte offsets into the codes of x and of the weights.
     if ((int64_t)a.m * L.k >= (int64_t)1 << 31 || (int64_t)L.n * L.k >= (int64_t)1 << 32) return false;
     return a.m >= 1;

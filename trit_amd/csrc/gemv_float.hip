@@ -17,6 +17,8 @@
 #include "device.h"
 #include "internal.h"
 
+#include <type_traits>
+
 namespace trit {
 namespace {
 
@@ -113,9 +115,11 @@ __global__ __launch_bounds__(THREADS) void f16_kernel(const uint16_t* __restrict
     }
 }
 
-// Any kind and k (a multiple of 16, of 32 for Q8): one element load a
-// step, the rows read in place (shared memory when they fit, else global
-// memory, where they stay in the caches).
+// Any kind and k (any k for f16 and f32, a multiple of 32 for Q8): one
+// element load a step, the rows read in place (shared memory when they
+// fit, else global memory, where they stay in the caches). Past k the
+// chains add 0 * 0 (zero weights in the layout, the inputs masked): Trit's
+// tail padded with zeros.
 template <int K, bool LDS>
 __global__ __launch_bounds__(THREADS) void float_any_kernel(const typename WT<K>::E* __restrict__ w,
                                                             const float* __restrict__ scales,
@@ -130,7 +134,7 @@ __global__ __launch_bounds__(THREADS) void float_any_kernel(const typename WT<K>
         xs = xs_lds;
     }
     const int lane = threadIdx.x & 15;
-    const int s_count = k / 16;
+    const int s_count = chain_steps(k);
     const int steps = (n + ROWS - 1) / ROWS;
     for (int step = blockIdx.x; step < steps; step += gridDim.x) {
         const int row = step * ROWS + (int)(threadIdx.x >> 4);
@@ -142,8 +146,10 @@ __global__ __launch_bounds__(THREADS) void float_any_kernel(const typename WT<K>
         for (int f = 0; f < m; ++f) {
             const float* xf = xs + (size_t)f * k + lane;
             float acc = 0.0f;
-            for (int sidx = 0; sidx < s_count; ++sidx)
-                acc = __builtin_fmaf(xf[16 * sidx], widen1<K>(chain, row_scales, sidx), acc);
+            for (int sidx = 0; sidx < s_count; ++sidx) {
+                const float xv = 16 * sidx + lane < k ? xf[16 * sidx] : 0.0f;
+                acc = __builtin_fmaf(xv, widen1<K>(chain, row_scales, sidx), acc);
+            }
             const float v = tree16(acc);
             if (live && lane == 0) store_out(a, bias, n, f, row, v);
         }
@@ -288,11 +294,55 @@ __global__ __launch_bounds__(THREADS) void float_chunked_kernel(const typename W
     }
 }
 
-// Lane-chain layout from row-major weights.
+// Many input rows of a layer with few inputs (k <= 16 S; an audio stem's
+// first convolution): block (x, y) takes 256 output columns and RB input
+// rows; a thread holds its column's 16 lane chains (S steps each) in
+// registers and runs them over the rows, then the tree16 order of the
+// small-batch kernels, so every row gets their bits.
+template <int K, int S>
+__global__ __launch_bounds__(THREADS) void float_rows_kernel(const typename WT<K>::E* __restrict__ w,
+                                                             const float* __restrict__ scales,
+                                                             const float* __restrict__ bias, int n, int k, GemvArgs a) {
+    constexpr int RB = 64;
+    const int col = blockIdx.x * THREADS + (int)threadIdx.x;
+    if (col >= n) return;
+    const int s_count = chain_steps(k);  // <= S
+    float wr[16][S];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+        for (int st = 0; st < S; ++st)
+            wr[i][st] = st < s_count ? widen1<K>(w + ((size_t)col * 16 + i) * s_count,
+                                                 scales ? scales + (size_t)col * (k / 32) : nullptr, st)
+                                     : 0.0f;
+    const int f1 = min(a.m, (int)(blockIdx.y + 1) * RB);
+    for (int f = blockIdx.y * RB; f < f1; ++f) {
+        const float* xf = a.x + (size_t)f * k;
+        float l[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int st = 0; st < S; ++st) {
+                const int kk = 16 * st + i;
+                acc = __builtin_fmaf(kk < k ? xf[kk] : 0.0f, wr[i][st], acc);
+            }
+            l[i] = acc;
+        }
+        float h[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) h[i] = l[i] + l[i + 8];
+        const float v = ((h[0] + h[4]) + (h[2] + h[6])) + ((h[1] + h[5]) + (h[3] + h[7]));
+        store_out(a, bias, n, f, col, v);
+    }
+}
+
+// Lane-chain layout from row-major weights (the padding past k is left as
+// the caller cleared it).
 template <typename E>
 __global__ void repack_kernel(const E* __restrict__ src, int n, int k, E* __restrict__ dst) {
     const size_t total = (size_t)n * k;
-    const int s_count = k / 16;
+    const int s_count = chain_steps(k);
     for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < total; e += (size_t)gridDim.x * blockDim.x) {
         const size_t row = e / k;
         const int kk = (int)(e - row * k);
@@ -305,7 +355,7 @@ __global__ void repack_kernel(const E* __restrict__ src, int n, int k, E* __rest
 template <int K>
 __global__ void row_kernel(const typename WT<K>::E* __restrict__ w, const float* __restrict__ scales, int k,
                            int index, float* __restrict__ out) {
-    const int s_count = k / 16;
+    const int s_count = chain_steps(k);
     const typename WT<K>::E* base = w + (size_t)index * 16 * s_count;
     const float* row_scales = scales ? scales + (size_t)index * (k / 32) : nullptr;
     for (int kk = threadIdx.x; kk < k; kk += blockDim.x) {
@@ -370,6 +420,34 @@ void gemv_float(const Layer& L, const GemvArgs& a, hipStream_t s) {
         case F32: launch_float<WK_F32>(L, a, s); break;
         case Q8_F32: launch_float<WK_Q8>(L, a, s); break;
         default: fail("float gemv: not a float-math layer");
+    }
+    TRIT_HIP(hipGetLastError());
+}
+
+bool gemm_float_supported(const Layer& L, const GemvArgs& a) {
+    return float_kind(L.kind) && L.k <= 128 && a.m >= 1 && !a.norm_w && a.epilogue != EPI_SILU_PAIR;
+}
+
+void gemm_float(const Layer& L, const GemvArgs& a, hipStream_t s) {
+    if (!gemm_float_supported(L, a)) fail("float rows: a float-math layer of k <= 128, no prologue or pair");
+    auto go = [&](auto K_, auto S_) {
+        constexpr int K = decltype(K_)::value, S = decltype(S_)::value;
+        using E = typename WT<K>::E;
+        const dim3 grid((L.n + THREADS - 1) / THREADS, (a.m + 63) / 64);
+        launch_timed(a, float_rows_kernel<K, S>, grid, dim3(THREADS), 0, s, L.codes.as<E>(),
+                     K == WK_Q8 ? L.scales.as<float>() : nullptr, L.bias.as<float>(), L.n, L.k, a);
+    };
+    auto by_steps = [&](auto K_) {
+        const int steps = chain_steps(L.k);
+        if (steps <= 1) go(K_, std::integral_constant<int, 1>{});
+        else if (steps <= 2) go(K_, std::integral_constant<int, 2>{});
+        else if (steps <= 4) go(K_, std::integral_constant<int, 4>{});
+        else go(K_, std::integral_constant<int, 8>{});
+    };
+    switch (L.kind) {
+        case F16: by_steps(std::integral_constant<int, WK_F16>{}); break;
+        case F32: by_steps(std::integral_constant<int, WK_F32>{}); break;
+        default: by_steps(std::integral_constant<int, WK_Q8>{}); break;
     }
     TRIT_HIP(hipGetLastError());
 }

@@ -177,9 +177,16 @@ bool gemv_stream(const Layer& L, const GemvArgs& a, hipStream_t s);
 // The one-row Q8_0 decode product (k 1024, 2048 or 3072); false when the
 // shape or kind is not one it takes.
 bool gemv_row(const Layer& L, const GemvArgs& a, hipStream_t s);
+// Chain steps of a float-math layer's lane-chain layout ([row][16][steps],
+// element 16 s + i at lane i, step s): k / 16 rounded up, the tail zero.
+__host__ __device__ inline int chain_steps(int k) { return (k + 15) >> 4; }
 // Float-math products (F16, F32, Q8), m <= 8; no RMSNorm prologue, no
 // SwiGLU epilogue.
 void gemv_float(const Layer& L, const GemvArgs& a, hipStream_t s);
+// Float-math products of any row count for k <= 128 (no prologue, no
+// SwiGLU pair): the same bits row by row.
+bool gemm_float_supported(const Layer& L, const GemvArgs& a);
+void gemm_float(const Layer& L, const GemvArgs& a, hipStream_t s);
 // Integer products of any row count on the matrix cores (Q8_0, Q4_K, INT8
 // with n % 128 == 0 and k % 256 == 0). `scratch` holds gemm_scratch_bytes(m, k) bytes of
 // device memory the product may overwrite.

@@ -333,6 +333,7 @@ template <class Scratch>
 void forward_rows(const Layer& L, GemvArgs a, int m, hipStream_t s, Scratch get) {
     a.m = m;
     if (m >= GEMM_MIN_ROWS && gemm_supported(L, a)) return gemm_int(L, a, get(gemm_scratch_bytes(m, L.k)), s);
+    if (m > 8 && !a.ev_start && !a.ev_stop && gemm_float_supported(L, a)) return gemm_float(L, a, s);
     if (m >= 2 && !float_kind(L.kind)) {
         a.scratch_bytes = gemv_scratch_bytes(m < 8 ? m : 8, L.k);
         a.scratch = get(a.scratch_bytes);
@@ -379,21 +380,30 @@ int finish(std::shared_ptr<Layer> L, TritHipLayer** out) {
     return 0;
 }
 
+// The lane-chain layout of a float-math layer's row-major device weights,
+// the steps past k (when k is not a multiple of 16) zero.
+void chain_layout(Layer& L, const void* raw, size_t elem) {
+    const size_t bytes = (size_t)L.n * 16 * chain_steps(L.k) * elem;
+    L.codes.alloc(bytes);
+    if (L.k % 16) TRIT_HIP(hipMemsetAsync(L.codes.ptr, 0, bytes, stream()));
+    float_repack(raw, L.kind, L.n, L.k, L.codes.ptr, stream());
+}
+
 // A float-math layer (F32, or Q8 with f32 scales n x k/32) from row-major
 // host weights, repacked into the lane-chain layout.
 int float_layer(int kind, int n, int k, const void* weights, const float* scales, const float* bias,
                 TritHipLayer** out, const char* what) {
-    check_shape(n, k, kind == Q8_F32 ? 32 : 16, what);
+    check_shape(n, k, kind == Q8_F32 ? 32 : 1, what);
     if (!weights) fail(std::string(what) + ": weights is NULL");
     auto L = std::make_shared<Layer>();
     L->kind = kind;
     L->n = n;
     L->k = k;
-    const size_t bytes = (size_t)n * k * (kind == F32 ? 4 : 1);
+    const size_t elem = kind == F32 ? 4 : 1;
+    const size_t bytes = (size_t)n * k * elem;
     DeviceMemory raw(bytes);
     raw.upload(weights, bytes);
-    L->codes.alloc(bytes);
-    float_repack(raw.ptr, kind, n, k, L->codes.ptr, stream());
+    chain_layout(*L, raw.ptr, elem);
     if (kind == Q8_F32) {
         L->scales.alloc((size_t)n * (k / 32) * 4);
         L->scales.upload(scales, (size_t)n * (k / 32) * 4);
@@ -653,7 +663,7 @@ int trit_hip_layer_q8_0_f32(int n, int k, const void* blocks, const float* bias,
 
 int trit_hip_layer_f16(int n, int k, const uint16_t* weights, const float* bias, TritHipLayer** out) {
     return guard(-1, [&] {
-        check_shape(n, k, 16, "f16 layer");
+        check_shape(n, k, 1, "f16 layer");
         if (!weights) fail("f16 layer: weights is NULL");
         auto L = std::make_shared<Layer>();
         L->kind = F16;
@@ -662,8 +672,7 @@ int trit_hip_layer_f16(int n, int k, const uint16_t* weights, const float* bias,
         const size_t bytes = (size_t)n * k * 2;
         DeviceMemory raw(bytes);
         raw.upload(weights, bytes);
-        L->codes.alloc(bytes);
-        float_repack(raw.ptr, F16, n, k, L->codes.ptr, stream());
+        chain_layout(*L, raw.ptr, 2);
         upload_bias(*L, bias);
         TRIT_HIP(hipStreamSynchronize(stream()));
         return finish(L, out);
