@@ -103,7 +103,7 @@ int trit_hip_layer_ggml(int n, int k, int ggml_type, const void *blocks, const f
 
 /* f32 weights, row-major n x k, f32 math in Trit's 16-lane order.
  * Replaces Dense::new / Weights::F32 and Dense::table under F32
- * (reference src/cpu/gemm.rs:190-204,395). k % 16 == 0. */
+ * (reference src/cpu/gemm.rs:190-204,395). Any k: the 16-lane tail padded with zeros. */
 int trit_hip_layer_f32(int n, int k, const float *weights, const float *bias, TritHipLayer **out);
 
 /* Int8 storage with f32 math (Weights::Q8, reference src/cpu/gemm.rs:37-44,
@@ -120,7 +120,7 @@ int trit_hip_layer_q8(int n, int k, const int8_t *codes, const float *scales, co
 int trit_hip_layer_q8_0_f32(int n, int k, const void *blocks, const float *bias, TritHipLayer **out);
 
 /* f16 weights (bits), row-major n x k. Replaces Dense::half / Dense::table
- * with F16 weights (reference src/cpu/gemm.rs:206-221,383-409). k % 16 == 0. */
+ * with F16 weights (reference src/cpu/gemm.rs:206-221,383-409). Any k: the 16-lane tail padded with zeros. */
 int trit_hip_layer_f16(int n, int k, const uint16_t *weights, const float *bias, TritHipLayer **out);
 
 /* y = x * W^T (+ bias, then max(y, 0) when relu): x is m x k f32, y m x n
@@ -330,6 +330,40 @@ void trit_hip_encoder_free(TritHipEncoder *encoder);
  * the exact GELU, layer norm in 32-lane order, Trit's attention over every
  * position. */
 int trit_hip_encoder_encode(const TritHipEncoder *encoder, const float *mel, float *out);
+
+/* The Qwen3-ASR audio encoder (AudioEncoder, reference
+ * src/models/families/qwen3_asr.rs:284-405); sizes as AudioConfig
+ * (:71-118): chunk = 2 * n_window mel frames, window_chunks =
+ * n_window_infer / chunk, out = output_dim. */
+typedef struct {
+    int d, layers, heads, ffn, mels, channels, chunk, window_chunks, out, max_positions;
+} TritHipAsrEncoderConfig;
+typedef struct TritHipAsrEncoder TritHipAsrEncoder;
+/* AudioEncoder::load (:284-317) from device layers with their biases:
+ * convs = conv2d1 (channels x 9), conv2d2 and conv2d3 (channels x 9 *
+ * channels), weights [out][in][bin tap][time tap] as rows; conv_out (d x
+ * channels * ceil^3(mels / 2)); per layer qkv (3d x d, q/k/v stacked),
+ * out (d x d), fc1 (ffn x d), fc2 (d x ffn), 4 a layer; norms per layer
+ * attn weight, attn bias, ffn weight, ffn bias (d each), then ln_post's
+ * weight and bias; proj1 (d x d), proj2 (out x d). The sinusoid positions
+ * (max_positions x d, src/layers.rs:257-270) are made here. Any layer kind
+ * (the first convolution's 9 inputs take f16 or f32). */
+int trit_hip_asr_encoder_new(const TritHipAsrEncoderConfig *config, const TritHipLayer *const *convs,
+                             const TritHipLayer *conv_out, const TritHipLayer *const *linears, const float *norms,
+                             const TritHipLayer *proj1, const TritHipLayer *proj2, TritHipAsrEncoder **out);
+void trit_hip_asr_encoder_free(TritHipAsrEncoder *encoder);
+/* Rows encode makes of `frames` mel frames (ceil^3(length / 2) of each
+ * chunk), or -1. */
+int trit_hip_asr_encoder_rows(const TritHipAsrEncoder *encoder, int frames);
+/* The sinusoid table the encoder holds (max_positions x d floats). */
+int trit_hip_asr_encoder_positions(const TritHipAsrEncoder *encoder, float *out);
+/* AudioEncoder::encode (:321-373): frames x mels log-mel features (host
+ * memory) to rows x out (host memory, rows as trit_hip_asr_encoder_rows);
+ * returns rows or -1. Chunks zero padded to the longest, the three
+ * convolutions with the exact GELU, the channel-major time columns,
+ * conv_out, the positions, layers whose attention sees only the rows of
+ * its window, ln_post, proj1, GELU, proj2 -- Trit's arithmetic throughout. */
+int trit_hip_asr_encoder_encode(const TritHipAsrEncoder *encoder, const float *mel, int frames, float *out);
 
 /* ---- Attention (reference src/layers.rs:343-504) ---------------------- */
 

@@ -7,6 +7,7 @@ this module, and only as the checker or the timed CPU baseline.
 from __future__ import annotations
 
 import ctypes as C
+import math
 import os
 import subprocess
 
@@ -203,6 +204,108 @@ class Encoder:
             x = (x + out_p(att)).astype(np.float32)
             x = (x + fc2_p(gelu(fc1_p(layer_norm(x, fw, fb))))).astype(np.float32)
         return layer_norm(x, self.norms[-2], self.norms[-1])
+
+
+def sinusoids(rows, d, first=0, ln_timescale=math.log(10000.0), scale=1.0) -> np.ndarray:
+    """sinusoids (src/layers.rs:257-270): row p is [sin | cos] of
+    (first + p) * exp(-i * ln_timescale / (d/2 - 1)) for i < d/2, times
+    scale, in float64 (the C library's sin, cos and exp, as Rust's f64
+    calls them), then rounded to f32."""
+    half = d // 2
+    inc = ln_timescale / (half - 1.0)
+    steps = [math.exp(-inc * i) for i in range(half)]
+    out = np.zeros((rows, d), np.float32)
+    for p in range(rows):
+        pos = float(first + p)
+        out[p, :half] = [math.sin(pos * e) * scale for e in steps]
+        out[p, half:] = [math.cos(pos * e) * scale for e in steps]
+    return out
+
+
+def half_len(n):
+    """Length after one kernel-3, stride-2, padding-1 convolution
+    (qwen3_asr.rs:120-123): n / 2 rounded up."""
+    return (n + 1) // 2
+
+
+def conv2d_columns(m, bins, times, channels) -> np.ndarray:
+    """conv2d's im2col (src/models/families/qwen3_asr.rs:408-428): a 3x3,
+    stride-2, padding-1 convolution over a [bin][time][channel] map. Row
+    bin' * times' + time' holds map[2 bin' + dy - 1][2 time' + dx - 1][c]
+    at column c * 9 + 3 dy + dx, zero outside the map."""
+    ob, ot = half_len(bins), half_len(times)
+    m = np.asarray(m, np.float32).reshape(bins, times, channels)
+    pad = np.zeros((bins + 2, times + 2, channels), np.float32)
+    pad[1:-1, 1:-1] = m
+    cols = np.empty((ob, ot, channels, 9), np.float32)
+    for dy in range(3):
+        for dx in range(3):
+            cols[:, :, :, 3 * dy + dx] = pad[dy:dy + 2 * ob:2, dx:dx + 2 * ot:2, :]
+    return cols.reshape(ob * ot, channels * 9)
+
+
+class AsrEncoder:
+    """The Qwen3-ASR audio encoder (AudioEncoder::encode and ::chunk,
+    src/models/families/qwen3_asr.rs:321-405) composed of the oracle's
+    pieces. The frames are cut into chunks of cfg["chunk"] (the last one
+    shorter) and every chunk is zero padded to the longest; per chunk the
+    [bin][time] map goes through three 3x3 stride-2 convolutions, each
+    followed by GELU, then per time step the channel-major columns
+    (channel * bins + bin) through conv_out, plus the sinusoid positions of
+    the chunk's time steps; the kept rows (half^3 of each chunk's real
+    length) are laid end to end. Per layer a pre-norm attention block whose
+    rows see only the rows of their window (half^3(longest) *
+    window_chunks rows) and a pre-norm GELU MLP; then ln_post, proj1, GELU,
+    proj2. `products` are callables x -> x W^T + bias: the three
+    convolutions, conv_out, then qkv, out, fc1, fc2 of each layer, then
+    proj1 and proj2; `norms` per layer (attn w, b, ffn w, b), then ln_post's
+    (w, b)."""
+
+    def __init__(self, cfg, products, norms, positions=None):
+        self.cfg, self.products, self.norms = cfg, products, norms
+        self.positions = (sinusoids(cfg["max_positions"], cfg["d"]) if positions is None
+                          else np.asarray(positions, np.float32))
+
+    def rows(self, frames):
+        c = self.cfg["chunk"]
+        return sum(half_len(half_len(half_len(min(c, frames - s)))) for s in range(0, frames, c))
+
+    def chunk(self, mel, frames):
+        c = self.cfg
+        length = mel.shape[0]
+        m = np.zeros((c["mels"], frames), np.float32)
+        m[:, :length] = mel.T
+        bins, times, channels = c["mels"], frames, 1
+        for conv in self.products[:3]:
+            m = gelu(conv(conv2d_columns(m, bins, times, channels)))
+            bins, times, channels = half_len(bins), half_len(times), m.shape[1]
+        cols = m.reshape(bins, times, channels).transpose(1, 2, 0).reshape(times, channels * bins)
+        return (self.products[3](np.ascontiguousarray(cols)) + self.positions[:times]).astype(np.float32)
+
+    def encode(self, mel, frames):
+        c = self.cfg
+        d, heads = c["d"], c["heads"]
+        mel = np.ascontiguousarray(mel, np.float32).reshape(frames, c["mels"])
+        spans = [(s, min(c["chunk"], frames - s)) for s in range(0, frames, c["chunk"])]
+        longest = max(n for _, n in spans)
+        x = np.concatenate([self.chunk(mel[s:s + n], longest)[:half_len(half_len(half_len(n)))]
+                            for s, n in spans]).astype(np.float32)
+        t = x.shape[0]
+        window = half_len(half_len(half_len(longest))) * c["window_chunks"]
+        hd = d // heads
+        for l in range(c["layers"]):
+            qkv_p, out_p, fc1_p, fc2_p = self.products[4 + 4 * l:8 + 4 * l]
+            aw, ab, fw, fb = self.norms[4 * l:4 * l + 4]
+            qkv = qkv_p(layer_norm(x, aw, ab))
+            att = np.empty((t, d), np.float32)
+            for s in range(0, t, window):
+                r = qkv[s:s + min(window, t - s)]
+                att[s:s + r.shape[0]] = attention(r[:, :d], r[:, d:2 * d], r[:, 2 * d:], heads, heads, hd,
+                                                  causal=False)
+            x = (x + out_p(att)).astype(np.float32)
+            x = (x + fc2_p(gelu(fc1_p(layer_norm(x, fw, fb))))).astype(np.float32)
+        h = gelu(self.products[-2](layer_norm(x, self.norms[-2], self.norms[-1])))
+        return self.products[-1](h).astype(np.float32)
 
 
 def f32_to_f16(values) -> np.ndarray:

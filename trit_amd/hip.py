@@ -47,6 +47,13 @@ class EncoderConfig(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("d", "layers", "heads", "ffn", "mels", "positions")]
 
 
+ASR_FIELDS = ("d", "layers", "heads", "ffn", "mels", "channels", "chunk", "window_chunks", "out", "max_positions")
+
+
+class AsrEncoderConfig(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ASR_FIELDS]
+
+
 def lib():
     global _lib
     if _lib is None:
@@ -106,6 +113,11 @@ def lib():
             "trit_hip_f32_to_f16": (i, [p, C.c_int64, p]),
             "trit_hip_f16_to_f32": (i, [p, C.c_int64, p]),
             "trit_hip_encoder_new": (i, [C.POINTER(EncoderConfig), p, p, p, p, p, pp]),
+            "trit_hip_asr_encoder_new": (i, [C.POINTER(AsrEncoderConfig), p, p, p, p, p, p, pp]),
+            "trit_hip_asr_encoder_free": (None, [p]),
+            "trit_hip_asr_encoder_rows": (i, [p, i]),
+            "trit_hip_asr_encoder_positions": (i, [p, p]),
+            "trit_hip_asr_encoder_encode": (i, [p, p, i, p]),
             "trit_hip_encoder_free": (None, [p]),
             "trit_hip_encoder_encode": (i, [p, p, p]),
             "trit_hip_bpe_open": (i, [C.c_char_p, pp]),
@@ -437,6 +449,53 @@ class Encoder:
     def free(self):
         if self.h:
             lib().trit_hip_encoder_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class AsrEncoder:
+    """The Qwen3-ASR audio encoder on the device (src/models/families/
+    qwen3_asr.rs:284-405): convs (conv2d1, conv2d2, conv2d3), conv_out,
+    then qkv, out, fc1, fc2 of each layer, then proj1 and proj2, as Dense
+    layers with their biases; norms per layer attn w, b, ffn w, b, then
+    ln_post's w, b. The sinusoid positions are made by the library."""
+
+    def __init__(self, cfg: dict, convs, conv_out: Dense, linears, norms, proj1: Dense, proj2: Dense):
+        c = AsrEncoderConfig(*(cfg[k] for k in ASR_FIELDS))
+        self.cfg = cfg
+        cv = (C.c_void_p * 3)(*[l.h for l in convs])
+        arr = (C.c_void_p * len(linears))(*[l.h for l in linears])
+        nrm = np.ascontiguousarray(np.concatenate([np.asarray(v, np.float32).reshape(-1) for v in norms]))
+        out = C.c_void_p()
+        check(lib().trit_hip_asr_encoder_new(C.byref(c), cv, conv_out.h, arr, ptr(nrm), proj1.h, proj2.h,
+                                             C.byref(out)))
+        self.h = out
+
+    def rows(self, frames: int) -> int:
+        return check(lib().trit_hip_asr_encoder_rows(self.h, frames))
+
+    def positions(self):
+        c = self.cfg
+        out = np.empty((c["max_positions"], c["d"]), np.float32)
+        check(lib().trit_hip_asr_encoder_positions(self.h, ptr(out)))
+        return out
+
+    def encode(self, mel, frames: int):
+        """AudioEncoder::encode: rows x out from frames x mels features."""
+        c = self.cfg
+        mel = np.ascontiguousarray(mel, np.float32).reshape(frames, c["mels"])
+        out = np.empty((self.rows(frames), c["out"]), np.float32)
+        check(lib().trit_hip_asr_encoder_encode(self.h, ptr(mel), frames, ptr(out)))
+        return out
+
+    def free(self):
+        if self.h:
+            lib().trit_hip_asr_encoder_free(self.h)
             self.h = None
 
     def __del__(self):
