@@ -296,7 +296,7 @@ def config_lines(H, sweeps=10):
     # runs it): its stem and 4 of its 32 layers (d 1280, 20 heads, MLP 5120,
     # 128 mel bins, 1500 positions) with Q8_0 products; wall clock of
     # trit_hip_encoder_encode (host copies of the 3000 x 128 window and the
-    # 1500 x 1280 output included), best of 3.
+    # 1500 x 1280 output included), best of 5.
     ecfg = dict(d=1280, layers=4, heads=20, ffn=5120, mels=128, positions=1500)
     ed, eff = ecfg["d"], ecfg["ffn"]
 
@@ -310,17 +310,48 @@ def config_lines(H, sweeps=10):
                       np.zeros((ecfg["positions"], ed), np.float32), shared * ecfg["layers"], norms)
     mel = synth.activations(synth.seed_for(0, 96), 2 * ecfg["positions"], ecfg["mels"])
     enc.encode(mel)  # warm-up
-    t_enc = min(_timed(lambda: enc.encode(mel)) for _ in range(3))
+    t_enc = min(_timed(lambda: enc.encode(mel)) for _ in range(5))
     enc0 = hip.Encoder(dict(ecfg, layers=1), eq8(ed, 3 * ecfg["mels"], 4), eq8(ed, 3 * ed, 5),
                        np.zeros((ecfg["positions"], ed), np.float32), shared, norms[:6])
     enc0.encode(mel)
-    t_one = min(_timed(lambda: enc0.encode(mel)) for _ in range(3))
+    t_one = min(_timed(lambda: enc0.encode(mel)) for _ in range(5))
     per_layer = (t_enc - t_one) / (ecfg["layers"] - 1)
     out["audio_encoder_whisper_large_v3"] = dict(
         encode_4_layers_ms=round(t_enc * 1e3, 2), per_layer_ms=round(per_layer * 1e3, 3),
         stem_and_one_layer_ms=round(t_one * 1e3, 2), full_32_layers_ms_estimate=round((t_one + 31 * per_layer) * 1e3, 1),
         note="Q8_0 products (int8 MFMA for the 1500-row products), Trit's exact attention over 1500 positions")
     del enc, enc0, shared
+
+    # The Qwen3-ASR audio encoder over 30 s of audio (3000 mel frames: 30
+    # chunks of 100, 390 rows, windows of 8 chunks): Qwen3-ASR's stem (128
+    # mel bins, 480 channels; the 9-input first convolution in f32, the
+    # others and conv_out Q8_0 on the matrix cores) under a d 1024, 16-head,
+    # MLP 4096 stack with Q8_0 products, 8 layers timed against 1 (wall
+    # clock of trit_hip_asr_encoder_encode, host copies included, best of 5).
+    acfg = dict(d=1024, layers=8, heads=16, ffn=4096, mels=128, channels=480, chunk=100, window_chunks=8,
+                out=2048, max_positions=1500)
+    ad, aff, ach, frames = acfg["d"], acfg["ffn"], acfg["channels"], 3000
+    c1 = synth.activations(synth.seed_for(0, 97), ach, 9) * np.float32(0.3)
+    convs = [hip.Dense.f32(c1, np.zeros(ach, np.float32)), eq8(ach, 9 * ach, 6), eq8(ach, 9 * ach, 7)]
+    conv_out = eq8(ad, ach * 16, 8)
+    shared = [eq8(3 * ad, ad, 9), eq8(ad, ad, 10), eq8(aff, ad, 11), eq8(ad, aff, 12)]
+    proj = [eq8(ad, ad, 13), eq8(acfg["out"], ad, 14)]
+    norms = [np.ones(ad, np.float32), np.zeros(ad, np.float32)] * (2 * acfg["layers"] + 1)
+    amel = synth.activations(synth.seed_for(0, 98), frames, acfg["mels"])
+    asr = hip.AsrEncoder(acfg, convs, conv_out, shared * acfg["layers"], norms, *proj)
+    asr.encode(amel, frames)  # warm-up
+    t_asr = min(_timed(lambda: asr.encode(amel, frames)) for _ in range(5))
+    asr1 = hip.AsrEncoder(dict(acfg, layers=1), convs, conv_out, shared, norms[:6], *proj)
+    asr1.encode(amel, frames)
+    t_asr1 = min(_timed(lambda: asr1.encode(amel, frames)) for _ in range(5))
+    per = (t_asr - t_asr1) / (acfg["layers"] - 1)
+    out["audio_encoder_qwen3_asr_30s"] = dict(
+        rows=asr.rows(frames), encode_8_layers_ms=round(t_asr * 1e3, 2), per_layer_ms=round(per * 1e3, 3),
+        stem_one_layer_and_projections_ms=round(t_asr1 * 1e3, 2),
+        layers_24_ms_estimate=round((t_asr1 + 23 * per) * 1e3, 1),
+        note="3000 mel frames; f32 first convolution, Q8_0 elsewhere (int8 MFMA for the many-row products, "
+             "K tails included), Trit's exact attention within 104-row windows")
+    del asr, asr1, shared, convs, conv_out, proj
 
     # C5 end to end: one decoder layer of the prefill's shape (hidden 2048,
     # 16/8 heads x 128, SwiGLU 3072) over the 1564-row prompt: the MFMA

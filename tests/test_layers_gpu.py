@@ -73,7 +73,7 @@ def test_q8_0_bias_relu(gpu):
 # More than 8 rows: the matrix-core product (int8 MFMA), same bits.
 @pytest.mark.parametrize("n,k,m", [(256, 512, 9), (384, 1024, 64), (128, 256, 100), (2048, 2048, 257),
                                    (1024, 3072, 40), (128, 384, 70), (256, 4320, 33), (128, 32, 12),
-                                   (384, 1248, 129)])
+                                   (384, 1248, 129), (480, 4320, 70), (32, 256, 40), (224, 512, 65), (96, 96, 17)])
 def test_q8_0_many_rows(gpu, n, k, m):
     print(f"case q8_0 matrix cores n={n} k={k} m={m}", flush=True)
     codes, sbits, blocks = q8_layer(synth.seed_for(2, n + k), n, k)
@@ -83,9 +83,10 @@ def test_q8_0_many_rows(gpu, n, k, m):
     assert bits_equal(got, ref), np.max(np.abs(got - ref))
 
 
-def test_q8_0_many_rows_bias_relu(gpu):
-    print("case q8_0 matrix cores bias relu", flush=True)
-    n, k, m = 256, 512, 33
+@pytest.mark.parametrize("n", [256, 224])
+def test_q8_0_many_rows_bias_relu(gpu, n):
+    print(f"case q8_0 matrix cores bias relu n={n}", flush=True)
+    k, m = 512, 33
     codes, sbits, blocks = q8_layer(14, n, k)
     bias = synth.activations(15, 1, n)[0]
     x = synth.activations(16, m, k)
@@ -112,7 +113,7 @@ def test_prefill_gemm_1564_rows(gpu, n):
 
 
 @pytest.mark.parametrize("n,k,m", [(512, 1024, 1), (384, 2048, 4), (256, 512, 33), (512, 1024, 70), (256, 384, 40),
-                                   (128, 128, 20)])
+                                   (128, 128, 20), (480, 384, 30)])
 def test_int8(gpu, n, k, m):
     print(f"case int8 n={n} k={k} m={m}", flush=True)
     codes = synth.ints(21, (n, k), -127, 127).astype(np.int8)

@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 
 #include "../../include/trit_hip.h"
 #include "decoder_impl.h"
@@ -154,6 +155,19 @@ int blocks_for(size_t n) { return (int)std::min<size_t>((n + 255) / 256, 4096); 
 
 }  // namespace
 
+// Device buffers an encoder keeps between calls, grown on demand: an
+// encode allocates only when it needs more than the calls before it. Calls
+// on one encoder take turns (the mutex); the buffers are the encoder's
+// until it is freed.
+struct Workspace {
+    std::mutex mu;
+    DeviceMemory bufs[16];
+    DeviceMemory& get(int i, size_t bytes) {
+        if (bufs[i].bytes < bytes) bufs[i].alloc(bytes);
+        return bufs[i];
+    }
+};
+
 struct EncoderImpl {
     TritHipEncoderConfig c{};
     LayerRef conv1, conv2;
@@ -161,6 +175,7 @@ struct EncoderImpl {
     DeviceMemory positions;        // positions x d
     DeviceMemory norms;            // per layer: attn w, b, ffn w, b (d each); then final w, b
     const float* norm(int l, int i) const { return norms.as<float>() + ((size_t)4 * l + i) * c.d; }
+    mutable Workspace ws;
 };
 
 struct AsrEncoderImpl {
@@ -170,6 +185,7 @@ struct AsrEncoderImpl {
     DeviceMemory positions;        // max_positions x d
     DeviceMemory norms;            // per layer: attn w, b, ffn w, b (d each); then ln_post w, b
     const float* norm(int l, int i) const { return norms.as<float>() + ((size_t)4 * l + i) * c.d; }
+    mutable Workspace ws;
 };
 
 // Length after a kernel-3, stride-2, padding-1 convolution (qwen3_asr.rs:
@@ -324,11 +340,21 @@ int trit_hip_encoder_encode(const TritHipEncoder* encoder, const float* mel, flo
         const auto& c = e.c;
         const int P = c.positions, frames = 2 * P, d = c.d, hd = d / c.heads;
         hipStream_t s = stream();
-        DeviceMemory dmel((size_t)frames * c.mels * 4), cols((size_t)frames * 3 * std::max(c.mels, d) * 4);
-        DeviceMemory h((size_t)frames * d * 4), x((size_t)P * d * 4), xn((size_t)P * d * 4);
-        DeviceMemory qkv((size_t)P * 3 * d * 4), att((size_t)P * d * 4), hid((size_t)P * c.ffn * 4);
-        DeviceMemory kc((size_t)P * d * 4), vc((size_t)P * d * 4), st(sizeof(State)), scratch;
-        TRIT_HIP(hipMemcpyAsync(dmel.ptr, mel, dmel.bytes, hipMemcpyHostToDevice, s));
+        std::lock_guard<std::mutex> lock(e.ws.mu);
+        Workspace& ws = e.ws;
+        DeviceMemory& dmel = ws.get(0, (size_t)frames * c.mels * 4);
+        DeviceMemory& cols = ws.get(1, (size_t)frames * 3 * std::max(c.mels, d) * 4);
+        DeviceMemory& h = ws.get(2, (size_t)frames * d * 4);
+        DeviceMemory& x = ws.get(3, (size_t)P * d * 4);
+        DeviceMemory& xn = ws.get(4, (size_t)P * d * 4);
+        DeviceMemory& qkv = ws.get(5, (size_t)P * 3 * d * 4);
+        DeviceMemory& att = ws.get(6, (size_t)P * d * 4);
+        DeviceMemory& hid = ws.get(7, (size_t)P * c.ffn * 4);
+        DeviceMemory& kc = ws.get(8, (size_t)P * d * 4);
+        DeviceMemory& vc = ws.get(9, (size_t)P * d * 4);
+        DeviceMemory& st = ws.get(10, sizeof(State));
+        DeviceMemory& scratch = ws.bufs[11];
+        TRIT_HIP(hipMemcpyAsync(dmel.ptr, mel, (size_t)frames * c.mels * 4, hipMemcpyHostToDevice, s));
         State h0{};  // pos = tk - tq = 0: every query sees every key (no mask)
         TRIT_HIP(hipMemcpyAsync(st.ptr, &h0, sizeof(State), hipMemcpyHostToDevice, s));
         // The stem (audio_encoder.rs:116-123).
@@ -462,11 +488,21 @@ int trit_hip_asr_encoder_encode(const TritHipAsrEncoder* encoder, const float* m
             col_floats = std::max(col_floats, positions * (i == 1 ? 9 : 9 * ch));
             map_floats = std::max(map_floats, positions * ch);
         }
-        DeviceMemory dmel((size_t)frames * c.mels * 4), cols(col_floats * 4), map(map_floats * 4);
-        DeviceMemory x((size_t)t * d * 4), xn((size_t)t * d * 4), qkv((size_t)t * 3 * d * 4), att((size_t)t * d * 4);
-        DeviceMemory hid((size_t)t * std::max(c.ffn, c.out) * 4);
-        DeviceMemory kc((size_t)window * d * 4), vc((size_t)window * d * 4), st(sizeof(State)), scratch;
-        TRIT_HIP(hipMemcpyAsync(dmel.ptr, mel, dmel.bytes, hipMemcpyHostToDevice, s));
+        std::lock_guard<std::mutex> lock(e.ws.mu);
+        Workspace& ws = e.ws;
+        DeviceMemory& dmel = ws.get(0, (size_t)frames * c.mels * 4);
+        DeviceMemory& cols = ws.get(1, col_floats * 4);
+        DeviceMemory& map = ws.get(2, map_floats * 4);
+        DeviceMemory& x = ws.get(3, (size_t)t * d * 4);
+        DeviceMemory& xn = ws.get(4, (size_t)t * d * 4);
+        DeviceMemory& qkv = ws.get(5, (size_t)t * 3 * d * 4);
+        DeviceMemory& att = ws.get(6, (size_t)t * d * 4);
+        DeviceMemory& hid = ws.get(7, (size_t)t * std::max(c.ffn, c.out) * 4);
+        DeviceMemory& kc = ws.get(8, (size_t)window * d * 4);
+        DeviceMemory& vc = ws.get(9, (size_t)window * d * 4);
+        DeviceMemory& st = ws.get(10, sizeof(State));
+        DeviceMemory& scratch = ws.bufs[11];
+        TRIT_HIP(hipMemcpyAsync(dmel.ptr, mel, (size_t)frames * c.mels * 4, hipMemcpyHostToDevice, s));
         State h0{};  // pos = tk - tq = 0: every row of a window sees the whole window
         TRIT_HIP(hipMemcpyAsync(st.ptr, &h0, sizeof(State), hipMemcpyHostToDevice, s));
         // The chunks (qwen3_asr.rs:389-405): three convolutions with GELU over

@@ -186,7 +186,12 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void gemm_kernel(const int8_t* __r
     const int mbase = bm * BM;
     // LDS weight row i holds weight row brow(i): 128 rows, or for the
     // SwiGLU pair 64 gate rows then their 64 up rows.
-    auto brow = [&](int i) { return P == 1 ? bn * 128 + i : (i < 64 ? bn * 64 + i : n / 2 + bn * 64 + (i - 64)); };
+    // Rows past n (the last tile when n % 128 != 0) load row n - 1 and
+    // store nothing.
+    auto brow = [&](int i) {
+        const int r = P == 1 ? bn * 128 + i : (i < 64 ? bn * 64 + i : n / 2 + bn * 64 + (i - 64));
+        return r < n ? r : n - 1;
+    };
 
     // Global loads of a chunk, 16 bytes a piece, 16 threads a row (256
     // contiguous bytes): 4 x pieces and 8 weight pieces per thread; threads
@@ -349,8 +354,8 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void gemm_kernel(const int8_t* __r
         if (row >= m) continue;
         float v0 = t0[r], v1 = t1[r];
         if (bias) {
-            v0 = v0 + bias[r0 + lr];
-            v1 = v1 + bias[r1 + lr];
+            v0 = v0 + bias[min(r0 + lr, n - 1)];  // columns past n are not stored
+            v1 = v1 + bias[min(r1 + lr, n - 1)];
         }
         if (a.relu) {
             v0 = __builtin_fmaxf(v0, 0.0f);
@@ -358,14 +363,11 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void gemm_kernel(const int8_t* __r
         }
         if (P == 2) {
             a.y[(size_t)row * ldy + r0 + lr] = silu_trit(v0) * v1;
-        } else if (a.epilogue == EPI_RESIDUAL) {
-            const size_t i0 = (size_t)row * ldy + r0 + lr, i1 = (size_t)row * ldy + r1 + lr;
-            a.y[i0] = a.residual[i0] + v0;
-            a.y[i1] = a.residual[i1] + v1;
-        } else {
-            a.y[(size_t)row * ldy + r0 + lr] = v0;
-            a.y[(size_t)row * ldy + r1 + lr] = v1;
+            continue;
         }
+        const size_t i0 = (size_t)row * ldy + r0 + lr, i1 = (size_t)row * ldy + r1 + lr;
+        if (r0 + lr < n) a.y[i0] = a.epilogue == EPI_RESIDUAL ? a.residual[i0] + v0 : v0;
+        if (r1 + lr < n) a.y[i1] = a.epilogue == EPI_RESIDUAL ? a.residual[i1] + v1 : v1;
     }
 }
 
@@ -394,7 +396,7 @@ Scratch carve(void* base, int m, int k) {
 
 template <int G, bool HALF, int P>
 void launch_gemm(const Layer& L, const GemvArgs& a, const Scratch& sc, hipStream_t s) {
-    const int nb = P == 1 ? L.n / 128 : (L.n / 2) / 64;
+    const int nb = P == 1 ? (L.n + 127) / 128 : (L.n / 2) / 64;
     const int mb = sc.mpad / BM;
     if (L.k % KC == 0)
         launch_timed(a, gemm_kernel<G, HALF, P, false>, dim3(nb * mb), dim3(GEMM_THREADS), 0, s,
@@ -413,7 +415,8 @@ bool gemm_supported(const Layer& L, const GemvArgs& a) {
     if (L.kind != Q8_0 && L.kind != Q4_K && L.kind != INT8) return false;
     // k a multiple of the group (a partial last chunk of K is zero past k);
     // RMSNorm computed here takes whole 256-value chunks.
-    if (L.n % 128 != 0 || L.k % group_of(L) != 0) return false;
+    if (L.k % group_of(L) != 0) return false;
+    if (a.epilogue == EPI_SILU_PAIR && (L.n / 2) % 64 != 0) return false;
     if (a.norm_w && !a.norm_inv && L.k % KC != 0) return false;
     // 32-bit byte offsets into the codes of x and of the weights.
     if ((int64_t)a.m * L.k >= (int64_t)1 << 31 || (int64_t)L.n * L.k >= (int64_t)1 << 32) return false;

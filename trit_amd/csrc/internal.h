@@ -187,8 +187,9 @@ void gemv_float(const Layer& L, const GemvArgs& a, hipStream_t s);
 // SwiGLU pair): the same bits row by row.
 bool gemm_float_supported(const Layer& L, const GemvArgs& a);
 void gemm_float(const Layer& L, const GemvArgs& a, hipStream_t s);
-// Integer products of any row count on the matrix cores (Q8_0, Q4_K, INT8
-// with n % 128 == 0 and k % 256 == 0). `scratch` holds gemm_scratch_bytes(m, k) bytes of
+// Integer products of any row count on the matrix cores (Q8_0, Q4_K, INT8;
+// k a multiple of the weight group, any n; the SwiGLU pair needs n / 2 a
+// multiple of 64). `scratch` holds gemm_scratch_bytes(m, k) bytes of
 // device memory the product may overwrite.
 bool gemm_supported(const Layer& L, const GemvArgs& a);
 size_t gemm_scratch_bytes(int m, int k);
