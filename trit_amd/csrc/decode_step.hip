@@ -8,7 +8,12 @@
 // and polled with agent-scope loads until the tag is the one the reader
 // waits for. The tag names the token step and the phase, so a word is never
 // mistaken for an older one, and no barrier, fence or cache flush is
-// needed between phases. A phase's weights do not depend on its inputs:
+// needed between phases. The key and value caches are written with
+// agent-scope stores (through the L2) and read with plain loads: each
+// appending wave waits for its stores before the block barrier that
+// precedes the block's next put, so a reader that saw a later tag reads
+// them from memory (no XCD has their lines cached before they are
+// written: a key's lines hold only that key). A phase's weights do not depend on its inputs:
 // each block issues their loads before it waits, so the weight stream
 // overlaps the hand-over instead of following it.
 //
@@ -23,10 +28,11 @@
 //
 // Products use the one-row kernel's arithmetic (gemv_decode.hip): Trit's
 // quantizer, exact i32 block dots and the f32 group chain in order, so
-// their values are Trit's bit for bit given the same input. The RMSNorm
-// sums are the one-row kernel's tree; attention sums run in parallel
-// (fast mode). Every wait has a deadline: a block that misses it marks the
-// session's error flag and the launch drains.
+// their values are Trit's bit for bit given the same input. The default
+// instance keeps Trit's sum orders (the serial RMSNorm, q/k norm, softmax
+// and p.V chains, bit for bit the f16-cache oracle); the tree-sum instance
+// sums those as trees. Every wait has a deadline: a block that misses it
+// marks the session's error flag and the launch drains.
 #include "decoder_impl.h"
 #include "device.h"
 
@@ -1259,6 +1265,13 @@ __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, in
 #pragma unroll
         for (int i = 0; i < WAVE / 4; ++i) asm volatile("" : "+v"(pr[i]));
     }
+    // The appended key and value are acknowledged (agent-scope stores write
+    // through the L2) before the barriers below, so before this block's
+    // attention outputs are put: whoever reads them in a later layer or step
+    // waited, through the tags, for that put. Issued microseconds ago, they
+    // have landed; the wait costs nothing.
+    if (b < kvh && (w == 1 || w == 2)) __builtin_amdgcn_s_waitcnt(VMCNT0);
+    if (nkw == 0) __syncthreads();  // no turns: still a barrier before the put
     // Every wave passes nkw barriers: the turns before its own, then its
     // turn's end and the rest.
     float acc = 0.0f;
@@ -1630,6 +1643,10 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         sm.bv[w] = best;
         sm.bi[w] = index;
     }
+    // Every store of the block in this step (the cache appends among them)
+    // is acknowledged before the candidates are put: the next step reads
+    // the caches only after it has polled every block's candidates.
+    __builtin_amdgcn_s_waitcnt(VMCNT0);
     __syncthreads();
     if (t == 0) {
         float bv = sm.bv[0];
