@@ -324,10 +324,11 @@ def test_step_default(qshape, monkeypatch):
 
 @pytest.mark.parametrize("window", [-1, 0])
 def test_step_norm_rechained(qshape, monkeypatch, window):
-    """The step's RMSNorm joins segments chained from candidate starts; with
-    no candidates (-1) every segment is chained again from its true start,
-    and with the estimate alone (0) most are: the same bits either way."""
-    print(f"case decoder persistent step, RMSNorm candidates window {window}", flush=True)
+    """The step's RMSNorm and softmax sums join segments chained from
+    candidate starts; with no candidates (-1) every segment is chained again
+    from its true start, and with the estimate alone (0) most are: the same
+    bits either way."""
+    print(f"case decoder persistent step, RMSNorm and softmax candidates window {window}", flush=True)
     w, ref, lm, ref16 = qshape
     monkeypatch.setenv("TRIT_HIP_NORM_WINDOW", str(window))
     check_generate_default(w, ref16, lm, QS, monkeypatch)

@@ -88,7 +88,7 @@ struct StepArgs {
     int rq, ro, rgu, rd;      // rows per block (gate_up: pairs), multiples of 4
     int rh;                   // head rows per block
     unsigned long long ticks; // wall-clock ticks a block may wait in a step
-    int norm_window;          // RMSNorm: candidate starts on either side of the estimate
+    int norm_window;          // RMSNorm and softmax sums: candidate starts on either side of the estimate
 };
 
 struct Smem {
@@ -115,6 +115,8 @@ struct Smem {
         alignas(16) _Float16 vs[T][HD / 2];
     };
     alignas(16) float probs[T];           // the exact attention's probabilities
+    float spart[NW];                      // its sum: each segment's tree sum
+    float sres[NW][WAVE];                 // its sum: each segment's chain from candidate L
     float carry[WAVE];                    // its p.V sums, passed from wave to wave
     float ppos;                           // the new key's probability
     float wmax[NW];
@@ -123,7 +125,6 @@ struct Smem {
     float bv[T];
     int bi[T];
     float inv;
-    float chain;  // a plain serial chain's result, passed between waves
     int abort;
     int token;
 };
@@ -970,22 +971,62 @@ __device__ bool attention_all(int t, const StepArgs& a, const LayerPtrs& L, int 
     return true;
 }
 
-// The chain sum ((0 + v_0) + v_1) + ... of n <= 32 N values in LDS, in
-// order, by one wave: lane L takes values [N L, N L + N) (zeros past n,
-// which add nothing) and lane_chain passes the carry through the lanes.
-// Every lane of the wave returns the sum.
-template <int N>
-__device__ __forceinline__ float wave_chain_sum(const float* v, int n, int lane) {
-    float x[N];
+// The chain sum ((0 + v_0) + v_1) + ... of the T values in LDS (zeros
+// past the n that matter add nothing to these non-negative sums), bit for
+// bit, by all the waves at once: norm_inv_spec's candidate-start segments.
+// Wave w chains segment w (S values, S * NW <= T) from 64 candidate starts
+// around the tree estimate of the chain before it; the segments are joined
+// in order, and a segment whose true start no candidate holds is chained
+// again from it. The join is the same in every wave (the same values and
+// ballots), so its barrier is uniform. Every thread returns the sum.
+__device__ float chain_sum_spec(int t, const float* v, int n, int window, Smem& sm) {
+    const int w = __builtin_amdgcn_readfirstlane(t / WAVE), lane = t % WAVE;
+    const int S = ((n + NW - 1) / NW + 3) & ~3;
+    const float* seg = v + S * w;
+    float part = 0.0f;
+    for (int i = lane; i < S; i += WAVE) part += seg[i];
+    const float ps = wave_sum(part);
+    if (lane == 0) sm.spart[w] = ps;
+    __syncthreads();
+    float est[NW];
+    est[0] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < N; i += 4) {
-        const float4 f = N * lane + i < n ? *(const float4*)(v + N * lane + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        x[i] = f.x, x[i + 1] = f.y, x[i + 2] = f.z, x[i + 3] = f.w;
+    for (int q = 1; q < NW; ++q) est[q] = est[q - 1] + sm.spart[q - 1];
+    const auto cand = [&](int q) {
+        const int off = lane - WAVE / 2;
+        if (q == 0) return 0.0f;
+        if (off < -window || off > window) return __builtin_nanf("");
+        const int bits = (int)__float_as_uint(est[q]) + off;
+        return __uint_as_float((uint32_t)(bits < 0 ? 0 : bits));
+    };
+    float c = cand(0);
+#pragma unroll
+    for (int q = 1; q < NW; ++q)
+        if (w == q) c = cand(q);
+    for (int i = 0; i < S; i += 4) {
+        const float4 x = *(const float4*)(seg + i);
+        c = c + x.x;
+        c = c + x.y;
+        c = c + x.z;
+        c = c + x.w;
     }
+    sm.sres[w][lane] = c;
+    __syncthreads();
+    float sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sm.sres[0][lane])));
+    bool again = false;
 #pragma unroll
-    for (int i = 0; i < N; ++i)
-        if (N * lane + i >= n) x[i] = 0.0f;
-    return lane_chain<N>(x, 0.0f, (n + N - 1) / N);
+    for (int q = 1; q < NW; ++q) {
+        const unsigned long long m = __ballot(cand(q) == sum);
+        if (m) {
+            sum = __builtin_bit_cast(float,
+                                     __builtin_amdgcn_readlane(__builtin_bit_cast(int, sm.sres[q][lane]), __builtin_ctzll(m)));
+        } else {
+            again = true;
+            for (int i = 0; i < S; ++i) sum = sum + v[S * q + i];
+        }
+    }
+    if (again) __syncthreads();  // the values stay read until every wave is done
+    return sum;
 }
 
 // The cached keys and values that the next attention of a key/value head
@@ -1221,16 +1262,10 @@ __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, in
     const float e = t < tk ? exp_trit(score - mx) : 0.0f;
     sm.probs[t] = e;
     __syncthreads();
-    // Their sum in key order from 0 (by the last wave, which holds no
-    // values for p.V while the session is short), then p_j = e_j * (1/sum).
-    if (w == NW - 1) {
-        const float sum = wave_chain_sum<16>(sm.probs, tk, lane);
-        if (lane == 0) sm.chain = 1.0f / sum;
-    }
-    __syncthreads();
-    // p_j = e_j * (1/sum); the chain below reads -0 (adding nothing) past
-    // the cached keys, and the new key's probability on its own.
-    const float p = e * sm.chain;
+    // Their sum in key order from 0, by every wave, then p_j = e_j *
+    // (1/sum); the chain below reads -0 (adding nothing) past the cached
+    // keys, and the new key's probability on its own.
+    const float p = e * (1.0f / chain_sum_spec(t, sm.probs, tk, a.norm_window, sm));
     sm.probs[t] = t < pos ? p : -0.0f;
     if (t == pos) sm.ppos = p;
     // p.V in key order: lane d chains dim 64 h2 + d, wave w over keys
@@ -1920,8 +1955,9 @@ void decode_step_launch(SessionImpl& S, int step, int pos, int nsteps, hipStream
     // path: 0 makes every block's first wait give up, and the launch drains).
     if (const char* v = getenv("TRIT_HIP_STEP_DEADLINE_US"))
         a.ticks = (unsigned long long)(rate_khz > 0 ? rate_khz : 100000) * strtoull(v, nullptr, 10) / 1000ull;
-    // TRIT_HIP_NORM_WINDOW narrows the RMSNorm's candidate starts (tests of
-    // the path that chains a segment again: 0 leaves only the estimate).
+    // TRIT_HIP_NORM_WINDOW narrows the candidate starts of the RMSNorm and
+    // softmax sums (tests of the path that chains a segment again: 0 leaves
+    // only the estimate, -1 none).
     a.norm_window = 31;
     if (const char* v = getenv("TRIT_HIP_NORM_WINDOW")) a.norm_window = (int)strtol(v, nullptr, 10);
     void* args[] = {&a, &step, &pos, (void*)&seq0, &nsteps};
