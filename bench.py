@@ -375,6 +375,47 @@ def config_lines(H, sweeps=10):
         layer_ms=round(t5 * 1e3, 3), rows_per_s=round(m / t5, 1), attention_ops=att_ops,
         note="one layer over 1564 rows, wall clock of the prefill call (host synchronisation included)")
     del sess, lm5
+
+    # Decoders the persistent step does not take (it holds d <= 2048 and an
+    # MLP of at most 3072) run the per-kernel loop, one graph replay a
+    # token: Qwen3-1.7B's shape (d 2048, MLP 6144, 28 layers, 16/8 heads x
+    # 128, vocab 151936, Q8_0 linears, tied f16 head), a 256-token prompt
+    # and 64 greedy steps, in Trit's sum orders with f16 caches; and the
+    # 0.6B shape on the same loop (TRIT_HIP_STEP=0) beside it.
+    def loop_rate(cfg, seed, steps=64, prompt_len=256):
+        lmx = model.build_decoder(synth.lm_weights(cfg, config=seed))
+        px = synth.prompt(seed, prompt_len, cfg["vocab"])
+        sx = lmx.session(prompt_len + steps, 0)
+        sx.prefill(px, want_logits=False)
+        sx.generate(8)  # warm-up: the step's graph is captured
+        sx.reset()
+        sx.prefill(px, want_logits=False)
+        ev_a, ev_b = H.event(), H.event()
+        toks = np.empty(steps, np.int32)
+        pers = C.c_int(0)
+        n = hip.check(hip.lib().trit_hip_session_generate_timed(sx.h, steps, None, 0,
+                                                                toks.ctypes.data_as(C.c_void_p), ev_a, ev_b,
+                                                                C.byref(pers)))
+        ms = H.elapsed_ms(ev_a, ev_b)
+        roof = step_roofline(cfg, prompt_len, n, ms, bool(pers.value), "default")
+        del sx, lmx
+        return dict(tok_s=round((n - 1) / (ms * 1e-3), 1), us_per_forward=roof["us_per_forward"],
+                    bytes_per_forward=roof["bytes_per_forward"], gb_s=roof["achieved"], frac=roof["frac"],
+                    persistent=bool(pers.value))
+
+    cfg17 = dict(synth.QWEN3_06B, d=2048, ffn=6144)
+    out["decode_qwen3_1.7b_shape_per_kernel_loop"] = dict(
+        loop_rate(cfg17, 17), note="256-token prompt, 64 steps; the per-kernel loop (graph replay a token)")
+    prev = os.environ.get("TRIT_HIP_STEP")
+    os.environ["TRIT_HIP_STEP"] = "0"
+    try:
+        out["decode_qwen3_0.6b_shape_per_kernel_loop"] = dict(
+            loop_rate(dict(synth.QWEN3_06B), 1), note="the same loop on the 0.6B shape (TRIT_HIP_STEP=0)")
+    finally:
+        if prev is None:
+            del os.environ["TRIT_HIP_STEP"]
+        else:
+            os.environ["TRIT_HIP_STEP"] = prev
     return out
 
 

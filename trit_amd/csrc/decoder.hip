@@ -38,32 +38,89 @@ constexpr int CHOOSE_SPAN = CHOOSE_THREADS * 4;  // logits per block
 
 // ---- small kernels ----------------------------------------------------
 
-// Exact RMSNorm factor of each row: 1 / sqrt(serial sum of v*v / d + eps)
-// (src/layers.rs:139). The squares are made in parallel; one lane adds
-// them in Trit's order.
-__global__ void norm_inv_kernel(const float* __restrict__ x, int d, float eps, float* __restrict__ inv,
-                                const State* st) {
+// RMSNorm factor of each row with Trit's sum -- the squares added one
+// after another from 0 (src/layers.rs:136-144) -- bit for bit, by the 8
+// waves of a 512-thread block at once: wave w chains segment w (S values,
+// zeros past d adding nothing) from 64 candidate starts, lane L from the
+// float L - 32 steps from the tree estimate of the chain before the
+// segment (within a few steps of it: each add of the chain rounds by at
+// most half a step); the segments are then joined in order -- the lane
+// whose start equals the chain so far holds the chain after the segment --
+// and a segment whose true start no candidate within `window` steps holds
+// is chained again from it.
+constexpr int NI_THREADS = 512, NI_WAVES = NI_THREADS / 64;
+
+__host__ __device__ inline int norm_inv_segment(int d) { return ((d + NI_WAVES - 1) / NI_WAVES + 3) & ~3; }
+
+__global__ __launch_bounds__(NI_THREADS) void norm_inv_kernel(const float* __restrict__ x, int d, float eps,
+                                                              float* __restrict__ inv, const State* st, int window) {
     if (st && st->done) return;
-    extern __shared__ float sq[];
+    extern __shared__ __align__(16) float sq[];  // S * NI_WAVES squares
+    __shared__ float part[NI_WAVES];
+    __shared__ float res[NI_WAVES][64];
+    const int t = threadIdx.x, w = t / 64, lane = t % 64;
+    const int S = norm_inv_segment(d);
     const float* row = x + (size_t)blockIdx.x * d;
-    for (int i = threadIdx.x; i < d; i += blockDim.x) {
-        const float v = row[i];
+    for (int i = t; i < S * NI_WAVES; i += NI_THREADS) {
+        const float v = i < d ? row[i] : 0.0f;
         sq[i] = v * v;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        float sum = 0.0f;
-        int i = 0;
-        for (; i + 4 <= d; i += 4) {
-            const float4 q4 = *(const float4*)(sq + i);
-            sum = sum + q4.x;
-            sum = sum + q4.y;
-            sum = sum + q4.z;
-            sum = sum + q4.w;
-        }
-        for (; i < d; ++i) sum = sum + sq[i];
-        inv[blockIdx.x] = 1.0f / __builtin_sqrtf(sum / (float)d + eps);
+    const float* seg = sq + S * w;
+    float p = 0.0f;
+    for (int i = lane; i < S; i += 64) p += seg[i];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) p += __shfl_xor(p, off);
+    if (lane == 0) part[w] = p;
+    __syncthreads();
+    float est[NI_WAVES];
+    est[0] = 0.0f;
+#pragma unroll
+    for (int q = 1; q < NI_WAVES; ++q) est[q] = est[q - 1] + part[q - 1];
+    const auto cand = [&](int q) {
+        const int off = lane - 32;
+        if (q == 0) return 0.0f;
+        if (off < -window || off > window) return __builtin_nanf("");
+        const int bits = (int)__float_as_uint(est[q]) + off;
+        return __uint_as_float((uint32_t)(bits < 0 ? 0 : bits));
+    };
+    float c = 0.0f;
+#pragma unroll
+    for (int q = 1; q < NI_WAVES; ++q)
+        if (w == q) c = cand(q);  // (est[] indexed by constants: registers)
+#pragma unroll 4
+    for (int i = 0; i < S; i += 4) {
+        const float4 v = *(const float4*)(seg + i);
+        c = c + v.x;
+        c = c + v.y;
+        c = c + v.z;
+        c = c + v.w;
     }
+    res[w][lane] = c;
+    __syncthreads();
+    if (w != 0) return;
+    float sum = __shfl(res[0][lane], 0);
+    for (int q = 1; q < NI_WAVES; ++q) {
+        const unsigned long long m = __ballot(cand(q) == sum);
+        if (m) {
+            sum = __shfl(res[q][lane], __builtin_ctzll(m));
+        } else {
+            for (int i = 0; i < S; ++i) sum = sum + sq[S * q + i];
+        }
+    }
+    if (lane == 0) inv[blockIdx.x] = 1.0f / __builtin_sqrtf(sum / (float)d + eps);
+}
+
+// The candidate window (TRIT_HIP_NORM_WINDOW narrows it: tests of the path
+// that chains a segment again; 0 leaves only the estimate, -1 none).
+int norm_window() {
+    const char* v = getenv("TRIT_HIP_NORM_WINDOW");
+    return v && *v ? (int)strtol(v, nullptr, 10) : 31;
+}
+
+void launch_norm_inv(const float* x, int rows, int d, float eps, float* inv, const State* st, hipStream_t s) {
+    hipLaunchKernelGGL(norm_inv_kernel, dim3(rows), dim3(NI_THREADS), (size_t)norm_inv_segment(d) * NI_WAVES * 4, s,
+                       x, d, eps, inv, st, norm_window());
 }
 
 // out = x * (inv * w), inv from `inv` (exact) or a fixed tree (fast); then,
@@ -1477,8 +1534,7 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
         // qkv with the attention norm in the prologue (a float-math qkv
         // takes the normed rows).
         if (S.exact) {
-            hipLaunchKernelGGL(norm_inv_kernel, dim3(rows), dim3(256), c.d * 4, s, x, c.d, c.eps,
-                               S.inv.as<float>(), st);
+            launch_norm_inv(x, rows, c.d, c.eps, S.inv.as<float>(), st, s);
             a.norm_inv = S.inv.as<float>();
         }
         if (float_kind(D.qkv[l]->kind)) {
@@ -1589,8 +1645,7 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
         gu.skip = &st->done;
         gu.eps = c.eps;
         if (S.exact) {
-            hipLaunchKernelGGL(norm_inv_kernel, dim3(rows), dim3(256), c.d * 4, s, x, c.d, c.eps,
-                               S.inv.as<float>(), st);
+            launch_norm_inv(x, rows, c.d, c.eps, S.inv.as<float>(), st, s);
             gu.norm_inv = S.inv.as<float>();
         }
         const bool float_gu = float_kind(D.gate_up[l]->kind);
@@ -1621,7 +1676,7 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
     // Final norm of the last row, then the head.
     const float* last = x + (size_t)(rows - 1) * c.d;
     if (S.exact) {
-        hipLaunchKernelGGL(norm_inv_kernel, dim3(1), dim3(256), c.d * 4, s, last, c.d, c.eps, S.inv.as<float>(), st);
+        launch_norm_inv(last, 1, c.d, c.eps, S.inv.as<float>(), st, s);
     }
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(256), 0, s, last, c.d, D.final_norm(), c.eps,
                        S.exact ? S.inv.as<float>() : nullptr, S.normed.as<float>(), st);
