@@ -1154,6 +1154,117 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_steps_kernel(const floa
     }
 }
 
+// attention_kernel's arithmetic for one query row (a decode step; every
+// key visible), same bits, with the values' memory latency hidden: the
+// values of the first VB bytes of keys are loaded into registers before
+// the scores are made, and p.V runs stage by stage -- the registers stored
+// to LDS, the next stage's loads issued, then lane e chains dim e over the
+// stage's keys in order. The serial sum reads 16 values ahead.
+constexpr int ONE_VB = 32768;  // bytes of values a stage: 8 16-byte pieces a thread
+
+size_t attention_one_lds(int max_pos) { return ONE_VB + (size_t)(MAX_HD + ((max_pos + 3) & ~3) + 8) * 4; }
+
+template <typename KV>
+__global__ __launch_bounds__(ATT_THREADS) void attention_one_kernel(const float* __restrict__ qkv, int heads, int kvh,
+                                                                    int hd, const KV* __restrict__ kcache,
+                                                                    const KV* __restrict__ vcache, int max_pos,
+                                                                    float* __restrict__ out, const State* st) {
+    if (st->done) return;
+    extern __shared__ __align__(16) float sm[];  // values[ONE_VB bytes] | qh[MAX_HD] | probs[tk] | red | inv
+    const int t = threadIdx.x, h = blockIdx.x;
+    const int g = h / (heads / kvh);
+    const int tk = st->pos + 1;
+    const int vch = ONE_VB / (hd * (int)sizeof(KV));  // keys a stage
+    char* vbuf = (char*)sm;
+    float* qh = sm + ONE_VB / 4;
+    float* probs = qh + MAX_HD;
+    float* red = probs + ((tk + 3) & ~3);
+    const KV* K = kcache + (size_t)g * max_pos * hd;
+    const KV* V = vcache + (size_t)g * max_pos * hd;
+    constexpr int PIECES = ONE_VB / 16 / ATT_THREADS;
+    uint4 vr[PIECES];
+    auto load_stage = [&](int s0) {
+        const int nbytes = min(tk - s0, vch) * hd * (int)sizeof(KV);
+        const char* src = (const char*)(V + (size_t)s0 * hd);
+#pragma unroll
+        for (int i = 0; i < PIECES; ++i) {
+            const int p = t + ATT_THREADS * i;
+            vr[i] = 16 * p < nbytes ? *(const uint4*)(src + 16 * p) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    load_stage(0);
+    const float scale = 1.0f / __builtin_sqrtf((float)hd);
+    const float* q = qkv + (size_t)h * hd;
+    for (int e = t; e < hd; e += ATT_THREADS) qh[e] = q[e] * scale;
+    __syncthreads();
+    float best = -INFINITY;
+    for (int j = t; j < tk; j += ATT_THREADS) {
+        float acc = 0.0f;
+        const KV* kr = K + (size_t)j * hd;
+        for (int e = 0; e < hd; e += 8) {
+            float kv[8];
+            kv_load8(kr + e, kv);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(qh[e + u], kv[u], acc);
+        }
+        probs[j] = acc;
+        best = __builtin_fmaxf(best, acc);
+    }
+    const int wave = t / 64, lane = t % 64;
+    for (int o = 32; o > 0; o >>= 1) best = __builtin_fmaxf(best, __shfl_xor(best, o));
+    if (lane == 0) red[wave] = best;
+    __syncthreads();
+    float mx = red[0];
+    for (int w = 1; w < ATT_THREADS / 64; ++w) mx = __builtin_fmaxf(mx, red[w]);
+    for (int j = t; j < tk; j += ATT_THREADS) probs[j] = exp_trit(probs[j] - mx);
+    __syncthreads();
+    if (t == 0) {
+        float sum = 0.0f;
+        int j = 0;
+        float4 cur[4], nxt[4];
+        if (tk >= 16) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) cur[k] = *(const float4*)(probs + 4 * k);
+        }
+        for (; j + 16 <= tk; j += 16) {
+            if (j + 32 <= tk) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) nxt[k] = *(const float4*)(probs + j + 16 + 4 * k);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                sum = sum + cur[k].x;
+                sum = sum + cur[k].y;
+                sum = sum + cur[k].z;
+                sum = sum + cur[k].w;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) cur[k] = nxt[k];
+        }
+        for (; j < tk; ++j) sum = sum + probs[j];
+        red[ATT_THREADS / 64] = 1.0f / sum;
+    }
+    __syncthreads();
+    const float inv = red[ATT_THREADS / 64];
+    for (int j = t; j < tk; j += ATT_THREADS) probs[j] = probs[j] * inv;
+    float acc = 0.0f;
+    for (int s0 = 0; s0 < tk; s0 += vch) {
+        __syncthreads();  // the probabilities are scaled; the last stage's reads are done
+#pragma unroll
+        for (int i = 0; i < PIECES; ++i) *(uint4*)(vbuf + 16 * (t + ATT_THREADS * i)) = vr[i];
+        __syncthreads();
+        if (s0 + vch < tk) load_stage(s0 + vch);  // in flight while this stage chains
+        if (t < hd) {
+            const int n = min(tk - s0, vch);
+            const KV* vs = (const KV*)vbuf + t;
+            const float* pj = probs + s0;
+#pragma unroll 8
+            for (int j = 0; j < n; ++j) acc = __builtin_fmaf(pj[j], (float)vs[(size_t)j * hd], acc);
+        }
+    }
+    if (t < hd) out[(size_t)h * hd + t] = acc;
+}
+
 // attention_kernel's arithmetic for R query rows of one head per block:
 // every row's scores, maximum, exponentials, serial sum and p.V chains in
 // the same orders (same bits), with each key and value read once for the R
@@ -1601,6 +1712,18 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
                                           rows, S.max_pos, S.att.as<float>(), st, 1, s));
             if (multi) {
                 // R query rows a block.
+            } else if (rows == 1 && hd <= MAX_HD && ATT_THREADS % hd == 0 && attention_one_lds(S.max_pos) <= 64 * 1024) {
+                // One decode row: the values' loads hidden behind the scores.
+                if (S.kv32)
+                    hipLaunchKernelGGL(attention_one_kernel<float>, dim3(c.heads), dim3(ATT_THREADS),
+                                       attention_one_lds(S.max_pos), s, S.qkv.as<float>(), c.heads, c.kv_heads, hd,
+                                       S.kcache.as<float>() + lo, S.vcache.as<float>() + lo, S.max_pos,
+                                       S.att.as<float>(), st);
+                else
+                    hipLaunchKernelGGL(attention_one_kernel<_Float16>, dim3(c.heads), dim3(ATT_THREADS),
+                                       attention_one_lds(S.max_pos), s, S.qkv.as<float>(), c.heads, c.kv_heads, hd,
+                                       S.kcache.as<_Float16>() + lo, S.vcache.as<_Float16>() + lo, S.max_pos,
+                                       S.att.as<float>(), st);
             } else if (S.kv32)
                 hipLaunchKernelGGL(attention_kernel<float>, dim3(c.heads, rows), dim3(ATT_THREADS), lds, s,
                                    S.qkv.as<float>(), stride, c.heads, c.kv_heads, hd, S.kcache.as<float>() + lo,
