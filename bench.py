@@ -50,7 +50,7 @@ GATE_UP_TRAFFIC_BYTES = round((3353.1 * 2.0 + 24.0) * 1024)
 # runs (profiles/decode_step_qwen3_0.6b_hbm_traffic.md): FETCH_SIZE and
 # WRITE_SIZE of one launch of 128 steps (127 forwards, positions 256..382)
 # over the forwards, FETCH_SIZE x 2.0 plus WRITE_SIZE x 1.0.
-STEP_FETCH_KIB, STEP_WRITE_KIB = 406905.77, 2600.06
+STEP_FETCH_KIB, STEP_WRITE_KIB = 406911.30, 2600.06
 STEP_TRAFFIC_BYTES = round((STEP_FETCH_KIB * 2.0 + STEP_WRITE_KIB) * 1024)
 
 
