@@ -73,6 +73,24 @@ def test_attention(gpu, tq, tk, heads, kv_heads, causal):
     assert rel(fast, exact) < 2e-2
 
 
+def test_attention_masked_tail_exact(gpu):
+    """Keys past a causal block's last row weigh exp_trit(-inf) / sum (about
+    1e-38): the exact kernel leaves them out only where they cannot move a
+    chain. Here every key a row sees has value 0 and the later keys 1000,
+    so the rows' outputs are those tiny masked terms alone, and they must
+    match Trit's attention over every key, bit for bit."""
+    print("case attention exact masked tail", flush=True)
+    tq = tk = 70
+    heads, hd = 2, 64
+    q, k, v = inputs(67, tq, tk, heads, heads, hd)
+    v[:60] = 0.0
+    v[60:] = 1000.0
+    got = hip.attention(q, k, v, heads, heads, hd, True, hip.EXACT)
+    want = O.attention(q, k, v, heads, heads, hd, causal=True)
+    assert bits_equal(got, want)
+    assert np.any(got[:56] != 0.0)  # the masked terms reached the outputs
+
+
 def test_attention_small_heads_exact(gpu):
     """The exact form at head_dim 64 (Whisper-size heads), no mask."""
     print("case attention exact hd 64", flush=True)

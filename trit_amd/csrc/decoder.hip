@@ -1283,6 +1283,12 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_rows_kernel(
     const int g = h / (heads / kvh);
     const int tk = st->pos + rows;
     const int pitch = (tk + 3) & ~3;
+    // Causal rows see no key past kmax (the block's last row's position):
+    // there every row's weight is exp_trit(-inf) ~ 1.2e-38, which leaves a
+    // sum of at least 1 (the maximum key's exp(0)) unchanged, so scores,
+    // exponentials and the sums stop at kmax; the p.V chains too where that
+    // is exact (below).
+    const int kmax = causal ? min(tk, st->pos + row0 + nr) : tk;
     float* qh = sm;
     float* probs = sm + R * MAX_HD;
     float* red = probs + R * pitch;
@@ -1298,7 +1304,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_rows_kernel(
     float best[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) best[r] = -INFINITY;
-    for (int j = threadIdx.x; j < tk; j += ATT_THREADS) {
+    for (int j = threadIdx.x; j < kmax; j += ATT_THREADS) {
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = 0.0f;
@@ -1330,8 +1336,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_rows_kernel(
         if (lane == 0) red[r * (ATT_THREADS / 64) + wave] = m;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < nr * tk; i += ATT_THREADS) {
-        const int r = i / tk, j = i - r * tk;
+    for (int i = threadIdx.x; i < nr * kmax; i += ATT_THREADS) {
+        const int r = i / kmax, j = i - r * kmax;
         float mx = red[r * (ATT_THREADS / 64)];
         for (int w = 1; w < ATT_THREADS / 64; ++w) mx = __builtin_fmaxf(mx, red[r * (ATT_THREADS / 64) + w]);
         probs[r * pitch + j] = exp_trit(probs[r * pitch + j] - mx);
@@ -1344,12 +1350,12 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_rows_kernel(
         float sum = 0.0f;
         int j = 0;
         float4 cur[4], nxt[4];
-        if (tk >= 16) {
+        if (kmax >= 16) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) cur[q] = *(const float4*)(pr + 4 * q);
         }
-        for (; j + 16 <= tk; j += 16) {
-            if (j + 32 <= tk) {
+        for (; j + 16 <= kmax; j += 16) {
+            if (j + 32 <= kmax) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) nxt[q] = *(const float4*)(pr + j + 16 + 4 * q);
             }
@@ -1363,12 +1369,12 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_rows_kernel(
 #pragma unroll
             for (int q = 0; q < 4; ++q) cur[q] = nxt[q];
         }
-        for (; j < tk; ++j) sum = sum + pr[j];
+        for (; j < kmax; ++j) sum = sum + pr[j];
         inv[threadIdx.x] = 1.0f / sum;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < nr * tk; i += ATT_THREADS) {
-        const int r = i / tk, j = i - r * tk;
+    for (int i = threadIdx.x; i < nr * kmax; i += ATT_THREADS) {
+        const int r = i / kmax, j = i - r * kmax;
         probs[r * pitch + j] = probs[r * pitch + j] * inv[r];
     }
     __syncthreads();
@@ -1381,7 +1387,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_rows_kernel(
 #pragma unroll
         for (int k = 0; k < MR; ++k) acc[k] = 0.0f;
         int j = 0;
-        for (; j + 16 <= tk; j += 16) {
+        for (; j + 16 <= kmax; j += 16) {
             float v[16];
 #pragma unroll
             for (int u = 0; u < 16; ++u) v[u] = kv_load(V + (size_t)(j + u) * hd + e);
@@ -1400,13 +1406,27 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_rows_kernel(
                 }
             }
         }
-        for (; j < tk; ++j) {
+        for (; j < kmax; ++j) {
             const float v = kv_load(V + (size_t)j * hd + e);
 #pragma unroll
             for (int k = 0; k < MR; ++k) {
                 const int r = group + k * G;
                 if (r >= nr) break;
                 acc[k] = __builtin_fmaf(probs[r * pitch + j], v, acc[k]);
+            }
+        }
+        // Keys past kmax: weight pm = exp_trit(-inf) * (1/sum) <= 1.2e-38.
+        // With f16 values (|v| <= 65504) each term is below 7.7e-34, under
+        // half a step of any |acc| >= 2^-80, so it leaves acc as it is;
+        // a chain nearer 0, or f32 values, takes the terms in order.
+        if (kmax < tk) {
+#pragma unroll
+            for (int k = 0; k < MR; ++k) {
+                const int r = group + k * G;
+                if (r >= nr) break;
+                if (sizeof(KV) == 2 && __builtin_fabsf(acc[k]) >= 0x1p-80f) continue;
+                const float pm = exp_trit(-INFINITY) * inv[r];
+                for (int jj = kmax; jj < tk; ++jj) acc[k] = __builtin_fmaf(pm, kv_load(V + (size_t)jj * hd + e), acc[k]);
             }
         }
 #pragma unroll
