@@ -209,6 +209,56 @@ def test_generate_additive(qshape, flags):
     s.free()
 
 
+# Granite's multipliers on Qwen3-0.6B's layer shapes: the persistent step
+# takes them in the default (Trit-order) instance.
+GRANITE_QS = dict(QS, qk_norm=0, embedding_multiplier=12.0, attention_multiplier=0.0078125 * 2,
+                  residual_multiplier=0.22, logits_scaling=8.0)
+
+
+def check_step(lm, ref16, p, n, max_pos=96):
+    """The default mode on the persistent step: prompt logits and every
+    greedy token bit for bit the f16-cache oracle's."""
+    ref16.reset()
+    want_logits = ref16.forward(p)
+    s = lm.session(max_pos, 0)
+    logits = s.prefill(p)
+    got = s.generate(n)
+    assert s.persistent, "the persistent step did not run"
+    assert same_bits(logits, want_logits), rel(logits, want_logits)
+    assert got.tolist() == greedy(ref16, want_logits, n)
+    s.free()
+    return got
+
+
+def test_granite_on_the_step(gpu):
+    """Embedding, attention and residual multipliers and the logits scaling
+    inside the persistent step (causal_lm.rs:387,420-424,438-442,456)."""
+    print("case granite multipliers on the persistent step", flush=True)
+    w = synth.lm_weights(GRANITE_QS, config=114, sigma=0.1, norm_jitter=0.2)
+    lm = model.build_decoder(w)
+    ref16 = O.Lm(GRANITE_QS, w, O.isa_best(), kv_f16=True)
+    got = check_step(lm, ref16, synth.prompt(114, 40, GRANITE_QS["vocab"]), 24)
+    print(f"granite step tokens {got[:8].tolist()} ...", flush=True)
+
+
+def test_ffn_scales_on_the_step(qshape):
+    """set_ffn_scales inside the persistent step: the normed MLP input times
+    each layer's scales; removing them gives the plain model again."""
+    print("case ffn scales on the persistent step", flush=True)
+    w, lm, ref, ref16 = qshape
+    scales = (1.0 + 0.5 * synth.normal(115, (QS["layers"], QS["d"]))).astype(np.float32)
+    p = synth.prompt(115, 30, QS["vocab"])
+    ref16.set_ffn_scales(scales)
+    lm.set_ffn_scales(scales)
+    try:
+        a = check_step(lm, ref16, p, 20)
+    finally:
+        ref16.set_ffn_scales(None)
+        lm.set_ffn_scales(None)
+    b = check_step(lm, ref16, p, 20)
+    assert a.tolist() != b.tolist()  # the scales are used
+
+
 def test_generate_additive_edges(qshape):
     """No tokens for an empty prompt or fewer rows than the prompt; one
     token when the rows end with the prompt; errors for a used session and

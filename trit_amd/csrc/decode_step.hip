@@ -89,6 +89,12 @@ struct StepArgs {
     int rh;                   // head rows per block
     unsigned long long ticks; // wall-clock ticks a block may wait in a step
     int norm_window;          // RMSNorm and softmax sums: candidate starts on either side of the estimate
+    // Granite's multipliers (1 where a model has none): the embedding rows
+    // times em, q times q_scale after the rotary, the residual adds x + rm y,
+    // the logits times logit_w; and per-layer MLP input scales (d a layer)
+    // or null. The Trit-order instance only.
+    float em, q_scale, rm, logit_w;
+    const float* ffn_scales;
 };
 
 struct Smem {
@@ -442,7 +448,8 @@ __device__ __forceinline__ void load_norm(int t, const float* norm_w, NormRegs<J
 // Trit's activation quantizer over x (K values in LDS), optionally after
 // RMSNorm x * (inv * w), into sm.xq / sm.xs; ends with a block barrier.
 template <int J>
-__device__ void quantize_block(int t, const float* x, const NormRegs<J>* nr, Smem& sm) {
+__device__ void quantize_block(int t, const float* x, const NormRegs<J>* nr, Smem& sm,
+                               const NormRegs<J>* fs = nullptr) {
     constexpr int ITEMS = J * 64;  // float4 items; a multiple of 64: whole waves
     const float inv = sm.inv;
 #pragma unroll
@@ -456,6 +463,13 @@ __device__ void quantize_block(int t, const float* x, const NormRegs<J>* nr, Sme
             v.y = v.y * (inv * nw.y);
             v.z = v.z * (inv * nw.z);
             v.w = v.w * (inv * nw.w);
+        }
+        if (fs) {  // the normed values times the layer's MLP scales
+            const float4 f = fs->w[i];
+            v.x = v.x * f.x;
+            v.y = v.y * f.y;
+            v.z = v.z * f.z;
+            v.w = v.w * f.w;
         }
         float peak = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
                                      __builtin_fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
@@ -1164,6 +1178,12 @@ __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, in
             x1 = bc + as;
         }
         if (w == 0) {
+            // Granite: q times attention_multiplier * sqrt(hd) after the
+            // rotary, then the attention's 1/sqrt(hd).
+            if (a.q_scale != 1.0f) {
+                x0 = x0 * a.q_scale;
+                x1 = x1 * a.q_scale;
+            }
             const float scale = 1.0f / __builtin_sqrtf((float)HD);
             x0 = x0 * scale;
             x1 = x1 * scale;
@@ -1464,7 +1484,8 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         const int s_count = a.d / 16;
         for (int kk = t; kk < a.d; kk += T) {
             const int s = kk / 16, i = kk % 16;
-            sm.xres[kk] = f16_to_f32(gmem(a.embed)[((size_t)token * 16 + i) * s_count + s]);
+            const float v = f16_to_f32(gmem(a.embed)[((size_t)token * 16 + i) * s_count + s]);
+            sm.xres[kk] = a.em != 1.0f ? v * a.em : v;
         }
         __syncthreads();
     }
@@ -1550,14 +1571,15 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         if (ao) {
             float acc[1];
             row_chain<JO, 1>(t, rr, sm, acc);
-            if ((lane & 15) == 14) put(a.X + rowo, sm.xres[rowo] + acc[0], tag_of(tag0, layer, 3));
+            if ((lane & 15) == 14) put(a.X + rowo, sm.xres[rowo] + a.rm * acc[0], tag_of(tag0, layer, 3));
         }
         // The touched words are consumed here, where they have long arrived
         // (before the polls of the gather below).
         asm volatile("" ::"v"(kvt[0]), "v"(kvt[1]), "v"(kvt[2]), "v"(kvt[3]));
         // gate_up + SwiGLU.
-        NormRegs<JD> ngu;
+        NormRegs<JD> ngu, nfs;
         load_norm<JD>(t, L.norm_mlp, ngu);
+        if (a.ffn_scales) load_norm<JD>(t, a.ffn_scales + (size_t)layer * a.d, nfs);
         __syncthreads();
         if (!gather<MAXK / T>(t, a.X, a.d, lin, tag_of(tag0, layer, 3), sm.xres, sm, deadline, st)) leave();
         if constexpr (EXACT) {
@@ -1568,7 +1590,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             if (lane == 0) sm.inv = inv;
         }
         __syncthreads();
-        quantize_block<JD>(t, sm.xres, &ngu, sm);
+        quantize_block<JD>(t, sm.xres, &ngu, sm, a.ffn_scales ? &nfs : nullptr);
         if (agu) {
             float acc[2];
             row_chain<JD, 2>(t, rr, sm, acc);
@@ -1587,7 +1609,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         if (ad) {
             float acc[1];
             row_chain<JF, 1>(t, rr, sm, acc);
-            if ((lane & 15) == 14) put(a.X + rowd, sm.xres[rowd] + acc[0], tag_of(tag0, layer, 5));
+            if ((lane & 15) == 14) put(a.X + rowd, sm.xres[rowd] + a.rm * acc[0], tag_of(tag0, layer, 5));
         }
         __syncthreads();
     }
@@ -1659,6 +1681,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         v = v + dpp<0x124>(v);
         v = v + dpp<DPP_ROR2>(v);
         v = v + dpp<0x121>(v);
+        if (a.logit_w != 1.0f) v = v * a.logit_w;  // Granite's 1 / logits_scaling
         const int row = row_of(p);
         if (l16 == 0 && row < a.vocab && (index == INT_MAX || v > best)) {
             best = v;
@@ -1781,9 +1804,10 @@ bool plan(const SessionImpl& S, Plan& p) {
     const DecoderImpl& D = *S.dec;
     const auto& c = D.c;
     if (S.kv32) return false;
-    // Granite's multipliers, per-layer MLP scales and added input rows run
-    // on the per-kernel loop.
-    if (D.granite() || D.has_ffn_scales || S.additive_rows) return false;
+    // Added input rows run on the per-kernel loop; Granite's multipliers and
+    // per-layer MLP scales on the Trit-order instance only.
+    if (S.additive_rows) return false;
+    if ((D.granite() || D.has_ffn_scales) && !S.exact) return false;
     if (c.head_dim != HD || c.kv_heads <= 0 || c.heads % c.kv_heads != 0) return false;
     const int group = c.heads / c.kv_heads, qd = c.heads * HD;
     if (c.d % 256 || qd % 256 || c.ffn % 256 || c.d > MAXD || qd > MAXK || c.ffn > MAXK) return false;
@@ -1960,6 +1984,12 @@ void decode_step_launch(SessionImpl& S, int step, int pos, int nsteps, hipStream
     // only the estimate, -1 none).
     a.norm_window = 31;
     if (const char* v = getenv("TRIT_HIP_NORM_WINDOW")) a.norm_window = (int)strtol(v, nullptr, 10);
+    // Granite (the per-kernel loop's factors, causal_lm.rs:387,420,438-442,456).
+    a.em = c.embedding_multiplier;
+    a.q_scale = c.attention_multiplier != 0.0f ? c.attention_multiplier * sqrtf((float)HD) : 1.0f;
+    a.rm = c.residual_multiplier;
+    a.logit_w = 1.0f / c.logits_scaling;
+    a.ffn_scales = D.has_ffn_scales ? D.ffn_scales.as<float>() : nullptr;
     void* args[] = {&a, &step, &pos, (void*)&seq0, &nsteps};
     TRIT_HIP(hipLaunchCooperativeKernel((const void*)p.fn, dim3(p.blocks), dim3(T), args, 0, s));
 }
