@@ -95,6 +95,10 @@ struct StepArgs {
     // or null. The Trit-order instance only.
     float em, q_scale, rm, logit_w;
     const float* ffn_scales;
+    // generate_additive: rows x d added to the input at their positions
+    // (before em, as the per-kernel loop adds them), or null.
+    const float* additive;
+    int additive_rows;
 };
 
 struct Smem {
@@ -1484,7 +1488,8 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         const int s_count = a.d / 16;
         for (int kk = t; kk < a.d; kk += T) {
             const int s = kk / 16, i = kk % 16;
-            const float v = f16_to_f32(gmem(a.embed)[((size_t)token * 16 + i) * s_count + s]);
+            float v = f16_to_f32(gmem(a.embed)[((size_t)token * 16 + i) * s_count + s]);
+            if (a.additive && pos < a.additive_rows) v = v + *gmem(a.additive + (size_t)pos * a.d + kk);
             sm.xres[kk] = a.em != 1.0f ? v * a.em : v;
         }
         __syncthreads();
@@ -1804,10 +1809,9 @@ bool plan(const SessionImpl& S, Plan& p) {
     const DecoderImpl& D = *S.dec;
     const auto& c = D.c;
     if (S.kv32) return false;
-    // Added input rows run on the per-kernel loop; Granite's multipliers and
-    // per-layer MLP scales on the Trit-order instance only.
-    if (S.additive_rows) return false;
-    if ((D.granite() || D.has_ffn_scales) && !S.exact) return false;
+    // Granite's multipliers, per-layer MLP scales and added input rows run
+    // on the Trit-order instance only.
+    if ((D.granite() || D.has_ffn_scales || S.additive_rows) && !S.exact) return false;
     if (c.head_dim != HD || c.kv_heads <= 0 || c.heads % c.kv_heads != 0) return false;
     const int group = c.heads / c.kv_heads, qd = c.heads * HD;
     if (c.d % 256 || qd % 256 || c.ffn % 256 || c.d > MAXD || qd > MAXK || c.ffn > MAXK) return false;
@@ -1990,6 +1994,8 @@ void decode_step_launch(SessionImpl& S, int step, int pos, int nsteps, hipStream
     a.rm = c.residual_multiplier;
     a.logit_w = 1.0f / c.logits_scaling;
     a.ffn_scales = D.has_ffn_scales ? D.ffn_scales.as<float>() : nullptr;
+    a.additive = S.additive_rows ? S.additive.as<float>() : nullptr;
+    a.additive_rows = S.additive_rows;
     void* args[] = {&a, &step, &pos, (void*)&seq0, &nsteps};
     TRIT_HIP(hipLaunchCooperativeKernel((const void*)p.fn, dim3(p.blocks), dim3(T), args, 0, s));
 }
