@@ -1164,12 +1164,15 @@ constexpr int ONE_VB = 32768;  // bytes of values a stage: 8 16-byte pieces a th
 
 size_t attention_one_lds(int max_pos) { return ONE_VB + (size_t)(MAX_HD + ((max_pos + 3) & ~3) + 8) * 4; }
 
-template <typename KV>
+// HD: the head size as a constant (its loops unrolled, so each key's loads
+// are issued together), or 0 for the size in hd.
+template <typename KV, int HD>
 __global__ __launch_bounds__(ATT_THREADS) void attention_one_kernel(const float* __restrict__ qkv, int heads, int kvh,
-                                                                    int hd, const KV* __restrict__ kcache,
+                                                                    int hd_arg, const KV* __restrict__ kcache,
                                                                     const KV* __restrict__ vcache, int max_pos,
                                                                     float* __restrict__ out, const State* st) {
     if (st->done) return;
+    const int hd = HD ? HD : hd_arg;
     extern __shared__ __align__(16) float sm[];  // values[ONE_VB bytes] | qh[MAX_HD] | probs[tk] | red | inv
     const int t = threadIdx.x, h = blockIdx.x;
     const int g = h / (heads / kvh);
@@ -1201,11 +1204,19 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_one_kernel(const float*
     for (int j = t; j < tk; j += ATT_THREADS) {
         float acc = 0.0f;
         const KV* kr = K + (size_t)j * hd;
-        for (int e = 0; e < hd; e += 8) {
-            float kv[8];
-            kv_load8(kr + e, kv);
+        if constexpr (HD > 0) {
+            float kv[HD];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(qh[e + u], kv[u], acc);
+            for (int e = 0; e < HD; e += 8) kv_load8(kr + e, kv + e);
+#pragma unroll
+            for (int e = 0; e < HD; ++e) acc = __builtin_fmaf(qh[e], kv[e], acc);
+        } else {
+            for (int e = 0; e < hd; e += 8) {
+                float kv[8];
+                kv_load8(kr + e, kv);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(qh[e + u], kv[u], acc);
+            }
         }
         probs[j] = acc;
         best = __builtin_fmaxf(best, acc);
@@ -1735,12 +1746,14 @@ void forward(SessionImpl& S, int rows, hipStream_t s) {
             } else if (rows == 1 && hd <= MAX_HD && ATT_THREADS % hd == 0 && attention_one_lds(S.max_pos) <= 64 * 1024) {
                 // One decode row: the values' loads hidden behind the scores.
                 if (S.kv32)
-                    hipLaunchKernelGGL(attention_one_kernel<float>, dim3(c.heads), dim3(ATT_THREADS),
+                    hipLaunchKernelGGL((hd == 128 ? attention_one_kernel<float, 128> : attention_one_kernel<float, 0>),
+                                       dim3(c.heads), dim3(ATT_THREADS),
                                        attention_one_lds(S.max_pos), s, S.qkv.as<float>(), c.heads, c.kv_heads, hd,
                                        S.kcache.as<float>() + lo, S.vcache.as<float>() + lo, S.max_pos,
                                        S.att.as<float>(), st);
                 else
-                    hipLaunchKernelGGL(attention_one_kernel<_Float16>, dim3(c.heads), dim3(ATT_THREADS),
+                    hipLaunchKernelGGL((hd == 128 ? attention_one_kernel<_Float16, 128> : attention_one_kernel<_Float16, 0>),
+                                       dim3(c.heads), dim3(ATT_THREADS),
                                        attention_one_lds(S.max_pos), s, S.qkv.as<float>(), c.heads, c.kv_heads, hd,
                                        S.kcache.as<_Float16>() + lo, S.vcache.as<_Float16>() + lo, S.max_pos,
                                        S.att.as<float>(), st);
