@@ -204,3 +204,134 @@ def test_cleanup_parts(pair):
     # Sentence ends need whitespace (or the end) after them.
     p = bpe.cleanup_parts("a.b c. d", 1)
     assert p[0] == "a.b" and " ".join(p).split() == ["a.b", "c.", "d"]
+
+
+def naive_merge(symbols, ranks):
+    """BPE by definition, one merge at a time: among the neighbouring pairs
+    that have a rank, join the one of lowest rank, the leftmost of equal
+    ranks (text::merge_symbols, src/text/mod.rs:6-74), by a full scan."""
+    symbols = list(symbols)
+    while True:
+        best = None
+        for i in range(len(symbols) - 1):
+            r = ranks.get((symbols[i], symbols[i + 1]))
+            if r is not None and (best is None or r < best[0]):
+                best = (r, i)
+        if best is None:
+            return symbols
+        i = best[1]
+        symbols[i:i + 2] = [symbols[i] + symbols[i + 1]]
+
+
+def test_merge_order_against_brute_force():
+    """Random merge tables over a four-letter alphabet, ranks in any order
+    (joins of joins may rank below their parts), words with long repeats:
+    the ids are those of the naive definition."""
+    rng = np.random.default_rng(7)
+    alphabet = "abcd"
+    for trial in range(40):
+        pieces = list(alphabet)
+        merges = []
+        for _ in range(int(rng.integers(5, 40))):
+            left, right = pieces[rng.integers(len(pieces))], pieces[rng.integers(len(pieces))]
+            merges.append((left, right))
+            if left + right not in pieces:
+                pieces.append(left + right)
+        order = rng.permutation(len(merges))
+        merges = [merges[i] for i in order]
+        ranks = {}
+        for r, pair in enumerate(merges):
+            ranks.setdefault(pair, r)
+        vocab = {chars: i for i, chars in enumerate(bytes_to_unicode_chars())}
+        for p in pieces:
+            vocab.setdefault(p, len(vocab))
+        # Leave some joins out of the vocabulary: they give no id.
+        dropped = {p for p in pieces[len(alphabet):] if rng.random() < 0.2}
+        for p in dropped:
+            del vocab[p]
+        spec = {"model": {"vocab": vocab, "merges": [f"{a} {b}" for a, b in merges]}, "added_tokens": []}
+        bpe = hip.Bpe(text=json.dumps(spec))
+        for _ in range(10):
+            word = "".join(alphabet[i] for i in rng.integers(0, 2 if rng.random() < 0.3 else 4, int(rng.integers(1, 60))))
+            want = [vocab[s] for s in naive_merge(word, ranks) if s in vocab]
+            assert bpe.encode(word) == want, (trial, word)
+
+
+def test_long_word_merges_quickly():
+    """A word of 10,000 letters (a heap, not a scan per merge) is merged in
+    well under a second, to the naive definition's result on a shorter
+    copy of the same pattern."""
+    import time
+    vocab = {c: i for i, c in enumerate(bytes_to_unicode_chars())}
+    vocab["ab"] = 256
+    vocab["abab"] = 257
+    spec = {"model": {"vocab": vocab, "merges": ["a b", "ab ab"]}}
+    bpe = hip.Bpe(text=json.dumps(spec))
+    t0 = time.perf_counter()
+    ids = bpe.encode("ab" * 5000)
+    assert time.perf_counter() - t0 < 1.0
+    assert ids == [257] * 2500
+    assert bpe.encode("ab" * 3 + "a") == [257, 256, vocab["a"]]
+
+
+def test_json_rules():
+    """serde_json's reading: the last of duplicate keys wins, ids must be
+    integers, trailing text and lone surrogates are errors, and the
+    vocabulary is taken in key order (the later key wins a shared id)."""
+    base = {c: i for i, c in enumerate(bytes_to_unicode_chars())}
+    text = json.dumps({"model": {"vocab": base}})
+    bpe = hip.Bpe(text=text[:-3] + ', "zz": 300, "zz": 301}}}')
+    assert bpe.id("zz") == 301
+    with pytest.raises(hip.TritError, match="bad id"):
+        hip.Bpe(text='{"model": {"vocab": {"a": 1.0}}}')
+    with pytest.raises(hip.TritError, match="bad id"):
+        hip.Bpe(text='{"model": {"vocab": {"a": -1}}}')
+    with pytest.raises(hip.TritError, match="not JSON"):
+        hip.Bpe(text='{"model": {"vocab": {"a": 1}}} x')
+    with pytest.raises(hip.TritError, match="not JSON"):
+        hip.Bpe(text='{"model": {"vocab": {"\\ud800": 1}}}')
+    with pytest.raises(hip.TritError, match="not JSON"):
+        hip.Bpe(text='{"model": {"vocab": {"a": 01}}}')
+    # Two texts with one id: the later in key order owns the piece.
+    two = dict(base)
+    two["q"] = 400
+    two["r"] = 400
+    bpe = hip.Bpe(text=json.dumps({"model": {"vocab": two}}))
+    assert bpe.decode([400]) == "r"
+    # Added tokens: a float id is skipped; "special": false decodes as text.
+    spec = {"model": {"vocab": base},
+            "added_tokens": [{"id": 500.0, "content": "<x>"}, {"id": 501, "content": "<y>", "special": False}]}
+    bpe = hip.Bpe(text=json.dumps(spec))
+    assert bpe.id("<x>") is None and bpe.id("<y>") == 501
+    assert bpe.encode("a<y>b") == [base["a"], 501, base["b"]]
+    assert bpe.decode([501]) == "<y>"
+
+
+def test_specials_earliest_then_longest():
+    """Added tokens in the text: the earliest occurrence first, the longest
+    of those starting at one place."""
+    base = {c: i for i, c in enumerate(bytes_to_unicode_chars())}
+    spec = {"model": {"vocab": base},
+            "added_tokens": [{"id": 600, "content": "<a>"}, {"id": 601, "content": "<a><b>"},
+                             {"id": 602, "content": "b>"}]}
+    bpe = hip.Bpe(text=json.dumps(spec))
+    assert bpe.encode("x<a><b>y") == [base["x"], 601, base["y"]]
+    assert bpe.encode("x<a>y") == [base["x"], 600, base["y"]]
+    assert bpe.encode("<ab>") == [base["<"], base["a"], 602]
+    assert bpe.encode_plain("<a>") == [base["<"], base["a"], base[">"]]
+
+
+def test_decode_cut_rule():
+    """text::lossy's cut: a final lead byte with fewer continuation bytes
+    than it announces is dropped even where the bytes could never have made
+    a character (0xE0 0x80); a lone final continuation byte is replaced."""
+    chars = bytes_to_unicode_chars()
+    base = {c: i for i, c in enumerate(chars)}
+    bpe = hip.Bpe(text=json.dumps({"model": {"vocab": base}}))
+    ids = lambda bs: [base[chars[b]] for b in bs]
+    assert bpe.decode(ids(b"a\xe0\x80")) == "a"
+    assert bpe.decode(ids(b"a\xc0")) == "a"
+    assert bpe.decode(ids(b"a\x80")) == "a�"
+    assert bpe.decode(ids(b"\xf8a")) == "�a"
+    assert bpe.decode(ids(b"\xed\xa0\x80a")) == "���a"  # a surrogate's bytes
+    assert bpe.decode(ids("日本".encode())) == "日本"
