@@ -2087,7 +2087,12 @@ namespace trit {
 namespace {
 
 constexpr char CACHE_MAGIC[8] = {'T', 'R', 'I', 'T', 'H', 'I', 'P', 'W'};
-constexpr uint32_t CACHE_FORMAT = 1;
+constexpr uint32_t CACHE_FORMAT = 2;
+// The version of the device layouts the file holds (the row-major integer
+// codes and scales, the float kinds' lane-chain layout, the 2-bit ternary
+// spans): bumped whenever a repack changes, so an older file is refused
+// by its key instead of handing the kernels buffers of another layout.
+constexpr int LAYOUT_VERSION = 2;
 
 struct Hash {
     uint64_t h = 0x9E3779B97F4A7C15ull;
@@ -2157,6 +2162,35 @@ struct CacheWriter {
     }
 };
 
+// The exact device bytes of a layer's codes and scales for its kind, n, k
+// and group (the layouts the layer calls make); false for a combination no
+// layer call makes.
+bool layout_bytes(int kind, int n, int k, int group, uint64_t* codes, uint64_t* scales) {
+    const uint64_t N = (uint64_t)n, K = (uint64_t)k, steps = (uint64_t)chain_steps(k);
+    switch (kind) {
+        case Q8_0:
+        case Q4_K:
+            if (group != 32 || k % 32) return false;
+            *codes = N * K, *scales = N * (K / 32) * 2;
+            return true;
+        case INT8:
+            if (group != 128 || k % 128) return false;
+            *codes = N * K, *scales = N * (K / 128) * 4;
+            return true;
+        case TERNARY:
+            if (group != 128 || k % 128) return false;
+            *codes = N * K / 4, *scales = N * (K / 128) * 4;
+            return true;
+        case F16: *codes = N * 16 * steps * 2, *scales = 0; return true;
+        case F32: *codes = N * 16 * steps * 4, *scales = 0; return true;
+        case Q8_F32:
+            if (k % 32) return false;
+            *codes = N * 16 * steps, *scales = N * (K / 32) * 4;
+            return true;
+        default: return false;
+    }
+}
+
 struct CacheReader {
     FILE* f;
     Hash hash;
@@ -2171,9 +2205,12 @@ struct CacheReader {
         get(&v, sizeof v);
         return v;
     }
-    void device(DeviceMemory& m, size_t limit) {
+    // A buffer of exactly `want` bytes (`alt`, when nonzero, is the one
+    // other size allowed: a bias may be absent).
+    void device(DeviceMemory& m, uint64_t want, uint64_t alt = UINT64_MAX) {
         const uint64_t bytes = val<uint64_t>();
-        if (bytes > limit) fail(std::string(path) + ": a buffer of the cache file is larger than its layer");
+        if (bytes != want && bytes != alt)
+            fail(std::string(path) + ": a buffer of the cache file does not have its layer's size");
         m.alloc(bytes);
         std::vector<uint8_t> host(std::min<size_t>(bytes, (size_t)64 << 20));
         for (size_t at = 0; at < bytes; at += host.size()) {
@@ -2188,17 +2225,29 @@ struct CacheReader {
         L->n = val<int32_t>();
         L->k = val<int32_t>();
         L->group = val<int32_t>();
-        if (L->kind < Q8_0 || L->kind > Q8_F32 || L->n <= 0 || L->k <= 0)
+        uint64_t codes = 0, scales = 0;
+        if (L->n <= 0 || L->k <= 0 || !layout_bytes(L->kind, L->n, L->k, L->group, &codes, &scales))
             fail(std::string(path) + ": a layer of the cache file is not valid");
-        const size_t limit = (size_t)L->n * L->k * 4 + (size_t)L->n * 4 + 64;
-        device(L->codes, limit);
-        device(L->scales, limit);
-        device(L->bias, (size_t)L->n * 4);
+        // The three buffers' sizes are checked before any is uploaded.
+        const off_t at = ftello(f);
+        const uint64_t want[3] = {codes, scales, (uint64_t)L->n * 4};
+        for (int i = 0; i < 3; ++i) {
+            uint64_t bytes = 0;
+            if (std::fread(&bytes, 8, 1, f) != 1) fail(std::string(path) + ": the cache file is cut short");
+            if (bytes != want[i] && !(i == 2 && bytes == 0))
+                fail(std::string(path) + ": a buffer of the cache file does not have its layer's size");
+            if (bytes > (uint64_t)INT64_MAX || fseeko(f, (off_t)bytes, SEEK_CUR) != 0)
+                fail(std::string(path) + ": the cache file is cut short");
+        }
+        if (fseeko(f, at, SEEK_SET) != 0) fail(std::string(path) + ": cannot read the cache file");
+        device(L->codes, codes);
+        device(L->scales, scales);
+        device(L->bias, (uint64_t)L->n * 4, 0);
         return L;
     }
 };
 
-std::string cache_key() { return trit_hip_version(); }
+std::string cache_key() { return std::string(trit_hip_version()) + " layout " + std::to_string(LAYOUT_VERSION); }
 
 }  // namespace
 }  // namespace trit
@@ -2283,9 +2332,12 @@ int trit_hip_decoder_load(const char* path, TritHipLmConfig* config, TritHipDeco
             TritHipLmConfig c;
             r.get(&c, sizeof c);
             if (c.layers <= 0 || c.layers > 4096 || c.d <= 0) fail(std::string(path) + ": a bad config");
+            // attn, mlp and (with QK-norm) q, k a layer, then the final norm:
+            // exactly what trit_hip_decoder_new reads.
+            if (c.d > (1 << 20) || c.head_dim < 0 || c.head_dim > (1 << 16)) fail(std::string(path) + ": a bad config");
+            const uint64_t per_layer = 2 * (uint64_t)c.d + (c.qk_norm ? 2 * (uint64_t)c.head_dim : 0);
             const uint64_t nn = r.val<uint64_t>();
-            if (nn > (uint64_t)(c.layers + 1) * (2 * (uint64_t)c.d + 2 * (uint64_t)c.head_dim))
-                fail(std::string(path) + ": a bad norm count");
+            if (nn != (uint64_t)c.layers * per_layer + (uint64_t)c.d) fail(std::string(path) + ": a bad norm count");
             std::vector<float> norms(nn);
             r.get(norms.data(), nn * 4);
             for (int i = 0; i < 4 * c.layers + 1; ++i) handles.push_back(layer_handle(r.layer()));
