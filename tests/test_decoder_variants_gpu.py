@@ -433,7 +433,7 @@ def test_tables(small_w, embed, head, flags):
 
 def test_tables_refused(small_w, qshape):
     """A head of int8 activations is refused (a table never takes them); a
-    Q8 table leaves the persistent step for the per-kernel loop."""
+    Q8 head runs on the persistent step."""
     print("case table kinds refused / step fallback", flush=True)
     w = small_w
     cfg = w.cfg
@@ -448,7 +448,7 @@ def test_tables_refused(small_w, qshape):
     with pytest.raises(hip.TritError, match="head must be a table"):
         hip.CausalLm(cfg, linears, w.norms_packed(), hip.Dense.f16(w.embed), int8_head)
     # The Qwen3-shaped model with a Q8 head: tokens as the oracle's, on the
-    # per-kernel loop.
+    # persistent step.
     wq = qshape[0]
     lm, (ref, ref16) = build(wq, [["q8_0"] * 4] * QS["layers"], ("f16",), ("q8",))
     p = synth.prompt(122, 20, QS["vocab"])
@@ -457,5 +457,5 @@ def test_tables_refused(small_w, qshape):
     s = lm.session(64, 0)
     s.prefill(p)
     got = s.generate(10)
-    assert not s.persistent
+    assert s.persistent
     assert got.tolist() == want

@@ -54,9 +54,17 @@ constexpr int MAXL = 41;       // layers: the exchange tags of a step fit in 8 b
 
 constexpr int cmax(int x, int y) { return x > y ? x : y; }
 
+// The linears' kinds the step takes: Q8_0 (and Q4_K after requantization):
+// 32-groups with f16 scales; Trit's int8: 128-groups with f32 scales. Codes
+// are row-major n x k int8 and scales row-major n x (k / group) either way.
+enum : int { WK_Q8_0 = 0, WK_INT8 = 1 };
+// The head's kinds: an f16 table, or int8 storage with an f32 scale per 32
+// (Q8, f32 math).
+enum : int { HK_F16 = 0, HK_Q8 = 1 };
+
 struct LayerPtrs {
-    const uint8_t* codes[4];  // qkv, o, gate_up, down: Q8_0 codes n x k
-    const uint16_t* scales[4];
+    const uint8_t* codes[4];  // qkv, o, gate_up, down: int8 codes n x k
+    const void* scales[4];    // f16 bits (WK_Q8_0) or f32 (WK_INT8)
     const float* norm_attn;
     const float* norm_mlp;
     const float* q_norm;
@@ -69,8 +77,11 @@ struct StepArgs {
     const LayerPtrs* layers;
     int n_layers, d, qd, ffn, heads, kvh, vocab, qk_norm, max_pos;
     float eps;
-    const uint16_t* embed;  // f16 lane-chain table, vocab x d
-    const uint16_t* head;   // f16 head in 4-row tiles (head_tile_kernel)
+    const void* embed;         // lane-chain table, vocab x d: f16 bits, or int8 codes (embed_q8)
+    const float* embed_scales; // the int8 table's scales, vocab x d / 32
+    int embed_q8;
+    const void* head;          // the head in 4-row tiles (head_tile_kernel): f16 bits or int8 codes
+    const float* head_scales;  // the int8 head's scales, vocab x d / 32
     const float* final_norm;
     const float* rope_sin;  // [position][HD / 2]
     const float* rope_cos;
@@ -284,20 +295,28 @@ struct Rows {
     uint32_t ws[NS];
 };
 
-template <int J, int P, int N, int NS>
-__device__ __forceinline__ void load_rows(int t, const uint8_t* codes, const uint16_t* scales, int part_rows, int row,
+// Lane l of a row takes chunk l + 16 j: for Q8_0 the scale of its 32-block
+// (l / 2 + 8 j), for int8 that of its 128-group (l / 8 + 2 j).
+template <int J, int P, int WK, int N, int NS>
+__device__ __forceinline__ void load_rows(int t, const uint8_t* codes, const void* scales, int part_rows, int row,
                                           Rows<N, NS>& r) {
     static_assert(P * J <= N && P * J <= NS, "the row registers hold the product");
-    constexpr int K = J * 256, G = K / 32;
+    constexpr int K = J * 256;
     const int l = t & 15;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
         const uint8_t* src = codes + (size_t)(p * part_rows + row) * K;
 #pragma unroll
         for (int j = 0; j < J; ++j) r.w[p * J + j] = load_stream(src + (size_t)(l + 16 * j) * 16);
-        const TRIT_GLOBAL uint16_t* sc = gmem(scales) + (size_t)(p * part_rows + row) * G + (l >> 1);
+        if constexpr (WK == WK_Q8_0) {
+            const TRIT_GLOBAL uint16_t* sc = gmem((const uint16_t*)scales) + (size_t)(p * part_rows + row) * (K / 32) + (l >> 1);
 #pragma unroll
-        for (int j = 0; j < J; ++j) r.ws[p * J + j] = sc[8 * j];
+            for (int j = 0; j < J; ++j) r.ws[p * J + j] = sc[8 * j];
+        } else {
+            const TRIT_GLOBAL uint32_t* sc = gmem((const uint32_t*)scales) + (size_t)(p * part_rows + row) * (K / 128) + (l >> 3);
+#pragma unroll
+            for (int j = 0; j < J; ++j) r.ws[p * J + j] = sc[2 * j];
+        }
     }
     // The rest of the set is zeroed: after any load no earlier rows stay live.
 #pragma unroll
@@ -451,7 +470,9 @@ __device__ __forceinline__ void load_norm(int t, const float* norm_w, NormRegs<J
 
 // Trit's activation quantizer over x (K values in LDS), optionally after
 // RMSNorm x * (inv * w), into sm.xq / sm.xs; ends with a block barrier.
-template <int J>
+// Q8_0: 32-groups (8 lanes), the scale stored f16-rounded; int8: 128-groups
+// (32 lanes), the f32 scale (src/cpu/kernels.rs:661-737).
+template <int J, int WK>
 __device__ void quantize_block(int t, const float* x, const NormRegs<J>* nr, Smem& sm,
                                const NormRegs<J>* fs = nullptr) {
     constexpr int ITEMS = J * 64;  // float4 items; a multiple of 64: whole waves
@@ -480,22 +501,64 @@ __device__ void quantize_block(int t, const float* x, const NormRegs<J>* nr, Sme
         peak = __builtin_fmaxf(peak, dpp<DPP_XOR1>(peak));
         peak = __builtin_fmaxf(peak, dpp<DPP_XOR2>(peak));
         peak = __builtin_fmaxf(peak, dpp<DPP_HALF_MIRROR>(peak));
+        if constexpr (WK == WK_INT8) {
+            peak = __builtin_fmaxf(peak, dpp<DPP_MIRROR>(peak));
+            peak = __builtin_fmaxf(peak, __shfl_xor(peak, 16));
+        }
         const float scale = peak > 0.0f ? peak / 127.0f : 1.0f;
         const float q = 1.0f / scale;
         *(uint32_t*)(sm.xq + item * 4) =
             pack4(act_code(v.x * q), act_code(v.y * q), act_code(v.z * q), act_code(v.w * q));
-        if ((item & 7) == 0) sm.xs[item >> 3] = f16_round(scale);
+        if constexpr (WK == WK_INT8) {
+            if ((item & 31) == 0) sm.xs[item >> 5] = scale;
+        } else {
+            if ((item & 7) == 0) sm.xs[item >> 3] = f16_round(scale);
+        }
     }
     __syncthreads();
 }
 
 // The one-row kernel's dots and f32 chain for a wave's rows; the total of
-// each row lands in lane 14 of its 16 lanes.
-template <int J, int P, int N, int NS>
+// each row lands in lane 14 of its 16 lanes. Trit's chain: total =
+// fma(f32(dot_g), ws_g * xs_g, total) over the groups in order from 0
+// (src/cpu/v2/product.rs:392-423). Q8_0: a block's two lanes add their
+// dots, and the chain passes through the 8 blocks of a chunk by row_ror:2;
+// int8: a group's 8 lanes add theirs, and the chain passes the chunk's two
+// groups by row_ror:8 (ending in lanes 8..15).
+template <int J, int P, int WK, int N, int NS>
 __device__ __forceinline__ void row_chain(int t, const Rows<N, NS>& r, const Smem& sm, float (&acc)[P]) {
     const int l = t & 15;
 #pragma unroll
     for (int p = 0; p < P; ++p) acc[p] = 0.0f;
+    if constexpr (WK == WK_INT8) {
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const uint4 xc = *(const uint4*)(sm.xq + (l + 16 * j) * 16);
+            const float sc = sm.xs[(l >> 3) + 2 * j];
+            float df[P], prod[P];
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                const uint4 wc = r.w[p * J + j];
+                int d = sdot4(wc.x, xc.x, 0);
+                d = sdot4(wc.y, xc.y, d);
+                d = sdot4(wc.z, xc.z, d);
+                d = sdot4(wc.w, xc.w, d);
+                d += dpp<DPP_XOR1>(d);
+                d += dpp<DPP_XOR2>(d);
+                d += dpp<DPP_HALF_MIRROR>(d);
+                df[p] = (float)d;
+                prod[p] = __uint_as_float(r.ws[p * J + j]) * sc;
+            }
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+#pragma unroll
+                for (int p = 0; p < P; ++p) {
+                    const float in = (j == 0 && q == 0) ? 0.0f : dpp<DPP_ROR8>(acc[p]);
+                    acc[p] = __builtin_fmaf(df[p], prod[p], in);
+                }
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         // Chunk j's dots (the block's two halves meet by DPP), then the
@@ -1386,7 +1449,7 @@ __device__ __forceinline__ void best_of_wave(float& bv, int& bi) {
     for (int r = 1; r < 4; ++r) better(bv, bi, v[r], i[r]);
 }
 
-template <int JD, int JO, int JF, int GROUP, int DPB, bool EXACT>
+template <int JD, int JO, int JF, int GROUP, int DPB, bool EXACT, int WK, int HK>
 __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int pos0, uint32_t seq0, int nsteps) {
     __shared__ Smem sm;
     State* st = a.st;
@@ -1443,7 +1506,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     // The first layer's qkv rows stream in during the choice. (Declared per
     // step so that nothing of it stays live through the head.)
     Rows<RN, RS> rr{};
-    if (aq) load_rows<JD, 1>(t, sm.layers[0].codes[0], sm.layers[0].scales[0], 0, rowq, rr);
+    if (aq) load_rows<JD, 1, WK>(t, sm.layers[0].codes[0], sm.layers[0].scales[0], 0, rowq, rr);
 
     // ---- the greedy choice over the blocks' candidates -------------------
     {
@@ -1484,11 +1547,16 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             if (!forward) st->done = 1;
         }
         if (!forward) return;
-        // Dense::row of the token (src/cpu/gemm.rs:412-429) is layer 0's input.
+        // Dense::row of the token (src/cpu/gemm.rs:412-429) is layer 0's input:
+        // the f16 value widened, or an int8 table's f32(code) * scale
+        // (widen_q8, :171-179).
         const int s_count = a.d / 16;
         for (int kk = t; kk < a.d; kk += T) {
             const int s = kk / 16, i = kk % 16;
-            float v = f16_to_f32(gmem(a.embed)[((size_t)token * 16 + i) * s_count + s]);
+            const size_t at = ((size_t)token * 16 + i) * s_count + s;
+            float v = a.embed_q8 ? (float)gmem((const int8_t*)a.embed)[at] *
+                                       gmem(a.embed_scales)[(size_t)token * (a.d / 32) + kk / 32]
+                                 : f16_to_f32(gmem((const uint16_t*)a.embed)[at]);
             if (a.additive && pos < a.additive_rows) v = v + *gmem(a.additive + (size_t)pos * a.d + kk);
             sm.xres[kk] = a.em != 1.0f ? v * a.em : v;
         }
@@ -1519,10 +1587,10 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             if (lane == 0) sm.inv = inv;
         }
         __syncthreads();
-        quantize_block<JD>(t, sm.xres, &nq, sm);
+        quantize_block<JD, WK>(t, sm.xres, &nq, sm);
         if (aq) {
             float acc[1];
-            row_chain<JD, 1>(t, rr, sm, acc);
+            row_chain<JD, 1, WK>(t, rr, sm, acc);
             if ((lane & 15) == 14) put(a.QKV + rowq, acc[0], tag_of(tag0, layer, 0));
         }
         __syncthreads();
@@ -1536,10 +1604,10 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             // o + residual; the o and gate_up rows stream in meanwhile, and
             // the qkv waves (nothing in flight) poll.
             if (ao)
-                load_rows<JO, 1>(t, L.codes[1], L.scales[1], 0, rowo, rr);
+                load_rows<JO, 1, WK>(t, L.codes[1], L.scales[1], 0, rowo, rr);
             else
                 zero_rows(rr);
-            if (agu) load_rows<JD, 2>(t, L.codes[2], L.scales[2], a.ffn, rowgu, rr);
+            if (agu) load_rows<JD, 2, WK>(t, L.codes[2], L.scales[2], a.ffn, rowgu, rr);
             // Then the attention blocks' waves before the qkv waves load the
             // next attention's keys and values into L2.
             if (EXACT && b < 2 * a.heads && w < NW - nqw) {
@@ -1557,14 +1625,14 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
                 leave();
             // combine; the o rows stream in meanwhile.
             if (ao)
-                load_rows<JO, 1>(t, L.codes[1], L.scales[1], 0, rowo, rr);
+                load_rows<JO, 1, WK>(t, L.codes[1], L.scales[1], 0, rowo, rr);
             else
                 zero_rows(rr);
             __syncthreads();
             if (!combine(t, a, tag_of(tag0, layer, 1), tag_of(tag0, layer, 2), sm, deadline, nu + no)) leave();
             // o + residual; the gate_up rows stream in meanwhile.
             if (agu)
-                load_rows<JD, 2>(t, L.codes[2], L.scales[2], a.ffn, rowgu, rr);
+                load_rows<JD, 2, WK>(t, L.codes[2], L.scales[2], a.ffn, rowgu, rr);
             else if (!ao)  // the o rows are still to be used
                 zero_rows(rr);
             __syncthreads();
@@ -1572,10 +1640,10 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             // in flight.
             if (!gather<8>(t, a.ATT, a.qd, lin, tag_of(tag0, layer, 2), sm.xin, sm, deadline, st, nu)) leave();
         }
-        quantize_block<JO>(t, sm.xin, (const NormRegs<JO>*)nullptr, sm);
+        quantize_block<JO, WK>(t, sm.xin, (const NormRegs<JO>*)nullptr, sm);
         if (ao) {
             float acc[1];
-            row_chain<JO, 1>(t, rr, sm, acc);
+            row_chain<JO, 1, WK>(t, rr, sm, acc);
             if ((lane & 15) == 14) put(a.X + rowo, sm.xres[rowo] + a.rm * acc[0], tag_of(tag0, layer, 3));
         }
         // The touched words are consumed here, where they have long arrived
@@ -1595,25 +1663,25 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             if (lane == 0) sm.inv = inv;
         }
         __syncthreads();
-        quantize_block<JD>(t, sm.xres, &ngu, sm, a.ffn_scales ? &nfs : nullptr);
+        quantize_block<JD, WK>(t, sm.xres, &ngu, sm, a.ffn_scales ? &nfs : nullptr);
         if (agu) {
             float acc[2];
-            row_chain<JD, 2>(t, rr, sm, acc);
+            row_chain<JD, 2, WK>(t, rr, sm, acc);
             if ((lane & 15) == 14) put(a.H + rowgu, silu_trit(acc[0]) * acc[1], tag_of(tag0, layer, 4));
         }
         // down + residual.
         if (ad)
-            load_rows<JF, 1>(t, L.codes[3], L.scales[3], 0, rowd, rr);
+            load_rows<JF, 1, WK>(t, L.codes[3], L.scales[3], 0, rowd, rr);
         else
             zero_rows(rr);
         if (aq && layer + 1 < a.n_layers)
-            load_rows<JD, 1>(t, sm.layers[layer + 1].codes[0], sm.layers[layer + 1].scales[0], 0, rowq, rr);
+            load_rows<JD, 1, WK>(t, sm.layers[layer + 1].codes[0], sm.layers[layer + 1].scales[0], 0, rowq, rr);
         __syncthreads();
         if (!gather<MAXK / T>(t, a.H, a.ffn, lin, tag_of(tag0, layer, 4), sm.xin, sm, deadline, st)) leave();
-        quantize_block<JF>(t, sm.xin, (const NormRegs<JF>*)nullptr, sm);
+        quantize_block<JF, WK>(t, sm.xin, (const NormRegs<JF>*)nullptr, sm);
         if (ad) {
             float acc[1];
-            row_chain<JF, 1>(t, rr, sm, acc);
+            row_chain<JF, 1, WK>(t, rr, sm, acc);
             if ((lane & 15) == 14) put(a.X + rowd, sm.xres[rowd] + a.rm * acc[0], tag_of(tag0, layer, 5));
         }
         __syncthreads();
@@ -1624,23 +1692,41 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     // group r row 32 (p nb + b) + r: the blocks sweep the table together.
     // Three passes of weights are in flight at a time, and each lane keeps
     // the normed x values of its lane chain in registers.
-    constexpr int S8 = JD * 2;  // 16-byte loads per lane chain: d / 128
+    // 16-byte units per lane chain: d / 128 (f16) or d / 256 (int8). An int8
+    // head's row has d / 32 f32 scales, SC a lane: lane i of a row holds
+    // scales SC i .. SC i + SC - 1, and the chain's step s, in group s / 2,
+    // reads its scale from lane (s / 2) / SC of the row by a row broadcast.
+    constexpr int SU = HK == HK_F16 ? JD * 2 : JD;
+    constexpr int SC = HK == HK_F16 ? 1 : JD / 2;
+    static_assert(HK == HK_F16 || JD % 2 == 0, "an int8 head's scales split over the row's lanes");
+    struct Pass {
+        uint4 w[SU];
+        float sc[SC];
+    };
     fresh();
     const int l16 = t & 15;
     const int rows_pass = T / 16, nb = (int)gridDim.x;
     const int passes = (a.vocab + rows_pass * nb - 1) / (rows_pass * nb);
     auto row_of = [&](int p) { return (p * nb + b) * rows_pass + (t >> 4); };
     // Wave w of pass p reads 4-row tile (p nb + b) 8 + w: instruction j
-    // reads the tile's 1 KB run j, in which lane 16g + i finds block j of
+    // reads the tile's 1 KB run j, in which lane 16g + i finds unit j of
     // lane chain i of the tile's row g.
     const int tiles = (a.vocab + 3) / 4;
-    auto load_pass = [&](int p, uint4 (&wv)[S8]) {
+    const size_t tile_bytes = (size_t)4 * a.d * (HK == HK_F16 ? 2 : 1);
+    auto load_pass = [&](int p, Pass& wv) {
         const int tile = (p * nb + b) * (rows_pass / 4) + w;
-        const uint4* src = (const uint4*)(a.head + (size_t)(tile < tiles ? tile : 0) * 4 * a.d);
+        const uint4* src = (const uint4*)((const uint8_t*)a.head + (size_t)(tile < tiles ? tile : 0) * tile_bytes);
 #pragma unroll
-        for (int j = 0; j < S8; ++j) wv[j] = load_stream(src + j * WAVE + lane);
+        for (int j = 0; j < SU; ++j) wv.w[j] = load_stream(src + j * WAVE + lane);
+        if constexpr (HK == HK_Q8) {
+            const int row = row_of(p);
+            const TRIT_GLOBAL float* sc =
+                gmem(a.head_scales) + (size_t)(row < a.vocab ? row : 0) * (a.d / 32) + SC * l16;
+#pragma unroll
+            for (int c = 0; c < SC; ++c) wv.sc[c] = sc[c];
+        }
     };
-    uint4 ring[3][S8];
+    Pass ring[3];
 #pragma unroll
     for (int q = 0; q < 3; ++q)
         if (q < passes) load_pass(q, ring[q]);
@@ -1661,21 +1747,37 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     for (int q = 0; q < (MAXD + T - 1) / T; ++q)
         if (t + T * q < a.d) sm.xin[t + T * q] = sm.xres[t + T * q] * (sm.inv * fn[q]);
     __syncthreads();
-    float xr[S8 * 8];  // lane chain l16 of the normed x
+    float xr[JD * 16];  // lane chain l16 of the normed x
 #pragma unroll
-    for (int s = 0; s < S8 * 8; ++s) xr[s] = sm.xin[16 * s + l16];
+    for (int s = 0; s < JD * 16; ++s) xr[s] = sm.xin[16 * s + l16];
     float best = -INFINITY;
     int index = INT_MAX;
-    auto head_pass = [&](int p, uint4 (&wv)[S8]) {
-        // Trit's 16-lane f16 order (gemv_float.hip): lane chain, then the tree.
+    auto head_pass = [&](int p, Pass& wv) {
+        // Trit's 16-lane order (gemv_float.hip): lane chain, then the tree.
+        // The weight is the f16 value widened, or f32(code) * scale of its
+        // 32-group, one rounding (widen_q8).
         float acc = 0.0f;
 #pragma unroll
-        for (int j = 0; j < S8; ++j) {
-            const uint32_t words[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+        for (int j = 0; j < SU; ++j) {
+            const uint32_t words[4] = {wv.w[j].x, wv.w[j].y, wv.w[j].z, wv.w[j].w};
+            if constexpr (HK == HK_F16) {
 #pragma unroll
-            for (int hh = 0; hh < 8; ++hh) {
-                const float wf = f16_to_f32((uint16_t)(words[hh >> 1] >> ((hh & 1) * 16)));
-                acc = __builtin_fmaf(xr[j * 8 + hh], wf, acc);
+                for (int hh = 0; hh < 8; ++hh) {
+                    const float wf = f16_to_f32((uint16_t)(words[hh >> 1] >> ((hh & 1) * 16)));
+                    acc = __builtin_fmaf(xr[j * 8 + hh], wf, acc);
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < 16; u += 2) {
+                    const int g = 8 * j + u / 2;  // the group of steps 16 j + u, + u + 1
+                    const float scale = row_bcast(wv.sc[g % SC], g / SC);
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const int h = u + e;
+                        const float wf = (float)(int8_t)(uint8_t)(words[h >> 2] >> ((h & 3) * 8)) * scale;
+                        acc = __builtin_fmaf(xr[16 * j + h], wf, acc);
+                    }
+                }
             }
         }
         // Lane i adds lane i - 8, - 4, - 2, - 1 of its row (rotations): in
@@ -1726,17 +1828,18 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
 }
 
 // The head's tiled layout: rows in tiles of four; in a tile, 16-byte run
-// (j, g, i) holds values 8j .. 8j + 7 of lane chain i of row g (element
-// kk = 16 s + i of the row is value s of chain i), runs ordered j, then g,
-// then i. From the lane-chain layout [row][i][s] of an F16 layer.
-__global__ void head_tile_kernel(const uint16_t* __restrict__ src, int n, int k, uint16_t* __restrict__ dst) {
-    const int s8 = k / 128;  // 8-value runs per chain
+// (j, g, i) holds unit j of lane chain i of row g (values 8j .. 8j + 7 of
+// an f16 chain, 16j .. 16j + 15 of an int8 one; element kk = 16 s + i of
+// the row is value s of chain i), runs ordered j, then g, then i. From the
+// lane-chain layout [row][i][s] of an F16 or Q8 layer; s8 16-byte units a
+// chain.
+__global__ void head_tile_kernel(const uint4* __restrict__ src, int n, int s8, uint4* __restrict__ dst) {
     const size_t chunks = (size_t)n * 16 * s8;
     for (size_t q = blockIdx.x * (size_t)blockDim.x + threadIdx.x; q < chunks; q += (size_t)gridDim.x * blockDim.x) {
         const size_t r = q / (16 * s8);
         const int rem = (int)(q - r * 16 * s8), i = rem / s8, j = rem % s8;
         const size_t to = (r / 4) * (size_t)(4 * 16 * s8) + (size_t)(j * 4 + (int)(r % 4)) * 16 + i;
-        ((uint4*)dst)[to] = ((const uint4*)src)[q];
+        dst[to] = src[q];
     }
 }
 
@@ -1771,16 +1874,27 @@ using StepFn = void (*)(StepArgs, int, int, uint32_t, int);
 // The instantiated shapes: (d/256, heads*hd/256, ffn/256, q heads per kv head).
 // dpb: output dims of one query head a block takes in the one-pass
 // attention, 0 for the split attention and its combine.
-StepFn step_fn(int jd, int jo, int jf, int group, int dpb, bool exact) {
+// wk, hk: the linears' and the head's kinds (WK_*, HK_*); the tree-sum
+// instances take Q8_0 linears and an f16 head only.
+template <int JD, int JO, int JF, int GROUP, int DPB>
+StepFn exact_fn(int wk, int hk) {
+    if (wk == WK_Q8_0) return hk == HK_F16 ? step_kernel<JD, JO, JF, GROUP, DPB, true, WK_Q8_0, HK_F16>
+                                           : step_kernel<JD, JO, JF, GROUP, DPB, true, WK_Q8_0, HK_Q8>;
+    return hk == HK_F16 ? step_kernel<JD, JO, JF, GROUP, DPB, true, WK_INT8, HK_F16>
+                        : step_kernel<JD, JO, JF, GROUP, DPB, true, WK_INT8, HK_Q8>;
+}
+
+StepFn step_fn(int jd, int jo, int jf, int group, int dpb, bool exact, int wk, int hk) {
+    if (!exact && (wk != WK_Q8_0 || hk != HK_F16)) return nullptr;
     if (jd == 4 && jo == 8 && jf == 12 && group == 2) {  // Qwen3-0.6B
-        if (exact) return dpb == 8 ? step_kernel<4, 8, 12, 2, 8, true> : nullptr;
-        if (dpb == 0) return step_kernel<4, 8, 12, 2, 0, false>;
-        if (dpb == 8) return step_kernel<4, 8, 12, 2, 8, false>;
+        if (exact) return dpb == 8 ? exact_fn<4, 8, 12, 2, 8>(wk, hk) : nullptr;
+        if (dpb == 0) return step_kernel<4, 8, 12, 2, 0, false, WK_Q8_0, HK_F16>;
+        if (dpb == 8) return step_kernel<4, 8, 12, 2, 8, false, WK_Q8_0, HK_F16>;
     }
     if (jd == 4 && jo == 4 && jf == 8 && group == 2) {
-        if (exact) return dpb == 4 ? step_kernel<4, 4, 8, 2, 4, true> : nullptr;
-        if (dpb == 0) return step_kernel<4, 4, 8, 2, 0, false>;
-        if (dpb == 4) return step_kernel<4, 4, 8, 2, 4, false>;
+        if (exact) return dpb == 4 ? exact_fn<4, 4, 8, 2, 4>(wk, hk) : nullptr;
+        if (dpb == 0) return step_kernel<4, 4, 8, 2, 0, false, WK_Q8_0, HK_F16>;
+        if (dpb == 4) return step_kernel<4, 4, 8, 2, 4, false, WK_Q8_0, HK_F16>;
     }
     return nullptr;
 }
@@ -1794,7 +1908,7 @@ int device_blocks() {
 }
 
 struct Plan {
-    int blocks, splits, comb, dpb, rq, ro, rgu, rd, rh;
+    int blocks, splits, comb, dpb, rq, ro, rgu, rd, rh, wk, hk;
     StepFn fn;
 };
 
@@ -1816,11 +1930,25 @@ bool plan(const SessionImpl& S, Plan& p) {
     const int group = c.heads / c.kv_heads, qd = c.heads * HD;
     if (c.d % 256 || qd % 256 || c.ffn % 256 || c.d > MAXD || qd > MAXK || c.ffn > MAXK) return false;
     if (c.layers <= 0 || c.layers > MAXL || c.layers * PH + PH >= 256) return false;
-    auto q8 = [](const LayerRef& L) { return (L->kind == Q8_0 || L->kind == Q4_K) && !L->bias.ptr; };
+    // Every linear Q8_0 / Q4_K (32-groups, f16 scales), or every linear
+    // Trit's int8 (128-groups, f32 scales); no bias.
+    auto wk_of = [](const LayerRef& L) {
+        if (L->bias.ptr) return -1;
+        if (L->kind == Q8_0 || L->kind == Q4_K) return (int)WK_Q8_0;
+        if (L->kind == INT8 && L->group == 128) return (int)WK_INT8;
+        return -1;
+    };
+    p.wk = wk_of(D.qkv[0]);
+    if (p.wk < 0) return false;
     for (int l = 0; l < c.layers; ++l)
-        if (!q8(D.qkv[l]) || !q8(D.o[l]) || !q8(D.gate_up[l]) || !q8(D.down[l])) return false;
+        if (wk_of(D.qkv[l]) != p.wk || wk_of(D.o[l]) != p.wk || wk_of(D.gate_up[l]) != p.wk || wk_of(D.down[l]) != p.wk)
+            return false;
+    // An f16 or int8-storage (Q8) head, and such a table for the embeddings.
     const Layer& head = D.head ? *D.head : *D.embed;
-    if (head.kind != F16 || head.k != c.d || head.bias.ptr || D.embed->kind != F16) return false;
+    if (head.k != c.d || head.bias.ptr || (D.embed->kind != F16 && D.embed->kind != Q8_F32)) return false;
+    if (head.kind == F16) p.hk = HK_F16;
+    else if (head.kind == Q8_F32 && c.d % 512 == 0) p.hk = HK_Q8;
+    else return false;
     p.blocks = device_blocks();
     if (p.blocks < c.kv_heads || p.blocks % c.kv_heads) return false;
     const int nq = (c.heads + 2 * c.kv_heads) * HD;
@@ -1849,7 +1977,7 @@ bool plan(const SessionImpl& S, Plan& p) {
         if (S.max_pos > T || (p.dpb != 4 && p.dpb != 8) || p.blocks % (c.kv_heads * group) ||
             !fits(qd, NW - nqw, 8))
             return false;
-        p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group, p.dpb, true);
+        p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group, p.dpb, true, p.wk, p.hk);
         if (!p.fn) return false;
         p.rh = (c.vocab + p.blocks - 1) / p.blocks;
         return true;
@@ -1857,14 +1985,14 @@ bool plan(const SessionImpl& S, Plan& p) {
     const bool one_pass = !split_forced() && S.max_pos <= 32 * MAXF && (p.dpb == 4 || p.dpb == 8) &&
                           p.blocks % (c.kv_heads * group) == 0 && fits(qd, NW - nqw, 8);
     if (one_pass) {
-        p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group, p.dpb, false);
+        p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group, p.dpb, false, p.wk, p.hk);
     } else {
         p.dpb = 0;
         if (S.max_pos > p.splits * 32 * MAXC) return false;
         if ((qd % p.blocks) || HD % p.comb) return false;
         if (p.splits > WAVE || p.comb > NW || p.splits * (2 + p.comb) > MAXK) return false;
         if (!fits(p.splits * (2 + p.comb), NW - nqw, 2) || !fits(qd, nu, 8)) return false;
-        p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group, 0, false);
+        p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group, 0, false, p.wk, p.hk);
     }
     if (!p.fn) return false;
     p.rh = (c.vocab + p.blocks - 1) / p.blocks;
@@ -1894,7 +2022,7 @@ void decode_step_prepare(SessionImpl& S, hipStream_t s) {
             const LayerRef* ls[4] = {&D.qkv[l], &D.o[l], &D.gate_up[l], &D.down[l]};
             for (int i = 0; i < 4; ++i) {
                 table[l].codes[i] = (*ls[i])->codes.as<uint8_t>();
-                table[l].scales[i] = (*ls[i])->scales.as<uint16_t>();
+                table[l].scales[i] = (*ls[i])->scales.ptr;
             }
             table[l].norm_attn = D.norm_attn(l);
             table[l].norm_mlp = D.norm_mlp(l);
@@ -1905,11 +2033,11 @@ void decode_step_prepare(SessionImpl& S, hipStream_t s) {
         }
         const Layer& head = D.head ? *D.head : *D.embed;
         std::call_once(D.step_head_once, [&] {
-            const size_t rows = (size_t)(c.vocab + 3) / 4 * 4;
-            D.step_head.alloc(rows * c.d * 2);
-            TRIT_HIP(hipMemsetAsync(D.step_head.ptr, 0, rows * c.d * 2, s));
-            hipLaunchKernelGGL(head_tile_kernel, dim3(4096), dim3(256), 0, s, head.codes.as<uint16_t>(), c.vocab, c.d,
-                               D.step_head.as<uint16_t>());
+            const size_t rows = (size_t)(c.vocab + 3) / 4 * 4, elem = head.kind == F16 ? 2 : 1;
+            D.step_head.alloc(rows * c.d * elem);
+            TRIT_HIP(hipMemsetAsync(D.step_head.ptr, 0, rows * c.d * elem, s));
+            hipLaunchKernelGGL(head_tile_kernel, dim3(4096), dim3(256), 0, s, head.codes.as<uint4>(), c.vocab,
+                               (int)(c.d * elem / 256), D.step_head.as<uint4>());
             TRIT_HIP(hipGetLastError());
             TRIT_HIP(hipStreamSynchronize(s));
         });
@@ -1953,8 +2081,12 @@ void decode_step_launch(SessionImpl& S, int step, int pos, int nsteps, hipStream
     a.qk_norm = c.qk_norm;
     a.max_pos = S.max_pos;
     a.eps = c.eps;
-    a.embed = D.embed->codes.as<uint16_t>();
-    a.head = D.step_head.as<uint16_t>();
+    a.embed = D.embed->codes.ptr;
+    a.embed_q8 = D.embed->kind == Q8_F32;
+    a.embed_scales = D.embed->kind == Q8_F32 ? D.embed->scales.as<float>() : nullptr;
+    a.head = D.step_head.ptr;
+    const Layer& head = D.head ? *D.head : *D.embed;
+    a.head_scales = head.kind == Q8_F32 ? head.scales.as<float>() : nullptr;
     a.final_norm = D.final_norm();
     a.rope_sin = S.rope_sin.as<float>();
     a.rope_cos = S.rope_cos.as<float>();

@@ -137,7 +137,10 @@ __device__ __forceinline__ uint4 load_stream(const void* p) {
 // DPP lane moves (gfx9 encodings): quad_perm [1,0,3,2] (xor 1), [2,3,0,1]
 // (xor 2), row_half_mirror (lane i <-> 7-i in each 8), row_mirror (i <->
 // 15-i in each 16), row_ror:2 (lane i takes lane i-2 in its row of 16).
-enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140, DPP_ROR2 = 0x122 };
+enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140, DPP_ROR2 = 0x122,
+             DPP_ROR8 = 0x128,
+             // row_newbcast:n (0x150 + n): every lane of a 16-lane row reads lane n of that row.
+             DPP_ROW_BCAST0 = 0x150 };
 
 template <int CTRL>
 __device__ __forceinline__ int dpp(int v) {
@@ -146,6 +149,29 @@ __device__ __forceinline__ int dpp(int v) {
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// Lane n of each 16-lane row, in every lane of that row (row_newbcast).
+// n must fold to a constant (an index of an unrolled loop).
+__device__ __forceinline__ float row_bcast(float v, int n) {
+    switch (n & 15) {
+        case 0: return dpp<DPP_ROW_BCAST0 + 0>(v);
+        case 1: return dpp<DPP_ROW_BCAST0 + 1>(v);
+        case 2: return dpp<DPP_ROW_BCAST0 + 2>(v);
+        case 3: return dpp<DPP_ROW_BCAST0 + 3>(v);
+        case 4: return dpp<DPP_ROW_BCAST0 + 4>(v);
+        case 5: return dpp<DPP_ROW_BCAST0 + 5>(v);
+        case 6: return dpp<DPP_ROW_BCAST0 + 6>(v);
+        case 7: return dpp<DPP_ROW_BCAST0 + 7>(v);
+        case 8: return dpp<DPP_ROW_BCAST0 + 8>(v);
+        case 9: return dpp<DPP_ROW_BCAST0 + 9>(v);
+        case 10: return dpp<DPP_ROW_BCAST0 + 10>(v);
+        case 11: return dpp<DPP_ROW_BCAST0 + 11>(v);
+        case 12: return dpp<DPP_ROW_BCAST0 + 12>(v);
+        case 13: return dpp<DPP_ROW_BCAST0 + 13>(v);
+        case 14: return dpp<DPP_ROW_BCAST0 + 14>(v);
+        default: return dpp<DPP_ROW_BCAST0 + 15>(v);
+    }
 }
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {

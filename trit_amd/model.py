@@ -20,3 +20,15 @@ def build_decoder(w) -> hip.CausalLm:
         layer.free()
     embed.free()
     return lm
+
+
+def build_decoder_auto(w) -> hip.CausalLm:
+    """A device decoder at Trit's Auto precision (synth.AutoWeights): int8
+    linears (Dense::int8) and a tied int8-storage table (Dense::q8)."""
+    linears = [hip.Dense.int8(codes, scales) for layer in w.linears for codes, scales in layer]
+    table = hip.Dense.q8(*w.table)
+    lm = hip.CausalLm(w.cfg, linears, w.norms_packed(), table)
+    for layer in linears:
+        layer.free()
+    table.free()
+    return lm

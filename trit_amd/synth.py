@@ -265,3 +265,54 @@ def lm_weights(cfg: dict, config: int = 1, sigma: float = 0.02, norm_jitter: flo
 def prompt(config: int, n: int, vocab: int) -> np.ndarray:
     """n token ids uniform in [0, vocab)."""
     return ints(seed_for(config, 0xFFFF), n, 0, vocab - 1).astype(np.int32)
+
+
+class AutoWeights:
+    """A decoder at Trit's Auto precision for safetensors (src/cpu/gemm.rs:
+    565-617; S1-mini's load): every linear int8 with an f32 scale per row and
+    128 inputs, and the token table (tied head) as int8 storage with an f32
+    scale per 32 values (Q8, f32 math). Norms and config come from `base`."""
+
+    def __init__(self, base: LmWeights, linears, table):
+        self.cfg, self.base = base.cfg, base
+        self.linears = linears  # per layer: [(codes n x k int8, scales n x k/128 f32)] * 4
+        self.table = table      # (codes vocab x d int8, scales vocab x d/32 f32)
+
+    def norms_packed(self):
+        return self.base.norms_packed()
+
+
+def _int8_of_blocks(blocks: np.ndarray, n: int, k: int):
+    """Int8 weights from Q8_0 blocks: the same codes, and for each 128-group
+    the magnitude of its first block's scale (a positive f32 scale)."""
+    b = np.asarray(blocks, np.uint8).reshape(n, k // 32, 34)
+    codes = np.ascontiguousarray(b[:, :, 2:]).view(np.int8).reshape(n, k)
+    half = np.ascontiguousarray(b[:, ::4, :2]).view(np.float16).reshape(n, k // 128)
+    scales = np.maximum(np.abs(half.astype(np.float32)), np.float32(1e-6)).astype(np.float32)
+    return codes, scales
+
+
+def q8_table(values: np.ndarray):
+    """Int8 storage of f32 rows, 32 values a scale, by ggml's Q8_0 rule
+    (d = max|v| / 127, codes round(v / d) half away from zero), the scale
+    kept in f32."""
+    v = np.asarray(values, np.float32)
+    n, k = v.shape
+    g = v.reshape(n, k // 32, 32)
+    d = (np.max(np.abs(g), axis=2) / np.float32(127.0)).astype(np.float32)
+    inv = np.where(d != 0, np.float32(1.0) / np.where(d != 0, d, 1), 0).astype(np.float32)
+    q = g * inv[:, :, None]
+    codes = (np.sign(q) * np.floor(np.abs(q) + np.float32(0.5))).astype(np.int8)
+    return codes.reshape(n, k), d
+
+
+def auto_weights(base: LmWeights) -> AutoWeights:
+    """The Auto-precision form of `base` (same codes, 128-group scales; the
+    f16 table requantized to int8 storage)."""
+    cfg = base.cfg
+    d, ffn, hd = cfg["d"], cfg["ffn"], cfg["head_dim"]
+    shapes = [((cfg["heads"] + 2 * cfg["kv_heads"]) * hd, d), (d, cfg["heads"] * hd), (2 * ffn, d), (d, ffn)]
+    linears = [[_int8_of_blocks(m, n, k) for m, (n, k) in zip((L.qkv, L.o, L.gate_up, L.down), shapes)]
+               for L in base.layers]
+    table = q8_table(base.embed.view(np.float16).astype(np.float32))
+    return AutoWeights(base, linears, table)
