@@ -115,9 +115,10 @@ def team_start(spread: int = 0, threads: int = 0) -> int:
     return lib().or_team_start(spread, threads)
 
 
-def vnni_peak(iters: int = 20_000_000) -> float:
+def vnni_peak(iters: int = 10_000_000) -> float:
     """int8 multiply-adds per second of the team on register-resident
-    vpdpbusd chains (0 without AVX-512 VNNI)."""
+    vpdpbusd chains, 24 a thread (0 without AVX-512 VNNI); the best of three
+    runs."""
     return lib().or_vnni_peak(iters)
 
 

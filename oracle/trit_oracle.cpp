@@ -484,16 +484,21 @@ AVX512 void int8_vnni_tile(const Int8Layer& L, const Quantized& q, int task, int
     int k = L.k, k4s = k / 4, groups = k / L.group, quads = L.group / 4;
     int blocks[2] = {2 * task, 2 * task + 1};
     __m512 acc[2][F];
+    #pragma GCC unroll 16
     for (int b = 0; b < 2; ++b)
+        #pragma GCC unroll 16
         for (int f = 0; f < F; ++f) acc[b][f] = _mm512_setzero_ps();
     const int8_t* W = L.weights.data();
     for (int g = 0; g < groups; ++g) {
         __m512i dots[2][F];
+        #pragma GCC unroll 16
         for (int b = 0; b < 2; ++b)
+            #pragma GCC unroll 16
             for (int f = 0; f < F; ++f) dots[b][f] = _mm512_setzero_si512();
         for (int k4 = g * quads; k4 < (g + 1) * quads; ++k4) {
             __m512i w0 = _mm512_loadu_si512(W + ((size_t)blocks[0] * k4s + k4) * 64);
             __m512i w1 = _mm512_loadu_si512(W + ((size_t)blocks[1] * k4s + k4) * 64);
+            #pragma GCC unroll 16
             for (int f = 0; f < F; ++f) {
                 int32_t xv;
                 std::memcpy(&xv, q.values.data() + (size_t)(frame0 + f) * k + k4 * 4, 4);
@@ -502,8 +507,10 @@ AVX512 void int8_vnni_tile(const Int8Layer& L, const Quantized& q, int task, int
                 dots[1][f] = _mm512_dpbusd_epi32(dots[1][f], w1, x);
             }
         }
+        #pragma GCC unroll 16
         for (int b = 0; b < 2; ++b) {
             __m512 ws = _mm512_loadu_ps(L.scales.data() + ((size_t)blocks[b] * groups + g) * 16);
+            #pragma GCC unroll 16
             for (int f = 0; f < F; ++f) {
                 size_t index = (size_t)(frame0 + f) * groups + g;
                 __m512i corrected = _mm512_sub_epi32(dots[b][f], _mm512_set1_epi32(128 * q.sums[index]));
@@ -512,7 +519,9 @@ AVX512 void int8_vnni_tile(const Int8Layer& L, const Quantized& q, int task, int
             }
         }
     }
+    #pragma GCC unroll 16
     for (int b = 0; b < 2; ++b)
+        #pragma GCC unroll 16
         for (int f = 0; f < F; ++f) _mm512_storeu_ps(out + (size_t)(frame0 + f) * L.n + blocks[b] * 16, acc[b][f]);
 }
 
@@ -538,13 +547,16 @@ AVX2T void int8_avx2_tile(const Int8Layer& L, const Quantized& q, int block, int
     int k = L.k, k4s = k / 4, groups = k / L.group, quads = L.group / 4;
     const __m256i ones = _mm256_set1_epi16(1);
     __m256 acc[F];
+    #pragma GCC unroll 16
     for (int f = 0; f < F; ++f) acc[f] = _mm256_setzero_ps();
     for (int g = 0; g < groups; ++g) {
         __m256i dots[F];
+        #pragma GCC unroll 16
         for (int f = 0; f < F; ++f) dots[f] = _mm256_setzero_si256();
         for (int k4 = g * quads; k4 < (g + 1) * quads; ++k4) {
             __m256i w = _mm256_loadu_si256((const __m256i*)(L.weights.data() + ((size_t)block * k4s + k4) * 32));
             __m256i mag = _mm256_abs_epi8(w);
+            #pragma GCC unroll 16
             for (int f = 0; f < F; ++f) {
                 int32_t xv;
                 std::memcpy(&xv, q.values.data() + (size_t)(frame0 + f) * k + k4 * 4, 4);
@@ -554,11 +566,13 @@ AVX2T void int8_avx2_tile(const Int8Layer& L, const Quantized& q, int block, int
             }
         }
         __m256 ws = _mm256_loadu_ps(L.scales.data() + ((size_t)block * groups + g) * 8);
+        #pragma GCC unroll 16
         for (int f = 0; f < F; ++f) {
             __m256 scale = _mm256_mul_ps(ws, _mm256_set1_ps(q.scales[(size_t)(frame0 + f) * groups + g]));
             acc[f] = _mm256_fmadd_ps(_mm256_cvtepi32_ps(dots[f]), scale, acc[f]);
         }
     }
+    #pragma GCC unroll 16
     for (int f = 0; f < F; ++f) _mm256_storeu_ps(out + (size_t)(frame0 + f) * L.n + block * 8, acc[f]);
 }
 
@@ -657,15 +671,20 @@ AVX512 void ternary_vnni_tile(const TernaryLayer& L, const Quantized& q, int tas
     int blocks[2] = {2 * task, 2 * task + 1};
     const __m512i low = _mm512_set1_epi8(3);
     __m512 acc[2][F];
+    #pragma GCC unroll 16
     for (int b = 0; b < 2; ++b)
+        #pragma GCC unroll 16
         for (int f = 0; f < F; ++f) acc[b][f] = _mm512_setzero_ps();
     for (int g = 0; g < groups; ++g) {
         __m512i dots[2][F];
+        #pragma GCC unroll 16
         for (int b = 0; b < 2; ++b)
+            #pragma GCC unroll 16
             for (int f = 0; f < F; ++f) dots[b][f] = _mm512_setzero_si512();
         for (int quad = 0; quad < TGROUP / 16; ++quad) {
             int k16 = g * (TGROUP / 16) + quad;
             __m512i w[2][4];
+            #pragma GCC unroll 16
             for (int b = 0; b < 2; ++b) {
                 __m512i z = _mm512_loadu_si512(L.codes.data() + ((size_t)blocks[b] * k16s + k16) * 64);
                 w[b][0] = _mm512_and_si512(z, low);
@@ -675,6 +694,7 @@ AVX512 void ternary_vnni_tile(const TernaryLayer& L, const Quantized& q, int tas
             }
             for (int s = 0; s < 4; ++s) {
                 int k4 = 4 * k16 + s;
+                #pragma GCC unroll 16
                 for (int f = 0; f < F; ++f) {
                     int32_t xv;
                     std::memcpy(&xv, q.values.data() + (size_t)(frame0 + f) * k + k4 * 4, 4);
@@ -684,8 +704,10 @@ AVX512 void ternary_vnni_tile(const TernaryLayer& L, const Quantized& q, int tas
                 }
             }
         }
+        #pragma GCC unroll 16
         for (int b = 0; b < 2; ++b) {
             __m512 ws = _mm512_loadu_ps(L.scales.data() + ((size_t)blocks[b] * groups + g) * 16);
+            #pragma GCC unroll 16
             for (int f = 0; f < F; ++f) {
                 size_t index = (size_t)(frame0 + f) * groups + g;
                 __m512i corrected = _mm512_sub_epi32(dots[b][f], _mm512_set1_epi32(q.sums[index]));
@@ -694,7 +716,9 @@ AVX512 void ternary_vnni_tile(const TernaryLayer& L, const Quantized& q, int tas
             }
         }
     }
+    #pragma GCC unroll 16
     for (int b = 0; b < 2; ++b)
+        #pragma GCC unroll 16
         for (int f = 0; f < F; ++f) _mm512_storeu_ps(out + (size_t)(frame0 + f) * L.n + blocks[b] * 16, acc[b][f]);
 }
 
@@ -777,12 +801,14 @@ AVX512 float reduce512(__m512 v) {
 template <int R, int C, typename W>
 AVX512 void f_tile512(const float* x, const W* w, int k, float* out, int n) {
     __m512 acc[R][C];
+    #pragma GCC unroll 16
     for (int r = 0; r < R; ++r)
         for (int c = 0; c < C; ++c) acc[r][c] = _mm512_setzero_ps();
     int kk = 0;
     for (; kk + 16 <= k; kk += 16) {
         __m512 wv[C];
         for (int c = 0; c < C; ++c) wv[c] = load16(w + (size_t)c * k + kk);
+        #pragma GCC unroll 16
         for (int r = 0; r < R; ++r) {
             __m512 xv = _mm512_loadu_ps(x + (size_t)r * k + kk);
             for (int c = 0; c < C; ++c) acc[r][c] = _mm512_fmadd_ps(xv, wv[c], acc[r][c]);
@@ -792,11 +818,13 @@ AVX512 void f_tile512(const float* x, const W* w, int k, float* out, int n) {
         __mmask16 mask = (__mmask16)((1u << (k - kk)) - 1);
         __m512 wv[C];
         for (int c = 0; c < C; ++c) wv[c] = load16_first(w + (size_t)c * k + kk, k - kk);
+        #pragma GCC unroll 16
         for (int r = 0; r < R; ++r) {
             __m512 xv = _mm512_maskz_loadu_ps(mask, x + (size_t)r * k + kk);
             for (int c = 0; c < C; ++c) acc[r][c] = _mm512_fmadd_ps(xv, wv[c], acc[r][c]);
         }
     }
+    #pragma GCC unroll 16
     for (int r = 0; r < R; ++r)
         for (int c = 0; c < C; ++c) out[(size_t)r * n + c] = reduce512(acc[r][c]);
 }
@@ -1318,13 +1346,20 @@ int or_team_size(void) { return team_threads(); }
 }  // extern "C"
 namespace {
 AVX512 int64_t vnni_spin(int64_t iters) {
-    __m512i acc[12];
-    for (int i = 0; i < 12; ++i) acc[i] = _mm512_set1_epi32(i);
+    // 24 independent chains: enough to cover vpdpbusd's latency at two
+    // issues a cycle (Zen 5's 512-bit pipes), with every operand in registers.
+    constexpr int CH = 24;
+    __m512i acc[CH];
+#pragma GCC unroll 32
+    for (int i = 0; i < CH; ++i) acc[i] = _mm512_set1_epi32(i);
     const __m512i a = _mm512_set1_epi32(0x01020304), b = _mm512_set1_epi32(0x05060708);
-    for (int64_t it = 0; it < iters; ++it)
-        for (int i = 0; i < 12; ++i) acc[i] = _mm512_dpbusd_epi32(acc[i], a, b);
+    for (int64_t it = 0; it < iters; ++it) {
+#pragma GCC unroll 32
+        for (int i = 0; i < CH; ++i) acc[i] = _mm512_dpbusd_epi32(acc[i], a, b);
+    }
     __m512i t = acc[0];
-    for (int i = 1; i < 12; ++i) t = _mm512_add_epi32(t, acc[i]);
+#pragma GCC unroll 32
+    for (int i = 1; i < CH; ++i) t = _mm512_add_epi32(t, acc[i]);
     return _mm512_reduce_add_epi32(t);
 }
 }  // namespace
@@ -1334,13 +1369,17 @@ double or_vnni_peak(int64_t iters) {
     if (or_isa_best() != OR_AVX512) return 0.0;
     const int n = team_threads();
     std::vector<int64_t> sink(n);
-    const auto t0 = std::chrono::steady_clock::now();
-    parallel(n, [&](int t) { sink[t] = vnni_spin(iters); });
-    const double s = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    double best = 0.0;
+    for (int round = 0; round < 3; ++round) {  // the best of three
+        const auto t0 = std::chrono::steady_clock::now();
+        parallel(n, [&](int t) { sink[t] = vnni_spin(iters); });
+        const double s = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        best = std::max(best, (double)n * (double)iters * 24.0 * 64.0 / s);
+    }
     volatile int64_t keep = 0;
     for (int64_t v : sink) keep = keep + v;
     (void)keep;
-    return (double)n * (double)iters * 12.0 * 64.0 / s;
+    return best;
 }
 
 uint16_t or_f32_to_f16(float value) { return f32_to_f16(value); }
