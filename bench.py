@@ -472,6 +472,77 @@ def step_roofline(cfg, prompt, steps, step_ms, persistent, mode, linears="q8_0",
                        "(trit_hip_session_generate_timed); the launch includes the final choice-only step")
 
 
+STAMP_PHASES = [  # (name, from stamp, to stamp, blocks: "all" / "attn" / "rest")
+    ("x hand-over (after down)", 0, 1, "all"), ("RMSNorm (Trit's serial sum)", 1, 2, "all"),
+    ("quantize (qkv input)", 2, 3, "all"), ("qkv rows and put", 3, 4, "all"),
+    ("attention: qkv hand-over", 5, 6, "attn"), ("attention: q/k norm, rotary, append", 6, 7, "attn"),
+    ("attention: scores, max, exp", 7, 8, "attn"), ("attention: softmax sum (serial)", 8, 9, "attn"),
+    ("attention: p.V (serial) and put", 9, 10, "attn"),
+    ("attention -> o hand-over (attention blocks)", 10, 11, "attn"),
+    ("attention -> o hand-over (other blocks, from qkv put)", 4, 11, "rest"),
+    ("quantize (o input)", 11, 12, "all"), ("o rows and put", 12, 13, "all"),
+    ("x hand-over (after o)", 13, 14, "all"), ("RMSNorm", 14, 15, "all"), ("quantize (gate_up input)", 15, 16, "all"),
+    ("gate_up rows, SwiGLU, put", 16, 17, "all"), ("h hand-over", 17, 18, "all"),
+    ("quantize (down input)", 18, 19, "all"), ("down rows and put", 19, 20, "all"),
+    ("a layer", 0, 20, "all")]
+HEAD_PHASES = [("x hand-over (last layer's down)", None, 21), ("final RMSNorm", 21, 22), ("head passes", 22, 23),
+               ("best of the block and put", 23, 24)]
+
+
+def stamp_pass(w, prompt, steps, step=8, layer=10):
+    """The persistent step's phases on the measurement build
+    (TRIT_HIP_LIBRARY=trit_amd/lib/libtrit_hip_stamps.so): thread 0 of each
+    block stamps fixed points of one (step, layer) of the launch; per phase,
+    the mean over the blocks that run it of the shader-clock interval,
+    converted to microseconds by each block's shader/wall clock ratio over
+    the layer."""
+    lib = hip.lib()
+    lm, linears, embed = build_layers(w)
+    sess = lm.session(len(prompt) + steps, 0)
+    cfg = w.cfg
+    blocks = 256
+    attn = 2 * cfg["heads"]
+
+    def run(stamp_layer):
+        hip.check(lib.trit_hip_step_stamps(step, stamp_layer))
+        sess.reset()
+        sess.prefill(prompt, want_logits=False)
+        sess.generate(steps)
+        assert sess.persistent
+        wall = np.zeros((blocks, 32), np.uint64)
+        clk = np.zeros((blocks, 32), np.uint64)
+        hip.check(lib.trit_hip_step_stamps_read(wall.ctypes.data_as(C.c_void_p), clk.ctypes.data_as(C.c_void_p),
+                                                blocks))
+        return wall.astype(np.float64), clk.astype(np.float64)
+
+    run(layer)  # warm-up
+    wall, clk = run(layer)
+    # Shader-clock ticks per microsecond, per block, over the layer (wall: 100 MHz).
+    rate = (clk[:, 20] - clk[:, 0]) / ((wall[:, 20] - wall[:, 0]) / 100.0)
+    sel = {"all": np.arange(blocks), "attn": np.arange(attn), "rest": np.arange(attn, blocks)}
+    rows = []
+    for name, a, b, who in STAMP_PHASES:
+        idx = sel[who]
+        us = (clk[idx, b] - clk[idx, a]) / rate[idx]
+        rows.append(dict(phase=name, us=round(float(np.mean(us)), 3), blocks=who))
+    hwall, hclk = run(cfg["layers"])
+    hrate = np.median(rate)
+    head = []
+    for name, a, b in HEAD_PHASES:
+        if a is None:
+            continue
+        us = (hclk[:, b] - hclk[:, a]) / hrate
+        head.append(dict(phase=name, us=round(float(np.mean(us)), 3)))
+    hip.check(lib.trit_hip_step_stamps(-1, -1))
+    sess.free()
+    lm.free()
+    for layer_ in linears:
+        layer_.free()
+    embed.free()
+    return dict(step=step, layer=layer, prompt=len(prompt), steps=steps, shader_mhz=round(float(np.median(rate)), 1),
+                layer_phases=rows, head_phases=head)
+
+
 def cpu_configs(configs, min_s=0.3):
     """The oracle (Trit's AVX-512 VNNI path, restated; the pinned team of
     cpu_baseline) on the same product shapes and seeds as config_lines:
@@ -754,6 +825,9 @@ def main():
     ap.add_argument("--load-pass", action="store_true",
                     help="only the load times of the workload's decoder: from host layers, from a GGUF file, "
                          "from the device weight-cache file")
+    ap.add_argument("--stamp-pass", action="store_true",
+                    help="only the persistent step's phase stamps (needs the measurement build: "
+                         "python -m trit_amd.build --stamps, then TRIT_HIP_LIBRARY=trit_amd/lib/libtrit_hip_stamps.so)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="only the roofline sweeps and a 256 MiB device copy (the counter scale for "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs)")
@@ -775,6 +849,9 @@ def main():
         return
     if args.load_pass:
         print(json.dumps({"load_pass": True, **load_times(w, prompt)}), flush=True)
+        return
+    if args.stamp_pass:
+        print(json.dumps({"stamp_pass": True, **stamp_pass(w, prompt, args.steps)}), flush=True)
         return
     lm, linears, embed = build_layers(w)
     if args.profile_pass:

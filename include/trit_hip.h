@@ -272,6 +272,17 @@ int trit_hip_session_generate(TritHipSession *session, int max_new, const int32_
 int trit_hip_session_generate_timed(TritHipSession *session, int max_new, const int32_t *stop, int n_stop,
                                     int32_t *out, void *start_event, void *stop_event, int *persistent);
 
+/* Measurement only; no counterpart in the reference. A library built with
+ * `python -m trit_amd.build --stamps` (libtrit_hip_stamps.so) stamps the
+ * persistent step's phases for one (step, layer) of each launch (layer ==
+ * layers: the final norm and the head): thread 0 of every block writes the
+ * device wall clock (100 MHz) and its shader clock at fixed points.
+ * _stamps chooses the (step, layer) (-1: none) for later launches; _read
+ * copies the stamps of the first `blocks` blocks (NSTAMP = 32 a block, the
+ * return value). The product library returns -1 from both. */
+int trit_hip_step_stamps(int step, int layer);
+int trit_hip_step_stamps_read(uint64_t *wall, uint64_t *clock, int blocks);
+
 /* Clears the caches (a new call). */
 int trit_hip_session_reset(TritHipSession *session);
 

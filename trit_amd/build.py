@@ -13,6 +13,8 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "lib", "libtrit_hip.so")
+# The measurement build: the persistent step's phase stamps compiled in.
+OUT_STAMPS = os.path.join(HERE, "lib", "libtrit_hip_stamps.so")
 SOURCES = ["layer.hip", "gemv.hip", "gemv_decode.hip", "gemv_stream.hip", "gemv_float.hip", "gemm.hip", "decoder.hip", "decode_step.hip", "attention_mfma.hip", "gguf.hip", "encoder.hip", "tokenizer.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -29,30 +31,33 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = False, jobs: int = 0) -> str:
-    """Compiles the sources in parallel (`jobs` at a time; 0: up to 8), then links."""
+def build(verbose: bool = False, jobs: int = 0, stamps: bool = False) -> str:
+    """Compiles the sources in parallel (`jobs` at a time; 0: up to 8), then
+    links. stamps: the measurement library with the step's phase stamps."""
     from concurrent.futures import ThreadPoolExecutor
 
-    os.makedirs(os.path.dirname(OUT), exist_ok=True)
+    out = OUT_STAMPS if stamps else OUT
+    os.makedirs(os.path.dirname(out), exist_ok=True)
     cmds, objs = [], []
+    extra = ["-DTRIT_HIP_STEP_STAMPS"] if stamps else []
     for src in SOURCES:
         path = os.path.join(CSRC, src)
         if not os.path.exists(path):
             raise RuntimeError(f"build: source {path} is missing")
-        obj = os.path.join(HERE, "lib", os.path.splitext(src)[0] + ".o")
-        cmds.append([HIPCC, *FLAGS, "-c", path, "-o", obj])
+        obj = os.path.join(HERE, "lib", os.path.splitext(src)[0] + (".stamps.o" if stamps else ".o"))
+        cmds.append([HIPCC, *FLAGS, *extra, "-c", path, "-o", obj])
         objs.append(obj)
     if verbose:
         for cmd in cmds:
             print(" ".join(cmd), flush=True)
     with ThreadPoolExecutor(jobs or min(8, os.cpu_count() or 1)) as pool:
         list(pool.map(run, cmds))
-    tmp = OUT + ".tmp"
+    tmp = out + ".tmp"
     run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
-    os.replace(tmp, OUT)
+    os.replace(tmp, out)
     for obj in objs:
         os.remove(obj)
-    return OUT
+    return out
 
 
 def run(cmd):
@@ -66,4 +71,4 @@ def run(cmd):
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    print(build(verbose="-v" in sys.argv, stamps="--stamps" in sys.argv))

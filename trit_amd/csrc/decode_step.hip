@@ -54,6 +54,42 @@ constexpr int MAXL = 41;       // layers: the exchange tags of a step fit in 8 b
 
 constexpr int cmax(int x, int y) { return x > y ? x : y; }
 
+// Phase stamps (a measurement build, TRIT_HIP_STEP_STAMPS): thread 0 of
+// each block writes the device wall clock (100 MHz, the same on every XCD)
+// and its shader clock at fixed points of one chosen (step, layer) of a
+// launch; trit_hip_step_stamps_read copies them out. Stamp points:
+//   0 layer start, 1 x gathered, 2 RMSNorm, 3 quantized, 4 qkv rows put;
+//   attention blocks: 5 before the qkv gather, 6 gathered, 7 q/k norm,
+//   rotary and append, 8 scores, max and exp, 9 softmax sum, 10 p.V put;
+//   11 attention gathered (o input), 12 quantized, 13 o rows put,
+//   14 x gathered, 15 RMSNorm, 16 quantized, 17 gate_up put, 18 h gathered,
+//   19 quantized, 20 down put; the head (layer = layers): 21 x gathered,
+//   22 normed, 23 passes done, 24 candidates put.
+#ifdef TRIT_HIP_STEP_STAMPS
+constexpr int NSTAMP = 32;
+constexpr int MAX_STAMP_BLOCKS = 1024;
+__device__ unsigned long long g_stamp_wall[MAX_STAMP_BLOCKS][NSTAMP];
+__device__ unsigned long long g_stamp_clk[MAX_STAMP_BLOCKS][NSTAMP];
+#define STAMP(k)                                                            \
+    do {                                                                    \
+        if (threadIdx.x == 0 && sm.stamp) {                                 \
+            g_stamp_wall[blockIdx.x][k] = wall_clock64();                   \
+            g_stamp_clk[blockIdx.x][k] = __builtin_readcyclecounter();      \
+        }                                                                   \
+    } while (0)
+#define STAMP_WHEN(cond)                         \
+    do {                                         \
+        if (threadIdx.x == 0) sm.stamp = (cond); \
+    } while (0)
+#else
+#define STAMP(k) \
+    do {         \
+    } while (0)
+#define STAMP_WHEN(cond) \
+    do {                 \
+    } while (0)
+#endif
+
 // The linears' kinds the step takes: Q8_0 (and Q4_K after requantization):
 // 32-groups with f16 scales; Trit's int8: 128-groups with f32 scales. Codes
 // are row-major n x k int8 and scales row-major n x (k / group) either way.
@@ -110,6 +146,7 @@ struct StepArgs {
     // (before em, as the per-kernel loop adds them), or null.
     const float* additive;
     int additive_rows;
+    int stamp_step, stamp_layer;  // the stamped (step, layer); layer == n_layers: the head
 };
 
 struct Smem {
@@ -148,6 +185,7 @@ struct Smem {
     float inv;
     int abort;
     int token;
+    int stamp;  // thread 0: this layer is the stamped one
 };
 
 __device__ __forceinline__ uint32_t tag_of(uint32_t tag0, int layer, int phase) {
@@ -1205,7 +1243,9 @@ __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, in
     // The last wave polls: it loads no value, and no key while the session
     // has at most (NW - 1) * 64 positions.
     const int p0 = pos <= VT ? NW - 1 : NW - a.rq / 4 - 1;
+    STAMP(5);
     if (!gather<8>(t, a.QKV, 3 * HD, index, tag_in, sm.qkv, sm, deadline, a.st, p0)) leave();
+    STAMP(6);
     asm volatile("" ::"v"(touch));
     // The cached values into LDS, row-major [key][64 dims].
 #pragma unroll
@@ -1281,6 +1321,7 @@ __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, in
         }
     }
     __syncthreads();
+    STAMP(7);
 
     // Scores: thread t key t, the fused chain over the dims in order (the
     // new key as cached: its f16 bits). q is read from LDS 16 values at a
@@ -1352,7 +1393,9 @@ __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, in
     // Their sum in key order from 0, by every wave, then p_j = e_j *
     // (1/sum); the chain below reads -0 (adding nothing) past the cached
     // keys, and the new key's probability on its own.
+    STAMP(8);
     const float p = e * (1.0f / chain_sum_spec(t, sm.probs, tk, a.norm_window, sm));
+    STAMP(9);
     sm.probs[t] = t < pos ? p : -0.0f;
     if (t == pos) sm.ppos = p;
     // p.V in key order: lane d chains dim 64 h2 + d, wave w over keys
@@ -1412,6 +1455,7 @@ __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, in
     // After a barrier (or in the wave that wrote it): the new key's term.
     if (wu == (nkw > 0 ? nkw - 1 : 0))
         put(a.ATT + (size_t)hq * HD + 64 * h2 + lane, __builtin_fmaf(sm.ppos, sm.kvn[1][64 * h2 + lane], acc), tag_out);
+    STAMP(10);
     return true;
 }
 
@@ -1569,6 +1613,8 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     for (int layer = 0; layer < a.n_layers; ++layer) {
         fresh();
         const LayerPtrs& L = sm.layers[layer];
+        STAMP_WHEN(layer == a.stamp_layer && it == a.stamp_step);
+        STAMP(0);
         // qkv: x (gathered, or the embedding) -> RMSNorm -> quantize -> rows.
         NormRegs<JD> nq;
         load_norm<JD>(t, L.norm_attn, nq);
@@ -1579,6 +1625,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         // Polled by the first waves (the down rows' wave stored x).
         if (layer > 0 && !gather<6>(t, a.X, a.d, lin, tag_of(tag0, layer - 1, 5), sm.xres, sm, deadline, st))
             leave();
+        STAMP(1);
         if constexpr (EXACT) {
             const float inv = norm_inv_spec<JD>(t, sm.xres, a.eps, a.norm_window, sm);
             if (t == 0) sm.inv = inv;
@@ -1587,13 +1634,16 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             if (lane == 0) sm.inv = inv;
         }
         __syncthreads();
+        STAMP(2);
         quantize_block<JD, WK>(t, sm.xres, &nq, sm);
+        STAMP(3);
         if (aq) {
             float acc[1];
             row_chain<JD, 1, WK>(t, rr, sm, acc);
             if ((lane & 15) == 14) put(a.QKV + rowq, acc[0], tag_of(tag0, layer, 0));
         }
         __syncthreads();
+        STAMP(4);
         if constexpr (DPB > 0) {
             // attention in one pass: its outputs are the o product's input.
             const bool ok = EXACT ? attention_exact<GROUP, DPB>(t, a, L, pos, tag_of(tag0, layer, 0),
@@ -1619,6 +1669,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             __syncthreads();
             if (!gather<8>(t, a.ATT, a.qd, lin, tag_of(tag0, layer, 2), sm.xin, sm, deadline, st, NW - nqw))
                 leave();
+            STAMP(11);
         } else {
             // attention partials.
             if (!attention<GROUP>(t, a, L, pos, tag_of(tag0, layer, 0), tag_of(tag0, layer, 1), sm, deadline))
@@ -1641,11 +1692,13 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             if (!gather<8>(t, a.ATT, a.qd, lin, tag_of(tag0, layer, 2), sm.xin, sm, deadline, st, nu)) leave();
         }
         quantize_block<JO, WK>(t, sm.xin, (const NormRegs<JO>*)nullptr, sm);
+        STAMP(12);
         if (ao) {
             float acc[1];
             row_chain<JO, 1, WK>(t, rr, sm, acc);
             if ((lane & 15) == 14) put(a.X + rowo, sm.xres[rowo] + a.rm * acc[0], tag_of(tag0, layer, 3));
         }
+        STAMP(13);
         // The touched words are consumed here, where they have long arrived
         // (before the polls of the gather below).
         asm volatile("" ::"v"(kvt[0]), "v"(kvt[1]), "v"(kvt[2]), "v"(kvt[3]));
@@ -1655,6 +1708,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         if (a.ffn_scales) load_norm<JD>(t, a.ffn_scales + (size_t)layer * a.d, nfs);
         __syncthreads();
         if (!gather<MAXK / T>(t, a.X, a.d, lin, tag_of(tag0, layer, 3), sm.xres, sm, deadline, st)) leave();
+        STAMP(14);
         if constexpr (EXACT) {
             const float inv = norm_inv_spec<JD>(t, sm.xres, a.eps, a.norm_window, sm);
             if (t == 0) sm.inv = inv;
@@ -1663,12 +1717,15 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             if (lane == 0) sm.inv = inv;
         }
         __syncthreads();
+        STAMP(15);
         quantize_block<JD, WK>(t, sm.xres, &ngu, sm, a.ffn_scales ? &nfs : nullptr);
+        STAMP(16);
         if (agu) {
             float acc[2];
             row_chain<JD, 2, WK>(t, rr, sm, acc);
             if ((lane & 15) == 14) put(a.H + rowgu, silu_trit(acc[0]) * acc[1], tag_of(tag0, layer, 4));
         }
+        STAMP(17);
         // down + residual.
         if (ad)
             load_rows<JF, 1, WK>(t, L.codes[3], L.scales[3], 0, rowd, rr);
@@ -1678,13 +1735,16 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             load_rows<JD, 1, WK>(t, sm.layers[layer + 1].codes[0], sm.layers[layer + 1].scales[0], 0, rowq, rr);
         __syncthreads();
         if (!gather<MAXK / T>(t, a.H, a.ffn, lin, tag_of(tag0, layer, 4), sm.xin, sm, deadline, st)) leave();
+        STAMP(18);
         quantize_block<JF, WK>(t, sm.xin, (const NormRegs<JF>*)nullptr, sm);
+        STAMP(19);
         if (ad) {
             float acc[1];
             row_chain<JF, 1, WK>(t, rr, sm, acc);
             if ((lane & 15) == 14) put(a.X + rowd, sm.xres[rowd] + a.rm * acc[0], tag_of(tag0, layer, 5));
         }
         __syncthreads();
+        STAMP(20);
     }
 
     // ---- final RMSNorm, the head, the block's best logit ----------------
@@ -1733,7 +1793,9 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     float fn[(MAXD + T - 1) / T];
 #pragma unroll
     for (int q = 0; q < (MAXD + T - 1) / T; ++q) fn[q] = t + T * q < a.d ? gmem(a.final_norm)[t + T * q] : 0.0f;
+    STAMP_WHEN(a.stamp_layer == a.n_layers && it == a.stamp_step);
     if (!gather<MAXD / T>(t, a.X, a.d, lin, tag_of(tag0, a.n_layers - 1, 5), sm.xres, sm, deadline, st)) return;
+    STAMP(21);
     if constexpr (EXACT) {
         const float inv = norm_inv_spec<JD>(t, sm.xres, a.eps, a.norm_window, sm);
         if (t == 0) sm.inv = inv;
@@ -1747,6 +1809,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     for (int q = 0; q < (MAXD + T - 1) / T; ++q)
         if (t + T * q < a.d) sm.xin[t + T * q] = sm.xres[t + T * q] * (sm.inv * fn[q]);
     __syncthreads();
+    STAMP(22);
     float xr[JD * 16];  // lane chain l16 of the normed x
 #pragma unroll
     for (int s = 0; s < JD * 16; ++s) xr[s] = sm.xin[16 * s + l16];
@@ -1801,6 +1864,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         if (p + 1 < passes) head_pass(p + 1, ring[1]);
         if (p + 2 < passes) head_pass(p + 2, ring[2]);
     }
+    STAMP(23);
     // The block's first maximum: the lanes of a row group agree; waves by
     // shuffles, then one thread over the waves.
     best_of_wave(best, index);
@@ -1823,6 +1887,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         put(a.CAND + 2 * b + 1, __int_as_float(bi), tag_c);
         if (b == 0) st->pos = pos + 1;
     }
+    STAMP(24);
     __syncthreads();  // sm.bv / sm.bi are the next choice's
     }
 }
@@ -2052,6 +2117,9 @@ void decode_step_prepare(SessionImpl& S, hipStream_t s) {
     }
 }
 
+// The (step, layer) the measurement build stamps (-1: none).
+int g_stamp_step = -1, g_stamp_layer = -1;
+
 void decode_step_launch(SessionImpl& S, int step, int pos, int nsteps, hipStream_t s) {
     Plan p;
     if (!plan(S, p)) fail("decode step: the session's model does not fit the persistent step");
@@ -2128,8 +2196,47 @@ void decode_step_launch(SessionImpl& S, int step, int pos, int nsteps, hipStream
     a.ffn_scales = D.has_ffn_scales ? D.ffn_scales.as<float>() : nullptr;
     a.additive = S.additive_rows ? S.additive.as<float>() : nullptr;
     a.additive_rows = S.additive_rows;
+    a.stamp_step = g_stamp_step;
+    a.stamp_layer = g_stamp_layer;
     void* args[] = {&a, &step, &pos, (void*)&seq0, &nsteps};
     TRIT_HIP(hipLaunchCooperativeKernel((const void*)p.fn, dim3(p.blocks), dim3(T), args, 0, s));
 }
 
 }  // namespace trit
+
+extern "C" {
+
+int trit_hip_step_stamps(int step, int layer) {
+    return trit::guard(-1, [&] {
+#ifdef TRIT_HIP_STEP_STAMPS
+        trit::g_stamp_step = step;
+        trit::g_stamp_layer = layer;
+        return 0;
+#else
+        (void)step;
+        (void)layer;
+        trit::fail("step stamps: this library was built without them (python -m trit_amd.build --stamps)");
+        return -1;
+#endif
+    });
+}
+
+int trit_hip_step_stamps_read(uint64_t* wall, uint64_t* clock, int blocks) {
+    return trit::guard(-1, [&] {
+#ifdef TRIT_HIP_STEP_STAMPS
+        if (!wall || !clock || blocks < 1 || blocks > trit::MAX_STAMP_BLOCKS) trit::fail("step stamps: bad arguments");
+        const size_t bytes = (size_t)blocks * trit::NSTAMP * 8;
+        TRIT_HIP(hipMemcpyFromSymbol(wall, HIP_SYMBOL(trit::g_stamp_wall), bytes, 0, hipMemcpyDeviceToHost));
+        TRIT_HIP(hipMemcpyFromSymbol(clock, HIP_SYMBOL(trit::g_stamp_clk), bytes, 0, hipMemcpyDeviceToHost));
+        return trit::NSTAMP;
+#else
+        (void)wall;
+        (void)clock;
+        (void)blocks;
+        trit::fail("step stamps: this library was built without them (python -m trit_amd.build --stamps)");
+        return -1;
+#endif
+    });
+}
+
+}  // extern "C"

@@ -15,7 +15,9 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "lib", "libtrit_hip.so")
+# TRIT_HIP_LIBRARY names another build of the library (the measurement
+# build with the step's phase stamps: lib/libtrit_hip_stamps.so).
+LIB_PATH = os.environ.get("TRIT_HIP_LIBRARY") or os.path.join(HERE, "lib", "libtrit_hip.so")
 
 Q8_0, INT8, TERNARY, Q4_K, F16, F32, Q8 = 1, 2, 3, 4, 5, 6, 7
 EXACT, KV_F32, TREE_SUMS = 1, 2, 4
@@ -64,6 +66,8 @@ def lib():
         pp = C.POINTER(C.c_void_p)
         sig = {
             "trit_hip_version": (C.c_char_p, []),
+            "trit_hip_step_stamps": (i, [i, i]),
+            "trit_hip_step_stamps_read": (i, [p, p, i]),
             "trit_hip_last_error": (C.c_char_p, []),
             "trit_hip_init": (i, [i]),
             "trit_hip_layer_q8_0": (i, [i, i, p, p, pp]),
