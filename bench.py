@@ -412,7 +412,24 @@ def config_lines(H, sweeps=10):
     out["decode_s1mini_auto_precision"] = dict(
         line, note="S1-mini's load: int8 linears (f32 scale per 128), tied int8-storage table (f32 scale per 32, "
                    "f32 math); 256-token prompt, 128 greedy steps on the persistent step, Trit's sums, f16 caches")
+    # A cleanup call's length (src/cleanup.rs:154,296): a 900-token prompt
+    # (system turn, control line and an 800-token part) and 256 steps, past
+    # 512 positions (the step's keys in rounds of 512).
+    line = loop_rate(dict(synth.QWEN3_06B), 1, steps=256, prompt_len=900, lmx=model.build_decoder_auto(auto),
+                     kinds=("int8", "q8"))
+    line.pop("tokens")
+    out["decode_s1mini_cleanup_900_prompt_256_steps"] = dict(
+        line, note="S1-mini's load, a 900-token prompt then 256 greedy steps on the persistent step (Trit's sums, "
+                   "f16 caches; the attention over up to 1156 keys in rounds of 512)")
     del auto
+    # An audio-LLM decode after its prompt (config 5's 1564 rows:
+    # 1500 audio-encoder rows and 64 text tokens): Qwen3-0.6B's shape, Q8_0
+    # linears, 64 greedy steps on the persistent step.
+    line = loop_rate(dict(synth.QWEN3_06B), 1, steps=64, prompt_len=1564)
+    line.pop("tokens")
+    out["decode_audio_llm_1564_prompt_64_steps"] = dict(
+        line, note="Qwen3-0.6B's shape, Q8_0 linears, tied f16 head; a 1564-row prompt then 64 greedy steps on "
+                   "the persistent step (Trit's sums, f16 caches; 1565-1627 keys in rounds of 512)")
 
     cfg17 = dict(synth.QWEN3_06B, d=2048, ffn=6144)
     out["decode_qwen3_1.7b_shape_per_kernel_loop"] = dict(

@@ -372,10 +372,14 @@ def test_short_prompt(qshape, m):
 
 
 @pytest.mark.parametrize("prompt,steps,max_pos,persistent", [(330, 54, 384, True), (440, 60, 512, True),
-                                                               (700, 40, 760, False)])
+                                                               (700, 40, 760, True), (1564, 64, 1630, True),
+                                                               (2040, 30, 2100, True), (4000, 24, 4096, True),
+                                                               (4100, 8, 4120, False)])
 def test_step_long(qshape, prompt, steps, max_pos, persistent):
     """Long sessions in the default mode: up to 512 positions on the
-    persistent step (a thread per key), past that the per-kernel loop;
+    persistent step with a thread per key, up to 4096 with the keys in
+    rounds of 512 (an audio-LLM decode after a 1564-row prompt, a cleanup
+    session's 2000 positions, the limit), past that the per-kernel loop;
     tokens and the logits after them bit for bit the f16-cache oracle's."""
     print(f"case decoder long session (prompt {prompt}, {steps} steps, {max_pos} positions)", flush=True)
     w, ref, lm, ref16 = qshape

@@ -159,3 +159,12 @@ def test_auto_precision_full_loop(gpu):
     assert same_bits(logits, want_logits), rel(logits, want_logits)
     print(f"{len(set(got.tolist()))} distinct tokens", flush=True)
     assert got.tolist() == greedy(ref, want_logits, 128)
+
+
+def test_auto_precision_long_session(auto_qs):
+    """A cleanup-length session at Auto precision: a 900-token prompt and
+    160 greedy steps (past 512 positions: the keys in rounds of 512)."""
+    print("case step: int8 linears, tied Q8 table, 900 + 160", flush=True)
+    w, lm = auto_qs
+    got = check(lm, auto_oracle(w, True), synth.prompt(145, 900, QS["vocab"]), 160, max_pos=1100)
+    assert len(set(got.tolist())) > 4

@@ -47,6 +47,7 @@ constexpr int NW = T / WAVE;   // waves per block
 constexpr int HD = 128;        // head_dim
 constexpr int MAXC = 4;        // 32-key chunks of a split held in registers
 constexpr int MAXF = 12;       // 32-key chunks of the one-pass attention (384 positions)
+constexpr int MAXT = 4096;     // positions of a Trit-order session on the step (the long attention)
 constexpr int MAXD = 2048;     // largest d
 constexpr int MAXK = 3072;     // largest product input
 constexpr int PH = 6;          // exchange phases per layer
@@ -172,7 +173,7 @@ struct Smem {
         // row-major (key j's 64 values: 128 contiguous bytes).
         alignas(16) _Float16 vs[T][HD / 2];
     };
-    alignas(16) float probs[T];           // the exact attention's probabilities
+    alignas(16) float probs[MAXT];        // the exact attention's scores, then probabilities
     float spart[NW];                      // its sum: each segment's tree sum
     float sres[NW][WAVE];                 // its sum: each segment's chain from candidate L
     float carry[WAVE];                    // its p.V sums, passed from wave to wave
@@ -1459,6 +1460,306 @@ __device__ bool attention_exact(int t, const StepArgs& a, const LayerPtrs& L, in
     return true;
 }
 
+// The score of one key: the fused chain over the 128 dims in order of q
+// (LDS, already times 1/sqrt(hd)) by the key's f16 bits widened inside each
+// multiply-add; q is read 16 values at a time, the next 16 in flight.
+__device__ __forceinline__ float score_of(const uint4 (&kk)[HD / 8], const float* q) {
+    float acc = 0.0f;
+    float4 qc[4], qn[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qc[i] = *(const float4*)(q + 4 * i);
+#pragma unroll
+    for (int part = 0; part < HD / 16; ++part) {
+        if (part + 1 < HD / 16) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) qn[i] = *(const float4*)(q + 16 * (part + 1) + 4 * i);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const uint4 kw = kk[2 * part + c];
+            const uint32_t wd[4] = {kw.x, kw.y, kw.z, kw.w};
+            const float q8[8] = {qc[2 * c].x,     qc[2 * c].y,     qc[2 * c].z,     qc[2 * c].w,
+                                 qc[2 * c + 1].x, qc[2 * c + 1].y, qc[2 * c + 1].z, qc[2 * c + 1].w};
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                acc = __builtin_fmaf(q8[u], f16_to_f32((uint16_t)(wd[u >> 1] >> (16 * (u & 1)))), acc);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qc[i] = qn[i];
+    }
+    return acc;
+}
+
+// attention_exact for sessions of up to MAXT positions: the same orders and
+// bits, over the keys in rounds of T. Scores: round r, thread t scores key
+// r T + t into sm.probs (the next round's keys load meanwhile); the maximum
+// over all of them, e_j = exp(s_j - max), their sum in key order from 0
+// (the candidate-start segments over all tk values), p_j = e_j * (1/sum).
+// p.V in stages of T cached keys: a stage's values (the block's 64 dims)
+// sit in LDS row-major, the waves chain their 64 keys in turn as in
+// attention_exact, the carry passes from the last wave of a stage to the
+// first of the next, and the next stage's values load into registers
+// during the turns. The new key's value comes last, from the qkv product.
+template <int GROUP, int DPB>
+__device__ bool attention_exact_long(int t, const StepArgs& a, const LayerPtrs& L, int pos, uint32_t tag_in,
+                                     uint32_t tag_out, Smem& sm, unsigned long long deadline) {
+    const int b = blockIdx.x, kvh = a.kvh;
+    if (b >= 2 * a.heads) {  // uniform over the block
+        __builtin_amdgcn_s_waitcnt(VMCNT0);
+        return true;
+    }
+    const int g = b % kvh, hq = g * GROUP + (b / kvh) % GROUP, h2 = b / (kvh * GROUP);
+    const int tk = pos + 1;  // at most MAXT (the host's plan)
+    const int heads = a.heads;
+    const auto index = [hq, g, heads, kvh](int i) {
+        if (i < HD) return hq * HD + i;
+        if (i < 2 * HD) return (heads + g) * HD + (i - HD);
+        return (heads + kvh + g) * HD + (i - 2 * HD);
+    };
+    const _Float16* K = L.kcache + (size_t)g * a.max_pos * HD;
+    const _Float16* V = L.vcache + (size_t)g * a.max_pos * HD;
+    const int w = t / WAVE, lane = t % WAVE;
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    // Round 0's keys (the first half now, the second after the hand-over)
+    // and stage 0's values (threads below VT) load while the qkv rows arrive.
+    constexpr int VT = T - WAVE, VC = (8 * T + VT - 1) / VT, SC = 8 * T / T;  // SC: value chunks a thread, later stages
+    const int n0 = min(pos, T);  // cached keys of round / stage 0
+    uint4 kk[HD / 8];
+#pragma unroll
+    for (int i = 0; i < HD / 8; ++i) kk[i] = make_uint4(0, 0, 0, 0);
+    uint32_t touch = 0;
+    if (t < n0) {
+#pragma unroll
+        for (int i = 0; i < HD / 16; ++i) kk[i] = gload_u4(K + (size_t)t * HD + 8 * i);
+        touch = *gmem((const uint32_t*)(K + (size_t)t * HD + HD / 2));
+    }
+    uint4 vr[VC];
+#pragma unroll
+    for (int i = 0; i < VC; ++i) {
+        vr[i] = make_uint4(0, 0, 0, 0);
+        const int c = t + VT * i;
+        if (t < VT && c < 8 * n0) vr[i] = gload_u4(V + (size_t)(c / 8) * HD + 64 * h2 + 8 * (c % 8));
+    }
+    float nw0 = 1.0f, nw1 = 1.0f, sn = 0.0f, cs = 1.0f;
+    if (w <= 1) {
+        if (a.qk_norm) {
+            const TRIT_GLOBAL float* nw = gmem(w == 0 ? L.q_norm : L.k_norm);
+            nw0 = nw[lane];
+            nw1 = nw[lane + HD / 2];
+        }
+        sn = gmem(a.rope_sin)[(size_t)pos * (HD / 2) + lane];
+        cs = gmem(a.rope_cos)[(size_t)pos * (HD / 2) + lane];
+    }
+    // The last wave polls: it loads no value, and no key while round 0
+    // leaves it none.
+    const int p0 = n0 <= VT ? NW - 1 : NW - a.rq / 4 - 1;
+    STAMP(5);
+    if (!gather<8>(t, a.QKV, 3 * HD, index, tag_in, sm.qkv, sm, deadline, a.st, p0)) leave();
+    STAMP(6);
+    asm volatile("" ::"v"(touch));
+#pragma unroll
+    for (int i = 0; i < VC; ++i) {
+        const int c = t + VT * i;
+        if (t < VT && c < 8 * n0) *(uint4*)&sm.vs[c / 8][8 * (c % 8)] = vr[i];
+    }
+    if (t < n0) {
+#pragma unroll
+        for (int i = HD / 16; i < HD / 8; ++i) kk[i] = gload_u4(K + (size_t)t * HD + 8 * i);
+    }
+    // q/k norm, rotary, append: as attention_exact.
+    if (w < 3) {
+        float x0 = sm.qkv[w * HD + lane], x1 = sm.qkv[w * HD + lane + HD / 2];
+        if (w <= 1) {
+            if (a.qk_norm) {
+                float sq[16];
+#pragma unroll
+                for (int i = 0; i < 16; i += 4) {
+                    const float4 f = lane < 8 ? *(const float4*)(sm.qkv + w * HD + 16 * lane + i)
+                                              : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    sq[i] = f.x * f.x, sq[i + 1] = f.y * f.y, sq[i + 2] = f.z * f.z, sq[i + 3] = f.w * f.w;
+                }
+                const float sum = lane_chain<16>(sq, 0.0f, HD / 16);
+                const float inv = 1.0f / __builtin_sqrtf(sum / (float)HD + a.eps);
+                x0 = x0 * (inv * nw0);
+                x1 = x1 * (inv * nw1);
+            }
+            const float ac = x0 * cs, bs = x1 * sn, bc = x1 * cs, as = x0 * sn;
+            x0 = ac - bs;
+            x1 = bc + as;
+        }
+        if (w == 0) {
+            if (a.q_scale != 1.0f) {
+                x0 = x0 * a.q_scale;
+                x1 = x1 * a.q_scale;
+            }
+            const float scale = 1.0f / __builtin_sqrtf((float)HD);
+            x0 = x0 * scale;
+            x1 = x1 * scale;
+        } else {
+            const int which = w - 1;
+            const _Float16 c0 = (_Float16)x0, c1 = (_Float16)x1;
+            if (b < kvh) {
+                TRIT_GLOBAL uint16_t* cache =
+                    gmem((uint16_t*)(which == 0 ? L.kcache : L.vcache)) + ((size_t)g * a.max_pos + pos) * HD;
+                __hip_atomic_store(cache + lane, __builtin_bit_cast(uint16_t, c0), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(cache + lane + HD / 2, __builtin_bit_cast(uint16_t, c1), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
+            sm.kvn[which][lane] = (float)c0;
+            sm.kvn[which][lane + HD / 2] = (float)c1;
+            if (which == 0) {
+                sm.knew[lane] = __builtin_bit_cast(uint16_t, c0);
+                sm.knew[lane + HD / 2] = __builtin_bit_cast(uint16_t, c1);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (w == 0) {
+            sm.qkv[lane] = x0;
+            sm.qkv[lane + HD / 2] = x1;
+        }
+    }
+    __syncthreads();
+    STAMP(7);
+
+    // Scores by rounds; each thread keeps the maximum of its keys.
+    const int rounds = (tk + T - 1) / T;
+    float mx = -INFINITY;
+    for (int r = 0; r < rounds; ++r) {
+        const int j = r * T + t;
+        // The first half of the next round's key loads during this round's
+        // chain; its second half after it.
+        uint4 kn[HD / 16];
+        const bool more = r + 1 < rounds;  // uniform
+        const int jn = j + T;
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < HD / 16; ++i)
+                kn[i] = jn < pos ? gload_u4(K + (size_t)jn * HD + 8 * i) : make_uint4(0, 0, 0, 0);
+        }
+        if (j == pos) {
+#pragma unroll
+            for (int c = 0; c < HD / 8; ++c) kk[c] = *(const uint4*)&sm.knew[8 * c];
+        }
+        const float score = j < tk ? score_of(kk, sm.qkv) : -INFINITY;
+        sm.probs[j] = score;
+        mx = __builtin_fmaxf(mx, score);
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < HD / 16; ++i) kk[i] = kn[i];
+#pragma unroll
+            for (int i = HD / 16; i < HD / 8; ++i)
+                kk[i] = jn < pos ? gload_u4(K + (size_t)jn * HD + 8 * i) : make_uint4(0, 0, 0, 0);
+        }
+    }
+    const float m_w = wave_max(mx);
+    if (lane == 0) sm.wmax[w] = m_w;
+    __syncthreads();
+    mx = sm.wmax[0];
+#pragma unroll
+    for (int q = 1; q < NW; ++q) mx = __builtin_fmaxf(mx, sm.wmax[q]);
+    // Each thread rewrites its own keys: e_j, zero past the keys (the sum's
+    // segments read up to rounds T values).
+    for (int r = 0; r < rounds; ++r) {
+        const int j = r * T + t;
+        sm.probs[j] = j < tk ? exp_trit(sm.probs[j] - mx) : 0.0f;
+    }
+    __syncthreads();
+    STAMP(8);
+    const float inv = 1.0f / chain_sum_spec(t, sm.probs, tk, a.norm_window, sm);
+    STAMP(9);
+    __syncthreads();  // every wave has read the sum's values
+    for (int r = 0; r < rounds; ++r) {
+        const int j = r * T + t;
+        const float p = sm.probs[j] * inv;
+        sm.probs[j] = j < pos ? p : -0.0f;
+        if (j == pos) sm.ppos = p;
+    }
+    __syncthreads();
+
+    // p.V by stages of T cached keys.
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    typedef __attribute__((address_space(3))) s16x4 LdsS16x4;
+    const int stages = (pos + T - 1) / T;
+    if (b < kvh && (w == 1 || w == 2)) __builtin_amdgcn_s_waitcnt(VMCNT0);
+    float acc = 0.0f;
+    int last_w = 0;  // the wave that chains the last cached key
+    for (int s = 0; s < stages; ++s) {
+        const int ns = min(pos - s * T, T);  // keys of this stage
+        const int nkw = (ns + WAVE - 1) / WAVE;
+        const bool more = s + 1 < stages;  // uniform
+        // The next stage's values, into registers during this stage's turns.
+        uint4 nv[SC];
+        if (more) {
+            const int nn = min(pos - (s + 1) * T, T);
+#pragma unroll
+            for (int i = 0; i < SC; ++i) {
+                const int c = t + T * i;
+                nv[i] = c < 8 * nn ? gload_u4(V + (size_t)((s + 1) * T + c / 8) * HD + 64 * h2 + 8 * (c % 8))
+                                   : make_uint4(0, 0, 0, 0);
+            }
+        }
+        f16x4 vv[WAVE / 4];
+        f32x4 pr[WAVE / 4];
+        if (wu < nkw) {
+            const int r = lane % 16, grp = lane / 16;
+#pragma unroll
+            for (int j = 0; j < WAVE / 4; ++j) {
+                const _Float16* row = &sm.vs[WAVE * w + 4 * j + r / 4][16 * grp + 4 * (r % 4)];
+                vv[j] = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsS16x4*)row));
+            }
+            const int nvk = min(ns - WAVE * wu, WAVE);
+#pragma unroll
+            for (int i = 0; i < WAVE / 4; ++i) pr[i] = *(const f32x4*)(sm.probs + s * T + WAVE * w + 4 * i);
+            if (nvk < WAVE) {  // the stage's last wave: the slots past its last key
+#pragma unroll
+                for (int j = 0; j < WAVE / 4; ++j) {
+                    u32x2 bits = __builtin_bit_cast(u32x2, vv[j]);
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const int k = 4 * j + 2 * h;
+                        bits[h] &= (k < nvk ? 0xffffu : 0u) | (k + 1 < nvk ? 0xffff0000u : 0u);
+                    }
+                    vv[j] = __builtin_bit_cast(f16x4, bits);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < WAVE / 4; ++j) asm volatile("" : "+v"(vv[j]));
+#pragma unroll
+            for (int i = 0; i < WAVE / 4; ++i) asm volatile("" : "+v"(pr[i]));
+        }
+        for (int cw = 0; cw < min(wu, nkw); ++cw) __syncthreads();
+        if (wu < nkw) {
+            if (s > 0 || wu > 0) acc = sm.carry[lane];
+#pragma unroll
+            for (int i = 0; i < WAVE; ++i) acc = __builtin_fmaf(pr[i / 4][i & 3], (float)vv[i / 4][i & 3], acc);
+            if (wu + 1 < nkw || more) sm.carry[lane] = acc;
+        }
+        for (int cw = wu; cw < nkw; ++cw) __syncthreads();
+        last_w = nkw - 1;
+        if (more) {
+            // Every wave has read this stage's values: the next stage's go in.
+#pragma unroll
+            for (int i = 0; i < SC; ++i) {
+                const int c = t + T * i;
+                *(uint4*)&sm.vs[c / 8][8 * (c % 8)] = nv[i];
+            }
+            __syncthreads();
+        }
+    }
+    if (stages == 0) __syncthreads();  // no turns: still a barrier before the put
+    __builtin_amdgcn_s_waitcnt(VMCNT0);
+    if (wu == last_w)
+        put(a.ATT + (size_t)hq * HD + 64 * h2 + lane, __builtin_fmaf(sm.ppos, sm.kvn[1][64 * h2 + lane], acc), tag_out);
+    STAMP(10);
+    return true;
+}
+
 __device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
     if (v > bv || (v == bv && i < bi)) {
         bv = v;
@@ -1493,7 +1794,8 @@ __device__ __forceinline__ void best_of_wave(float& bv, int& bi) {
     for (int r = 1; r < 4; ++r) better(bv, bi, v[r], i[r]);
 }
 
-template <int JD, int JO, int JF, int GROUP, int DPB, bool EXACT, int WK, int HK>
+// LONG: Trit-order sessions of more than T positions (attention_exact_long).
+template <int JD, int JO, int JF, int GROUP, int DPB, bool EXACT, int WK, int HK, bool LONG = false>
 __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int pos0, uint32_t seq0, int nsteps) {
     __shared__ Smem sm;
     State* st = a.st;
@@ -1646,10 +1948,16 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         STAMP(4);
         if constexpr (DPB > 0) {
             // attention in one pass: its outputs are the o product's input.
-            const bool ok = EXACT ? attention_exact<GROUP, DPB>(t, a, L, pos, tag_of(tag0, layer, 0),
-                                                                tag_of(tag0, layer, 2), sm, deadline)
-                                  : attention_all<GROUP, DPB>(t, a, L, pos, tag_of(tag0, layer, 0),
-                                                              tag_of(tag0, layer, 2), sm, deadline);
+            bool ok;
+            if constexpr (EXACT && LONG)
+                ok = attention_exact_long<GROUP, DPB>(t, a, L, pos, tag_of(tag0, layer, 0), tag_of(tag0, layer, 2), sm,
+                                                      deadline);
+            else if constexpr (EXACT)
+                ok = attention_exact<GROUP, DPB>(t, a, L, pos, tag_of(tag0, layer, 0), tag_of(tag0, layer, 2), sm,
+                                                 deadline);
+            else
+                ok = attention_all<GROUP, DPB>(t, a, L, pos, tag_of(tag0, layer, 0), tag_of(tag0, layer, 2), sm,
+                                               deadline);
             if (!ok) leave();
             // o + residual; the o and gate_up rows stream in meanwhile, and
             // the qkv waves (nothing in flight) poll.
@@ -1786,9 +2094,12 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             for (int c = 0; c < SC; ++c) wv.sc[c] = sc[c];
         }
     };
-    Pass ring[3];
+    // Passes in flight: three, or two in the long-session instances (whose
+    // attention leaves fewer registers).
+    constexpr int RING = LONG ? 2 : 3;
+    Pass ring[RING];
 #pragma unroll
-    for (int q = 0; q < 3; ++q)
+    for (int q = 0; q < RING; ++q)
         if (q < passes) load_pass(q, ring[q]);
     float fn[(MAXD + T - 1) / T];
 #pragma unroll
@@ -1857,12 +2168,13 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             best = v;
             index = row;
         }
-        if (p + 3 < passes) load_pass(p + 3, wv);
+        if (p + RING < passes) load_pass(p + RING, wv);
     };
-    for (int p = 0; p < passes; p += 3) {
+    for (int p = 0; p < passes; p += RING) {
         head_pass(p, ring[0]);
         if (p + 1 < passes) head_pass(p + 1, ring[1]);
-        if (p + 2 < passes) head_pass(p + 2, ring[2]);
+        if constexpr (RING > 2)
+            if (p + 2 < passes) head_pass(p + 2, ring[2]);
     }
     STAMP(23);
     // The block's first maximum: the lanes of a row group agree; waves by
@@ -1941,23 +2253,33 @@ using StepFn = void (*)(StepArgs, int, int, uint32_t, int);
 // attention, 0 for the split attention and its combine.
 // wk, hk: the linears' and the head's kinds (WK_*, HK_*); the tree-sum
 // instances take Q8_0 linears and an f16 head only.
+// lng: sessions of more than T positions, instantiated for Qwen3-0.6B's
+// shape with Q8_0 linears and an f16 head, and with int8 linears and a Q8
+// head (S1-mini).
 template <int JD, int JO, int JF, int GROUP, int DPB>
-StepFn exact_fn(int wk, int hk) {
+StepFn exact_fn(int wk, int hk, bool lng) {
+    if (lng) {
+        if constexpr (JD == 4 && JO == 8 && JF == 12) {
+            if (wk == WK_Q8_0 && hk == HK_F16) return step_kernel<JD, JO, JF, GROUP, DPB, true, WK_Q8_0, HK_F16, true>;
+            if (wk == WK_INT8 && hk == HK_Q8) return step_kernel<JD, JO, JF, GROUP, DPB, true, WK_INT8, HK_Q8, true>;
+        }
+        return nullptr;
+    }
     if (wk == WK_Q8_0) return hk == HK_F16 ? step_kernel<JD, JO, JF, GROUP, DPB, true, WK_Q8_0, HK_F16>
                                            : step_kernel<JD, JO, JF, GROUP, DPB, true, WK_Q8_0, HK_Q8>;
     return hk == HK_F16 ? step_kernel<JD, JO, JF, GROUP, DPB, true, WK_INT8, HK_F16>
                         : step_kernel<JD, JO, JF, GROUP, DPB, true, WK_INT8, HK_Q8>;
 }
 
-StepFn step_fn(int jd, int jo, int jf, int group, int dpb, bool exact, int wk, int hk) {
-    if (!exact && (wk != WK_Q8_0 || hk != HK_F16)) return nullptr;
+StepFn step_fn(int jd, int jo, int jf, int group, int dpb, bool exact, int wk, int hk, bool lng = false) {
+    if (!exact && (wk != WK_Q8_0 || hk != HK_F16 || lng)) return nullptr;
     if (jd == 4 && jo == 8 && jf == 12 && group == 2) {  // Qwen3-0.6B
-        if (exact) return dpb == 8 ? exact_fn<4, 8, 12, 2, 8>(wk, hk) : nullptr;
+        if (exact) return dpb == 8 ? exact_fn<4, 8, 12, 2, 8>(wk, hk, lng) : nullptr;
         if (dpb == 0) return step_kernel<4, 8, 12, 2, 0, false, WK_Q8_0, HK_F16>;
         if (dpb == 8) return step_kernel<4, 8, 12, 2, 8, false, WK_Q8_0, HK_F16>;
     }
     if (jd == 4 && jo == 4 && jf == 8 && group == 2) {
-        if (exact) return dpb == 4 ? exact_fn<4, 4, 8, 2, 4>(wk, hk) : nullptr;
+        if (exact) return dpb == 4 ? exact_fn<4, 4, 8, 2, 4>(wk, hk, lng) : nullptr;
         if (dpb == 0) return step_kernel<4, 4, 8, 2, 0, false, WK_Q8_0, HK_F16>;
         if (dpb == 4) return step_kernel<4, 4, 8, 2, 4, false, WK_Q8_0, HK_F16>;
     }
@@ -2038,11 +2360,12 @@ bool plan(const SessionImpl& S, Plan& p) {
     p.dpb = (qd % p.blocks) ? 0 : qd / p.blocks;
     if (S.exact) {
         // Trit's sum orders: the one-pass attention with a thread per key
-        // (up to T positions), wave w output dim w of the block's DPB.
-        if (S.max_pos > T || (p.dpb != 4 && p.dpb != 8) || p.blocks % (c.kv_heads * group) ||
+        // (up to T positions), wave w output dim w of the block's DPB; the
+        // long form (keys in rounds of T) up to MAXT positions.
+        if (S.max_pos > MAXT || (p.dpb != 4 && p.dpb != 8) || p.blocks % (c.kv_heads * group) ||
             !fits(qd, NW - nqw, 8))
             return false;
-        p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group, p.dpb, true, p.wk, p.hk);
+        p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group, p.dpb, true, p.wk, p.hk, S.max_pos > T);
         if (!p.fn) return false;
         p.rh = (c.vocab + p.blocks - 1) / p.blocks;
         return true;
