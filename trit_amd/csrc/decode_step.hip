@@ -1471,10 +1471,14 @@ __device__ __forceinline__ float score_of(const uint4 (&kk)[HD / 8], const float
 #pragma unroll
     for (int part = 0; part < HD / 16; ++part) {
         if (part + 1 < HD / 16) {
+            // The next part's q loads wait for the chain's value so far: the
+            // compiler can neither gather every load of q ahead of the chain
+            // (128 registers in a loop over keys) nor sink the chain below them.
+            int off = 16 * (part + 1);
+            asm volatile("" : "+v"(off) : "v"(acc));
 #pragma unroll
-            for (int i = 0; i < 4; ++i) qn[i] = *(const float4*)(q + 16 * (part + 1) + 4 * i);
+            for (int i = 0; i < 4; ++i) qn[i] = *(const float4*)(q + off + 4 * i);
         }
-        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const uint4 kw = kk[2 * part + c];
@@ -1485,7 +1489,6 @@ __device__ __forceinline__ float score_of(const uint4 (&kk)[HD / 8], const float
             for (int u = 0; u < 8; ++u)
                 acc = __builtin_fmaf(q8[u], f16_to_f32((uint16_t)(wd[u >> 1] >> (16 * (u & 1)))), acc);
         }
-        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) qc[i] = qn[i];
     }
@@ -2094,8 +2097,8 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             for (int c = 0; c < SC; ++c) wv.sc[c] = sc[c];
         }
     };
-    // Passes in flight: three, or two in the long-session instances (whose
-    // attention leaves fewer registers).
+    // Passes in flight: three, or two in the long-session instances (their
+    // attention leaves fewer registers; three would spill).
     constexpr int RING = LONG ? 2 : 3;
     Pass ring[RING];
 #pragma unroll
@@ -2174,7 +2177,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         head_pass(p, ring[0]);
         if (p + 1 < passes) head_pass(p + 1, ring[1]);
         if constexpr (RING > 2)
-            if (p + 2 < passes) head_pass(p + 2, ring[2]);
+            if (p + 2 < passes) head_pass(p + 2, ring[2 % RING]);
     }
     STAMP(23);
     // The block's first maximum: the lanes of a row group agree; waves by
