@@ -1400,7 +1400,9 @@ void or_quantize(int isa, const float* x, int m, int k, int group, int half_scal
 }
 
 // src/cpu/gemm.rs:58-76: d = max|x|/127; codes round(x * (1/d)) half away
-// from zero from the f32 d; d stored through f16.
+// from zero from the f32 d, cast as Rust's `as i8` casts (saturating, NaN
+// to 0: a block with an infinite value has d = inf and every code 0); d
+// stored through f16.
 void or_q8_0_quantize(const float* values, int64_t count, int8_t* codes, float* scales) {
     for (int64_t b = 0; b < count / 32; ++b) {
         const float* blk = values + b * 32;
@@ -1409,9 +1411,8 @@ void or_q8_0_quantize(const float* values, int64_t count, int8_t* codes, float* 
         float d = mx / 127.0f;
         float inverse = d != 0.0f ? 1.0f / d : 0.0f;
         for (int i = 0; i < 32; ++i) {
-            float r = std::round(blk[i] * inverse);
-            r = std::fmin(127.0f, std::fmax(-128.0f, r));
-            codes[b * 32 + i] = (int8_t)r;
+            const float r = std::round(blk[i] * inverse);
+            codes[b * 32 + i] = std::isnan(r) ? 0 : (int8_t)std::fmin(127.0f, std::fmax(-128.0f, r));
         }
         scales[b] = f16r(d);
     }

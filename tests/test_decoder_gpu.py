@@ -522,6 +522,56 @@ def test_int8_linears(small):
         assert got.tolist() == want.tolist()
 
 
+def q4_k_decoder(w, cfg, seed):
+    """The same model with Q4_K super-blocks for every linear: device layers
+    from the blocks, and the oracle with the Q8_0 codes Trit requantizes
+    them to (q4_k_expand, then Blocks::quantize)."""
+    import types
+
+    d, ffn, hd = cfg["d"], cfg["ffn"], cfg["head_dim"]
+    shapes = {"qkv": ((cfg["heads"] + 2 * cfg["kv_heads"]) * hd, d), "o": (d, cfg["heads"] * hd),
+              "gate_up": (2 * ffn, d), "down": (d, ffn)}
+    layers, linears = [], []
+    for li, L in enumerate(w.layers):
+        q8 = {}
+        for which, (name, (n, k)) in enumerate(shapes.items()):
+            blocks = synth.q4_k_blocks(synth.seed_for(seed, 4 * li + which), n, k)
+            codes, scales = O.q8_0_quantize(O.q4_k_expand(blocks))
+            q8[name] = synth.q8_0_blocks(codes.reshape(n, k), scales.astype(np.float16).view(np.uint16))
+            linears.append(hip.Dense.q4_k(n, k, blocks))
+        layers.append(types.SimpleNamespace(**{**vars(L), **q8}))
+    w4 = synth.LmWeights(cfg, layers, w.embed, w.final_norm)
+    embed = hip.Dense.f16(w.embed)
+    lm = hip.CausalLm(cfg, linears, w.norms_packed(), embed)
+    for layer in linears:
+        layer.free()
+    embed.free()
+    return O.Lm(cfg, w4, O.isa_best()), O.Lm(cfg, w4, O.isa_best(), kv_f16=True), lm
+
+
+@pytest.mark.parametrize("step", ["0", "1"])
+def test_q4_k_linears(qshape, monkeypatch, step):
+    """A decoder whose linears are Q4_K blocks (Qwen3-0.6B's layer shapes):
+    EXACT and the default mode bit for bit against the oracle on Trit's
+    requantized codes, greedy tokens identical. The layers are made with
+    TRIT_HIP_Q4K=1: with the per-kernel loop (TRIT_HIP_STEP=0) every decode
+    product runs natively on the super-blocks, the RMSNorm prologue and the
+    SwiGLU pair included; the persistent step reads the requantized codes."""
+    print(f"case decoder Q4_K linears step={step}", flush=True)
+    w = qshape[0]
+    monkeypatch.setenv("TRIT_HIP_Q4K", "1")  # the layers keep their super-blocks
+    ref, ref16, lm = q4_k_decoder(w, QS, 89)
+    monkeypatch.setenv("TRIT_HIP_STEP", step)
+    p = synth.prompt(89, 24, QS["vocab"])
+    for flags, r in [(hip.EXACT, ref), (0, ref16)]:
+        want, want_logits = r.generate(p, 12)
+        s = lm.session(64, flags)
+        logits = s.prefill(p)
+        got = s.generate(12)
+        assert same_bits(logits, want_logits), (flags, rel(logits, want_logits))
+        assert got.tolist() == want.tolist(), flags
+
+
 def test_step_deadline_abort(qshape, monkeypatch):
     """A decode step that misses its deadline: forced from the host with a
     zero deadline, so that every block gives up at its first wait and the

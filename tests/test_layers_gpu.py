@@ -189,20 +189,63 @@ def test_ternary_base3(gpu):
 
 
 # The 3B layer set of the Q4_K configuration (Wqkv 3072 -> 4096, Wo 3072 ->
-# 3072, gate/up 3072 -> 16384, down 8192 -> 3072) at 1 and 4 rows, and small
-# shapes through the tiled and matrix-core kernels.
+# 3072, gate/up 3072 -> 16384, down 8192 -> 3072) at 1 to 4 rows, and small
+# shapes through the tiled and matrix-core kernels. Each layer is made with
+# TRIT_HIP_Q4K=1 (it keeps its super-blocks); each case runs the native
+# product (1..4 rows) and, with TRIT_HIP_Q4K=0 at the call, the products on
+# Trit's requantized Q8_0 codes.
 @pytest.mark.parametrize("n,k,m", [(4096, 3072, 1), (4096, 3072, 4), (3072, 3072, 1), (3072, 3072, 4),
                                    (16384, 3072, 1), (16384, 3072, 4), (3072, 8192, 1), (3072, 8192, 4),
+                                   (3072, 8192, 2), (4096, 3072, 3), (512, 256, 1), (768, 1024, 2),
                                    (256, 512, 3), (256, 512, 20)])
-def test_q4_k(gpu, n, k, m):
-    print(f"case q4_k n={n} k={k} m={m}", flush=True)
+def test_q4_k(gpu, n, k, m, monkeypatch):
     blocks = synth.q4_k_blocks(41 + n, n, k)
     vals = O.q4_k_expand(blocks)
     codes, scales = O.q8_0_quantize(vals)
     x = synth.activations(42 + m, m, k)
     ref = O.Int8(codes.reshape(n, k), scales.reshape(n, k // 32), 32, True, O.isa_best())(x)
-    got = gpu.Dense.q4_k(n, k, blocks).forward(x)
-    assert bits_equal(got, ref)
+    monkeypatch.setenv("TRIT_HIP_Q4K", "1")
+    layer = gpu.Dense.q4_k(n, k, blocks)
+    assert layer.info()["bytes"] == n * k + n * k // 32 * 2 + n * k // 256 * 144
+    for mode in ("1", "0"):
+        print(f"case q4_k n={n} k={k} m={m} native={mode}", flush=True)
+        monkeypatch.setenv("TRIT_HIP_Q4K", mode)
+        got = layer.forward(x)
+        assert bits_equal(got, ref), mode
+
+
+def same_or_both_nan(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    nan = np.isnan(a)
+    return np.array_equal(nan, np.isnan(b)) and np.array_equal(a[~nan].view(np.uint32), b[~nan].view(np.uint32))
+
+
+def test_q4_k_non_finite_blocks(gpu, monkeypatch):
+    """Super-blocks whose d or dmin is infinite or NaN: their codes follow
+    Trit's expression (Rust's `as i8`: NaN codes 0), on the native product
+    and on the requantized codes alike; the rows they reach are NaN or
+    infinite in both (NaN payloads aside)."""
+    n, k = 512, 1024
+    blocks = synth.q4_k_blocks(44, n, k).reshape(n, k // 256, 144).copy()
+    half = lambda v: np.array([v], np.float16).view(np.uint8)
+    blocks[3, 1, 0:2] = half(np.inf)          # d infinite
+    blocks[70, 2, 2:4] = half(np.nan)         # dmin NaN
+    blocks[100, 0, 0:2] = half(-np.inf)       # d -inf
+    blocks[101, 3, 0:4] = np.concatenate([half(np.inf), half(np.inf)])  # both infinite
+    blocks[200, 1, 0:2] = half(0.0)           # d 0: codes from the mins alone
+    blocks = blocks.reshape(-1)
+    vals = O.q4_k_expand(blocks)
+    codes, scales = O.q8_0_quantize(vals)
+    monkeypatch.setenv("TRIT_HIP_Q4K", "1")
+    layer = gpu.Dense.q4_k(n, k, blocks)
+    for m in (1, 3):
+        x = synth.activations(45 + m, m, k)
+        ref = O.Int8(codes.reshape(n, k), scales.reshape(n, k // 32), 32, True, O.isa_best())(x)
+        for mode in ("1", "0"):
+            print(f"case q4_k non-finite m={m} native={mode}", flush=True)
+            monkeypatch.setenv("TRIT_HIP_Q4K", mode)
+            got = layer.forward(x)
+            assert same_or_both_nan(got, ref), mode
 
 
 @pytest.mark.parametrize("n,k,m", [(4096, 1024, 1), (1000, 1024, 3), (300, 2048, 2), (77, 160, 5), (300, 384, 8),

@@ -213,6 +213,20 @@ def test_q8_0_quantize_known_answer():
     assert np.all(z == 0) and zs[0] == 0.0
 
 
+def test_q8_0_quantize_non_finite():
+    """Rust's `as i8` (gemm.rs:71) saturates and takes NaN to 0: a NaN value
+    is skipped by the peak (f32::max) and its code is 0; a block holding an
+    infinity has d = inf and 1/d = 0, so every code round(v * 0) is 0 (for
+    the infinity itself inf * 0 is NaN, hence 0 too)."""
+    v = np.zeros(32, np.float32)
+    v[:4] = [np.nan, 127.0, -63.5, 1.0]
+    codes, scales = O.q8_0_quantize(v)
+    assert scales[0] == 1.0 and codes[:4].tolist() == [0, 127, -64, 1]
+    v[0] = -np.inf
+    codes, scales = O.q8_0_quantize(v)
+    assert np.isinf(scales[0]) and np.all(codes == 0)
+
+
 def test_q4_k_known_answer():
     # d = 1, dmin = 0.5; sub-block scales 1..8 and mins 0..7 in the 6-bit packing.
     blk = np.zeros(144, np.uint8)

@@ -106,7 +106,11 @@ inline bool float_kind(int kind) { return kind == F16 || kind == F32 || kind == 
 struct Layer {
     int kind = 0, n = 0, k = 0, group = 0;
     DeviceMemory codes, scales, bias;
-    int64_t weight_bytes() const { return (int64_t)(codes.bytes + scales.bytes); }
+    // Q4_K made with TRIT_HIP_Q4K=1: the 144-byte super-blocks as stored,
+    // row-major n x k/256, for the native product (codes / scales hold
+    // Trit's Q8_0 requantization either way).
+    DeviceMemory raw;
+    int64_t weight_bytes() const { return (int64_t)(codes.bytes + scales.bytes + raw.bytes); }
 };
 
 using LayerRef = std::shared_ptr<Layer>;
@@ -170,7 +174,9 @@ void gemv_int(const Layer& L, const GemvArgs& a, hipStream_t s);
 // Scratch bytes that let gemv_int quantize m rows of k inputs once.
 size_t gemv_scratch_bytes(int m, int k);
 // Q8_0 / Q4_K / ternary products of 1..8 rows by persistent streaming
-// waves; false when the shape, the kind or the size is not one it takes.
+// waves (Q4_K of 1..4 rows from its super-blocks when L.raw holds them and
+// TRIT_HIP_Q4K allows); false when the shape, the kind or the size is not
+// one it takes.
 // Rows of more than 16384 inputs in all, and RMSNorm without the caller's
 // factors, need the quantization pass's image in a.pre.
 bool gemv_stream(const Layer& L, const GemvArgs& a, hipStream_t s);

@@ -1,5 +1,6 @@
 // The layer half of the C ABI (include/trit_hip.h): construction of the
 // device weight cache for each weight kind, and the products.
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 
@@ -137,7 +138,8 @@ __device__ void expand32(const uint8_t* __restrict__ blocks, int64_t sb, float (
 
 // Output blocks of ggml type T, each requantized as Blocks::quantize
 // (src/cpu/gemm.rs:58-76): d8 = max|y| / 127, code = round(y * (1/d8))
-// half away from zero, d8 stored as f16. One thread per 32-value block.
+// half away from zero, cast as Rust's `as i8` (saturating, NaN to 0), d8
+// stored as f16. One thread per 32-value block.
 template <int T>
 __global__ void requant_kernel(const uint8_t* __restrict__ blocks, int64_t nsub, int8_t* __restrict__ codes,
                                uint16_t* __restrict__ scales) {
@@ -150,9 +152,8 @@ __global__ void requant_kernel(const uint8_t* __restrict__ blocks, int64_t nsub,
         const float d8 = mx / 127.0f;
         const float inverse = d8 != 0.0f ? 1.0f / d8 : 0.0f;
         for (int l = 0; l < 32; ++l) {
-            float r = __builtin_roundf(y[l] * inverse);
-            r = __builtin_fminf(__builtin_fmaxf(r, -128.0f), 127.0f);
-            codes[sb * 32 + l] = (int8_t)(int)r;
+            const float r = __builtin_roundf(y[l] * inverse);
+            codes[sb * 32 + l] = r != r ? 0 : (int8_t)(int)__builtin_fminf(__builtin_fmaxf(r, -128.0f), 127.0f);
         }
         scales[sb] = f32_to_f16(d8);
     }
@@ -436,6 +437,10 @@ int ggml_layer(int n, int k, int type, const void* blocks, const float* bias, bo
         L->codes.alloc((size_t)n * k);
         L->scales.alloc((size_t)nsub * 2);
         ggml_requantize(raw.as<uint8_t>(), type, n, k, L->codes.as<int8_t>(), L->scales.as<uint16_t>(), stream());
+        // TRIT_HIP_Q4K=1: the super-blocks stay too, for the native product
+        // (measured slower than the requantized codes on MI355X, so opt-in).
+        const char* native = getenv("TRIT_HIP_Q4K");
+        if (type == 12 && native && native[0] == '1') std::swap(L->raw.ptr, raw.ptr), std::swap(L->raw.bytes, raw.bytes);
     } else {
         L->kind = Q8_F32;
         DeviceMemory codes((size_t)n * k), half((size_t)nsub * 2);
