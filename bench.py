@@ -165,6 +165,23 @@ def timed_sweeps(H, stream, layers, x, y, m, sweeps):
     return float(np.mean(durations))
 
 
+def back_to_back(H, stream, layers, x, y, m, sweeps):
+    """Average time (ms) per product when `layers` run back to back on one
+    stream with no per-launch events: one event pair around `sweeps` passes
+    (the rate of a sequence of products, launch overheads overlapped)."""
+    fwd = hip.lib().trit_hip_layer_forward_device
+    for layer in layers:
+        hip.check(fwd(layer.h, x, m, 0, y, stream))
+    a, b = H.event(), H.event()
+    H.record(a, stream)
+    for _ in range(sweeps):
+        for layer in layers:
+            hip.check(fwd(layer.h, x, m, 0, y, stream))
+    H.record(b, stream)
+    H.sync(stream)
+    return H.elapsed_ms(a, b) / (sweeps * len(layers))
+
+
 def config_lines(H, sweeps=10):
     """The per-product configurations: C1 Q8_0 GEMV, C3 ternary GEMV, C4
     Q4_K set, C5 prefill GEMM on the matrix cores."""
@@ -177,15 +194,30 @@ def config_lines(H, sweeps=10):
     def gbs(nbytes, ms):
         return round(nbytes / (ms * 1e-3) / 1e9, 1)
 
+    # The floor of one timed product: a 64 x 1024 Q8_0 product (68 KB of
+    # weights), 64 copies, by the same per-launch events -- launch, the
+    # activation and weight latencies and the store, next to no streaming.
+    codes, sbits = synth.q8_0_matrix(synth.seed_for(0, 2), 64, 1024)
+    tiny = [hip.Dense.q8_0(64, 1024, synth.q8_0_blocks(codes, sbits)) for _ in range(64)]
+    floor_ms = timed_sweeps(H, stream, tiny, xbuf, ybuf, 1, sweeps)
+    out["product_floor_q8_0_64x1024_b1"] = dict(
+        avg_us=round(floor_ms * 1e3, 3), back_to_back_us=round(back_to_back(H, stream, tiny, xbuf, ybuf, 1, sweeps) * 1e3, 3),
+        note="one launch moving 68 KB: the time any single timed product pays before its bytes")
+    del tiny
+
     # C1: Q8_0 2048 x 2048, one row; 64 copies (285 MB) rotate past the caches.
     n = k = 2048
     codes, sbits = synth.q8_0_matrix(synth.seed_for(0, 1), n, k)
     blocks = synth.q8_0_blocks(codes, sbits)
     copies = [hip.Dense.q8_0(n, k, blocks) for _ in range(64)]
     ms = timed_sweeps(H, stream, copies, xbuf, ybuf, 1, sweeps)
+    b2b = back_to_back(H, stream, copies, xbuf, ybuf, 1, sweeps)
     algo = n * k * 34 // 32 + 4 * k + 4 * n
     out["c1_q8_0_gemv_2048x2048_b1"] = dict(avg_us=round(ms * 1e3, 3), bytes=algo, gb_s=gbs(algo, ms),
-                                            frac=round(gbs(algo, ms) / HBM_PEAK_GBS, 4), copies=64)
+                                            frac=round(gbs(algo, ms) / HBM_PEAK_GBS, 4), copies=64,
+                                            back_to_back_us=round(b2b * 1e3, 3),
+                                            back_to_back_frac=round(gbs(algo, b2b) / HBM_PEAK_GBS, 4),
+                                            above_floor_us=round((ms - floor_ms) * 1e3, 3))
     del copies
 
     # C3: ternary 4096 x 4096, rows 1 and 8; 64 copies (270 MB).
@@ -194,9 +226,12 @@ def config_lines(H, sweeps=10):
     copies = [hip.Dense.ternary(tcodes, tscales) for _ in range(64)]
     for b in (1, 8):
         ms = timed_sweeps(H, stream, copies, xbuf, ybuf, b, sweeps)
+        b2b = back_to_back(H, stream, copies, xbuf, ybuf, b, sweeps)
         algo = n * k // 4 + n * 4 + b * (4 * k + 4 * n)
         out[f"c3_ternary_gemv_4096x4096_b{b}"] = dict(avg_us=round(ms * 1e3, 3), bytes=algo, gb_s=gbs(algo, ms),
-                                                      frac=round(gbs(algo, ms) / HBM_PEAK_GBS, 4), copies=64)
+                                                      frac=round(gbs(algo, ms) / HBM_PEAK_GBS, 4), copies=64,
+                                                      back_to_back_us=round(b2b * 1e3, 3),
+                                                      back_to_back_frac=round(gbs(algo, b2b) / HBM_PEAK_GBS, 4))
     del copies
 
     # C4: the Q4_K set of a 3B layer (K x N): qkv 3072 x 4096, o 3072 x 3072,
@@ -221,7 +256,11 @@ def config_lines(H, sweeps=10):
             os.environ["TRIT_HIP_Q4K"] = native
             set_ms[native] = timed_sweeps(H, stream, sets, xbuf, ybuf, b, sweeps) * len(shapes)
         ms = set_ms["0"]
+        os.environ["TRIT_HIP_Q4K"] = "0"  # back to back on the default path
+        b2b = back_to_back(H, stream, sets, xbuf, ybuf, b, sweeps) * len(shapes)
         out[f"c4_q4_k_set_b{b}"] = dict(set_us=round(ms * 1e3, 2), q4_k_bytes=q4k + io,
+                                        back_to_back_set_us=round(b2b * 1e3, 2),
+                                        back_to_back_frac=round(gbs(q4k + io, b2b) / HBM_PEAK_GBS, 4),
                                         gb_s_q4_k_bytes=gbs(q4k + io, ms),
                                         frac=round(gbs(q4k + io, ms) / HBM_PEAK_GBS, 4),
                                         device_bytes=dev + io, gb_s_device_bytes=gbs(dev + io, ms),

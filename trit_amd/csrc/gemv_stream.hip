@@ -28,6 +28,7 @@
 #include <cstdlib>
 #include <map>
 #include <mutex>
+#include <tuple>
 
 namespace trit {
 namespace {
@@ -240,10 +241,10 @@ __global__ __launch_bounds__(THREADS) void gemv_stream_kernel(const uint8_t* __r
     float* xs = (float*)(smem_raw + align16((size_t)F * k));
     int* xsum = (int*)(smem_raw + align16((size_t)F * k) + align16((size_t)F * gs * 4));
     const int lane = threadIdx.x & 63, l = lane & 15;
-    const int wave = threadIdx.x >> 6;
+    const int wave = threadIdx.x >> 6, waves = (int)blockDim.x >> 6;
     const int part_rows = n / P;
     const int quads = part_rows / 4;
-    const int gw = blockIdx.x * WAVES + wave, nw = gridDim.x * WAVES;
+    const int gw = blockIdx.x * waves + wave, nw = gridDim.x * waves;
     const int nseg = k / (W::S * 16 * W::KPC);
     const int total = gw < quads ? ((quads - 1 - gw) / nw + 1) * nseg : 0;
 
@@ -261,11 +262,11 @@ __global__ __launch_bounds__(THREADS) void gemv_stream_kernel(const uint8_t* __r
         // 2..8 rows: the image the quantization pass wrote, in this layout.
         const size_t bytes = align16((size_t)F * k) + (W::TERN ? 2 : 1) * align16((size_t)F * gs * 4);
 #pragma unroll 8
-        for (int i = threadIdx.x; i < (int)(bytes / 16); i += THREADS) ((uint4*)smem_raw)[i] = ((const uint4*)a.pre)[i];
+        for (int i = threadIdx.x; i < (int)(bytes / 16); i += (int)blockDim.x) ((uint4*)smem_raw)[i] = ((const uint4*)a.pre)[i];
     } else {
         // The rows in the block (few inputs in all): no RMSNorm, or with the
         // caller's factors.
-        quantize_rows<W>(a.x, a.norm_w, a.norm_inv, F, k, xq, xs, xsum, gs);
+        quantize_rows<W>(a.x, a.norm_w, a.norm_inv, F, k, xq, xs, xsum, gs, (int)blockDim.x);
     }
     __syncthreads();
 
@@ -296,15 +297,15 @@ size_t stream_lds(int m, int k) {
     return align16((size_t)m * k) + (W::TERN ? 2 : 1) * align16((size_t)m * dot_stride(k / W::G) * 4);
 }
 
-int resident(const void* kernel, size_t lds) {
+int resident(const void* kernel, size_t lds, int threads = THREADS) {
     static std::mutex mu;
-    static std::map<std::pair<const void*, size_t>, int> cache;
+    static std::map<std::tuple<const void*, size_t, int>, int> cache;
     std::lock_guard<std::mutex> lock(mu);
-    const auto key = std::make_pair(kernel, lds);
+    const auto key = std::make_tuple(kernel, lds, threads);
     auto it = cache.find(key);
     if (it != cache.end()) return it->second;
     int per_cu = 0, dev = 0, cus = 0;
-    TRIT_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, THREADS, lds));
+    TRIT_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds));
     TRIT_HIP(hipGetDevice(&dev));
     TRIT_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
     return cache[key] = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
@@ -316,9 +317,12 @@ void launch(const Layer& L, const GemvArgs& a, hipStream_t s) {
     auto kernel = gemv_stream_kernel<W, F, P, D>;
     const size_t lds = stream_lds<W>(F, L.k);
     const int quads = L.n / P / 4;
-    int grid = resident((const void*)kernel, lds);
-    if (grid * WAVES > quads) grid = (quads + WAVES - 1) / WAVES;
-    launch_timed(a, kernel, dim3(grid), dim3(THREADS), lds, s, L.codes.as<uint8_t>(), (const void*)L.scales.ptr,
+    // Four waves a block: measured against one and two (more blocks, each
+    // quantizing the rows itself), four is faster at every C1 / C4 shape.
+    const int waves = WAVES, threads = 64 * waves;
+    int grid = resident((const void*)kernel, lds, threads);
+    if (grid * waves > quads) grid = (quads + waves - 1) / waves;
+    launch_timed(a, kernel, dim3(grid), dim3(threads), lds, s, L.codes.as<uint8_t>(), (const void*)L.scales.ptr,
                  L.bias.as<float>(), L.n, L.k, a);
     TRIT_HIP(hipGetLastError());
 }
