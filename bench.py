@@ -488,12 +488,19 @@ def config_lines(H, sweeps=10):
                    "the persistent step (Trit's sums, f16 caches; 1565-1627 keys in rounds of 512)")
 
     cfg17 = dict(synth.QWEN3_06B, d=2048, ffn=6144)
-    out["decode_qwen3_1.7b_shape_per_kernel_loop"] = dict(
-        loop_rate(cfg17, 17), note="256-token prompt, 64 steps; the per-kernel loop (graph replay a token)")
-    out["decode_qwen3_1.7b_shape_per_kernel_loop"].pop("tokens")
+    lm17 = model.build_decoder(synth.lm_weights(cfg17, config=17))
+    out["decode_qwen3_1.7b_shape"] = dict(
+        loop_rate(cfg17, 17, lmx=lm17), note="Qwen3-1.7B's shape (d 2048, ffn 6144, 28 layers), Q8_0 linears, tied "
+                                             "f16 head; 256-token prompt, 64 greedy steps on the persistent step")
+    out["decode_qwen3_1.7b_shape"].pop("tokens")
     prev = os.environ.get("TRIT_HIP_STEP")
     os.environ["TRIT_HIP_STEP"] = "0"
     try:
+        out["decode_qwen3_1.7b_shape_per_kernel_loop"] = dict(
+            loop_rate(cfg17, 17, lmx=lm17), note="the same model on the per-kernel loop (TRIT_HIP_STEP=0; graph "
+                                                 "replay a token)")
+        out["decode_qwen3_1.7b_shape_per_kernel_loop"].pop("tokens")
+        del lm17
         out["decode_qwen3_0.6b_shape_per_kernel_loop"] = dict(
             loop_rate(dict(synth.QWEN3_06B), 1), note="the same loop on the 0.6B shape (TRIT_HIP_STEP=0)")
         out["decode_qwen3_0.6b_shape_per_kernel_loop"].pop("tokens")
@@ -614,6 +621,35 @@ def stamp_pass(w, prompt, steps, step=8, layer=10):
     embed.free()
     return dict(step=step, layer=layer, prompt=len(prompt), steps=steps, shader_mhz=round(float(np.median(rate)), 1),
                 layer_phases=rows, head_phases=head)
+
+
+def loop_pass(steps):
+    """The per-kernel decode loop (no persistent step) of the Qwen3-0.6B and
+    Qwen3-1.7B shapes: a 256-token prompt, then `steps` greedy steps, timed
+    around the steps. Meant to run with TRIT_HIP_STEP=0 (and TRIT_HIP_GRAPH=0
+    for a per-kernel profile: each kernel then launches on its own)."""
+    H = Hip()
+    out = {}
+    for name, cfg, seed in (("qwen3_0.6b", dict(synth.QWEN3_06B), 1),
+                            ("qwen3_1.7b", dict(synth.QWEN3_06B, d=2048, ffn=6144), 17)):
+        lm = model.build_decoder(synth.lm_weights(cfg, config=seed))
+        p = synth.prompt(seed, 256, cfg["vocab"])
+        s = lm.session(256 + steps + 8, 0)
+        s.prefill(p, want_logits=False)
+        s.generate(4)
+        s.reset()
+        s.prefill(p, want_logits=False)
+        a, b = H.event(), H.event()
+        toks = np.empty(steps, np.int32)
+        pers = C.c_int(0)
+        n = hip.check(hip.lib().trit_hip_session_generate_timed(s.h, steps, None, 0, toks.ctypes.data_as(C.c_void_p),
+                                                                a, b, C.byref(pers)))
+        ms = H.elapsed_ms(a, b)
+        out[name] = dict(steps=n, ms=round(ms, 3), us_per_forward=round(ms * 1e3 / max(n - 1, 1), 1),
+                         persistent=bool(pers.value))
+        print(f"[loop-pass] {name}: {out[name]}", file=sys.stderr, flush=True)
+        del s, lm
+    return out
 
 
 def cpu_configs(configs, min_s=0.3):
@@ -901,6 +937,9 @@ def main():
     ap.add_argument("--stamp-pass", action="store_true",
                     help="only the persistent step's phase stamps (needs the measurement build: "
                          "python -m trit_amd.build --stamps, then TRIT_HIP_LIBRARY=trit_amd/lib/libtrit_hip_stamps.so)")
+    ap.add_argument("--loop-pass", action="store_true",
+                    help="only the per-kernel decode loop of the 0.6B and 1.7B shapes (run it with TRIT_HIP_STEP=0 "
+                         "TRIT_HIP_GRAPH=0 under rocprofv3 --kernel-trace --stats)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="only the roofline sweeps and a 256 MiB device copy (the counter scale for "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs)")
@@ -922,6 +961,9 @@ def main():
         return
     if args.load_pass:
         print(json.dumps({"load_pass": True, **load_times(w, prompt)}), flush=True)
+        return
+    if args.loop_pass:
+        print(json.dumps({"loop_pass": True, **loop_pass(args.steps)}), flush=True)
         return
     if args.stamp_pass:
         print(json.dumps({"stamp_pass": True, **stamp_pass(w, prompt, args.steps)}), flush=True)

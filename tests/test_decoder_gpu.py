@@ -322,6 +322,42 @@ def test_step_default(qshape, monkeypatch):
     check_generate_default(w, ref16, lm, QS, monkeypatch)
 
 
+WIDE = dict(d=2048, ffn=6144, layers=2, heads=16, kv_heads=8, head_dim=128, vocab=3000, eps=1e-6, rope_base=1e6,
+            qk_norm=1)
+
+
+@pytest.fixture(scope="module")
+def wide(gpu):
+    """Qwen3-1.7B's layer shapes (d 2048, ffn 6144) with two layers: the
+    step's wide-model layout (gate_up in the last waves, the down product in
+    two rounds, the head's x from LDS)."""
+    w = synth.lm_weights(WIDE, config=97, sigma=0.1, norm_jitter=0.2)
+    return w, O.Lm(WIDE, w, O.isa_best()), model.build_decoder(w), O.Lm(WIDE, w, O.isa_best(), kv_f16=True)
+
+
+def test_step_wide(wide, monkeypatch):
+    """The persistent decode step on Qwen3-1.7B's layer shapes in the default
+    mode: Trit's sums, bit for bit, on the step."""
+    print("case decoder persistent step (qwen3 1.7b shapes, Trit's sums)", flush=True)
+    w, ref, lm, ref16 = wide
+    check_generate_default(w, ref16, lm, WIDE, monkeypatch)
+
+
+def test_step_wide_q4_k(wide, monkeypatch):
+    """The same shapes with Q4_K linears on the step (the requantized codes)."""
+    print("case decoder persistent step (qwen3 1.7b shapes, Q4_K linears)", flush=True)
+    w = wide[0]
+    ref, ref16, lm = q4_k_decoder(w, WIDE, 91)
+    p = synth.prompt(91, 30, WIDE["vocab"])
+    want, want_logits = ref16.generate(p, 16)
+    s = lm.session(64, 0)
+    logits = s.prefill(p)
+    got = s.generate(16)
+    assert s.persistent
+    assert same_bits(logits, want_logits), rel(logits, want_logits)
+    assert got.tolist() == want.tolist()
+
+
 @pytest.mark.parametrize("window", [-1, 0])
 def test_step_norm_rechained(qshape, monkeypatch, window):
     """The step's RMSNorm and softmax sums join segments chained from

@@ -49,7 +49,7 @@ constexpr int MAXC = 4;        // 32-key chunks of a split held in registers
 constexpr int MAXF = 12;       // 32-key chunks of the one-pass attention (384 positions)
 constexpr int MAXT = 4096;     // positions of a Trit-order session on the step (the long attention)
 constexpr int MAXD = 2048;     // largest d
-constexpr int MAXK = 3072;     // largest product input
+constexpr int MAXK = 6144;     // largest product input
 constexpr int PH = 6;          // exchange phases per layer
 constexpr int MAXL = 41;       // layers: the exchange tags of a step fit in 8 bits
 
@@ -172,6 +172,9 @@ struct Smem {
         // The exact attention: the cached values of the block's 64 dims,
         // row-major (key j's 64 values: 128 contiguous bytes).
         alignas(16) _Float16 vs[T][HD / 2];
+        // The head of a wide model: the normed x by lane chain, chain i at
+        // [i (d / 16 + 4)] (padded: the 16 chains' reads fall in distinct banks).
+        alignas(16) float xt[16 * (MAXD / 16 + 4)];
     };
     alignas(16) float probs[MAXT];        // the exact attention's scores, then probabilities
     float spart[NW];                      // its sum: each segment's tree sum
@@ -183,11 +186,13 @@ struct Smem {
     float gl[32][2];
     float bv[T];
     int bi[T];
+    float dcarry[4 * NW];  // a down product in two rounds: the first round's row totals
     float inv;
     int abort;
     int token;
     int stamp;  // thread 0: this layer is the stamped one
 };
+static_assert(sizeof(Smem) <= 160 * 1024, "the step's LDS fits one block a CU");
 
 __device__ __forceinline__ uint32_t tag_of(uint32_t tag0, int layer, int phase) {
     return tag0 + (uint32_t)(layer * PH + phase + 1);
@@ -335,26 +340,29 @@ struct Rows {
 };
 
 // Lane l of a row takes chunk l + 16 j: for Q8_0 the scale of its 32-block
-// (l / 2 + 8 j), for int8 that of its 128-group (l / 8 + 2 j).
-template <int J, int P, int WK, int N, int NS>
+// (l / 2 + 8 j), for int8 that of its 128-group (l / 8 + 2 j). Rows of JT
+// chunks a lane (256 JT inputs); the set takes chunks J0 .. J0 + J - 1 (a
+// product in rounds).
+template <int J, int P, int WK, int N, int NS, int JT = J, int J0 = 0>
 __device__ __forceinline__ void load_rows(int t, const uint8_t* codes, const void* scales, int part_rows, int row,
                                           Rows<N, NS>& r) {
     static_assert(P * J <= N && P * J <= NS, "the row registers hold the product");
-    constexpr int K = J * 256;
+    static_assert(J0 + J <= JT, "the round lies in the row");
+    constexpr int K = JT * 256;
     const int l = t & 15;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
         const uint8_t* src = codes + (size_t)(p * part_rows + row) * K;
 #pragma unroll
-        for (int j = 0; j < J; ++j) r.w[p * J + j] = load_stream(src + (size_t)(l + 16 * j) * 16);
+        for (int j = 0; j < J; ++j) r.w[p * J + j] = load_stream(src + (size_t)(l + 16 * (J0 + j)) * 16);
         if constexpr (WK == WK_Q8_0) {
             const TRIT_GLOBAL uint16_t* sc = gmem((const uint16_t*)scales) + (size_t)(p * part_rows + row) * (K / 32) + (l >> 1);
 #pragma unroll
-            for (int j = 0; j < J; ++j) r.ws[p * J + j] = sc[8 * j];
+            for (int j = 0; j < J; ++j) r.ws[p * J + j] = sc[8 * (J0 + j)];
         } else {
             const TRIT_GLOBAL uint32_t* sc = gmem((const uint32_t*)scales) + (size_t)(p * part_rows + row) * (K / 128) + (l >> 3);
 #pragma unroll
-            for (int j = 0; j < J; ++j) r.ws[p * J + j] = sc[2 * j];
+            for (int j = 0; j < J; ++j) r.ws[p * J + j] = sc[2 * (J0 + j)];
         }
     }
     // The rest of the set is zeroed: after any load no earlier rows stay live.
@@ -563,17 +571,22 @@ __device__ void quantize_block(int t, const float* x, const NormRegs<J>* nr, Sme
 // (src/cpu/v2/product.rs:392-423). Q8_0: a block's two lanes add their
 // dots, and the chain passes through the 8 blocks of a chunk by row_ror:2;
 // int8: a group's 8 lanes add theirs, and the chain passes the chunk's two
-// groups by row_ror:8 (ending in lanes 8..15).
-template <int J, int P, int WK, int N, int NS>
-__device__ __forceinline__ void row_chain(int t, const Rows<N, NS>& r, const Smem& sm, float (&acc)[P]) {
+// groups by row_ror:8 (ending in lanes 8..15). A round that starts at chunk
+// J0 > 0 continues the chain from `start` (the total after the chunks
+// before, in every lane of the row).
+template <int J, int P, int WK, int N, int NS, int J0 = 0>
+__device__ __forceinline__ void row_chain(int t, const Rows<N, NS>& r, const Smem& sm, float (&acc)[P],
+                                          const float* start = nullptr) {
     const int l = t & 15;
 #pragma unroll
     for (int p = 0; p < P; ++p) acc[p] = 0.0f;
+    // The first step's input: 0 at the row's start, else the carried total.
+    auto first_in = [&](int p) { return J0 == 0 ? 0.0f : start[p]; };
     if constexpr (WK == WK_INT8) {
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            const uint4 xc = *(const uint4*)(sm.xq + (l + 16 * j) * 16);
-            const float sc = sm.xs[(l >> 3) + 2 * j];
+            const uint4 xc = *(const uint4*)(sm.xq + (l + 16 * (J0 + j)) * 16);
+            const float sc = sm.xs[(l >> 3) + 2 * (J0 + j)];
             float df[P], prod[P];
 #pragma unroll
             for (int p = 0; p < P; ++p) {
@@ -592,7 +605,7 @@ __device__ __forceinline__ void row_chain(int t, const Rows<N, NS>& r, const Sme
             for (int q = 0; q < 2; ++q)
 #pragma unroll
                 for (int p = 0; p < P; ++p) {
-                    const float in = (j == 0 && q == 0) ? 0.0f : dpp<DPP_ROR8>(acc[p]);
+                    const float in = (j == 0 && q == 0) ? first_in(p) : dpp<DPP_ROR8>(acc[p]);
                     acc[p] = __builtin_fmaf(df[p], prod[p], in);
                 }
         }
@@ -602,8 +615,8 @@ __device__ __forceinline__ void row_chain(int t, const Rows<N, NS>& r, const Sme
     for (int j = 0; j < J; ++j) {
         // Chunk j's dots (the block's two halves meet by DPP), then the
         // chain's steps over blocks 8j .. 8j + 7.
-        const uint4 xc = *(const uint4*)(sm.xq + (l + 16 * j) * 16);
-        const float sc = sm.xs[(l >> 1) + 8 * j];
+        const uint4 xc = *(const uint4*)(sm.xq + (l + 16 * (J0 + j)) * 16);
+        const float sc = sm.xs[(l >> 1) + 8 * (J0 + j)];
         float df[P], prod[P];
 #pragma unroll
         for (int p = 0; p < P; ++p) {
@@ -620,7 +633,7 @@ __device__ __forceinline__ void row_chain(int t, const Rows<N, NS>& r, const Sme
         for (int q = 0; q < 8; ++q)
 #pragma unroll
             for (int p = 0; p < P; ++p) {
-                const float in = (j == 0 && q == 0) ? 0.0f : dpp<DPP_ROR2>(acc[p]);
+                const float in = (j == 0 && q == 0) ? first_in(p) : dpp<DPP_ROR2>(acc[p]);
                 acc[p] = __builtin_fmaf(df[p], prod[p], in);
             }
     }
@@ -1810,15 +1823,29 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     __syncthreads();
 
     // Waves by product, four rows a wave: gate_up [0, nu), o [nu, nu + no),
-    // down [nu, nu + nd), qkv [NW - nqw, NW). Each product's rows load one
+    // down [nu, nu + DR nd), qkv [NW - nqw, NW). Each product's rows load one
     // phase ahead of it (o during the combine's wait, gate_up during o's,
     // down and the next layer's qkv during down's); a wave holds one
-    // product's rows at a time, so all share one register set.
+    // product's rows at a time, so all share one register set. Where those
+    // ranges do not fit in the waves (wide MLPs), gate_up moves to the last
+    // nu waves and o / down to the first: gate_up's rows then load during
+    // the attention in waves that also poll for its outputs (every wave has
+    // loads in flight there), and no two sets live at once in one wave.
+    // A down product of more than 16 chunks a lane (ffn > 4096) runs in DR =
+    // 2 rounds of JF / 2 chunks, held by two sets of nd waves and chained
+    // one after the other (the first round's totals pass through LDS).
+    constexpr int DR = JF > 16 ? 2 : 1, JFR = JF / DR;
+    static_assert(JF % DR == 0, "down rounds of whole chunks");
     const int nu = a.rgu / 4, no = a.ro / 4, nd = a.rd / 4, nqw = a.rq / 4;
+    const bool packed = nu + cmax(no, DR * nd) + nqw <= NW;
+    const int u0 = packed ? 0 : NW - nu, od0 = packed ? nu : 0;
     // The one row register set (see Rows); the first layer's qkv rows
     // stream in during the choice.
-    constexpr int RN = cmax(cmax(2 * JD, JO), JF);
+    constexpr int RN = cmax(cmax(2 * JD, JO), JFR);
     constexpr int RS = RN;
+    // Words a lane of a gather takes for a product input of up to
+    // max(JF, 12) chunks.
+    constexpr int MWK = cmax(JF, 12) * 256 / T;
     const Linear lin;
 
     // Token steps: step it forwards the token chosen from step it - 1's
@@ -1833,7 +1860,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     // product, a lane's rows) is computed within that part, rather than
     // hoisted out of the loops and held in registers through the others
     // (the head needs them).
-    int t, w, lane, rowq, rowo, rowgu, rowd;
+    int t, w, lane, rowq, rowo, rowgu, rowd, dround;
     bool aq, agu, ao, ad;
     auto fresh = [&] {
         t = threadIdx.x;
@@ -1842,13 +1869,14 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         w = t / WAVE;
         lane = t % WAVE;
         aq = w >= NW - nqw;
-        agu = w < nu;
-        ao = w >= nu && w < nu + no;
-        ad = w >= nu && w < nu + nd;
+        agu = w >= u0 && w < u0 + nu;
+        ao = w >= od0 && w < od0 + no;
+        ad = w >= od0 && w < od0 + DR * nd;
+        dround = ad ? (w - od0) / nd : 0;
         rowq = b * a.rq + 4 * (w - (NW - nqw)) + (lane >> 4);
-        rowo = b * a.ro + 4 * (w - nu) + (lane >> 4);
-        rowgu = b * a.rgu + 4 * w + (lane >> 4);
-        rowd = b * a.rd + 4 * (w - nu) + (lane >> 4);
+        rowo = b * a.ro + 4 * (w - od0) + (lane >> 4);
+        rowgu = b * a.rgu + 4 * (w - u0) + (lane >> 4);
+        rowd = b * a.rd + 4 * ((w - od0) % nd) + (lane >> 4);
     };
     fresh();
 
@@ -2018,7 +2046,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         load_norm<JD>(t, L.norm_mlp, ngu);
         if (a.ffn_scales) load_norm<JD>(t, a.ffn_scales + (size_t)layer * a.d, nfs);
         __syncthreads();
-        if (!gather<MAXK / T>(t, a.X, a.d, lin, tag_of(tag0, layer, 3), sm.xres, sm, deadline, st)) leave();
+        if (!gather<MWK>(t, a.X, a.d, lin, tag_of(tag0, layer, 3), sm.xres, sm, deadline, st)) leave();
         STAMP(14);
         if constexpr (EXACT) {
             const float inv = norm_inv_spec<JD>(t, sm.xres, a.eps, a.norm_window, sm);
@@ -2038,21 +2066,40 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         }
         STAMP(17);
         // down + residual.
-        if (ad)
-            load_rows<JF, 1, WK>(t, L.codes[3], L.scales[3], 0, rowd, rr);
+        if (ad && dround == 0)
+            load_rows<JFR, 1, WK, RN, RS, JF, 0>(t, L.codes[3], L.scales[3], 0, rowd, rr);
+        else if (DR > 1 && ad)
+            load_rows<JFR, 1, WK, RN, RS, JF, (DR > 1 ? JFR : 0)>(t, L.codes[3], L.scales[3], 0, rowd, rr);
         else
             zero_rows(rr);
         if (aq && layer + 1 < a.n_layers)
             load_rows<JD, 1, WK>(t, sm.layers[layer + 1].codes[0], sm.layers[layer + 1].scales[0], 0, rowq, rr);
         __syncthreads();
-        if (!gather<MAXK / T>(t, a.H, a.ffn, lin, tag_of(tag0, layer, 4), sm.xin, sm, deadline, st)) leave();
+        if (!gather<MWK>(t, a.H, a.ffn, lin, tag_of(tag0, layer, 4), sm.xin, sm, deadline, st)) leave();
         STAMP(18);
         quantize_block<JF, WK>(t, sm.xin, (const NormRegs<JF>*)nullptr, sm);
         STAMP(19);
-        if (ad) {
-            float acc[1];
-            row_chain<JF, 1, WK>(t, rr, sm, acc);
-            if ((lane & 15) == 14) put(a.X + rowd, sm.xres[rowd] + a.rm * acc[0], tag_of(tag0, layer, 5));
+        if constexpr (DR == 1) {
+            if (ad) {
+                float acc[1];
+                row_chain<JF, 1, WK>(t, rr, sm, acc);
+                if ((lane & 15) == 14) put(a.X + rowd, sm.xres[rowd] + a.rm * acc[0], tag_of(tag0, layer, 5));
+            }
+        } else {
+            // The first round's waves chain inputs [0, 256 JFR) and leave each
+            // row's total in LDS; the second round's continue from it.
+            if (ad && dround == 0) {
+                float acc[1];
+                row_chain<JFR, 1, WK>(t, rr, sm, acc);
+                if ((lane & 15) == 14) sm.dcarry[rowd - b * a.rd] = acc[0];
+            }
+            __syncthreads();
+            if (ad && dround == 1) {
+                float acc[1];
+                const float start[1] = {sm.dcarry[rowd - b * a.rd]};
+                row_chain<JFR, 1, WK, RN, RS, JFR>(t, rr, sm, acc, start);
+                if ((lane & 15) == 14) put(a.X + rowd, sm.xres[rowd] + a.rm * acc[0], tag_of(tag0, layer, 5));
+            }
         }
         __syncthreads();
         STAMP(20);
@@ -2098,8 +2145,14 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         }
     };
     // Passes in flight: three, or two in the long-session instances (their
-    // attention leaves fewer registers; three would spill).
-    constexpr int RING = LONG ? 2 : 3;
+    // attention leaves fewer registers; three would spill), one for d > 1024
+    // (a pass of 2048 f16 weights a row is 64 registers; the chip then has
+    // 32 MB of head rows in flight, past HBM's bandwidth-latency product).
+    constexpr int RING = LONG ? 2 : JD > 4 ? 1 : 3;
+    // The normed x of the lane's chain: in registers up to d = 1024, else
+    // read from LDS (sm.xt) as the chain goes.
+    constexpr bool XLDS = JD > 4;
+    constexpr int XS = JD * 16 + 4;
     Pass ring[RING];
 #pragma unroll
     for (int q = 0; q < RING; ++q)
@@ -2124,9 +2177,31 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         if (t + T * q < a.d) sm.xin[t + T * q] = sm.xres[t + T * q] * (sm.inv * fn[q]);
     __syncthreads();
     STAMP(22);
-    float xr[JD * 16];  // lane chain l16 of the normed x
+    float xr[XLDS ? 1 : JD * 16];  // lane chain l16 of the normed x
+    if constexpr (XLDS) {
+        for (int kk = t; kk < a.d; kk += T) sm.xt[(kk & 15) * XS + (kk >> 4)] = sm.xin[kk];
+        __syncthreads();
+    } else {
 #pragma unroll
-    for (int s = 0; s < JD * 16; ++s) xr[s] = sm.xin[16 * s + l16];
+        for (int s = 0; s < JD * 16; ++s) xr[s] = sm.xin[16 * s + l16];
+    }
+    // Values s0 .. s0 + N - 1 of the lane's chain.
+    auto chain_x = [&](int s0, auto& out) {
+        constexpr int N = sizeof(out) / sizeof(float);
+        if constexpr (XLDS) {
+#pragma unroll
+            for (int q = 0; q < N; q += 4) {
+                const float4 v = *(const float4*)(sm.xt + l16 * XS + s0 + q);
+                out[q] = v.x;
+                out[q + 1] = v.y;
+                out[q + 2] = v.z;
+                out[q + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < N; ++q) out[q] = xr[s0 + q];
+        }
+    };
     float best = -INFINITY;
     int index = INT_MAX;
     auto head_pass = [&](int p, Pass& wv) {
@@ -2138,12 +2213,16 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         for (int j = 0; j < SU; ++j) {
             const uint32_t words[4] = {wv.w[j].x, wv.w[j].y, wv.w[j].z, wv.w[j].w};
             if constexpr (HK == HK_F16) {
+                float xx[8];
+                chain_x(j * 8, xx);
 #pragma unroll
                 for (int hh = 0; hh < 8; ++hh) {
                     const float wf = f16_to_f32((uint16_t)(words[hh >> 1] >> ((hh & 1) * 16)));
-                    acc = __builtin_fmaf(xr[j * 8 + hh], wf, acc);
+                    acc = __builtin_fmaf(xx[hh], wf, acc);
                 }
             } else {
+                float xx[16];
+                chain_x(16 * j, xx);
 #pragma unroll
                 for (int u = 0; u < 16; u += 2) {
                     const int g = 8 * j + u / 2;  // the group of steps 16 j + u, + u + 1
@@ -2152,7 +2231,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
                     for (int e = 0; e < 2; ++e) {
                         const int h = u + e;
                         const float wf = (float)(int8_t)(uint8_t)(words[h >> 2] >> ((h & 3) * 8)) * scale;
-                        acc = __builtin_fmaf(xr[16 * j + h], wf, acc);
+                        acc = __builtin_fmaf(xx[h], wf, acc);
                     }
                 }
             }
@@ -2175,7 +2254,8 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     };
     for (int p = 0; p < passes; p += RING) {
         head_pass(p, ring[0]);
-        if (p + 1 < passes) head_pass(p + 1, ring[1]);
+        if constexpr (RING > 1)
+            if (p + 1 < passes) head_pass(p + 1, ring[1 % RING]);
         if constexpr (RING > 2)
             if (p + 2 < passes) head_pass(p + 2, ring[2 % RING]);
     }
@@ -2286,6 +2366,10 @@ StepFn step_fn(int jd, int jo, int jf, int group, int dpb, bool exact, int wk, i
         if (dpb == 0) return step_kernel<4, 4, 8, 2, 0, false, WK_Q8_0, HK_F16>;
         if (dpb == 4) return step_kernel<4, 4, 8, 2, 4, false, WK_Q8_0, HK_F16>;
     }
+    // Qwen3-1.7B (d 2048, ffn 6144): Trit's orders, Q8_0 / Q4_K linears, an
+    // f16 table, sessions of up to T positions.
+    if (jd == 8 && jo == 8 && jf == 24 && group == 2 && exact && dpb == 8 && !lng && wk == WK_Q8_0 && hk == HK_F16)
+        return step_kernel<8, 8, 24, 2, 8, true, WK_Q8_0, HK_F16>;
     return nullptr;
 }
 
@@ -2349,12 +2433,19 @@ bool plan(const SessionImpl& S, Plan& p) {
     };
     if (!rows(nq, p.rq) || !rows(c.d, p.ro) || !rows(c.ffn, p.rgu) || !rows(c.d, p.rd)) return false;
     // The kernel's wave ranges by product (disjoint where rows are live
-    // together) and the waves each gather polls with.
+    // together; the kernel derives the same layout) and the waves each
+    // gather polls with. A down product of more than 16 chunks a lane runs
+    // in two rounds on two sets of waves.
     const int nu = p.rgu / 4, no = p.ro / 4, nd = p.rd / 4, nqw = p.rq / 4;
-    if (nu + std::max(no, nd) + nqw > NW) return false;
+    const int dr = c.ffn / 256 > 16 ? 2 : 1;
+    const bool packed = nu + std::max(no, dr * nd) + nqw <= NW;
+    // Otherwise gate_up takes the last waves (the one-pass Trit-order
+    // attention only): gate_up beside o, down beside qkv.
+    if (!packed && (!S.exact || nu + no > NW || dr * nd + nqw > NW)) return false;
     auto fits = [](int n, int p0, int mw) { return p0 + (n + WAVE * mw - 1) / (WAVE * mw) <= NW; };
     if (!fits((group + 2) * HD, NW - nqw - 1, 8)) return false;
-    if (!fits(c.d, 0, 6) || !fits(c.ffn, 0, MAXK / T)) return false;
+    const int mwk = std::max(c.ffn / 256, 12) * 256 / T;  // the kernel's MWK
+    if (!fits(c.d, 0, 6) || !fits(c.ffn, 0, mwk) || !fits(c.d, 0, mwk)) return false;
     if (!fits(2 * p.blocks, 0, MAXD / T)) return false;  // the candidates' words
     p.splits = p.blocks / c.kv_heads;
     p.comb = qd / p.blocks;
