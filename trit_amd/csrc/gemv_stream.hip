@@ -700,22 +700,7 @@ void qk_launch(const Layer& L, const GemvArgs& a, const QkShape& sh, hipStream_t
     auto kernel = gemv_q4k_kernel<F, P, I>;
     const size_t lds = qk_lds(F, L.k, sh.R * P);
     const int threads = sh.waves * 64, tiles = L.n / P / sh.R;
-    static std::mutex mu;
-    static std::map<std::pair<size_t, int>, int> cache;  // resident blocks by (LDS, threads)
-    int grid;
-    {
-        std::lock_guard<std::mutex> lock(mu);
-        const auto key = std::make_pair(lds, threads);
-        auto it = cache.find(key);
-        if (it == cache.end()) {
-            int per_cu = 0, dev = 0, cus = 0;
-            TRIT_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds));
-            TRIT_HIP(hipGetDevice(&dev));
-            TRIT_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-            it = cache.emplace(key, (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1)).first;
-        }
-        grid = std::min(it->second, tiles);
-    }
+    const int grid = std::min(resident((const void*)kernel, lds, threads), tiles);
     launch_timed(a, kernel, dim3(grid), dim3(threads), lds, s, L.raw.as<uint8_t>(), L.bias.as<float>(), L.n, L.k,
                  sh.R, a);
     TRIT_HIP(hipGetLastError());
