@@ -182,9 +182,10 @@ def back_to_back(H, stream, layers, x, y, m, sweeps):
     return H.elapsed_ms(a, b) / (sweeps * len(layers))
 
 
-def config_lines(H, sweeps=10):
+def config_lines(H, sweeps=10, decode=True):
     """The per-product configurations: C1 Q8_0 GEMV, C3 ternary GEMV, C4
-    Q4_K set, C5 prefill GEMM on the matrix cores."""
+    Q4_K set, C5 prefill GEMM on the matrix cores; then (decode) the decode
+    loops of the other workloads."""
     stream = H.stream()
     out = {}
     xbuf = H.malloc(1564 * 8192 * 4)
@@ -431,13 +432,12 @@ def config_lines(H, sweeps=10):
         layer_ms=round(t5 * 1e3, 3), rows_per_s=round(m / t5, 1), attention_ops=att_ops,
         note="one layer over 1564 rows, wall clock of the prefill call (host synchronisation included)")
     del sess, lm5
+    if not decode:
+        return out
 
-    # Decoders the persistent step does not take (it holds d <= 2048 and an
-    # MLP of at most 3072) run the per-kernel loop, one graph replay a
-    # token: Qwen3-1.7B's shape (d 2048, MLP 6144, 28 layers, 16/8 heads x
-    # 128, vocab 151936, Q8_0 linears, tied f16 head), a 256-token prompt
-    # and 64 greedy steps, in Trit's sum orders with f16 caches; and the
-    # 0.6B shape on the same loop (TRIT_HIP_STEP=0) beside it.
+    # The decode loops: a greedy run timed by events around the generate
+    # call (the persistent step where the model fits it, else the per-kernel
+    # loop, one graph replay a token), in Trit's sum orders with f16 caches.
     def loop_rate(cfg, seed, steps=64, prompt_len=256, lmx=None, kinds=("q8_0", "f16")):
         lmx = lmx or model.build_decoder(synth.lm_weights(cfg, config=seed))
         px = synth.prompt(seed, prompt_len, cfg["vocab"])
@@ -517,10 +517,10 @@ def step_roofline(cfg, prompt, steps, step_ms, persistent, mode, linears="q8_0",
     step of a generate call) timed with HIP events around it. Algorithmic
     bytes per forward: every linear weight once (Q8_0: 34 B per 32; int8:
     132 B per 128), the head (f16: 2 B a value; int8 storage: 36 B per 32),
-    the f16 keys and values of the positions attended (the average over the
-    timed tokens), the embedding row and the norm weights; one launch holds
-    steps - 1 forwards. The per-kernel fallback is one graph replay a
-    step."""
+    the keys and values of the positions attended (f16, or f32 in the exact
+    mode; the average over the timed tokens), the embedding row and the norm
+    weights; one launch holds steps - 1 forwards. The per-kernel fallback is
+    one graph replay a step."""
     d, ffn, hd, L = cfg["d"], cfg["ffn"], cfg["head_dim"], cfg["layers"]
     qkv = (cfg["heads"] + 2 * cfg["kv_heads"]) * hd
     num, den = (34, 32) if linears == "q8_0" else (132, 128)
@@ -530,7 +530,7 @@ def step_roofline(cfg, prompt, steps, step_ms, persistent, mode, linears="q8_0",
     # prompt + i + 1 keys; the last step only makes the final choice.
     forwards = steps - 1
     mean_keys = prompt + (forwards - 1) / 2.0 + 1
-    kv = int(L * cfg["kv_heads"] * hd * 2 * 2 * mean_keys)
+    kv = int(L * cfg["kv_heads"] * hd * 2 * (4 if mode == "exact" else 2) * mean_keys)
     small = (d * 2 if table == "f16" else d * 36 // 32) + L * (2 * d + 2 * hd) * 4 + d * 4
     per_forward = weights + head + kv + small
     launches = 1 if persistent else steps
@@ -539,15 +539,18 @@ def step_roofline(cfg, prompt, steps, step_ms, persistent, mode, linears="q8_0",
     achieved = per_launch / (avg_ms * 1e-3) / 1e9
     return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                 frac=round(achieved / HBM_PEAK_GBS, 4),
-                traffic=STEP_TRAFFIC_BYTES * forwards if persistent else None,
+                traffic=STEP_TRAFFIC_BYTES * forwards if persistent and mode == "default" else None,
                 kernel=(f"step_kernel<4,8,12,2,8,{'false' if mode == 'tree' else 'true'},"
-                        f"{0 if linears == 'q8_0' else 1},{0 if table == 'f16' else 1}>: the persistent decode "
-                        f"step ({'tree sums' if mode == 'tree' else 'Trit sum orders'}, one-pass attention), {steps} "
+                        f"{0 if linears == 'q8_0' else 1},{0 if table == 'f16' else 1},false,"
+                        f"{'true' if mode == 'exact' else 'false'}>: the persistent decode step "
+                        f"({'tree sums' if mode == 'tree' else 'Trit sum orders'}, one-pass attention, "
+                        f"{'f32' if mode == 'exact' else 'f16'} keys and values), {steps} "
                         "steps (choice, 28 layers, head) in one launch") if persistent
                        else "the per-kernel decode step (graph replay)",
                 bytes_per_launch=per_launch, bytes_per_forward=per_forward, forwards=forwards,
                 avg_us=round(avg_ms * 1e3, 3), us_per_forward=round(step_ms * 1e3 / forwards, 3),
-                traffic_per_forward=STEP_TRAFFIC_BYTES if persistent else None, launches=launches,
+                traffic_per_forward=STEP_TRAFFIC_BYTES if persistent and mode == "default" else None,
+                launches=launches,
                 timing="HIP events recorded on the library's stream before and after the step launch "
                        "(trit_hip_session_generate_timed); the launch includes the final choice-only step")
 
@@ -916,6 +919,33 @@ def cpu_baseline(w, prompt, steps, rounds):
                 rounds=rounds, threads=threads, isa={0: "scalar", 1: "avx2", 2: "avx512-vnni"}[isa])
 
 
+def timed_mode(lm, prompt, steps, warmup, flags, H):
+    """The same workload in another session mode (a session of its own):
+    warm-up runs, then the prompt and one timed generate call, timed as the
+    headline line is."""
+    sess = lm.session(len(prompt) + steps, flags)
+    for _ in range(warmup):
+        sess.reset()
+        sess.prefill(prompt, want_logits=False)
+        sess.generate(steps)
+    sess.reset()
+    sess.prefill(prompt, want_logits=False)
+    ev_a, ev_b = H.event(), H.event()
+    out_tokens = np.empty(steps, np.int32)
+    persistent = C.c_int(0)
+    t0 = time.perf_counter()
+    n = hip.check(hip.lib().trit_hip_session_generate_timed(sess.h, steps, None, 0,
+                                                            out_tokens.ctypes.data_as(C.c_void_p), ev_a, ev_b,
+                                                            C.byref(persistent)))
+    t = time.perf_counter() - t0
+    step_ms = H.elapsed_ms(ev_a, ev_b)
+    sess.free()
+    forwards = max(n - 1, 1)
+    return dict(value=round(forwards / t, 2), ms_per_step=round(t / forwards * 1e3, 4), step_ms=step_ms,
+                persistent=bool(persistent.value), tokens=[int(x) for x in out_tokens[:n]],
+                kv_cache="f32", sums="trit order (bit-exact: Trit's own arithmetic)")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -937,6 +967,9 @@ def main():
     ap.add_argument("--stamp-pass", action="store_true",
                     help="only the persistent step's phase stamps (needs the measurement build: "
                          "python -m trit_amd.build --stamps, then TRIT_HIP_LIBRARY=trit_amd/lib/libtrit_hip_stamps.so)")
+    ap.add_argument("--products-pass", action="store_true",
+                    help="only the per-product configurations (C1, C3, C4, C5 and the others before the decode "
+                         "loops): no persistent-step launch, for rocprofv3")
     ap.add_argument("--loop-pass", action="store_true",
                     help="only the per-kernel decode loop of the 0.6B and 1.7B shapes (run it with TRIT_HIP_STEP=0 "
                          "TRIT_HIP_GRAPH=0 under rocprofv3 --kernel-trace --stats)")
@@ -961,6 +994,10 @@ def main():
         return
     if args.load_pass:
         print(json.dumps({"load_pass": True, **load_times(w, prompt)}), flush=True)
+        return
+    if args.products_pass:
+        print(json.dumps({"products_pass": True, "configs": config_lines(Hip(), sweeps=args.sweeps, decode=False)}),
+              flush=True)
         return
     if args.loop_pass:
         print(json.dumps({"loop_pass": True, **loop_pass(args.steps)}), flush=True)
@@ -1011,6 +1048,13 @@ def main():
     print(f"[bench] gpu decode {value:.1f} tok/s (device {forwards / step_ms * 1e3:.1f}), "
           f"prefill {args.prompt / t_prefill:.1f} tok/s", file=sys.stderr, flush=True)
     step_roof = step_roofline(cfg, args.prompt, args.steps, step_ms, bool(persistent.value), args.mode)
+    exact = None
+    if args.mode == "default":
+        print("[bench] exact mode (f32 keys and values) ...", file=sys.stderr, flush=True)
+        exact = timed_mode(lm, prompt, args.steps, args.warmup, hip.EXACT, H)
+        exact["roofline"] = step_roofline(cfg, args.prompt, args.steps, exact.pop("step_ms"), exact["persistent"],
+                                          "exact")
+        print(f"[bench] exact mode {exact['value']} tok/s", file=sys.stderr, flush=True)
 
     print("[bench] roofline sweep ...", file=sys.stderr, flush=True)
     roof = gemv_roofline(H, linears, cfg, args.sweeps)
@@ -1054,6 +1098,9 @@ def main():
         if fair:
             out["cpu_baseline"]["fairness"] = fair
         out["tokens_identical"] = [int(t) for t in tokens] == cb["tokens"]
+        if exact:
+            exact["tokens_identical"] = exact.pop("tokens") == cb["tokens"]
+            exact["gpu_vs_cpu"] = round(exact["value"] / cpu_value, 2)
         out["gpu_vs_cpu"] = round(value / cpu_value, 2)
         # The workload's weights settle on one repeated token, so the check
         # above cannot see a wrong step; the same model with livelier weights
@@ -1064,6 +1111,9 @@ def main():
         if configs:
             print("[bench] cpu configurations ...", file=sys.stderr, flush=True)
             cpu_configs(configs)
+    if exact:
+        exact.pop("tokens", None)
+        out["exact_mode"] = exact
     if configs:
         for line in configs.values():
             line.pop("tokens", None)

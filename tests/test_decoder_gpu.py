@@ -358,6 +358,42 @@ def test_step_wide_q4_k(wide, monkeypatch):
     assert got.tolist() == want.tolist()
 
 
+@pytest.mark.parametrize("flags,prompt,steps,max_pos,persistent",
+                         [(hip.EXACT, 40, 24, 96, True), (hip.KV_F32, 40, 24, 96, True),
+                          (hip.EXACT, 440, 60, 512, True), (hip.EXACT, 500, 12, 700, False)])
+def test_step_f32_caches(qshape, monkeypatch, flags, prompt, steps, max_pos, persistent):
+    """Trit's f32 keys and values on the persistent step (EXACT, or KV_F32
+    with Trit's orders), up to 512 positions; past that the per-kernel loop.
+    Logits and greedy tokens bit for bit the oracle's, the per-kernel loop's
+    tokens, and the caches the steps wrote (one more token through the
+    prompt path gives the oracle's logits bit for bit)."""
+    print(f"case decoder step, f32 caches (flags {flags}, prompt {prompt}, {steps} steps, {max_pos} positions)",
+          flush=True)
+    w, ref, lm, _ = qshape
+    p = synth.prompt(99, prompt, QS["vocab"])
+    s = lm.session(max_pos, flags)
+    logits = s.prefill(p)
+    got = s.generate(steps)
+    assert s.persistent == persistent
+    assert len(got) == steps and s.position == prompt + steps - 1
+    ref.reset()
+    assert same_bits(logits, ref.forward(p))
+    check_tokens(got, ref, p, steps)
+    if persistent and max_pos <= 96:
+        monkeypatch.setenv("TRIT_HIP_STEP", "0")
+        k = lm.session(max_pos, flags)
+        k.prefill(p)
+        kern = k.generate(steps)
+        assert not k.persistent
+        monkeypatch.delenv("TRIT_HIP_STEP")
+        assert got.tolist() == kern.tolist()
+    nxt = np.array([int(got[-1])])
+    after = s.prefill(nxt)
+    ref.reset()
+    ref.forward(np.concatenate([p, got[:-1]]))
+    assert same_bits(after, ref.forward(nxt))
+
+
 @pytest.mark.parametrize("window", [-1, 0])
 def test_step_norm_rechained(qshape, monkeypatch, window):
     """The step's RMSNorm and softmax sums join segments chained from

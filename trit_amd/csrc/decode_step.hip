@@ -106,7 +106,9 @@ struct LayerPtrs {
     const float* norm_mlp;
     const float* q_norm;
     const float* k_norm;
-    _Float16* kcache;  // [kv head][position][HD]
+    // [kv head][position][HD], f16 -- or f32 in the f32-cache instance,
+    // whose attention reads them as float (attention_exact32).
+    _Float16* kcache;
     _Float16* vcache;
 };
 
@@ -1169,12 +1171,13 @@ __device__ float chain_sum_spec(int t, const float* v, int n, int window, Smem& 
 // line of the head's n_keys keys and values, from `threads` threads, NT
 // words a thread. The words stay in registers until the caller consumes
 // them (a load whose value is dropped is not made).
-template <int NT>
+// ESZ: bytes of a cached value (2: f16, 4: f32).
+template <int NT, int ESZ = 2>
 __device__ __forceinline__ void touch_kv(int t, int threads, const LayerPtrs& L, int g, int r, int nb, int n_keys,
                                          int max_pos, uint32_t (&v)[NT]) {
-    const uint8_t* kb = (const uint8_t*)(L.kcache + (size_t)g * max_pos * HD);
-    const uint8_t* vb = (const uint8_t*)(L.vcache + (size_t)g * max_pos * HD);
-    constexpr int LINE = 128, PER_KEY = HD * 2 / LINE;
+    const uint8_t* kb = (const uint8_t*)L.kcache + (size_t)g * max_pos * HD * ESZ;
+    const uint8_t* vb = (const uint8_t*)L.vcache + (size_t)g * max_pos * HD * ESZ;
+    constexpr int LINE = 128, PER_KEY = HD * ESZ / LINE;
     const int lines = PER_KEY * n_keys;
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
@@ -1508,6 +1511,209 @@ __device__ __forceinline__ float score_of(const uint4 (&kk)[HD / 8], const float
     return acc;
 }
 
+// attention_exact with Trit's own f32 keys and values (TRIT_HIP_EXACT,
+// TRIT_HIP_KV_F32): the same blocks, phases and orders, the keys and values
+// as f32 (each appended value as computed, no f16 rounding). Thread t scores
+// key t in two halves of 64 dims: the first half loads while the qkv rows
+// arrive, the second right after them, under the q/k norms. For p.V, wave w
+// loads the values of keys [64 w, 64 w + 64), lane d its dim 64 h2 + d, from
+// the cache (its lines came to this XCD's L2 with the layer's touches) into
+// registers while the softmax sum runs, and chains them in its turn as
+// attention_exact does. Sessions of up to T positions.
+template <int GROUP, int DPB>
+__device__ bool attention_exact32(int t, const StepArgs& a, const LayerPtrs& L, int pos, uint32_t tag_in,
+                                  uint32_t tag_out, Smem& sm, unsigned long long deadline) {
+    const int b = blockIdx.x, kvh = a.kvh;
+    if (b >= 2 * a.heads) {  // uniform over the block
+        __builtin_amdgcn_s_waitcnt(VMCNT0);
+        return true;
+    }
+    const int g = b % kvh, hq = g * GROUP + (b / kvh) % GROUP, h2 = b / (kvh * GROUP);
+    const int tk = pos + 1;  // at most T (the host's plan)
+    const int heads = a.heads;
+    const auto index = [hq, g, heads, kvh](int i) {
+        if (i < HD) return hq * HD + i;
+        if (i < 2 * HD) return (heads + g) * HD + (i - HD);
+        return (heads + kvh + g) * HD + (i - 2 * HD);
+    };
+    const float* K = (const float*)L.kcache + (size_t)g * a.max_pos * HD;
+    const float* V = (const float*)L.vcache + (size_t)g * a.max_pos * HD;
+    const int w = t / WAVE, lane = t % WAVE;
+    // Key t's first 64 dims (16 units of 4), and one word of each line of its
+    // second half: those lines come to the caches now.
+    uint4 kk[HD / 8];
+#pragma unroll
+    for (int i = 0; i < HD / 8; ++i) kk[i] = make_uint4(0, 0, 0, 0);
+    uint32_t touch0 = 0, touch1 = 0;
+    if (t < pos) {
+#pragma unroll
+        for (int i = 0; i < HD / 8; ++i) kk[i] = gload_u4(K + (size_t)t * HD + 4 * i);
+        touch0 = *gmem((const uint32_t*)(K + (size_t)t * HD + HD / 2));
+        touch1 = *gmem((const uint32_t*)(K + (size_t)t * HD + 3 * HD / 4));
+    }
+    float nw0 = 1.0f, nw1 = 1.0f, sn = 0.0f, cs = 1.0f;
+    if (w <= 1) {
+        if (a.qk_norm) {
+            const TRIT_GLOBAL float* nw = gmem(w == 0 ? L.q_norm : L.k_norm);
+            nw0 = nw[lane];
+            nw1 = nw[lane + HD / 2];
+        }
+        sn = gmem(a.rope_sin)[(size_t)pos * (HD / 2) + lane];
+        cs = gmem(a.rope_cos)[(size_t)pos * (HD / 2) + lane];
+    }
+    const int p0 = pos <= T - WAVE ? NW - 1 : NW - a.rq / 4 - 1;
+    STAMP(5);
+    if (!gather<8>(t, a.QKV, 3 * HD, index, tag_in, sm.qkv, sm, deadline, a.st, p0)) leave();
+    STAMP(6);
+    asm volatile("" ::"v"(touch0), "v"(touch1));
+
+    // Qwen3's per-head RMSNorm and the rotary halves, as attention_exact;
+    // the new key and value appended as f32.
+    if (w < 3) {
+        float x0 = sm.qkv[w * HD + lane], x1 = sm.qkv[w * HD + lane + HD / 2];
+        if (w <= 1) {
+            if (a.qk_norm) {
+                float sq[16];
+#pragma unroll
+                for (int i = 0; i < 16; i += 4) {
+                    const float4 f = lane < 8 ? *(const float4*)(sm.qkv + w * HD + 16 * lane + i)
+                                              : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    sq[i] = f.x * f.x, sq[i + 1] = f.y * f.y, sq[i + 2] = f.z * f.z, sq[i + 3] = f.w * f.w;
+                }
+                const float sum = lane_chain<16>(sq, 0.0f, HD / 16);
+                const float inv = 1.0f / __builtin_sqrtf(sum / (float)HD + a.eps);
+                x0 = x0 * (inv * nw0);
+                x1 = x1 * (inv * nw1);
+            }
+            const float ac = x0 * cs, bs = x1 * sn, bc = x1 * cs, as = x0 * sn;
+            x0 = ac - bs;
+            x1 = bc + as;
+        }
+        if (w == 0) {
+            if (a.q_scale != 1.0f) {
+                x0 = x0 * a.q_scale;
+                x1 = x1 * a.q_scale;
+            }
+            const float scale = 1.0f / __builtin_sqrtf((float)HD);
+            x0 = x0 * scale;
+            x1 = x1 * scale;
+        } else {
+            const int which = w - 1;
+            if (b < kvh) {
+                TRIT_GLOBAL uint32_t* cache =
+                    gmem((uint32_t*)(which == 0 ? L.kcache : L.vcache)) + ((size_t)g * a.max_pos + pos) * HD;
+                __hip_atomic_store(cache + lane, __float_as_uint(x0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(cache + lane + HD / 2, __float_as_uint(x1), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
+            sm.kvn[which][lane] = x0;
+            sm.kvn[which][lane + HD / 2] = x1;
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (w == 0) {
+            sm.qkv[lane] = x0;
+            sm.qkv[lane + HD / 2] = x1;
+        }
+    }
+    __syncthreads();
+    STAMP(7);
+    uint4 kh[HD / 8];
+#pragma unroll
+    for (int i = 0; i < HD / 8; ++i) kh[i] = make_uint4(0, 0, 0, 0);
+    if (t < pos) {
+#pragma unroll
+        for (int i = 0; i < HD / 8; ++i) kh[i] = gload_u4(K + (size_t)t * HD + HD / 2 + 4 * i);
+    }
+
+    // Scores: thread t key t, the fused chain over the dims in order (the
+    // new key from LDS).
+    if (t == pos) {
+#pragma unroll
+        for (int c = 0; c < HD / 8; ++c) {
+            kk[c] = *(const uint4*)&sm.kvn[0][4 * c];
+            kh[c] = *(const uint4*)&sm.kvn[0][HD / 2 + 4 * c];
+        }
+    }
+    float score = -INFINITY;
+    if (t < tk) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+#pragma unroll
+            for (int part = 0; part < HD / 32; ++part) {
+                // q dims 64 half + 16 part .. + 15, in four loads
+                const int q0 = HD / 2 * half + 16 * part;
+                float4 qc[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) qc[i] = *(const float4*)(sm.qkv + q0 + 4 * i);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint4 kw = half == 0 ? kk[4 * part + i] : kh[4 * part + i];
+                    acc = __builtin_fmaf(qc[i].x, __uint_as_float(kw.x), acc);
+                    acc = __builtin_fmaf(qc[i].y, __uint_as_float(kw.y), acc);
+                    acc = __builtin_fmaf(qc[i].z, __uint_as_float(kw.z), acc);
+                    acc = __builtin_fmaf(qc[i].w, __uint_as_float(kw.w), acc);
+                }
+            }
+        }
+        score = acc;
+    }
+    // The values for p.V: wave w keys [64 w, 64 w + 64) before pos, lane d
+    // the block's dim 64 h2 + d (256 contiguous bytes a key across the
+    // wave), zero past the last cached key.
+    const int nkw = (pos + WAVE - 1) / WAVE;
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    const float m_w = wave_max(score);
+    if (lane == 0) sm.wmax[w] = m_w;
+    float vf[WAVE];
+    if (wu < nkw) {
+        const float* vcol = V + 64 * h2 + lane;
+#pragma unroll
+        for (int i = 0; i < WAVE; ++i) {
+            const int j = WAVE * wu + i;
+            vf[i] = j < pos ? *gmem(vcol + (size_t)j * HD) : 0.0f;
+        }
+    }
+    __syncthreads();
+    float mx = sm.wmax[0];
+#pragma unroll
+    for (int q = 1; q < NW; ++q) mx = __builtin_fmaxf(mx, sm.wmax[q]);
+    const float e = t < tk ? exp_trit(score - mx) : 0.0f;
+    sm.probs[t] = e;
+    __syncthreads();
+    STAMP(8);
+    const float p = e * (1.0f / chain_sum_spec(t, sm.probs, tk, a.norm_window, sm));
+    STAMP(9);
+    sm.probs[t] = t < pos ? p : -0.0f;
+    if (t == pos) sm.ppos = p;
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    f32x4 pr[WAVE / 4];
+    if (wu < nkw) {
+#pragma unroll
+        for (int i = 0; i < WAVE / 4; ++i) pr[i] = *(const f32x4*)(sm.probs + WAVE * w + 4 * i);
+#pragma unroll
+        for (int i = 0; i < WAVE; ++i) asm volatile("" : "+v"(vf[i]));
+#pragma unroll
+        for (int i = 0; i < WAVE / 4; ++i) asm volatile("" : "+v"(pr[i]));
+    }
+    if (b < kvh && (w == 1 || w == 2)) __builtin_amdgcn_s_waitcnt(VMCNT0);
+    if (nkw == 0) __syncthreads();
+    float acc = 0.0f;
+    for (int cw = 0; cw < min(wu, nkw); ++cw) __syncthreads();
+    if (wu < nkw) {
+        if (wu > 0) acc = sm.carry[lane];
+#pragma unroll
+        for (int i = 0; i < WAVE; ++i) acc = __builtin_fmaf(pr[i / 4][i & 3], vf[i], acc);
+        if (wu + 1 < nkw) sm.carry[lane] = acc;
+    }
+    for (int cw = wu; cw < nkw; ++cw) __syncthreads();
+    __builtin_amdgcn_s_waitcnt(VMCNT0);
+    if (wu == (nkw > 0 ? nkw - 1 : 0))
+        put(a.ATT + (size_t)hq * HD + 64 * h2 + lane, __builtin_fmaf(sm.ppos, sm.kvn[1][64 * h2 + lane], acc), tag_out);
+    STAMP(10);
+    return true;
+}
+
 // attention_exact for sessions of up to MAXT positions: the same orders and
 // bits, over the keys in rounds of T. Scores: round r, thread t scores key
 // r T + t into sm.probs (the next round's keys load meanwhile); the maximum
@@ -1811,8 +2017,11 @@ __device__ __forceinline__ void best_of_wave(float& bv, int& bi) {
 }
 
 // LONG: Trit-order sessions of more than T positions (attention_exact_long).
-template <int JD, int JO, int JF, int GROUP, int DPB, bool EXACT, int WK, int HK, bool LONG = false>
+// KV32: Trit's own f32 keys and values (attention_exact32; T positions).
+template <int JD, int JO, int JF, int GROUP, int DPB, bool EXACT, int WK, int HK, bool LONG = false,
+          bool KV32 = false>
 __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int pos0, uint32_t seq0, int nsteps) {
+    static_assert(!KV32 || (EXACT && !LONG && DPB > 0), "f32 caches: the one-pass Trit-order attention");
     __shared__ Smem sm;
     State* st = a.st;
     if (st->done) return;
@@ -1980,7 +2189,10 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         if constexpr (DPB > 0) {
             // attention in one pass: its outputs are the o product's input.
             bool ok;
-            if constexpr (EXACT && LONG)
+            if constexpr (KV32)
+                ok = attention_exact32<GROUP, DPB>(t, a, L, pos, tag_of(tag0, layer, 0), tag_of(tag0, layer, 2), sm,
+                                                   deadline);
+            else if constexpr (EXACT && LONG)
                 ok = attention_exact_long<GROUP, DPB>(t, a, L, pos, tag_of(tag0, layer, 0), tag_of(tag0, layer, 2), sm,
                                                       deadline);
             else if constexpr (EXACT)
@@ -2002,8 +2214,8 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             if (EXACT && b < 2 * a.heads && w < NW - nqw) {
                 const bool last = layer + 1 == a.n_layers;
                 const int kvh = a.kvh;
-                touch_kv(t, (NW - nqw) * WAVE, sm.layers[last ? 0 : layer + 1], b % kvh, b / kvh, 2 * a.heads / kvh,
-                         last ? pos + 1 : pos, a.max_pos, kvt);
+                touch_kv<4, KV32 ? 4 : 2>(t, (NW - nqw) * WAVE, sm.layers[last ? 0 : layer + 1], b % kvh, b / kvh,
+                                          2 * a.heads / kvh, last ? pos + 1 : pos, a.max_pos, kvt);
             }
             __syncthreads();
             if (!gather<8>(t, a.ATT, a.qd, lin, tag_of(tag0, layer, 2), sm.xin, sm, deadline, st, NW - nqw))
@@ -2354,8 +2566,17 @@ StepFn exact_fn(int wk, int hk, bool lng) {
                         : step_kernel<JD, JO, JF, GROUP, DPB, true, WK_INT8, HK_Q8>;
 }
 
-StepFn step_fn(int jd, int jo, int jf, int group, int dpb, bool exact, int wk, int hk, bool lng = false) {
+StepFn step_fn(int jd, int jo, int jf, int group, int dpb, bool exact, int wk, int hk, bool lng = false,
+               bool kv32 = false) {
     if (!exact && (wk != WK_Q8_0 || hk != HK_F16 || lng)) return nullptr;
+    if (kv32) {
+        // Trit's f32 caches: Qwen3-0.6B's shape, Q8_0 / Q4_K linears, an f16
+        // table, Trit's orders, up to T positions.
+        if (jd == 4 && jo == 8 && jf == 12 && group == 2 && exact && dpb == 8 && !lng && wk == WK_Q8_0 &&
+            hk == HK_F16)
+            return step_kernel<4, 8, 12, 2, 8, true, WK_Q8_0, HK_F16, false, true>;
+        return nullptr;
+    }
     if (jd == 4 && jo == 8 && jf == 12 && group == 2) {  // Qwen3-0.6B
         if (exact) return dpb == 8 ? exact_fn<4, 8, 12, 2, 8>(wk, hk, lng) : nullptr;
         if (dpb == 0) return step_kernel<4, 8, 12, 2, 0, false, WK_Q8_0, HK_F16>;
@@ -2396,7 +2617,8 @@ bool split_forced() {
 bool plan(const SessionImpl& S, Plan& p) {
     const DecoderImpl& D = *S.dec;
     const auto& c = D.c;
-    if (S.kv32) return false;
+    // f32 caches: the Trit-order instance of up to T positions only.
+    if (S.kv32 && (!S.exact || S.max_pos > T)) return false;
     // Granite's multipliers, per-layer MLP scales and added input rows run
     // on the Trit-order instance only.
     if ((D.granite() || D.has_ffn_scales || S.additive_rows) && !S.exact) return false;
@@ -2459,7 +2681,7 @@ bool plan(const SessionImpl& S, Plan& p) {
         if (S.max_pos > MAXT || (p.dpb != 4 && p.dpb != 8) || p.blocks % (c.kv_heads * group) ||
             !fits(qd, NW - nqw, 8))
             return false;
-        p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group, p.dpb, true, p.wk, p.hk, S.max_pos > T);
+        p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group, p.dpb, true, p.wk, p.hk, S.max_pos > T, S.kv32);
         if (!p.fn) return false;
         p.rh = (c.vocab + p.blocks - 1) / p.blocks;
         return true;
@@ -2510,8 +2732,10 @@ void decode_step_prepare(SessionImpl& S, hipStream_t s) {
             table[l].norm_mlp = D.norm_mlp(l);
             table[l].q_norm = D.q_norm(l);
             table[l].k_norm = D.k_norm(l);
-            table[l].kcache = S.kcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * HD;
-            table[l].vcache = S.vcache.as<_Float16>() + (size_t)l * c.kv_heads * S.max_pos * HD;
+            // A layer's caches in bytes: f16 values, or f32 (S.kv32).
+            const size_t layer_bytes = (size_t)c.kv_heads * S.max_pos * HD * (S.kv32 ? 4 : 2);
+            table[l].kcache = (_Float16*)(S.kcache.as<uint8_t>() + (size_t)l * layer_bytes);
+            table[l].vcache = (_Float16*)(S.vcache.as<uint8_t>() + (size_t)l * layer_bytes);
         }
         const Layer& head = D.head ? *D.head : *D.embed;
         std::call_once(D.step_head_once, [&] {
