@@ -427,6 +427,35 @@ __device__ __forceinline__ float lane_chain(const float (&v)[N], float c0, int l
     return carry;
 }
 
+// The serial chain ((c + p_0) + p_1) + ... over n4 float4 of LDS that
+// every lane of the wave reads alike (broadcast reads), with D reads in
+// flight: each read's result is used D reads after it issues, so the adds
+// do not wait on the LDS latency between reads.
+template <int D>
+__device__ __forceinline__ float lds_chain(float c, const float* p, int n4) {
+    float4 buf[D];
+#pragma unroll
+    for (int j = 0; j < D; ++j)
+        if (j < n4) buf[j] = ((const float4*)p)[j];
+    for (int i = 0; i < n4; i += D) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+            if (i + j < n4) {
+                const float4 v = buf[j];
+                if (i + j + D < n4) buf[j] = ((const float4*)p)[i + j + D];
+                // The refill issues before these adds (the scheduler would
+                // otherwise sink it next to its use).
+                __builtin_amdgcn_sched_barrier(0);
+                c = c + v.x;
+                c = c + v.y;
+                c = c + v.z;
+                c = c + v.w;
+            }
+        }
+    }
+    return c;
+}
+
 // RMSNorm factor of x (K = 256 J values in LDS) with Trit's sum -- the
 // squares added one after another from 0 (src/layers.rs:138-139) -- bit
 // for bit, by all the waves at once. Wave w chains segment w (values
@@ -473,15 +502,7 @@ __device__ float norm_inv_spec(int t, const float* x, float eps, int window, Sme
 #pragma unroll
     for (int q = 1; q < NW; ++q)
         if (w == q) c = cand(q);
-    const float* seg_p = sq + S * w;
-#pragma unroll
-    for (int i = 0; i < S; i += 4) {
-        const float4 v = *(const float4*)(seg_p + i);
-        c = c + v.x;
-        c = c + v.y;
-        c = c + v.z;
-        c = c + v.w;
-    }
+    c = lds_chain<8>(c, sq + S * w, S / 4);
     sm.ns.res[w][lane] = c;
     __syncthreads();
     float r[NW];
