@@ -266,8 +266,10 @@ int trit_hip_session_generate(TritHipSession *session, int max_new, const int32_
  * library's stream right before the first step launch and right after the
  * last, so their interval is the device time of the steps. *persistent (may
  * be NULL) tells whether the steps ran as the persistent decode step (one
- * kernel launch for all the call's tokens) or as the per-kernel loop. The
- * counterpart of
+ * kernel launch for all the call's tokens: nonzero, bit 0 set) or as the
+ * per-kernel loop (0); on the step, bit 1 is set when the attention runs
+ * on every block, the q/k/v rows and scores of each key/value head passing
+ * through the L2 of the XCD that attends to it. The counterpart of
  * Trit's decode timing (src/cpu/v2/bench.rs:42-54). */
 int trit_hip_session_generate_timed(TritHipSession *session, int max_new, const int32_t *stop, int n_stop,
                                     int32_t *out, void *start_event, void *stop_event, int *persistent);

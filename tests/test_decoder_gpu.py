@@ -226,17 +226,21 @@ def test_generate_long_prompt(small, flags):
         assert got.tolist() == want.tolist()
 
 
-def check_generate_default(w, ref16, lm, cfg, monkeypatch):
+def check_generate_default(w, ref16, lm, cfg, monkeypatch, layout=None):
     """Default-mode greedy tokens (Trit's sums, f16 caches) on the persistent
     step: logits and tokens bit for bit the f16-cache oracle's and the
     per-kernel loop's, positions, a stop token, a second generate call that
     continues the first, and the caches the steps wrote (one more token
-    through the prompt path gives the oracle's logits bit for bit)."""
+    through the prompt path gives the oracle's logits bit for bit). layout:
+    the step's layout flags the session must report (3: the attention on
+    every block, each key/value head's exchanges in one XCD's L2)."""
     p = synth.prompt(98, 40, cfg["vocab"])
     s = lm.session(96, 0)
     logits = s.prefill(p)
     got = s.generate(24)
     assert s.persistent
+    if layout is not None:
+        assert s.step_layout == layout, s.step_layout
     assert len(got) == 24
     assert s.position == 40 + 23
     ref16.reset()
@@ -316,10 +320,21 @@ def check_generate_tree(w, ref16, lm, cfg, monkeypatch, persistent):
 
 def test_step_default(qshape, monkeypatch):
     """The persistent decode step on Qwen3-0.6B's layer shapes in the
-    default mode: Trit's sums, bit for bit."""
+    default mode: Trit's sums, bit for bit, with the attention on every
+    block (8 key/value heads: one an XCD)."""
     print("case decoder persistent step (qwen3 shapes, Trit's sums)", flush=True)
     w, ref, lm, ref16 = qshape
-    check_generate_default(w, ref16, lm, QS, monkeypatch)
+    check_generate_default(w, ref16, lm, QS, monkeypatch, layout=3)
+
+
+def test_step_default_two_blocks_a_head(qshape, monkeypatch):
+    """The same with TRIT_HIP_STEP_LOCAL=0: the attention on two blocks a
+    query head and every exchange at agent scope (the layout of models
+    without one key/value head an XCD), bit for bit."""
+    print("case decoder persistent step (qwen3 shapes, two blocks a head)", flush=True)
+    w, ref, lm, ref16 = qshape
+    monkeypatch.setenv("TRIT_HIP_STEP_LOCAL", "0")
+    check_generate_default(w, ref16, lm, QS, monkeypatch, layout=1)
 
 
 WIDE = dict(d=2048, ffn=6144, layers=2, heads=16, kv_heads=8, head_dim=128, vocab=3000, eps=1e-6, rope_base=1e6,
@@ -340,7 +355,7 @@ def test_step_wide(wide, monkeypatch):
     mode: Trit's sums, bit for bit, on the step."""
     print("case decoder persistent step (qwen3 1.7b shapes, Trit's sums)", flush=True)
     w, ref, lm, ref16 = wide
-    check_generate_default(w, ref16, lm, WIDE, monkeypatch)
+    check_generate_default(w, ref16, lm, WIDE, monkeypatch, layout=3)
 
 
 def test_step_wide_q4_k(wide, monkeypatch):
@@ -496,7 +511,7 @@ def test_mid_step_default(mid, monkeypatch):
     """Four KV heads: four dims of one query head a block, Trit's sums."""
     print("case decoder mid persistent step (Trit's sums)", flush=True)
     w, ref, lm, ref16 = mid
-    check_generate_default(w, ref16, lm, MID, monkeypatch)
+    check_generate_default(w, ref16, lm, MID, monkeypatch, layout=1)
 
 
 @pytest.mark.parametrize("attention", ["one-pass", "split"])

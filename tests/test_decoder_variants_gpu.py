@@ -203,7 +203,9 @@ def test_generate_additive(qshape, flags):
     s.reset()
     s.prefill(p)
     g = s.generate(10)
-    assert s.persistent == (flags == 0)
+    # Both modes decode on the step: 48 positions, within the f32-cache
+    # instance's 512.
+    assert s.persistent
     r.reset()
     assert g.tolist() == greedy(r, r.forward(p), 10)
     s.free()

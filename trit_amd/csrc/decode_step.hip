@@ -36,7 +36,9 @@
 #include "decoder_impl.h"
 #include "device.h"
 
+#include <algorithm>
 #include <climits>
+#include <cstdio>
 #include <type_traits>
 
 namespace trit {
@@ -52,6 +54,8 @@ constexpr int MAXD = 2048;     // largest d
 constexpr int MAXK = 6144;     // largest product input
 constexpr int PH = 6;          // exchange phases per layer
 constexpr int MAXL = 41;       // layers: the exchange tags of a step fit in 8 bits
+constexpr int BPH = 16;        // the wide attention: blocks a query head
+constexpr int WD = HD / BPH;   // its output dims a block
 
 constexpr int cmax(int x, int y) { return x > y ? x : y; }
 
@@ -78,11 +82,21 @@ __device__ unsigned long long g_stamp_clk[MAX_STAMP_BLOCKS][NSTAMP];
             g_stamp_clk[blockIdx.x][k] = __builtin_readcyclecounter();      \
         }                                                                   \
     } while (0)
+#define STAMP_BY(k, thr)                                                    \
+    do {                                                                    \
+        if ((int)threadIdx.x == (thr) && sm.stamp) {                        \
+            g_stamp_wall[blockIdx.x][k] = wall_clock64();                   \
+            g_stamp_clk[blockIdx.x][k] = __builtin_readcyclecounter();      \
+        }                                                                   \
+    } while (0)
 #define STAMP_WHEN(cond)                         \
     do {                                         \
         if (threadIdx.x == 0) sm.stamp = (cond); \
     } while (0)
 #else
+#define STAMP_BY(k, thr) \
+    do {                 \
+    } while (0)
 #define STAMP(k) \
     do {         \
     } while (0)
@@ -130,6 +144,7 @@ struct StepArgs {
     uint64_t* ATT;   // heads * HD words
     uint64_t* H;     // ffn words
     uint64_t* CAND;  // 2 words per block: its best logit and that row's index
+    uint64_t* SC;    // the wide attention's scores: T words a query head
     float2* cand;    // per block: best logit, its index (int bits)
     int* out;
     State* st;
@@ -150,6 +165,15 @@ struct StepArgs {
     const float* additive;
     int additive_rows;
     int stamp_step, stamp_layer;  // the stamped (step, layer); layer == n_layers: the head
+    // Nonzero: the q/k/v rows of key/value head x are made by the blocks on
+    // XCD x, the attention of head x runs on them (attention_wide_a/_b),
+    // and the qkv rows and the scores pass through that XCD's L2
+    // (put_local). Set by the host where the model and the device allow it
+    // (the Trit-order instance of up to T positions, one key/value head an
+    // XCD). xcd_count: NX counters, zero at the launch, that give each
+    // block its rank on its XCD.
+    int local_qkv;
+    unsigned int* xcd_count;
 };
 
 struct Smem {
@@ -177,6 +201,10 @@ struct Smem {
         // The head of a wide model: the normed x by lane chain, chain i at
         // [i (d / 16 + 4)] (padded: the 16 chains' reads fall in distinct banks).
         alignas(16) float xt[16 * (MAXD / 16 + 4)];
+        // The wide attention: the cached values of the block's WD dims (f16
+        // bits), dim-major (row d: the T keys, padded so that the lanes'
+        // reads of a row fall in distinct banks).
+        alignas(16) uint16_t vth[WD][T + 8];
     };
     alignas(16) float probs[MAXT];        // the exact attention's scores, then probabilities
     float spart[NW];                      // its sum: each segment's tree sum
@@ -193,6 +221,7 @@ struct Smem {
     int abort;
     int token;
     int stamp;  // thread 0: this layer is the stamped one
+    int xcd, xrank;  // with local_qkv: the block's XCD and its rank there
 };
 static_assert(sizeof(Smem) <= 160 * 1024, "the step's LDS fits one block a CU");
 
@@ -206,6 +235,26 @@ __device__ __forceinline__ void put(uint64_t* p, float v, uint32_t tag) {
 
 __device__ __forceinline__ uint64_t peek(const uint64_t* p) {
     return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// XCDs of the device. The dispatcher deals workgroups to the XCDs in turn,
+// but not always from XCD 0, so a block learns its XCD from the hardware
+// and its rank there from a counter (the step's launch start).
+constexpr int NX = 8;
+__device__ __forceinline__ int xcc_id() {
+    return __builtin_amdgcn_s_getreg((3 << 11) | 20) & 0xf;  // HW_REG_XCC_ID, bits 3:0
+}
+
+// An exchange word for readers on the writer's XCD only: a store without
+// scope bits goes through the CU's write-through L1 into the XCD's L2 and
+// stays there; an agent-scope load (peek) from a CU of the same XCD
+// returns that line (about 0.13 us from store to sight on MI355X, against
+// 0.5-0.6 us for an agent-scope store, which writes through to memory).
+// Readers on other XCDs would not see it until the line leaves the L2, so
+// a word written with put_local is read on its writer's XCD only, and no
+// other XCD writes its 128-byte line in the same launch.
+__device__ __forceinline__ void put_local(uint64_t* p, float v, uint32_t tag) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
 }
 
 // Reductions over a wave: DPP inside each row of 16 lanes (every lane gets
@@ -1532,6 +1581,234 @@ __device__ __forceinline__ float score_of(const uint4 (&kk)[HD / 8], const float
     return acc;
 }
 
+// Attention in Trit's order on every block, for models with one key/value
+// head per XCD (StepArgs::local_qkv): XCD x's 32 blocks take head g = x,
+// BPH blocks a query head -- the block of rank r there query head
+// g GROUP + r / BPH, slot s = r % BPH. Everything a head exchanges stays in
+// that XCD's L2, and each block reads a slice of the cache instead of all
+// of it (the attention of one block per head half was bound by what one CU
+// can read: the keys and values of a head, 100-150 KB).
+//   part a: the q/k/v rows (local exchange), Qwen3's q/k norms and the
+//   rotary, the append; slot s scores keys [s kn, s kn + kn), kn =
+//   ceil(tk / BPH), one thread a key, each score the fused chain over the
+//   128 dims in order (as attention_exact), and puts them (local exchange,
+//   tag_sc).
+//   part b: every block of the head gathers the tk scores, takes their
+//   maximum, e_j = exp(s_j - max), their sum in key order from 0, p_j =
+//   e_j * (1/sum) -- the same bits in every block -- and chains p_j v_j
+//   over the keys in order for its WD dims [WD s, WD s + WD), the new key
+//   last; the outputs are the o product's input.
+// The block's values load before the qkv rows arrive (thread j key j, 16
+// bytes), and go to LDS as f32 by dim. Sessions of up to T positions.
+template <int GROUP>
+__device__ bool attention_wide_a(int t, const StepArgs& a, const LayerPtrs& L, int pos, uint32_t tag_in,
+                                 uint32_t tag_sc, Smem& sm, unsigned long long deadline) {
+    static_assert(WD == 8, "a block's value dims are one 16-byte load of f16");
+    const int r = sm.xrank, g = sm.xcd;
+    const int hq = g * GROUP + r / BPH, s = r % BPH;
+    const int tk = pos + 1, kn = (tk + BPH - 1) / BPH, j0 = s * kn;
+    const int heads = a.heads, kvh = a.kvh;
+    const auto index = [hq, g, heads, kvh](int i) {
+        if (i < HD) return hq * HD + i;
+        if (i < 2 * HD) return (heads + g) * HD + (i - HD);
+        return (heads + kvh + g) * HD + (i - 2 * HD);
+    };
+    const _Float16* K = L.kcache + (size_t)g * a.max_pos * HD;
+    const _Float16* V = L.vcache + (size_t)g * a.max_pos * HD;
+    const int w = t / WAVE, lane = t % WAVE;
+    // The slot's keys: thread t (t < kn) key j0 + t, all 128 dims.
+    uint4 kk[HD / 8];
+#pragma unroll
+    for (int i = 0; i < HD / 8; ++i) kk[i] = make_uint4(0, 0, 0, 0);
+    const int jk = j0 + t;
+    if (t < kn && jk < pos) {
+#pragma unroll
+        for (int i = 0; i < HD / 8; ++i) kk[i] = gload_u4(K + (size_t)jk * HD + 8 * i);
+    }
+    // The block's value dims of key t.
+    uint4 vr = make_uint4(0, 0, 0, 0);
+    if (t < pos) vr = gload_u4(V + (size_t)t * HD + WD * s);
+    float nw0 = 1.0f, nw1 = 1.0f, sn = 0.0f, cs = 1.0f;
+    if (w <= 1) {
+        if (a.qk_norm) {
+            const TRIT_GLOBAL float* nw = gmem(w == 0 ? L.q_norm : L.k_norm);
+            nw0 = nw[lane];
+            nw1 = nw[lane + HD / 2];
+        }
+        sn = gmem(a.rope_sin)[(size_t)pos * (HD / 2) + lane];
+        cs = gmem(a.rope_cos)[(size_t)pos * (HD / 2) + lane];
+    }
+    // Polled by the last wave: its threads load a value only past 448
+    // positions, and no key.
+    STAMP(5);
+    if (!gather<8>(t, a.QKV, 3 * HD, index, tag_in, sm.qkv, sm, deadline, a.st, NW - 1)) leave();
+    STAMP(6);
+
+    // Qwen3's per-head RMSNorm (Trit's serial sum of the squares) and the
+    // rotary halves, wave 0 the q head and wave 1 the k head, lane i dims i
+    // and i + 64 (src/models/parts/causal_lm.rs:428-446, src/layers.rs:
+    // 136-144,303-334); v as cached. Block r = 0 of the XCD appends the new
+    // key and value (agent scope: later steps read them on this XCD, the
+    // per-kernel loop anywhere).
+    if (w < 3) {
+        float x0 = sm.qkv[w * HD + lane], x1 = sm.qkv[w * HD + lane + HD / 2];
+        if (w <= 1) {
+            if (a.qk_norm) {
+                float sq[16];
+#pragma unroll
+                for (int i = 0; i < 16; i += 4) {
+                    const float4 f = lane < 8 ? *(const float4*)(sm.qkv + w * HD + 16 * lane + i)
+                                              : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    sq[i] = f.x * f.x, sq[i + 1] = f.y * f.y, sq[i + 2] = f.z * f.z, sq[i + 3] = f.w * f.w;
+                }
+                const float sum = lane_chain<16>(sq, 0.0f, HD / 16);
+                const float inv = 1.0f / __builtin_sqrtf(sum / (float)HD + a.eps);
+                x0 = x0 * (inv * nw0);
+                x1 = x1 * (inv * nw1);
+            }
+            const float ac = x0 * cs, bs = x1 * sn, bc = x1 * cs, as = x0 * sn;
+            x0 = ac - bs;
+            x1 = bc + as;
+        }
+        if (w == 0) {
+            if (a.q_scale != 1.0f) {
+                x0 = x0 * a.q_scale;
+                x1 = x1 * a.q_scale;
+            }
+            const float scale = 1.0f / __builtin_sqrtf((float)HD);
+            x0 = x0 * scale;
+            x1 = x1 * scale;
+        } else {
+            const int which = w - 1;
+            const _Float16 c0 = (_Float16)x0, c1 = (_Float16)x1;
+            if (r == 0) {
+                TRIT_GLOBAL uint16_t* cache =
+                    gmem((uint16_t*)(which == 0 ? L.kcache : L.vcache)) + ((size_t)g * a.max_pos + pos) * HD;
+                __hip_atomic_store(cache + lane, __builtin_bit_cast(uint16_t, c0), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(cache + lane + HD / 2, __builtin_bit_cast(uint16_t, c1), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
+            sm.kvn[which][lane] = (float)c0;
+            sm.kvn[which][lane + HD / 2] = (float)c1;
+            if (which == 0) {
+                sm.knew[lane] = __builtin_bit_cast(uint16_t, c0);
+                sm.knew[lane + HD / 2] = __builtin_bit_cast(uint16_t, c1);
+            }
+        }
+        // The norm's chain read the raw values of this head: rewrite them
+        // only after every lane of the wave has read its values.
+        __builtin_amdgcn_wave_barrier();
+        if (w == 0) {
+            sm.qkv[lane] = x0;
+            sm.qkv[lane + HD / 2] = x1;
+        }
+    }
+    __syncthreads();
+    // The values by dim (f16 bits): the cached ones, the new key's (as
+    // cached), zeros past it.
+    {
+        const uint32_t wv[4] = {vr.x, vr.y, vr.z, vr.w};
+#pragma unroll
+        for (int d = 0; d < WD; ++d) {
+            const uint16_t cached = (uint16_t)(wv[d / 2] >> (16 * (d & 1)));
+            sm.vth[d][t] = t < pos ? cached : t == pos ? f32_to_f16(sm.kvn[1][WD * s + d]) : (uint16_t)0;
+        }
+    }
+    // The appended key and value are acknowledged before the block's
+    // attention outputs are put (after barriers in part b): whoever reads
+    // them later waited, through the tags, for that put.
+    if (r == 0 && (w == 1 || w == 2)) __builtin_amdgcn_s_waitcnt(VMCNT0);
+    STAMP(7);
+    // The slot's scores (the new key as cached: its f16 bits).
+    if (t < kn && jk < tk) {
+        if (jk == pos) {
+#pragma unroll
+            for (int c = 0; c < HD / 8; ++c) kk[c] = *(const uint4*)&sm.knew[8 * c];
+        }
+        put_local(a.SC + (size_t)hq * T + jk, score_of(kk, sm.qkv), tag_sc);
+    }
+    STAMP(25);
+    return true;
+}
+
+template <int GROUP>
+__device__ bool attention_wide_b(int t, const StepArgs& a, int pos, uint32_t tag_sc, uint32_t tag_out, Smem& sm,
+                                 unsigned long long deadline, int p0) {
+    const int r = sm.xrank, g = sm.xcd;
+    const int hq = g * GROUP + r / BPH, s = r % BPH;
+    const int tk = pos + 1;
+    const int w = t / WAVE, lane = t % WAVE;
+    // The head's scores, from its BPH blocks on this XCD.
+    STAMP(26);
+    if (!gather<T / (4 * WAVE)>(t, a.SC + (size_t)hq * T, tk, Linear(), tag_sc, sm.probs, sm, deadline, a.st, p0))
+        leave();
+    STAMP(27);
+    const float score = t < tk ? sm.probs[t] : -INFINITY;
+    const float m_w = wave_max(score);
+    if (lane == 0) sm.wmax[w] = m_w;
+    __syncthreads();
+    float mx = sm.wmax[0];
+#pragma unroll
+    for (int q = 1; q < NW; ++q) mx = __builtin_fmaxf(mx, sm.wmax[q]);
+    const float e = t < tk ? exp_trit(score - mx) : 0.0f;
+    sm.probs[t] = e;
+    __syncthreads();
+    STAMP(8);
+    // Their sum in key order from 0, by every wave; p_j = e_j * (1/sum),
+    // -0 past the keys (adding nothing to the chains below).
+    const float p = e * (1.0f / chain_sum_spec(t, sm.probs, tk, a.norm_window, sm));
+    STAMP(9);
+    sm.probs[t] = t < tk ? p : -0.0f;
+    __syncthreads();
+    // p.V in key order: wave w takes keys [64 w, 64 w + 64), lane d its
+    // dim's values (lane l: dim l % WD; lanes from WD on are not used) and
+    // their probabilities (every lane alike), read from LDS PD fours ahead
+    // of the multiply-adds; the waves chain in turn, the carry passing
+    // through LDS, the new key last.
+    const int nkw = (tk + WAVE - 1) / WAVE;  // the waves that hold keys
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+    constexpr int PD = 6;
+    f32x4 pq[PD];
+    f16x4 vq[PD];
+    const float* pw = sm.probs + WAVE * wu;
+    const uint16_t* vw = sm.vth[lane % WD] + WAVE * wu;
+    if (wu < nkw) {
+#pragma unroll
+        for (int i = 0; i < PD; ++i) {
+            pq[i] = *(const f32x4*)(pw + 4 * i);
+            vq[i] = *(const f16x4*)(vw + 4 * i);
+        }
+    }
+    float acc = 0.0f;
+    for (int cw = 0; cw < min(wu, nkw); ++cw) __syncthreads();
+    if (wu < nkw) {
+        if (wu > 0) acc = sm.carry[lane];
+#pragma unroll
+        for (int i = 0; i < WAVE / 4; ++i) {
+            const f32x4 pc = pq[i % PD];
+            const f16x4 vc = vq[i % PD];
+            if (i + PD < WAVE / 4) {
+                // The reads issue after the chain so far: PD of each in
+                // flight, not all of them hoisted to the turn's start.
+                int off = 4 * (i + PD);
+                asm volatile("" : "+v"(off) : "v"(acc));
+                pq[i % PD] = *(const f32x4*)(pw + off);
+                vq[i % PD] = *(const f16x4*)(vw + off);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc = __builtin_fmaf(pc[u], (float)vc[u], acc);
+        }
+        if (wu + 1 < nkw) sm.carry[lane] = acc;
+    }
+    for (int cw = wu; cw < nkw; ++cw) __syncthreads();
+    if (wu == nkw - 1 && lane < WD) put(a.ATT + (size_t)hq * HD + WD * s + lane, acc, tag_out);
+    STAMP_BY(10, WAVE * (nkw - 1));
+    return true;
+}
+
 // attention_exact with Trit's own f32 keys and values (TRIT_HIP_EXACT,
 // TRIT_HIP_KV_F32): the same blocks, phases and orders, the keys and values
 // as f32 (each appended value as computed, no f16 rounding). Thread t scores
@@ -2047,6 +2324,22 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     State* st = a.st;
     if (st->done) return;
     const int b = blockIdx.x;
+    if (a.local_qkv) {
+        // The block's XCD and its rank among the XCD's blocks (each XCD
+        // holds gridDim / NX of them: one a CU). Were it otherwise, the
+        // launch fails here (the others' waits reach their deadlines)
+        // rather than run with a role taken twice.
+        if (threadIdx.x == 0) {
+            const int x = xcc_id();
+            sm.xcd = x;
+            sm.xrank = x < NX ? (int)atomicAdd(a.xcd_count + x, 1u) : INT_MAX;
+        }
+        __syncthreads();
+        if (__builtin_amdgcn_readfirstlane(sm.xrank) >= (int)gridDim.x / NX) {
+            if (threadIdx.x == 0) atomicOr(&st->err, 2);
+            leave();
+        }
+    }
     if (threadIdx.x == 0) sm.abort = 0;
     for (int i = threadIdx.x; i < a.n_layers * (int)(sizeof(LayerPtrs) / 8); i += T)
         ((uint64_t*)sm.layers)[i] = gmem((const uint64_t*)a.layers)[i];
@@ -2109,11 +2402,23 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         rowd = b * a.rd + 4 * ((w - od0) % nd) + (lane >> 4);
     };
     fresh();
+    // The qkv row a lane of the qkv waves takes: row rowq, or with the
+    // XCD-local exchange, the block of rank r on XCD x makes rows
+    // [r rq, r rq + rq) of key/value head x's (GROUP + 2) HD rows -- its
+    // GROUP query heads, its key, its value (the host's plan: the rows of a
+    // head fill its XCD's blocks). Computed where it is used.
+    auto qkv_row = [&]() {
+        if (!a.local_qkv) return rowq;
+        const int x = sm.xcd, lr = sm.xrank * a.rq + (rowq - b * a.rq), gq = GROUP * HD;
+        return lr < gq ? x * gq + lr
+             : lr < gq + HD ? (a.heads + x) * HD + (lr - gq)
+                            : (a.heads + a.kvh + x) * HD + (lr - gq - HD);
+    };
 
     // The first layer's qkv rows stream in during the choice. (Declared per
     // step so that nothing of it stays live through the head.)
     Rows<RN, RS> rr{};
-    if (aq) load_rows<JD, 1, WK>(t, sm.layers[0].codes[0], sm.layers[0].scales[0], 0, rowq, rr);
+    if (aq) load_rows<JD, 1, WK>(t, sm.layers[0].codes[0], sm.layers[0].scales[0], 0, qkv_row(), rr);
 
     // ---- the greedy choice over the blocks' candidates -------------------
     {
@@ -2203,14 +2508,27 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         if (aq) {
             float acc[1];
             row_chain<JD, 1, WK>(t, rr, sm, acc);
-            if ((lane & 15) == 14) put(a.QKV + rowq, acc[0], tag_of(tag0, layer, 0));
+            if ((lane & 15) == 14) {
+                if (a.local_qkv)
+                    put_local(a.QKV + qkv_row(), acc[0], tag_of(tag0, layer, 0));
+                else
+                    put(a.QKV + rowq, acc[0], tag_of(tag0, layer, 0));
+            }
         }
         __syncthreads();
         STAMP(4);
         if constexpr (DPB > 0) {
             // attention in one pass: its outputs are the o product's input.
             bool ok;
-            if constexpr (KV32)
+            // The attention on every block (one key/value head an XCD).
+            // The attention on every block (one key/value head an XCD).
+            const bool wide = EXACT && !LONG && !KV32 && a.local_qkv;
+            if (wide)
+                ok = attention_wide_a<GROUP>(t, a, L, pos, tag_of(tag0, layer, 0), tag_of(tag0, layer, 1), sm,
+                                             deadline) &&
+                     attention_wide_b<GROUP>(t, a, pos, tag_of(tag0, layer, 1), tag_of(tag0, layer, 2), sm, deadline,
+                                             NW - nqw);
+            else if constexpr (KV32)
                 ok = attention_exact32<GROUP, DPB>(t, a, L, pos, tag_of(tag0, layer, 0), tag_of(tag0, layer, 2), sm,
                                                    deadline);
             else if constexpr (EXACT && LONG)
@@ -2230,13 +2548,18 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             else
                 zero_rows(rr);
             if (agu) load_rows<JD, 2, WK>(t, L.codes[2], L.scales[2], a.ffn, rowgu, rr);
-            // Then the attention blocks' waves before the qkv waves load the
-            // next attention's keys and values into L2.
-            if (EXACT && b < 2 * a.heads && w < NW - nqw) {
+            // Then the attention waves before the qkv waves load the next
+            // attention's keys and values into L2 (with the wide attention,
+            // every block of the XCD a share).
+            if (EXACT && w < NW - nqw) {
                 const bool last = layer + 1 == a.n_layers;
                 const int kvh = a.kvh;
-                touch_kv<4, KV32 ? 4 : 2>(t, (NW - nqw) * WAVE, sm.layers[last ? 0 : layer + 1], b % kvh, b / kvh,
-                                          2 * a.heads / kvh, last ? pos + 1 : pos, a.max_pos, kvt);
+                if (wide)
+                    touch_kv<4, 2>(t, (NW - nqw) * WAVE, sm.layers[last ? 0 : layer + 1], sm.xcd, sm.xrank,
+                                   (int)gridDim.x / NX, last ? pos + 1 : pos, a.max_pos, kvt);
+                else if (b < 2 * a.heads)
+                    touch_kv<4, KV32 ? 4 : 2>(t, (NW - nqw) * WAVE, sm.layers[last ? 0 : layer + 1], b % kvh, b / kvh,
+                                              2 * a.heads / kvh, last ? pos + 1 : pos, a.max_pos, kvt);
             }
             __syncthreads();
             if (!gather<8>(t, a.ATT, a.qd, lin, tag_of(tag0, layer, 2), sm.xin, sm, deadline, st, NW - nqw))
@@ -2306,7 +2629,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         else
             zero_rows(rr);
         if (aq && layer + 1 < a.n_layers)
-            load_rows<JD, 1, WK>(t, sm.layers[layer + 1].codes[0], sm.layers[layer + 1].scales[0], 0, rowq, rr);
+            load_rows<JD, 1, WK>(t, sm.layers[layer + 1].codes[0], sm.layers[layer + 1].scales[0], 0, qkv_row(), rr);
         __syncthreads();
         if (!gather<MWK>(t, a.H, a.ffn, lin, tag_of(tag0, layer, 4), sm.xin, sm, deadline, st)) leave();
         STAMP(18);
@@ -2625,6 +2948,7 @@ int device_blocks() {
 
 struct Plan {
     int blocks, splits, comb, dpb, rq, ro, rgu, rd, rh, wk, hk;
+    int local_qkv;
     StepFn fn;
 };
 
@@ -2633,6 +2957,23 @@ struct Plan {
 bool split_forced() {
     const char* v = getenv("TRIT_HIP_STEP_SPLIT");
     return v && v[0] == '1';
+}
+
+// The attention on every block with each key/value head's exchanges in one
+// XCD's L2 (StepArgs::local_qkv): the Trit-order instance of up to T
+// positions with f16 caches, one key/value head an XCD whose (group + 2) HD
+// qkv rows fill that XCD's blocks at rq rows each, BPH blocks a query head,
+// and the head's scores polled by the qkv waves (two words a lane).
+// TRIT_HIP_STEP_LOCAL=0 keeps the attention on two blocks a query head and
+// every exchange at agent scope.
+bool local_fits(const SessionImpl& S, const Plan& p) {
+    const char* v = getenv("TRIT_HIP_STEP_LOCAL");
+    if (v && v[0] == '0') return false;
+    const auto& c = S.dec->c;
+    const int group = c.heads / c.kv_heads, nbx = p.blocks / NX, nqw = p.rq / 4;
+    constexpr int mw = T / (4 * WAVE);  // attention_wide_b's gather
+    return S.exact && !S.kv32 && S.max_pos <= T && p.dpb > 0 && c.kv_heads == NX && p.blocks % NX == 0 &&
+           nbx * p.rq == (group + 2) * HD && nbx == group * BPH && NW - nqw + (T + WAVE * mw - 1) / (WAVE * mw) <= NW;
 }
 
 bool plan(const SessionImpl& S, Plan& p) {
@@ -2705,6 +3046,7 @@ bool plan(const SessionImpl& S, Plan& p) {
         p.fn = step_fn(c.d / 256, qd / 256, c.ffn / 256, group, p.dpb, true, p.wk, p.hk, S.max_pos > T, S.kv32);
         if (!p.fn) return false;
         p.rh = (c.vocab + p.blocks - 1) / p.blocks;
+        p.local_qkv = local_fits(S, p);
         return true;
     }
     const bool one_pass = !split_forced() && S.max_pos <= 32 * MAXF && (p.dpb == 4 || p.dpb == 8) &&
@@ -2721,14 +3063,30 @@ bool plan(const SessionImpl& S, Plan& p) {
     }
     if (!p.fn) return false;
     p.rh = (c.vocab + p.blocks - 1) / p.blocks;
+    p.local_qkv = 0;
     return true;
 }
 
 }  // namespace
 
+// Where the wide attention's score words start in the exchange buffer:
+// after every other region, on a 128-byte line of their own (no line of
+// them is written from another XCD).
+size_t sc_words(const TritHipLmConfig& c, const Plan& p) {
+    const int nq = (c.heads + 2 * c.kv_heads) * HD, qd = c.heads * HD;
+    const size_t end = (size_t)c.d + nq + (size_t)c.heads * p.splits * (HD + 2) + qd + c.ffn + 2 * (size_t)p.blocks;
+    return (end + 15) / 16 * 16;
+}
+
 bool decode_step_supported(const SessionImpl& S) {
     Plan p;
     return plan(S, p);
+}
+
+int decode_step_layout(const SessionImpl& S) {
+    Plan p;
+    if (!plan(S, p)) return 0;
+    return 1 | (p.local_qkv ? 2 : 0);
 }
 
 void decode_step_prepare(SessionImpl& S, hipStream_t s) {
@@ -2736,8 +3094,7 @@ void decode_step_prepare(SessionImpl& S, hipStream_t s) {
     if (!plan(S, p)) fail("decode step: the session's model does not fit the persistent step");
     const DecoderImpl& D = *S.dec;
     const auto& c = D.c;
-    const int nq = (c.heads + 2 * c.kv_heads) * HD, qd = c.heads * HD;
-    const size_t words = (size_t)c.d + nq + (size_t)c.heads * p.splits * (HD + 2) + qd + c.ffn + 2 * (size_t)p.blocks;
+    const size_t words = sc_words(c, p) + (size_t)c.heads * T + 16;  // + the XCD rank counters' line
     if (!S.step_words.ptr) {
         S.step_words.alloc(words * 8);
         TRIT_HIP(hipMemsetAsync(S.step_words.ptr, 0, words * 8, s));
@@ -2793,7 +3150,7 @@ void decode_step_launch(SessionImpl& S, int step, int pos, int nsteps, hipStream
     // counter would wrap, the words start over from zero.
     if (S.step_seq + (uint32_t)nsteps >= (1u << 24)) {
         const size_t words =
-            (size_t)c.d + nq + (size_t)c.heads * p.splits * (HD + 2) + qd + c.ffn + 2 * (size_t)p.blocks;
+            sc_words(c, p) + (size_t)c.heads * T + 16;  // + the XCD rank counters' line
         TRIT_HIP(hipMemsetAsync(S.step_words.ptr, 0, words * 8, s));
         S.step_seq = 0;
     }
@@ -2827,6 +3184,7 @@ void decode_step_launch(SessionImpl& S, int step, int pos, int nsteps, hipStream
     a.ATT = a.PART + (size_t)c.heads * p.splits * (HD + 2);
     a.H = a.ATT + qd;
     a.CAND = a.H + c.ffn;
+    a.SC = w + sc_words(c, p);
     a.cand = S.step_cand.as<float2>();
     a.out = S.tokens_out.as<int>();
     a.st = S.st();
@@ -2860,6 +3218,10 @@ void decode_step_launch(SessionImpl& S, int step, int pos, int nsteps, hipStream
     a.additive_rows = S.additive_rows;
     a.stamp_step = g_stamp_step;
     a.stamp_layer = g_stamp_layer;
+    a.local_qkv = p.local_qkv;
+    // The XCD rank counters, zeroed for this launch.
+    a.xcd_count = (unsigned int*)(w + sc_words(c, p) + (size_t)c.heads * T);
+    if (p.local_qkv) TRIT_HIP(hipMemsetAsync(a.xcd_count, 0, NX * sizeof(unsigned int), s));
     void* args[] = {&a, &step, &pos, (void*)&seq0, &nsteps};
     TRIT_HIP(hipLaunchCooperativeKernel((const void*)p.fn, dim3(p.blocks), dim3(T), args, 0, s));
 }

@@ -2490,6 +2490,9 @@ static int generate_common(TritHipSession* session, int max_new, const int32_t* 
         S.broken = true;
         S.host_pos = h.pos;
         S.step_cand_fresh = false;
+        if (h.err & 2)
+            fail("generate: a decode-step block ran on another XCD than its local exchange needs (the step was "
+                 "abandoned; reset the session, with TRIT_HIP_STEP_LOCAL=0)");
         fail("generate: a decode-step block waited past its deadline (the step was abandoned; reset the session)");
     }
     TRIT_HIP(hipMemcpy(out, S.tokens_out.ptr, (size_t)h.n_out * 4, hipMemcpyDeviceToHost));
@@ -2504,7 +2507,7 @@ int trit_hip_session_generate(TritHipSession* session, int max_new, const int32_
 int trit_hip_session_generate_timed(TritHipSession* session, int max_new, const int32_t* stop, int n_stop,
                                     int32_t* out, void* start_event, void* stop_event, int* persistent) {
     return guard(-1, [&] {
-        if (persistent) *persistent = session && use_step(session->impl) ? 1 : 0;
+        if (persistent) *persistent = session && use_step(session->impl) ? decode_step_layout(session->impl) : 0;
         return generate_common(session, max_new, stop, n_stop, out, (hipEvent_t)start_event, (hipEvent_t)stop_event);
     });
 }

@@ -110,6 +110,10 @@ void exact_attention(const float* q, int qs, const float* k, const float* v, int
 // The persistent decode step (decode_step.hip).
 // Whether the session's model and mode run on it.
 bool decode_step_supported(const SessionImpl& S);
+// How the step runs the session: 1, or 3 when its attention runs on every
+// block with each key/value head's exchanges in one XCD's L2; 0 when the
+// session does not run on the step.
+int decode_step_layout(const SessionImpl& S);
 // Prepares the exchange buffers and, when the last logits are newer than
 // the step's candidates, the candidates from the logits.
 void decode_step_prepare(SessionImpl& S, hipStream_t s);

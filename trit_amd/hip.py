@@ -694,7 +694,10 @@ class Session:
         persistent = C.c_int(0)
         n = check(lib().trit_hip_session_generate_timed(self.h, max_new, ptr(stop) if stop.size else None,
                                                         stop.size, ptr(out), None, None, C.byref(persistent)))
-        self.persistent = bool(persistent.value)
+        self.persistent = bool(persistent.value & 1)
+        # On the step: bit 1 when the attention runs on every block, each
+        # key/value head's exchanges in one XCD's L2.
+        self.step_layout = int(persistent.value)
         return out[:n].copy()
 
     def reset(self):
