@@ -49,9 +49,12 @@ GATE_UP_TRAFFIC_BYTES = round((3353.1 * 2.0 + 24.0) * 1024)
 # HBM bytes per forward of the persistent decode step, from the same kind of
 # runs (profiles/decode_step_qwen3_0.6b_hbm_traffic.md): FETCH_SIZE and
 # WRITE_SIZE of one launch of 128 steps (127 forwards, positions 256..382)
-# over the forwards, FETCH_SIZE x 2.0 plus WRITE_SIZE x 1.0.
-STEP_FETCH_KIB, STEP_WRITE_KIB = 406911.30, 2600.06
+# over the forwards, FETCH_SIZE x 2.0 plus WRITE_SIZE x 1.0; the default
+# mode (f16 caches) and the exact mode (f32 caches).
+STEP_FETCH_KIB, STEP_WRITE_KIB = 51675338.375 / 127, 224158.5 / 127
 STEP_TRAFFIC_BYTES = round((STEP_FETCH_KIB * 2.0 + STEP_WRITE_KIB) * 1024)
+EXACT_FETCH_KIB, EXACT_WRITE_KIB = 54501672.875 / 127, 1387986.21875 / 127
+EXACT_TRAFFIC_BYTES = round((EXACT_FETCH_KIB * 2.0 + EXACT_WRITE_KIB) * 1024)
 
 
 class Hip:
@@ -512,7 +515,7 @@ def config_lines(H, sweeps=10, decode=True):
     return out
 
 
-def step_roofline(cfg, prompt, steps, step_ms, persistent, mode, linears="q8_0", table="f16"):
+def step_roofline(cfg, prompt, steps, step_ms, persistent, mode, linears="q8_0", table="f16", counted=False):
     """The decode loop's kernel: the persistent step (one launch runs every
     step of a generate call) timed with HIP events around it. Algorithmic
     bytes per forward: every linear weight once (Q8_0: 34 B per 32; int8:
@@ -536,10 +539,15 @@ def step_roofline(cfg, prompt, steps, step_ms, persistent, mode, linears="q8_0",
     launches = 1 if persistent else steps
     per_launch = per_forward * forwards // launches
     avg_ms = step_ms / launches
+    # The counters were read for the bench's own workload only (counted: the
+    # metric's line, 256-token prompt and 128 steps, on the step).
+    measured = counted and persistent and prompt == 256 and steps == 128
+    traffic = (STEP_TRAFFIC_BYTES if mode == "default" else EXACT_TRAFFIC_BYTES if mode == "exact" else None) \
+        if measured else None
     achieved = per_launch / (avg_ms * 1e-3) / 1e9
     return dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                 frac=round(achieved / HBM_PEAK_GBS, 4),
-                traffic=STEP_TRAFFIC_BYTES * forwards if persistent and mode == "default" else None,
+                traffic=traffic * forwards if traffic else None,
                 kernel=(f"step_kernel<4,8,12,2,8,{'false' if mode == 'tree' else 'true'},"
                         f"{0 if linears == 'q8_0' else 1},{0 if table == 'f16' else 1},false,"
                         f"{'true' if mode == 'exact' else 'false'}>: the persistent decode step "
@@ -549,25 +557,26 @@ def step_roofline(cfg, prompt, steps, step_ms, persistent, mode, linears="q8_0",
                        else "the per-kernel decode step (graph replay)",
                 bytes_per_launch=per_launch, bytes_per_forward=per_forward, forwards=forwards,
                 avg_us=round(avg_ms * 1e3, 3), us_per_forward=round(step_ms * 1e3 / forwards, 3),
-                traffic_per_forward=STEP_TRAFFIC_BYTES if persistent and mode == "default" else None,
+                traffic_per_forward=traffic,
                 launches=launches,
                 timing="HIP events recorded on the library's stream before and after the step launch "
                        "(trit_hip_session_generate_timed); the launch includes the final choice-only step")
 
 
-STAMP_PHASES = [  # (name, from stamp, to stamp, blocks: "all" / "attn" / "rest")
-    ("x hand-over (after down)", 0, 1, "all"), ("RMSNorm (Trit's serial sum)", 1, 2, "all"),
-    ("quantize (qkv input)", 2, 3, "all"), ("qkv rows and put", 3, 4, "all"),
-    ("attention: qkv hand-over", 5, 6, "attn"), ("attention: q/k norm, rotary, append", 6, 7, "attn"),
-    ("attention: scores, max, exp", 7, 8, "attn"), ("attention: softmax sum (serial)", 8, 9, "attn"),
-    ("attention: p.V (serial) and put", 9, 10, "attn"),
-    ("attention -> o hand-over (attention blocks)", 10, 11, "attn"),
-    ("attention -> o hand-over (other blocks, from qkv put)", 4, 11, "rest"),
-    ("quantize (o input)", 11, 12, "all"), ("o rows and put", 12, 13, "all"),
-    ("x hand-over (after o)", 13, 14, "all"), ("RMSNorm", 14, 15, "all"), ("quantize (gate_up input)", 15, 16, "all"),
-    ("gate_up rows, SwiGLU, put", 16, 17, "all"), ("h hand-over", 17, 18, "all"),
-    ("quantize (down input)", 18, 19, "all"), ("down rows and put", 19, 20, "all"),
-    ("a layer", 0, 20, "all")]
+STAMP_PHASES = [  # (name, from stamp, to stamp); every block runs every phase
+    ("x hand-over (after down)", 0, 1), ("RMSNorm (Trit's serial sum)", 1, 2),
+    ("quantize (qkv input)", 2, 3), ("qkv rows and put (XCD-local)", 3, 4),
+    ("attention: key and value loads issued", 4, 5), ("attention: qkv hand-over (XCD-local)", 5, 6),
+    ("attention: q/k norm, rotary, append, values to LDS", 6, 7),
+    ("attention: 1/16 of the keys scored and put (XCD-local)", 7, 25),
+    ("attention: score hand-over", 25, 27), ("attention: max, exp", 27, 8),
+    ("attention: softmax sum (serial)", 8, 9), ("attention: p.V (serial) and put", 9, 10),
+    ("attention -> o hand-over", 10, 11),
+    ("quantize (o input)", 11, 12), ("o rows and put", 12, 13),
+    ("x hand-over (after o)", 13, 14), ("RMSNorm", 14, 15), ("quantize (gate_up input)", 15, 16),
+    ("gate_up rows, SwiGLU, put", 16, 17), ("h hand-over", 17, 18),
+    ("quantize (down input)", 18, 19), ("down rows and put", 19, 20),
+    ("a layer", 0, 20)]
 HEAD_PHASES = [("x hand-over (last layer's down)", None, 21), ("final RMSNorm", 21, 22), ("head passes", 22, 23),
                ("best of the block and put", 23, 24)]
 
@@ -576,22 +585,23 @@ def stamp_pass(w, prompt, steps, step=8, layer=10):
     """The persistent step's phases on the measurement build
     (TRIT_HIP_LIBRARY=trit_amd/lib/libtrit_hip_stamps.so): thread 0 of each
     block stamps fixed points of one (step, layer) of the launch; per phase,
-    the mean over the blocks that run it of the shader-clock interval,
-    converted to microseconds by each block's shader/wall clock ratio over
-    the layer."""
+    the mean over the blocks of the shader-clock interval, converted to
+    microseconds by each block's shader/wall clock ratio over the layer.
+    Stamp 10 (the attention's outputs put) is the putting wave's; the
+    others are thread 0's. For the layout of one key/value head an XCD
+    (step_layout 3), where every block runs every phase."""
     lib = hip.lib()
     lm, linears, embed = build_layers(w)
     sess = lm.session(len(prompt) + steps, 0)
     cfg = w.cfg
     blocks = 256
-    attn = 2 * cfg["heads"]
 
     def run(stamp_layer):
         hip.check(lib.trit_hip_step_stamps(step, stamp_layer))
         sess.reset()
         sess.prefill(prompt, want_logits=False)
         sess.generate(steps)
-        assert sess.persistent
+        assert sess.step_layout == 3, sess.step_layout
         wall = np.zeros((blocks, 32), np.uint64)
         clk = np.zeros((blocks, 32), np.uint64)
         hip.check(lib.trit_hip_step_stamps_read(wall.ctypes.data_as(C.c_void_p), clk.ctypes.data_as(C.c_void_p),
@@ -602,12 +612,10 @@ def stamp_pass(w, prompt, steps, step=8, layer=10):
     wall, clk = run(layer)
     # Shader-clock ticks per microsecond, per block, over the layer (wall: 100 MHz).
     rate = (clk[:, 20] - clk[:, 0]) / ((wall[:, 20] - wall[:, 0]) / 100.0)
-    sel = {"all": np.arange(blocks), "attn": np.arange(attn), "rest": np.arange(attn, blocks)}
     rows = []
-    for name, a, b, who in STAMP_PHASES:
-        idx = sel[who]
-        us = (clk[idx, b] - clk[idx, a]) / rate[idx]
-        rows.append(dict(phase=name, us=round(float(np.mean(us)), 3), blocks=who))
+    for name, a, b in STAMP_PHASES:
+        us = (clk[:, b] - clk[:, a]) / rate
+        rows.append(dict(phase=name, us=round(float(np.mean(us)), 3)))
     hwall, hclk = run(cfg["layers"])
     hrate = np.median(rate)
     head = []
@@ -1047,13 +1055,13 @@ def main():
     value = forwards / t_decode
     print(f"[bench] gpu decode {value:.1f} tok/s (device {forwards / step_ms * 1e3:.1f}), "
           f"prefill {args.prompt / t_prefill:.1f} tok/s", file=sys.stderr, flush=True)
-    step_roof = step_roofline(cfg, args.prompt, args.steps, step_ms, bool(persistent.value), args.mode)
+    step_roof = step_roofline(cfg, args.prompt, args.steps, step_ms, bool(persistent.value), args.mode, counted=True)
     exact = None
     if args.mode == "default":
         print("[bench] exact mode (f32 keys and values) ...", file=sys.stderr, flush=True)
         exact = timed_mode(lm, prompt, args.steps, args.warmup, hip.EXACT, H)
         exact["roofline"] = step_roofline(cfg, args.prompt, args.steps, exact.pop("step_ms"), exact["persistent"],
-                                          "exact")
+                                          "exact", counted=True)
         print(f"[bench] exact mode {exact['value']} tok/s", file=sys.stderr, flush=True)
 
     print("[bench] roofline sweep ...", file=sys.stderr, flush=True)

@@ -327,6 +327,29 @@ def test_step_default(qshape, monkeypatch):
     check_generate_default(w, ref16, lm, QS, monkeypatch, layout=3)
 
 
+def test_step_plain_launch(qshape, monkeypatch):
+    """TRIT_HIP_STEP_LAUNCH=plain (the profiling option: the same step by an
+    ordinary launch) gives the cooperative launch's tokens and the same
+    logits after them."""
+    print("case decoder persistent step (ordinary launch)", flush=True)
+    w, ref, lm, ref16 = qshape
+    p = synth.prompt(99, 33, QS["vocab"])
+    out = []
+    for plain in (False, True):
+        if plain:
+            monkeypatch.setenv("TRIT_HIP_STEP_LAUNCH", "plain")
+        s = lm.session(96, 0)
+        s.prefill(p)
+        got = s.generate(20)
+        assert s.persistent
+        after = s.prefill(np.array([int(got[-1])]))
+        out.append((got.tolist(), after))
+        s.free()
+    monkeypatch.delenv("TRIT_HIP_STEP_LAUNCH")
+    assert out[0][0] == out[1][0]
+    assert same_bits(out[0][1], out[1][1])
+
+
 def test_step_default_two_blocks_a_head(qshape, monkeypatch):
     """The same with TRIT_HIP_STEP_LOCAL=0: the attention on two blocks a
     query head and every exchange at agent scope (the layout of models

@@ -3223,7 +3223,16 @@ void decode_step_launch(SessionImpl& S, int step, int pos, int nsteps, hipStream
     a.xcd_count = (unsigned int*)(w + sc_words(c, p) + (size_t)c.heads * T);
     if (p.local_qkv) TRIT_HIP(hipMemsetAsync(a.xcd_count, 0, NX * sizeof(unsigned int), s));
     void* args[] = {&a, &step, &pos, (void*)&seq0, &nsteps};
-    TRIT_HIP(hipLaunchCooperativeKernel((const void*)p.fn, dim3(p.blocks), dim3(T), args, 0, s));
+    // TRIT_HIP_STEP_LAUNCH=plain (measurement only: profilers that end badly
+    // after cooperative launches): the same grid by an ordinary launch. One
+    // block fits a CU (its LDS), so the grid of one block a CU is resident
+    // on an otherwise idle device; were it not, the waits reach their
+    // deadlines and the call fails.
+    const char* how = getenv("TRIT_HIP_STEP_LAUNCH");
+    if (how && std::string(how) == "plain")
+        TRIT_HIP(hipLaunchKernel((const void*)p.fn, dim3(p.blocks), dim3(T), args, 0, s));
+    else
+        TRIT_HIP(hipLaunchCooperativeKernel((const void*)p.fn, dim3(p.blocks), dim3(T), args, 0, s));
 }
 
 }  // namespace trit
