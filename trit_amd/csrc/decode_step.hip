@@ -2346,10 +2346,11 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     __syncthreads();
 
     // Waves by product, four rows a wave: gate_up [0, nu), o [nu, nu + no),
-    // down [nu, nu + DR nd), qkv [NW - nqw, NW). Each product's rows load one
-    // phase ahead of it (o during the combine's wait, gate_up during o's,
-    // down and the next layer's qkv during down's); a wave holds one
-    // product's rows at a time, so all share one register set. Where those
+    // down [nu, nu + DR nd), qkv [NW - nqw, NW). Each product's rows load
+    // during the hand-over just before it (o's during the attention
+    // outputs', gate_up's during x's after o, down's during h's, the next
+    // layer's qkv during x's after down); a wave holds one product's rows
+    // at a time, so all share one register set. Where those
     // ranges do not fit in the waves (wide MLPs), gate_up moves to the last
     // nu waves and o / down to the first: gate_up's rows then load during
     // the attention in waves that also poll for its outputs (every wave has
@@ -2547,7 +2548,9 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
                 load_rows<JO, 1, WK>(t, L.codes[1], L.scales[1], 0, rowo, rr);
             else
                 zero_rows(rr);
-            if (agu) load_rows<JD, 2, WK>(t, L.codes[2], L.scales[2], a.ffn, rowgu, rr);
+            // (Packed: the gate_up rows load after the o product instead,
+            // but in the f32-cache instance, where that spills registers.)
+            if ((!packed || KV32) && agu) load_rows<JD, 2, WK>(t, L.codes[2], L.scales[2], a.ffn, rowgu, rr);
             // Then the attention waves before the qkv waves load the next
             // attention's keys and values into L2 (with the wide attention,
             // every block of the XCD a share).
@@ -2598,11 +2601,22 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         // (before the polls of the gather below).
         asm volatile("" ::"v"(kvt[0]), "v"(kvt[1]), "v"(kvt[2]), "v"(kvt[3]));
         // gate_up + SwiGLU.
+        // Each product's rows stream in during the hand-over just before it:
+        // o's during the attention outputs', gate_up's here (packed: their
+        // waves hold no other rows), down's during h's, the next qkv's
+        // during x's after down. (Measured: with gate_up's and the next
+        // qkv's loads a hand-over earlier, each hand-over with two loads in
+        // flight took 2.0-2.7 us; 675 -> 635 us a forward.) This gather is
+        // then polled by the last waves, clear of the gate_up waves [0, nu).
+        constexpr bool GU_LATE = DPB > 0 && !KV32;
+        if (GU_LATE && packed && agu) load_rows<JD, 2, WK>(t, L.codes[2], L.scales[2], a.ffn, rowgu, rr);
+        const int need = (a.d + WAVE * MWK - 1) / (WAVE * MWK);
+        const int px = GU_LATE && packed && NW - need >= nu ? NW - need : 0;
         NormRegs<JD> ngu, nfs;
         load_norm<JD>(t, L.norm_mlp, ngu);
         if (a.ffn_scales) load_norm<JD>(t, a.ffn_scales + (size_t)layer * a.d, nfs);
         __syncthreads();
-        if (!gather<MWK>(t, a.X, a.d, lin, tag_of(tag0, layer, 3), sm.xres, sm, deadline, st)) leave();
+        if (!gather<MWK>(t, a.X, a.d, lin, tag_of(tag0, layer, 3), sm.xres, sm, deadline, st, px)) leave();
         STAMP(14);
         if constexpr (EXACT) {
             const float inv = norm_inv_spec<JD>(t, sm.xres, a.eps, a.norm_window, sm);
@@ -2628,8 +2642,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             load_rows<JFR, 1, WK, RN, RS, JF, (DR > 1 ? JFR : 0)>(t, L.codes[3], L.scales[3], 0, rowd, rr);
         else
             zero_rows(rr);
-        if (aq && layer + 1 < a.n_layers)
-            load_rows<JD, 1, WK>(t, sm.layers[layer + 1].codes[0], sm.layers[layer + 1].scales[0], 0, qkv_row(), rr);
+
         __syncthreads();
         if (!gather<MWK>(t, a.H, a.ffn, lin, tag_of(tag0, layer, 4), sm.xin, sm, deadline, st)) leave();
         STAMP(18);
@@ -2657,6 +2670,9 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
                 if ((lane & 15) == 14) put(a.X + rowd, sm.xres[rowd] + a.rm * acc[0], tag_of(tag0, layer, 5));
             }
         }
+        // The next layer's qkv rows stream in during the x hand-over.
+        if (aq && layer + 1 < a.n_layers)
+            load_rows<JD, 1, WK>(t, sm.layers[layer + 1].codes[0], sm.layers[layer + 1].scales[0], 0, qkv_row(), rr);
         __syncthreads();
         STAMP(20);
     }
