@@ -321,7 +321,7 @@ __device__ __forceinline__ bool aborted(Smem& sm) {
 // Ends with a block barrier; false when a word missed the deadline (the
 // block then leaves the launch).
 template <int MW, typename Index>
-__device__ bool gather(int t, const uint64_t* src, int n, Index index, uint32_t tag, float* dst, Smem& sm,
+__device__ __forceinline__ bool gather(int t, const uint64_t* src, int n, Index index, uint32_t tag, float* dst, Smem& sm,
                        unsigned long long deadline, State* st, int p0 = 0) {
     const int i0 = (t / WAVE - p0) * WAVE * MW + t % WAVE;
     if (i0 >= 0 && i0 < n) {  // uniform per wave: whether the wave polls
