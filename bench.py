@@ -38,9 +38,13 @@ from trit_amd import hip, model, synth  # noqa: E402
 METRIC = "decode tokens/sec + GEMV HBM GB/s (% of peak), Qwen3-0.6B-shape Q8_0, 1 GPU"
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
-# Vector ALU lane operations per second without packed math: 256 CUs x 4
-# SIMDs x 16 lanes x 2.4 GHz (one wave64 instruction per 4 cycles a SIMD).
-VALU_PEAK_TOPS = 39.32
+# Vector ALU lane operations per second: MI355X's published FP32 vector rate,
+# 157.3 TFLOP/s, is 78.6 T lane FMAs/s (256 CUs x 128 lanes a cycle x 2.4 GHz;
+# a wave64 f32 instruction issues every 2 cycles a SIMD). A loop of the exact
+# chain's operations (convert, multiply, FMA, and an integer add, over 32
+# independent values a lane, no memory) ran at 63.7 T/s with the clock at
+# 2.27 GHz.
+VALU_PEAK_TOPS = 78.64
 # HBM bytes per launch of the roofline kernel, from rocprofv3 --pmc runs of
 # `bench.py --profile-pass` (profiles/gemv_stream_q8_0_6144x1024_hbm_traffic.md):
 # FETCH_SIZE 3353.1 KiB x 2.0 (the scale a 256 MiB device copy gives) plus

@@ -371,6 +371,268 @@ __global__ __launch_bounds__(GEMM_THREADS, 2) void gemm_kernel(const int8_t* __r
     }
 }
 
+// The same product with the K stages loaded straight into LDS
+// (global_load_lds_dwordx4: no staging registers) and double-buffered, so
+// one barrier a stage suffices and several blocks share a CU: the vector
+// ALUs, which bound this bit-exact product, stay busy while waves wait on
+// LDS, the matrix cores or a barrier. A stage holds 128 bytes of K (four
+// Q8_0 groups or one int8 group) of the block's 64 x rows and 64 TW weight
+// rows, and the stage's scales as they lie in memory (x scales f32
+// group-major, weight scales f16 or f32 per row). A row's eight 16-byte
+// pieces sit in LDS in the order piece ^ ((row >> 1) & 7), so the 32 rows
+// a wave's MFMA operand reads start in different banks. Waves 2 x 2: a wave
+// owns 32 x rows by TW 32-row weight tiles (TW = 2: 128-row blocks, 3 a CU,
+// 52 KB of LDS each; TW = 1: 64-row blocks, 4 a CU, 35 KB -- for products
+// too narrow to give every CU the same number of wide blocks). The SwiGLU
+// pair takes TW = 2 (a lane holds the gate and the up output it joins).
+// k must be a multiple of 128.
+constexpr int KD = 128;
+typedef __attribute__((address_space(3))) void LdsVoid;
+
+template <int TW>
+struct alignas(16) DStage {
+    alignas(16) int8_t a[BM * KD];
+    alignas(16) int8_t b[64 * TW * KD];
+    alignas(16) float xs[4 * BM];            // [group of the stage][x row]
+    alignas(16) uint32_t ws[2 * 64 * TW];    // f16: row r's four at [2r, 2r + 2); f32: row r's one at [r]
+};
+
+__device__ __forceinline__ int piece_swizzle(int row) { return (row >> 1) & 7; }
+
+// Loads of 16 (4) bytes a lane from g into LDS at l + 16 (4) x lane (l the
+// same for the wave). Written out rather than as the compiler's builtin,
+// whose wait counting, unable to tell the stages apart, can wait for every
+// load in flight before a read of the other stage; the kernel waits for
+// these loads itself (vmcnt).
+__device__ __forceinline__ uint32_t lds_address(const void* l) { return (uint32_t)(uintptr_t)(const LdsVoid*)l; }
+
+__device__ __forceinline__ void load16_to_lds(const void* g, void* l) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_address(l)) : "memory");
+}
+
+__device__ __forceinline__ void load4_to_lds(const void* g, void* l) {
+    asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(lds_address(l)) : "memory");
+}
+
+template <int G, bool HALF, int P, int TW>
+__global__ __launch_bounds__(GEMM_THREADS, TW == 2 ? 3 : 4) void gemm_dma_kernel(
+    const int8_t* __restrict__ xq, const float* __restrict__ xs, int m, int mpad, const int8_t* __restrict__ codes,
+    const void* __restrict__ scales, const float* __restrict__ bias, int n, int k, int nb, int mb, GemvArgs a) {
+    constexpr int GPC = KD / G;  // groups per stage
+    constexpr int CH = G / 32;   // MFMA steps per group
+    constexpr int BN = 64 * TW;  // weight rows per block
+    static_assert(GPC * CH == 4, "a stage is four 32-byte MFMA steps");
+    static_assert(P == 1 || TW == 2, "the SwiGLU pair: gate and up tiles in one wave");
+    __shared__ DStage<TW> st0, st1;
+    if (a.skip && *a.skip) return;
+    const int groups = k / G, chunks = k / KD;
+    const int blk = blockIdx.x;
+    int bn, bm;
+    if (nb % 8 == 0) {
+        const int q = blk / 8;
+        bn = blk % 8 + 8 * (q / mb);
+        bm = q % mb;
+    } else {
+        bn = blk % nb;
+        bm = blk / nb;
+    }
+    const int t = threadIdx.x;
+    const int lane = t % WAVE, w = __builtin_amdgcn_readfirstlane(t / WAVE);
+    const int lr = lane % 32, h = lane / 32;
+    const int mbase = bm * BM;
+    // LDS weight row i holds weight row brow(i); for the SwiGLU pair, 64
+    // gate rows then their 64 up rows. Rows past n load row n - 1.
+    auto brow = [&](int i) {
+        const int r = P == 1 ? bn * BN + i : (i < 64 ? bn * 64 + i : n / 2 + bn * 64 + (i - 64));
+        return r < n ? r : n - 1;
+    };
+
+    // The wave's loads of a stage: 1 KB an instruction (eight rows of 128
+    // bytes), x rows [16w, +16) and weight rows [16 TW w, +16 TW); then SPW
+    // scale loads: item 0 the x scales (1 KB: four groups of 64 rows, or one
+    // group and copies), items 1.. the weight scales (f16: 32 rows an item,
+    // two dwords a row; f32: 64 rows an item, one dword a row), items
+    // w, w + 4, ... for wave w (a wave past the last item repeats it: the
+    // same bytes to the same place).
+    uint32_t ag[2], bg[2 * TW];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int rl = 8 * (2 * w + i) + lane / 8;
+        const int mrow = mbase + rl < m ? mbase + rl : m - 1;
+        ag[i] = (uint32_t)mrow * (uint32_t)k + 16 * ((lane % 8) ^ piece_swizzle(rl));
+    }
+#pragma unroll
+    for (int i = 0; i < 2 * TW; ++i) {
+        const int rl = 8 * (2 * TW * w + i) + lane / 8;
+        bg[i] = (uint32_t)brow(rl) * (uint32_t)k + 16 * ((lane % 8) ^ piece_swizzle(rl));
+    }
+    constexpr int NWS = HALF ? 2 * TW : TW;  // weight-scale items
+    constexpr int SPW = (1 + NWS + 3) / 4;   // scale loads a wave
+    int item[SPW];
+    size_t soff[SPW];
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+        const int it = w + 4 * j < 1 + NWS ? w + 4 * j : NWS;
+        item[j] = it;
+        if (it == 0)
+            soff[j] = (size_t)(GPC == 4 ? lane / 16 : 0) * mpad + mbase + 4 * (lane % 16);
+        else if (HALF)
+            soff[j] = (size_t)brow(32 * (it - 1) + lane / 2) * (groups / 2) + lane % 2;
+        else
+            soff[j] = (size_t)brow(64 * (it - 1) + lane) * groups;
+    }
+    auto issue = [&](int c, DStage<TW>& s) {
+        const size_t off = (size_t)c * KD;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) load16_to_lds(xq + ag[i] + off, s.a + 1024 * (2 * w + i));
+#pragma unroll
+        for (int i = 0; i < 2 * TW; ++i) load16_to_lds(codes + bg[i] + off, s.b + 1024 * (2 * TW * w + i));
+#pragma unroll
+        for (int j = 0; j < SPW; ++j) {
+            if (item[j] == 0)
+                load16_to_lds(xs + soff[j] + (size_t)c * GPC * mpad, s.xs);
+            else if (HALF)
+                load4_to_lds((const uint32_t*)scales + soff[j] + 2 * c, s.ws + 64 * (item[j] - 1));
+            else
+                load4_to_lds((const float*)scales + soff[j] + c, s.ws + 64 * (item[j] - 1));
+        }
+    };
+
+    // The wave's tiles: x rows [32 (w % 2), +32); weight LDS rows sub0 (and
+    // sub1 for TW = 2), 32 each. Lane (lr, h) reads piece 2 s + h of its
+    // rows for step s; its rows all share (lr >> 1) & 7.
+    const int wn = w / 2;
+    const int sub0 = TW == 1 ? wn * 32 : P == 1 ? wn * 64 : wn * 32;
+    const int sub1 = TW == 1 ? sub0 : P == 1 ? wn * 64 + 32 : 64 + wn * 32;
+    const int xrow = (w % 2) * 32 + 4 * h;
+    uint32_t pa[4], pb[4];
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+        const int po = 16 * ((2 * s4 + h) ^ piece_swizzle(lr));
+        pa[s4] = ((w % 2) * 32 + lr) * KD + po;
+        pb[s4] = (sub0 + lr) * KD + po;
+    }
+    constexpr int B1 = (P == 1 ? 32 : 64) * KD;  // sub1 - sub0 rows, in bytes (TW = 2)
+
+    float t0[16], t1[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) t0[r] = t1[r] = 0.0f;
+
+    auto compute = [&](const DStage<TW>& s) {
+        const int8_t* sa = s.a;
+        const int8_t* sb = s.b;
+        // The stage's weight scales of the lane's columns.
+        float wsc0[GPC], wsc1[GPC];
+        if (HALF) {
+            const uint2 u0 = *(const uint2*)(s.ws + 2 * (sub0 + lr));
+            const uint2 u1 = TW == 2 ? *(const uint2*)(s.ws + 2 * (sub1 + lr)) : u0;
+            const uint32_t v0[2] = {u0.x, u0.y}, v1[2] = {u1.x, u1.y};
+#pragma unroll
+            for (int g = 0; g < GPC; ++g) {
+                wsc0[g] = f16_to_f32((uint16_t)(v0[g / 2] >> (16 * (g % 2))));
+                wsc1[g] = f16_to_f32((uint16_t)(v1[g / 2] >> (16 * (g % 2))));
+            }
+        } else {
+            wsc0[0] = __builtin_bit_cast(float, s.ws[sub0 + lr]);
+            wsc1[0] = __builtin_bit_cast(float, s.ws[sub1 + lr]);
+        }
+        Frags<CH> f;
+#pragma unroll
+        for (int c4 = 0; c4 < CH; ++c4) {
+            f.a[c4] = *(const v4i*)(sa + pa[c4]);
+            f.b0[c4] = *(const v4i*)(sb + pb[c4]);
+            if (TW == 2) f.b1[c4] = *(const v4i*)(sb + pb[c4] + B1);
+        }
+#pragma unroll
+        for (int gi = 0; gi < GPC; ++gi) {
+            v16i d0 = {}, d1 = {};
+#pragma unroll
+            for (int c4 = 0; c4 < CH; ++c4) {
+                d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[c4], f.b0[c4], d0, 0, 0, 0);
+                if (TW == 2) d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[c4], f.b1[c4], d1, 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (gi + 1 < GPC) {
+#pragma unroll
+                for (int c4 = 0; c4 < CH; ++c4) {
+                    const int s4 = (gi + 1) * CH + c4;
+                    f.a[c4] = *(const v4i*)(sa + pa[s4]);
+                    f.b0[c4] = *(const v4i*)(sb + pb[s4]);
+                    if (TW == 2) f.b1[c4] = *(const v4i*)(sb + pb[s4] + B1);
+                }
+            }
+            float4 xv4[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) xv4[q] = *(const float4*)(s.xs + gi * BM + xrow + 8 * q);
+            __builtin_amdgcn_sched_barrier(0);
+            // Output (row 8*(r/4) + 4h + r%4, column lr) of a tile is register r.
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float xv[4] = {xv4[q].x, xv4[q].y, xv4[q].z, xv4[q].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int r = 4 * q + j;
+                    t0[r] = __builtin_fmaf((float)d0[r], wsc0[gi] * xv[j], t0[r]);
+                    if (TW == 2) t1[r] = __builtin_fmaf((float)d1[r], wsc1[gi] * xv[j], t1[r]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // Three stages in a ring, two in flight while one computes: a stage
+    // takes about a microsecond to arrive, longer than one stage's work.
+    // Before computing stage c a wave waits for its own loads of stage c
+    // (those of stage c + 1 may stay in flight: the wave's loads a stage
+    // are counted below), then the barrier makes every wave's loads of c
+    // visible and frees the buffer of stage c - 1 for stage c + 2.
+    // Two stages: stage c + 1 loads while stage c computes. (A third stage
+    // in flight, with a block fewer a CU for its LDS, measured slower.)
+    auto step = [&](int c, DStage<TW>& cur, DStage<TW>& next) {
+        // This wave's loads of stage c (the only ones in flight) landed; the
+        // barrier: every wave's, and every wave is done with stage c - 1,
+        // whose buffer stage c + 1 takes. A bare barrier: __syncthreads
+        // would add nothing the wait does not already give.
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+        asm volatile("s_barrier" ::: "memory");
+        if (c + 1 < chunks) issue(c + 1, next);
+        compute(cur);
+    };
+    issue(0, st0);
+    for (int c = 0; c < chunks; c += 2) {
+        step(c, st0, st1);
+        if (c + 1 >= chunks) break;
+        step(c + 1, st1, st0);
+    }
+
+    // Epilogue, as gemm_kernel's (src/models/parts/causal_lm.rs:464-473).
+    const int r0 = P == 1 ? bn * BN + sub0 : bn * 64 + wn * 32;
+    const int r1 = P == 1 ? bn * BN + sub1 : n / 2 + r0;
+    const int m0 = mbase + (w % 2) * 32;
+    const int ldy = n / P;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int row = m0 + 8 * (r / 4) + 4 * h + r % 4;
+        if (row >= m) continue;
+        float v0 = t0[r], v1 = t1[r];
+        if (bias) {
+            v0 = v0 + bias[min(r0 + lr, n - 1)];
+            v1 = v1 + bias[min(r1 + lr, n - 1)];
+        }
+        if (a.relu) {
+            v0 = __builtin_fmaxf(v0, 0.0f);
+            v1 = __builtin_fmaxf(v1, 0.0f);
+        }
+        if (P == 2) {
+            a.y[(size_t)row * ldy + r0 + lr] = silu_trit(v0) * v1;
+            continue;
+        }
+        const size_t i0 = (size_t)row * ldy + r0 + lr, i1 = (size_t)row * ldy + r1 + lr;
+        if (r0 + lr < n) a.y[i0] = a.epilogue == EPI_RESIDUAL ? a.residual[i0] + v0 : v0;
+        if (TW == 2 && r1 + lr < n) a.y[i1] = a.epilogue == EPI_RESIDUAL ? a.residual[i1] + v1 : v1;
+    }
+}
+
 int group_of(const Layer& L) { return L.kind == INT8 ? 128 : 32; }
 
 struct Scratch {
@@ -394,11 +656,36 @@ Scratch carve(void* base, int m, int k) {
     return s;
 }
 
+// Whether 64-row weight blocks (four a CU) spread the product more evenly
+// than 128-row ones (three a CU) -- TRIT_HIP_GEMM_TILE=64 or 128 forces one.
+bool narrow(int n, int mb) {
+    static const int forced = [] {
+        const char* v = getenv("TRIT_HIP_GEMM_TILE");
+        return v && *v ? (int)strtol(v, nullptr, 10) : 0;
+    }();
+    if (forced) return forced == 64;
+    return true;
+}
+
 template <int G, bool HALF, int P>
 void launch_gemm(const Layer& L, const GemvArgs& a, const Scratch& sc, hipStream_t s) {
     const int nb = P == 1 ? (L.n + 127) / 128 : (L.n / 2) / 64;
     const int mb = sc.mpad / BM;
-    if (L.k % KC == 0)
+    if constexpr (P == 1) {
+        if (L.k % KD == 0 && narrow(L.n, mb)) {
+            const int nb1 = (L.n + 63) / 64;
+            launch_timed(a, gemm_dma_kernel<G, HALF, P, 1>, dim3(nb1 * mb), dim3(GEMM_THREADS), 0, s,
+                         (const int8_t*)sc.xq, (const float*)sc.xs, a.m, sc.mpad, L.codes.as<int8_t>(),
+                         (const void*)L.scales.ptr, L.bias.as<float>(), L.n, L.k, nb1, mb, a);
+            TRIT_HIP(hipGetLastError());
+            return;
+        }
+    }
+    if (L.k % KD == 0)
+        launch_timed(a, gemm_dma_kernel<G, HALF, P, 2>, dim3(nb * mb), dim3(GEMM_THREADS), 0, s,
+                     (const int8_t*)sc.xq, (const float*)sc.xs, a.m, sc.mpad, L.codes.as<int8_t>(),
+                     (const void*)L.scales.ptr, L.bias.as<float>(), L.n, L.k, nb, mb, a);
+    else if (L.k % KC == 0)
         launch_timed(a, gemm_kernel<G, HALF, P, false>, dim3(nb * mb), dim3(GEMM_THREADS), 0, s,
                      (const int8_t*)sc.xq, (const float*)sc.xs, a.m, sc.mpad, L.codes.as<int8_t>(),
                      (const void*)L.scales.ptr, L.bias.as<float>(), L.n, L.k, nb, mb, a);
