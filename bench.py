@@ -55,9 +55,9 @@ GATE_UP_TRAFFIC_BYTES = round((3353.1 * 2.0 + 24.0) * 1024)
 # WRITE_SIZE of one launch of 128 steps (127 forwards, positions 256..382)
 # over the forwards, FETCH_SIZE x 2.0 plus WRITE_SIZE x 1.0; the default
 # mode (f16 caches) and the exact mode (f32 caches).
-STEP_FETCH_KIB, STEP_WRITE_KIB = 51675338.375 / 127, 224158.5 / 127
+STEP_FETCH_KIB, STEP_WRITE_KIB = 51636554.562500 / 127, 222703.812500 / 127
 STEP_TRAFFIC_BYTES = round((STEP_FETCH_KIB * 2.0 + STEP_WRITE_KIB) * 1024)
-EXACT_FETCH_KIB, EXACT_WRITE_KIB = 54501672.875 / 127, 1387986.21875 / 127
+EXACT_FETCH_KIB, EXACT_WRITE_KIB = 54617490.937500 / 127, 1644912.000000 / 127
 EXACT_TRAFFIC_BYTES = round((EXACT_FETCH_KIB * 2.0 + EXACT_WRITE_KIB) * 1024)
 
 
