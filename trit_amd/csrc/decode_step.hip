@@ -592,10 +592,10 @@ __device__ __forceinline__ void load_norm(int t, const float* norm_w, NormRegs<J
 // Q8_0: 32-groups (8 lanes), the scale stored f16-rounded; int8: 128-groups
 // (32 lanes), the f32 scale (src/cpu/kernels.rs:661-737).
 template <int J, int WK>
-__device__ void quantize_block(int t, const float* x, const NormRegs<J>* nr, Smem& sm,
-                               const NormRegs<J>* fs = nullptr) {
+__device__ void quantize_block(int t, const float* x, const NormRegs<J>* nr, float inv_in, Smem& sm,
+                               const NormRegs<J>* fs = nullptr, bool inv_lds = false) {
     constexpr int ITEMS = J * 64;  // float4 items; a multiple of 64: whole waves
-    const float inv = sm.inv;
+    const float inv = inv_lds ? sm.inv : inv_in;
 #pragma unroll
     for (int i = 0; i < NormRegs<J>::N; ++i) {
         const int item = t + T * i;
@@ -2386,6 +2386,12 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
     // (the head needs them).
     int t, w, lane, rowq, rowo, rowgu, rowd, dround;
     bool aq, agu, ao, ad;
+    // The RMSNorm factor of sm.xres. The exact instances with registers to
+    // spare take it in every thread from Trit's serial sum, which every wave
+    // joins and returns itself: no barrier before the quantizer, which
+    // touches none of the norm's LDS. The others pass it through LDS
+    // (sm.inv, read by the quantizer: INV_LDS).
+    constexpr bool INV_LDS = !EXACT || KV32 || LONG;
     auto fresh = [&] {
         t = threadIdx.x;
         asm volatile("" : "+v"(t));
@@ -2495,16 +2501,21 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         if (layer > 0 && !gather<6>(t, a.X, a.d, lin, tag_of(tag0, layer - 1, 5), sm.xres, sm, deadline, st))
             leave();
         STAMP(1);
-        if constexpr (EXACT) {
-            const float inv = norm_inv_spec<JD>(t, sm.xres, a.eps, a.norm_window, sm);
-            if (t == 0) sm.inv = inv;
-        } else if (w == 0) {
-            const float inv = norm_inv_wave<JD>(t, sm.xres, a.eps);
-            if (lane == 0) sm.inv = inv;
+        float inv = 0.0f;
+        if constexpr (!INV_LDS) {
+            inv = norm_inv_spec<JD>(t, sm.xres, a.eps, a.norm_window, sm);
+        } else {
+            if constexpr (EXACT) {
+                const float v = norm_inv_spec<JD>(t, sm.xres, a.eps, a.norm_window, sm);
+                if (t == 0) sm.inv = v;
+            } else if (w == 0) {
+                const float v = norm_inv_wave<JD>(t, sm.xres, a.eps);
+                if (lane == 0) sm.inv = v;
+            }
+            __syncthreads();
         }
-        __syncthreads();
         STAMP(2);
-        quantize_block<JD, WK>(t, sm.xres, &nq, sm);
+        quantize_block<JD, WK>(t, sm.xres, &nq, inv, sm, nullptr, INV_LDS);
         STAMP(3);
         if (aq) {
             float acc[1];
@@ -2589,7 +2600,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
             // in flight.
             if (!gather<8>(t, a.ATT, a.qd, lin, tag_of(tag0, layer, 2), sm.xin, sm, deadline, st, nu)) leave();
         }
-        quantize_block<JO, WK>(t, sm.xin, (const NormRegs<JO>*)nullptr, sm);
+        quantize_block<JO, WK>(t, sm.xin, (const NormRegs<JO>*)nullptr, 1.0f, sm);
         STAMP(12);
         if (ao) {
             float acc[1];
@@ -2618,16 +2629,21 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         __syncthreads();
         if (!gather<MWK>(t, a.X, a.d, lin, tag_of(tag0, layer, 3), sm.xres, sm, deadline, st, px)) leave();
         STAMP(14);
-        if constexpr (EXACT) {
-            const float inv = norm_inv_spec<JD>(t, sm.xres, a.eps, a.norm_window, sm);
-            if (t == 0) sm.inv = inv;
-        } else if (w == 0) {
-            const float inv = norm_inv_wave<JD>(t, sm.xres, a.eps);
-            if (lane == 0) sm.inv = inv;
+        float inv_gu = 0.0f;
+        if constexpr (!INV_LDS) {
+            inv_gu = norm_inv_spec<JD>(t, sm.xres, a.eps, a.norm_window, sm);
+        } else {
+            if constexpr (EXACT) {
+                const float v = norm_inv_spec<JD>(t, sm.xres, a.eps, a.norm_window, sm);
+                if (t == 0) sm.inv = v;
+            } else if (w == 0) {
+                const float v = norm_inv_wave<JD>(t, sm.xres, a.eps);
+                if (lane == 0) sm.inv = v;
+            }
+            __syncthreads();
         }
-        __syncthreads();
         STAMP(15);
-        quantize_block<JD, WK>(t, sm.xres, &ngu, sm, a.ffn_scales ? &nfs : nullptr);
+        quantize_block<JD, WK>(t, sm.xres, &ngu, inv_gu, sm, a.ffn_scales ? &nfs : nullptr, INV_LDS);
         STAMP(16);
         if (agu) {
             float acc[2];
@@ -2646,7 +2662,7 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
         __syncthreads();
         if (!gather<MWK>(t, a.H, a.ffn, lin, tag_of(tag0, layer, 4), sm.xin, sm, deadline, st)) leave();
         STAMP(18);
-        quantize_block<JF, WK>(t, sm.xin, (const NormRegs<JF>*)nullptr, sm);
+        quantize_block<JF, WK>(t, sm.xin, (const NormRegs<JF>*)nullptr, 1.0f, sm);
         STAMP(19);
         if constexpr (DR == 1) {
             if (ad) {
