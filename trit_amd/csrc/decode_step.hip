@@ -2527,12 +2527,12 @@ __global__ __launch_bounds__(T, 1) void step_kernel(StepArgs a, int step0, int p
                     put(a.QKV + rowq, acc[0], tag_of(tag0, layer, 0));
             }
         }
-        __syncthreads();
+        // No barrier here: the attention's first writes to LDS (the
+        // gathered q/k/v, the values) touch nothing the qkv product reads.
         STAMP(4);
         if constexpr (DPB > 0) {
             // attention in one pass: its outputs are the o product's input.
             bool ok;
-            // The attention on every block (one key/value head an XCD).
             // The attention on every block (one key/value head an XCD).
             const bool wide = EXACT && !LONG && !KV32 && a.local_qkv;
             if (wide)
